@@ -1,0 +1,192 @@
+/*
+ * ss_hip.h - C-ABI of the MI355X (gfx950) backend.
+ *
+ * The C host code (engine, GGUF loader) reaches the GPU only through these
+ * functions: plain pointers and sizes, no HIP or C++ types. They replace the
+ * reference's Metal backend plug (SlipStream/src/backends/metal_backend.h:21-75)
+ * and the CPU kernels it falls back to (src/core/quantize.h:106-117,
+ * src/core/tensor.h:38-123), and take over the whole per-token sweep that
+ * src/core/layer_scheduler.c:291-679 runs on the CPU.
+ *
+ * Conventions: functions return 0 or a negative ss_error_t value
+ * (SS_ERROR_INVALID_PARAMS -5, SS_ERROR_OUT_OF_MEMORY -3, SS_ERROR_BACKEND -7)
+ * and never throw; ss_hip_last_error() holds a message for the calling
+ * thread. "dev" pointers are device memory; a NULL stream means the
+ * context's own stream. One context is used by one thread at a time.
+ *
+ * Device weight layout: a GGUF Q4_0/Q8_0 matrix of R rows and C columns
+ * (R*C/32 blocks of fp16 d + 16/32 code bytes) is stored on the device as
+ * two planes, codes first: code bytes [R][C/32][16 or 32] then, at the next
+ * 256-byte boundary, scales [R][C/32] as binary16. ss_hip_pack_matrix makes
+ * it; ss_hip_packed_bytes gives its size. Bytes per weight are unchanged.
+ */
+#ifndef SS_HIP_H
+#define SS_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ss_hip_ctx ss_hip_ctx_t;
+typedef struct ss_hip_model ss_hip_model_t;
+
+/* ggml tensor types accepted (src/core/gguf_loader.h:41-55) */
+#define SS_HIP_F32 0
+#define SS_HIP_F16 1
+#define SS_HIP_Q4_0 2
+#define SS_HIP_Q8_0 8
+
+/* KV cache types (match ss_kv_type_t in slipstream.h) */
+#define SS_HIP_KV_F16 0
+#define SS_HIP_KV_INT8 1
+
+/* ---- context (metal_backend.h:21 ss_metal_init, :75 ss_metal_free) ---- */
+ss_hip_ctx_t *ss_hip_init(int32_t device);
+void ss_hip_free(ss_hip_ctx_t *ctx);
+const char *ss_hip_last_error(void);
+int32_t ss_hip_device_count(void);
+int32_t ss_hip_device_name(int32_t device, char *buf, int32_t len);
+void *ss_hip_stream(ss_hip_ctx_t *ctx);          /* the context's hipStream_t */
+int32_t ss_hip_sync(ss_hip_ctx_t *ctx);
+
+/* ---- device memory, so C callers need no HIP headers ---- */
+void *ss_hip_malloc(ss_hip_ctx_t *ctx, size_t bytes);
+int32_t ss_hip_mfree(ss_hip_ctx_t *ctx, void *dev);
+int32_t ss_hip_memcpy_h2d(ss_hip_ctx_t *ctx, void *dev, const void *host, size_t bytes);
+int32_t ss_hip_memcpy_d2h(ss_hip_ctx_t *ctx, void *host, const void *dev, size_t bytes);
+
+/* ---- weight packing: GGUF block layout (host) -> device planes ---- */
+size_t ss_hip_packed_bytes(int32_t ggml_type, int32_t rows, int32_t cols);
+int32_t ss_hip_pack_matrix(ss_hip_ctx_t *ctx, void *dst_dev, const void *src_host,
+                           int32_t ggml_type, int32_t rows, int32_t cols);
+
+/* ---- single ops on device buffers ---- */
+
+/* y = W x, W packed Q4_0/Q8_0 [rows x cols], fp32 x/y, fp32 accumulation.
+ * Replaces ss_dequant_matvec (quantize.h:111-112, quantize.c:446-494) and
+ * ss_metal_matvec_q4_0 (metal_backend.h:37-42). */
+int32_t ss_hip_matvec(ss_hip_ctx_t *ctx, float *y_dev, const void *w_dev, const float *x_dev,
+                      int32_t rows, int32_t cols, int32_t ggml_type, void *stream);
+
+/* y = W rmsnorm(x, nw, eps) (+ y when accumulate != 0): the matvec with the
+ * RMSNorm of tensor.c:114-131 folded in front and the residual add of
+ * layer_scheduler.c:484 folded behind. nw may be NULL (no norm). */
+int32_t ss_hip_matvec_fused(ss_hip_ctx_t *ctx, float *y_dev, const void *w_dev,
+                            const float *x_dev, const float *nw_dev, float eps, int32_t accumulate,
+                            int32_t rows, int32_t cols, int32_t ggml_type, void *stream);
+
+/* out = u * silu(g) with g = Wg rmsnorm(x), u = Wu rmsnorm(x):
+ * layer_scheduler.c:489-549 in one kernel. */
+int32_t ss_hip_ffn_gate_up(ss_hip_ctx_t *ctx, float *out_dev, const void *wg_dev,
+                           const void *wu_dev, const float *x_dev, const float *nw_dev, float eps,
+                           int32_t rows, int32_t cols, int32_t ggml_type, void *stream);
+
+/* tensor.c:114-131 */
+int32_t ss_hip_rmsnorm(ss_hip_ctx_t *ctx, float *out_dev, const float *x_dev, const float *w_dev,
+                       int32_t n, float eps, void *stream);
+
+/* tensor.c:220-275 (GPT-J pairs when is_neox == 0, halves otherwise) */
+int32_t ss_hip_rope(ss_hip_ctx_t *ctx, float *q_dev, float *k_dev, int32_t n_heads,
+                    int32_t n_kv_heads, int32_t head_dim, int32_t rope_dim, int32_t pos,
+                    float theta, int32_t is_neox, void *stream);
+
+/* KV append at pos (layer_scheduler.c:409-413). Cache layout
+ * [n_kv_heads][max_seq][head_dim] of binary16 (SS_HIP_KV_F16) or int8
+ * codes (SS_HIP_KV_INT8, with k_scale/v_scale [max_seq] fp32, one absmax
+ * scale per position over all heads, layer_scheduler.c:101-118). */
+int32_t ss_hip_kv_append(ss_hip_ctx_t *ctx, void *k_cache, void *v_cache, float *k_scale,
+                         float *v_scale, const float *k_dev, const float *v_dev,
+                         int32_t n_kv_heads, int32_t head_dim, int32_t max_seq, int32_t pos,
+                         int32_t kv_type, void *stream);
+
+/* Single-query GQA attention over positions 0..seq_len-1 of one layer's
+ * cache (layer_scheduler.c:415-468): out[n_heads*head_dim]. */
+int32_t ss_hip_attention(ss_hip_ctx_t *ctx, float *out_dev, const float *q_dev,
+                         const void *k_cache, const void *v_cache, const float *k_scale,
+                         const float *v_scale, int32_t n_heads, int32_t n_kv_heads,
+                         int32_t head_dim, int32_t max_seq, int32_t seq_len, int32_t kv_type,
+                         void *stream);
+
+/* out[i] = up[i] * (g / (1 + exp(-g))), g = gate[i] (layer_scheduler.c:533-549) */
+int32_t ss_hip_swiglu(ss_hip_ctx_t *ctx, float *out_dev, const float *gate_dev,
+                      const float *up_dev, int32_t n, void *stream);
+
+/* index of the first maximum (tensor.c:318-328) into *out_dev (int32) */
+int32_t ss_hip_argmax(ss_hip_ctx_t *ctx, int32_t *out_dev, const float *x_dev, int32_t n,
+                      void *stream);
+
+/* dequantise row `token` of a packed [rows x cols] table (layer_scheduler.c:584-595) */
+int32_t ss_hip_embed_row(ss_hip_ctx_t *ctx, float *out_dev, const void *table_dev,
+                         int32_t ggml_type, int32_t rows, int32_t cols, int32_t token,
+                         void *stream);
+
+/* ---- Metal-shaped plug on host pointers (metal_backend.h:27-70) ----
+ * W is a host pointer in GGUF block layout (e.g. into the GGUF mmap); it is
+ * packed and uploaded the first time it is seen and kept, keyed by pointer
+ * (the zero-copy registry of metal_backend.m:190-235). Returns false on any
+ * failure, like the Metal calls. */
+int32_t ss_hip_matvec_host(ss_hip_ctx_t *ctx, float *out, const void *mat, const float *vec,
+                           int32_t rows, int32_t cols, int32_t ggml_type);
+int32_t ss_hip_should_use_gpu(int32_t rows, int32_t cols);
+
+/* ---- whole-model decode ---- */
+
+typedef struct {
+    const void *data;   /* host pointer, GGUF layout (borrowed during create) */
+    int32_t type;       /* SS_HIP_* */
+    int32_t rows;       /* GGUF dims[1]; 1 for vectors */
+    int32_t cols;       /* GGUF dims[0] */
+} ss_hip_tensor_t;
+
+/* per-layer tensor order in ss_hip_model_desc_t.layers */
+enum {
+    SS_HIP_ATTN_NORM = 0, SS_HIP_WQ, SS_HIP_WK, SS_HIP_WV, SS_HIP_WO,
+    SS_HIP_FFN_NORM, SS_HIP_W_GATE, SS_HIP_W_UP, SS_HIP_W_DOWN, SS_HIP_LAYER_TENSORS
+};
+
+typedef struct {
+    int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, rope_dim, ffn, vocab, max_seq;
+    float rms_eps, rope_theta;
+    int32_t kv_type;     /* SS_HIP_KV_* */
+    int32_t use_graph;   /* replay the token sweep as one HIP graph */
+    ss_hip_tensor_t token_embd, output_norm, output;
+    const ss_hip_tensor_t *layers;   /* n_layers * SS_HIP_LAYER_TENSORS */
+} ss_hip_model_desc_t;
+
+/* ss_scheduler_init (layer_scheduler.h:95-96): upload + pack all weights,
+ * allocate the KV cache and working buffers. */
+ss_hip_model_t *ss_hip_model_create(ss_hip_ctx_t *ctx, const ss_hip_model_desc_t *desc);
+void ss_hip_model_free(ss_hip_model_t *m);
+
+/* ss_scheduler_forward (layer_scheduler.h:107) */
+int32_t ss_hip_eval_token(ss_hip_model_t *m, int32_t token, int32_t pos, float *logits_host,
+                          int32_t *argmax_out);
+/* ss_scheduler_prefill (layer_scheduler.h:119) */
+int32_t ss_hip_eval_prompt(ss_hip_model_t *m, const int32_t *tokens, int32_t n,
+                           int32_t start_pos, float *logits_host, int32_t *argmax_out);
+/* device-side greedy continuation (see ss_decode_greedy) */
+int32_t ss_hip_decode_greedy(ss_hip_model_t *m, int32_t n_steps, int32_t *tokens_out);
+/* ss_scheduler_reset (layer_scheduler.h:132) */
+int32_t ss_hip_kv_reset(ss_hip_model_t *m);
+int32_t ss_hip_kv_write(ss_hip_model_t *m, int32_t layer, int32_t pos0, int32_t n_pos,
+                        const uint16_t *k_f16, const uint16_t *v_f16);
+/* final hidden state (after the output norm) of the last evaluated token */
+int32_t ss_hip_hidden(ss_hip_model_t *m, float *host_out);
+/* cancellation flag polled between layers when the sweep is not a graph */
+void ss_hip_set_cancel_flag(ss_hip_model_t *m, const volatile int32_t *flag);
+/* bytes of device memory held by the model (weights, KV, buffers) */
+uint64_t ss_hip_model_bytes(const ss_hip_model_t *m);
+
+/* ---- timing support for the benchmark ----
+ * Records per-kernel-class device time (HIP events on the launching
+ * stream) for the next eval calls; kinds: 0 = all matvecs, 1 = attention. */
+int32_t ss_hip_profile_begin(ss_hip_model_t *m);
+int32_t ss_hip_profile_end(ss_hip_model_t *m, double *ms_out, int32_t n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SS_HIP_H */

@@ -1,0 +1,1002 @@
+/*
+ * ss_oracle.c - CPU restatement of SlipStream's per-token decode path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP product and the CPU
+ * baseline timed beside it. The product never links, loads or calls this.
+ *
+ * Citations are file:line in the reference repository, relative to its
+ * SlipStream/ directory. Deliberate differences from the reference:
+ *  - The context cap of 512 positions (src/core/layer_scheduler.c:202) and the
+ *    stack arrays scores[512]/tmp_kv[256] (:430-431) are lifted; max_seq is
+ *    the caller's.
+ *  - Apple vDSP_dotpr (quantize.c:488, layer_scheduler.c:442), whose
+ *    summation order is unspecified, is restated as orc_dot: eight strided
+ *    fp32 partial sums folded pairwise. cblas_saxpy (:466) is y = w*x + y
+ *    element by element. No FMA contraction (built with -ffp-contract=off).
+ *  - GCD dispatch_apply (quantize.c:475, layer_scheduler.c:424) is restated
+ *    as a pthread pool with the same chunking: rows in ceil(rows/ncpu)
+ *    chunks, attention one task per query head.
+ *  - Besides the reference's int8 KV cache there is an fp16 KV mode: K and V
+ *    are rounded to binary16 when appended and widened when read, inside the
+ *    fp32 KV structure of layer_scheduler.c.orig:289-342.
+ *  - Only the llama block is restated (no fused qkv, biases, Gemma or NeoX
+ *    branches); orc_model_open rejects files that need them.
+ */
+#define _GNU_SOURCE
+#include "ss_oracle.h"
+
+#include <fcntl.h>
+#include <float.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <sys/mman.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+/* ------------------------------------------------------------------------ */
+/* Element ops                                                              */
+/* ------------------------------------------------------------------------ */
+
+/* quantize.c:20-56 - exact half to float, with subnormals, inf and NaN. */
+float orc_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)(h & 0x8000) << 16;
+    uint32_t e = (h >> 10) & 0x1F;
+    uint32_t m = h & 0x3FF;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {
+            e = 1;
+            while (!(m & 0x400)) { m <<= 1; e--; }
+            m &= 0x3FF;
+            bits = sign | ((e + 127 - 15) << 23) | (m << 13);
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 127 - 15) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+/* IEEE binary16 with round-to-nearest-even (what a hardware f32->f16
+ * conversion does); used by the fp16 KV mode. */
+uint16_t orc_f32_to_f16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u;
+    uint32_t ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x7F800000u) {                       /* inf / nan */
+        if (ax == 0x7F800000u) return (uint16_t)(sign | 0x7C00u);
+        return (uint16_t)(sign | 0x7E00u | ((ax >> 13) & 0x3FFu));
+    }
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u); /* >= 65520 -> inf */
+    uint32_t ef = ax >> 23;
+    if (ef >= 113) {                               /* normal half */
+        uint32_t mant = ax & 0x7FFFFFu;
+        uint32_t h = ((ef - 112) << 10) | (mant >> 13);
+        uint32_t rem = mant & 0x1FFFu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+        return (uint16_t)(sign | h);
+    }
+    if (ef < 102) return (uint16_t)sign;           /* below half of the smallest subnormal */
+    uint32_t m = (ax & 0x7FFFFFu) | 0x800000u;
+    uint32_t shift = 126 - ef;                     /* 14..24 */
+    uint32_t h = m >> shift;
+    uint32_t rem = m & ((1u << shift) - 1u);
+    uint32_t half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+
+/* quantize.c:60-72 (Q4_0), :139-149 (Q8_0), :389-442 (dispatch; F32 copy,
+ * F16 widen). Blocks: Q4_0 = fp16 d + 16 bytes of nibbles (18 B),
+ * Q8_0 = fp16 d + 32 int8 (34 B) (quantize.h:14-17,43-46). */
+void orc_dequantize(const void *src, float *dst, int32_t n, int32_t type) {
+    const uint8_t *p = (const uint8_t *)src;
+    switch (type) {
+    case ORC_F32:
+        memcpy(dst, src, (size_t)n * sizeof(float));
+        break;
+    case ORC_F16:
+        for (int32_t i = 0; i < n; i++) {
+            uint16_t h;
+            memcpy(&h, p + 2 * (size_t)i, 2);
+            dst[i] = orc_f16_to_f32(h);
+        }
+        break;
+    case ORC_Q4_0:
+        for (int32_t b = 0; b < n / 32; b++) {
+            const uint8_t *blk = p + (size_t)b * 18;
+            uint16_t dh;
+            memcpy(&dh, blk, 2);
+            float scale = orc_f16_to_f32(dh);
+            for (int32_t i = 0; i < 16; i++) {
+                uint8_t byte = blk[2 + i];
+                dst[b * 32 + i] = scale * ((int32_t)(byte & 0xF) - 8);
+                dst[b * 32 + i + 16] = scale * ((int32_t)(byte >> 4) - 8);
+            }
+        }
+        break;
+    case ORC_Q8_0:
+        for (int32_t b = 0; b < n / 32; b++) {
+            const uint8_t *blk = p + (size_t)b * 34;
+            uint16_t dh;
+            memcpy(&dh, blk, 2);
+            float scale = orc_f16_to_f32(dh);
+            for (int32_t i = 0; i < 32; i++)
+                dst[b * 32 + i] = scale * (float)(int8_t)blk[2 + i];
+        }
+        break;
+    default:
+        memset(dst, 0, (size_t)n * sizeof(float));
+        break;
+    }
+}
+
+static size_t orc_row_bytes(int32_t cols, int32_t type) {
+    switch (type) {
+    case ORC_F32: return (size_t)cols * 4;
+    case ORC_F16: return (size_t)cols * 2;
+    case ORC_Q4_0: return (size_t)(cols / 32) * 18;
+    case ORC_Q8_0: return (size_t)(cols / 32) * 34;
+    default: return 0;
+    }
+}
+
+/* Stand-in for vDSP_dotpr: eight strided partial sums, folded pairwise. */
+float orc_dot(const float *a, const float *b, int32_t n) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int32_t i = 0;
+    for (; i + 8 <= n; i += 8)
+        for (int j = 0; j < 8; j++) acc[j] += a[i + j] * b[i + j];
+    float s = ((acc[0] + acc[4]) + (acc[1] + acc[5])) + ((acc[2] + acc[6]) + (acc[3] + acc[7]));
+    for (; i < n; i++) s += a[i] * b[i];
+    return s;
+}
+
+/* cpu_neon.c:109-115 (scalar branch of ss_neon_rmsnorm, reached through
+ * tensor.c:114-118 for F32 weights). */
+void orc_rmsnorm(float *out, const float *x, const float *w, int32_t n, float eps) {
+    float ss = 0.0f;
+    for (int32_t i = 0; i < n; i++) ss += x[i] * x[i];
+    float scale = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int32_t i = 0; i < n; i++) out[i] = x[i] * scale * w[i];
+}
+
+/* tensor.c:154-173 */
+void orc_softmax(float *x, int32_t n) {
+    float max_val = -FLT_MAX;
+    for (int32_t i = 0; i < n; i++)
+        if (x[i] > max_val) max_val = x[i];
+    float sum = 0.0f;
+    for (int32_t i = 0; i < n; i++) {
+        x[i] = expf(x[i] - max_val);
+        sum += x[i];
+    }
+    float inv = 1.0f / sum;
+    for (int32_t i = 0; i < n; i++) x[i] *= inv;
+}
+
+/* layer_scheduler.c:540-547: up * (g / (1 + exp(-g))) */
+float orc_silu_mul(float g, float u) { return u * (g / (1.0f + expf(-g))); }
+
+/* tensor.c:220-275 */
+void orc_rope(float *q, float *k, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+              int32_t rope_dim, int32_t pos, float theta, int32_t is_neox) {
+    if (is_neox) {
+        int32_t half_d = rope_dim / 2;
+        for (int32_t i = 0; i < half_d; i++) {
+            float freq = 1.0f / powf(theta, (float)(i * 2) / (float)rope_dim);
+            float angle = (float)pos * freq;
+            float c = cosf(angle), s = sinf(angle);
+            for (int32_t h = 0; h < n_heads; h++) {
+                float *qh = q + h * head_dim;
+                float a = qh[i], b = qh[i + half_d];
+                qh[i] = a * c - b * s;
+                qh[i + half_d] = a * s + b * c;
+            }
+            for (int32_t h = 0; h < n_kv_heads; h++) {
+                float *kh = k + h * head_dim;
+                float a = kh[i], b = kh[i + half_d];
+                kh[i] = a * c - b * s;
+                kh[i + half_d] = a * s + b * c;
+            }
+        }
+        return;
+    }
+    for (int32_t i = 0; i < rope_dim; i += 2) {
+        float freq = 1.0f / powf(theta, (float)i / (float)rope_dim);
+        float angle = (float)pos * freq;
+        float c = cosf(angle), s = sinf(angle);
+        for (int32_t h = 0; h < n_heads; h++) {
+            float *qh = q + h * head_dim;
+            float a = qh[i], b = qh[i + 1];
+            qh[i] = a * c - b * s;
+            qh[i + 1] = a * s + b * c;
+        }
+        for (int32_t h = 0; h < n_kv_heads; h++) {
+            float *kh = k + h * head_dim;
+            float a = kh[i], b = kh[i + 1];
+            kh[i] = a * c - b * s;
+            kh[i + 1] = a * s + b * c;
+        }
+    }
+}
+
+/* The (cos, sin) pairs tensor.c:250-254 computes, tabulated per position:
+ * cs[(pos * rope_dim/2 + i/2) * 2 + {0,1}]. */
+void orc_rope_table(float *cs, int32_t rope_dim, int32_t n_pos, float theta) {
+    for (int32_t p = 0; p < n_pos; p++)
+        for (int32_t i = 0; i < rope_dim; i += 2) {
+            float freq = 1.0f / powf(theta, (float)i / (float)rope_dim);
+            float angle = (float)p * freq;
+            size_t o = ((size_t)p * (rope_dim / 2) + i / 2) * 2;
+            cs[o] = cosf(angle);
+            cs[o + 1] = sinf(angle);
+        }
+}
+
+/* tensor.c:318-328: index of the first strict maximum. */
+int32_t orc_argmax(const float *x, int32_t n) {
+    int32_t idx = 0;
+    float mv = x[0];
+    for (int32_t i = 1; i < n; i++)
+        if (x[i] > mv) { mv = x[i]; idx = i; }
+    return idx;
+}
+
+/* layer_scheduler.c:101-118 */
+void orc_kv_int8_encode(const float *src, int8_t *q, float *scale, int32_t n) {
+    float max_val = 0.0f;
+    for (int32_t i = 0; i < n; i++) {
+        float v = fabsf(src[i]);
+        if (v > max_val) max_val = v;
+    }
+    float s = max_val / 127.0f;
+    *scale = s;
+    float inv = s > 0.0f ? 1.0f / s : 0.0f;
+    for (int32_t i = 0; i < n; i++) q[i] = (int8_t)roundf(src[i] * inv);
+}
+
+/* One head of layer_scheduler.c:421-467 over fp32 keys/values whose
+ * consecutive positions are kv_stride floats apart. */
+void orc_attention_head(float *out, const float *q, const float *keys, const float *values,
+                        int32_t head_dim, int32_t seq_len, int32_t kv_stride) {
+    float scale = 1.0f / sqrtf((float)head_dim);
+    float *scores = (float *)malloc((size_t)seq_len * sizeof(float));
+    for (int32_t t = 0; t < seq_len; t++)
+        scores[t] = orc_dot(q, keys + (size_t)t * kv_stride, head_dim) * scale;
+    orc_softmax(scores, seq_len);
+    memset(out, 0, (size_t)head_dim * sizeof(float));
+    for (int32_t t = 0; t < seq_len; t++) {
+        const float *vt = values + (size_t)t * kv_stride;
+        for (int32_t d = 0; d < head_dim; d++) out[d] = scores[t] * vt[d] + out[d];
+    }
+    free(scores);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Thread pool (stand-in for GCD dispatch_apply)                             */
+/* ------------------------------------------------------------------------ */
+
+#define ORC_MAX_THREADS 128
+
+typedef void (*orc_task_fn)(void *arg, int32_t idx);
+
+static struct {
+    pthread_mutex_t mu;
+    pthread_cond_t cv_go, cv_idle;
+    pthread_t th[ORC_MAX_THREADS];
+    int nworkers;    /* threads besides the caller */
+    int nthreads;    /* total, caller included */
+    unsigned gen;
+    int active;
+    int stop;
+    orc_task_fn fn;
+    void *arg;
+    int32_t count;
+    int32_t next;
+} g_pool = {PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER, PTHREAD_COND_INITIALIZER};
+
+static void pool_drain(orc_task_fn fn, void *arg, int32_t count) {
+    for (;;) {
+        int32_t i = __atomic_fetch_add(&g_pool.next, 1, __ATOMIC_RELAXED);
+        if (i >= count) break;
+        fn(arg, i);
+    }
+}
+
+static void *pool_worker(void *unused) {
+    (void)unused;
+    unsigned seen = 0;
+    pthread_mutex_lock(&g_pool.mu);
+    seen = g_pool.gen;
+    for (;;) {
+        while (g_pool.gen == seen && !g_pool.stop) pthread_cond_wait(&g_pool.cv_go, &g_pool.mu);
+        if (g_pool.stop) break;
+        seen = g_pool.gen;
+        orc_task_fn fn = g_pool.fn;
+        void *arg = g_pool.arg;
+        int32_t count = g_pool.count;
+        pthread_mutex_unlock(&g_pool.mu);
+        pool_drain(fn, arg, count);
+        pthread_mutex_lock(&g_pool.mu);
+        if (--g_pool.active == 0) pthread_cond_signal(&g_pool.cv_idle);
+    }
+    pthread_mutex_unlock(&g_pool.mu);
+    return NULL;
+}
+
+static void pool_stop(void) {
+    pthread_mutex_lock(&g_pool.mu);
+    g_pool.stop = 1;
+    pthread_cond_broadcast(&g_pool.cv_go);
+    pthread_mutex_unlock(&g_pool.mu);
+    for (int i = 0; i < g_pool.nworkers; i++) pthread_join(g_pool.th[i], NULL);
+    g_pool.nworkers = 0;
+    g_pool.stop = 0;
+}
+
+void orc_set_threads(int32_t n) {
+    if (n <= 0) {
+        const char *env = getenv("OMP_NUM_THREADS");
+        n = env ? atoi(env) : 0;
+        if (n <= 0) n = (int32_t)sysconf(_SC_NPROCESSORS_ONLN);
+    }
+    if (n < 1) n = 1;
+    if (n > ORC_MAX_THREADS) n = ORC_MAX_THREADS;
+    if (g_pool.nthreads == n) return;
+    if (g_pool.nworkers) pool_stop();
+    pthread_mutex_lock(&g_pool.mu);
+    g_pool.nthreads = n;
+    int started = 0;
+    for (int i = 0; i < n - 1; i++)
+        if (pthread_create(&g_pool.th[started], NULL, pool_worker, NULL) == 0) started++;
+    g_pool.nworkers = started;
+    g_pool.nthreads = started + 1;
+    pthread_mutex_unlock(&g_pool.mu);
+}
+
+int32_t orc_get_threads(void) {
+    if (g_pool.nthreads == 0) orc_set_threads(0);
+    return g_pool.nthreads;
+}
+
+static void pool_run(orc_task_fn fn, void *arg, int32_t count) {
+    if (g_pool.nthreads == 0) orc_set_threads(0);
+    if (count <= 0) return;
+    if (g_pool.nworkers == 0 || count == 1) {
+        for (int32_t i = 0; i < count; i++) fn(arg, i);
+        return;
+    }
+    pthread_mutex_lock(&g_pool.mu);
+    g_pool.fn = fn;
+    g_pool.arg = arg;
+    g_pool.count = count;
+    g_pool.next = 0;
+    g_pool.active = g_pool.nworkers;
+    g_pool.gen++;
+    pthread_cond_broadcast(&g_pool.cv_go);
+    pthread_mutex_unlock(&g_pool.mu);
+    pool_drain(fn, arg, count);
+    pthread_mutex_lock(&g_pool.mu);
+    while (g_pool.active > 0) pthread_cond_wait(&g_pool.cv_idle, &g_pool.mu);
+    pthread_mutex_unlock(&g_pool.mu);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Matvec: quantize.c:446-494                                               */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+    float *out;
+    const uint8_t *w;
+    const float *x;
+    float *tmp;
+    int32_t rows, cols, type, rows_per_chunk;
+    size_t row_bytes;
+} mv_job_t;
+
+static void mv_chunk(void *arg, int32_t chunk) {
+    mv_job_t *j = (mv_job_t *)arg;
+    int32_t r0 = chunk * j->rows_per_chunk;
+    int32_t r1 = r0 + j->rows_per_chunk;
+    if (r1 > j->rows) r1 = j->rows;
+    float *tmp = j->tmp + (size_t)chunk * j->cols;
+    for (int32_t r = r0; r < r1; r++) {
+        orc_dequantize(j->w + (size_t)r * j->row_bytes, tmp, j->cols, j->type);
+        j->out[r] = orc_dot(tmp, j->x, j->cols);
+    }
+}
+
+void orc_dequant_matvec(float *out, const void *w, const float *x, int32_t rows, int32_t cols,
+                        int32_t type) {
+    size_t rb = orc_row_bytes(cols, type);
+    if (rb == 0 || rows <= 0) return;
+    int32_t ncpu = orc_get_threads();
+    if (ncpu > rows) ncpu = rows;
+    mv_job_t j = {out, (const uint8_t *)w, x, NULL, rows, cols, type, (rows + ncpu - 1) / ncpu, rb};
+    j.tmp = (float *)malloc((size_t)ncpu * cols * sizeof(float));
+    if (!j.tmp) return;
+    pool_run(mv_chunk, &j, ncpu);
+    free(j.tmp);
+}
+
+/* ------------------------------------------------------------------------ */
+/* GGUF parse: gguf_loader.c:22-62, 174-206, 210-485                         */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+    char name[256];
+    uint32_t n_dims;
+    uint64_t dims[4];
+    int32_t type;
+    uint64_t offset; /* absolute */
+    uint64_t size;
+    int32_t layer;
+} orc_tensor_t;
+
+typedef struct {
+    const orc_tensor_t *attn_norm, *wq, *wk, *wv, *wo, *ffn_norm, *wg, *wu, *wd;
+} orc_layer_t;
+
+struct orc_model {
+    int fd;
+    uint8_t *base;
+    uint64_t fsize;
+    orc_tensor_t *tensors;
+    uint64_t n_tensors;
+    orc_layer_t *layers;
+    const orc_tensor_t *embd, *out_norm, *out;
+    char arch[64];
+    uint32_t n_layers, d, n_heads, n_kv_heads, vocab_meta, ctx_len, ffn, key_len, rope_dim_meta;
+    float theta, eps;
+    int32_t hd, rope_dim, vocab, max_seq, kv_mode, kv_dim, neox;
+    /* KV cache, [L][max_seq][kv_dim] (+ per-(L,pos) scales in int8 mode) */
+    int8_t *kq, *vq;
+    float *ks, *vs;
+    uint16_t *kh, *vh;
+    /* working state */
+    float *hidden, *residual, *attn_out, *ffn_buf, *ffn_gate, *q, *k, *v, *logits;
+};
+
+typedef struct {
+    const uint8_t *p;
+    uint64_t pos, size;
+    int bad;
+} rd_t;
+
+static uint32_t rd_u32(rd_t *r) {
+    if (r->pos + 4 > r->size) { r->bad = 1; return 0; }
+    uint32_t v;
+    memcpy(&v, r->p + r->pos, 4);
+    r->pos += 4;
+    return v;
+}
+static uint64_t rd_u64(rd_t *r) {
+    if (r->pos + 8 > r->size) { r->bad = 1; return 0; }
+    uint64_t v;
+    memcpy(&v, r->p + r->pos, 8);
+    r->pos += 8;
+    return v;
+}
+static float rd_f32(rd_t *r) {
+    uint32_t u = rd_u32(r);
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+/* returns pointer into the file and its length; NULL on overrun */
+static const char *rd_str(rd_t *r, uint64_t *len) {
+    *len = rd_u64(r);
+    if (r->bad || r->pos + *len > r->size) { r->bad = 1; return NULL; }
+    const char *s = (const char *)r->p + r->pos;
+    r->pos += *len;
+    return s;
+}
+
+static void rd_skip(rd_t *r, uint32_t type) {  /* gguf_loader.c:130-165 */
+    uint64_t len;
+    switch (type) {
+    case 0: case 1: case 7: r->pos += 1; break;
+    case 2: case 3: r->pos += 2; break;
+    case 4: case 5: case 6: r->pos += 4; break;
+    case 10: case 11: case 12: r->pos += 8; break;
+    case 8: rd_str(r, &len); break;
+    case 9: {
+        uint32_t at = rd_u32(r);
+        uint64_t n = rd_u64(r);
+        for (uint64_t i = 0; i < n && !r->bad; i++) rd_skip(r, at);
+        break;
+    }
+    default: break;
+    }
+}
+
+static int key_is(const char *k, uint64_t kl, const char *s) {
+    return kl == strlen(s) && memcmp(k, s, kl) == 0;
+}
+static int key_ends(const char *k, uint64_t kl, const char *s) {
+    size_t sl = strlen(s);
+    return kl >= sl && memcmp(k + kl - sl, s, sl) == 0;
+}
+
+static uint32_t type_block(int32_t t) { return (t == ORC_Q4_0 || t == ORC_Q8_0) ? 32 : 1; }
+static uint32_t type_size(int32_t t) {
+    switch (t) {
+    case ORC_F32: return 4;
+    case ORC_F16: return 2;
+    case ORC_Q4_0: return 18;
+    case ORC_Q8_0: return 34;
+    default: return 0;
+    }
+}
+
+/* gguf_loader.c:174-189 */
+static int32_t parse_layer(const char *name) {
+    const char *blk = strstr(name, "blk.");
+    if (!blk) return -1;
+    int32_t idx = 0;
+    const char *p = blk + 4;
+    while (*p >= '0' && *p <= '9') { idx = idx * 10 + (*p - '0'); p++; }
+    return *p == '.' ? idx : -1;
+}
+
+/* layer_scheduler.c:27-39: first tensor of the layer whose name ends in suffix */
+static const orc_tensor_t *find_suffix(const orc_model_t *m, int32_t layer, const char *suffix) {
+    size_t sl = strlen(suffix);
+    for (uint64_t i = 0; i < m->n_tensors; i++) {
+        const orc_tensor_t *t = &m->tensors[i];
+        if (t->layer != layer) continue;
+        size_t nl = strlen(t->name);
+        if (nl >= sl && strcmp(t->name + nl - sl, suffix) == 0) return t;
+    }
+    return NULL;
+}
+static const orc_tensor_t *find_global(const orc_model_t *m, const char *name) {
+    for (uint64_t i = 0; i < m->n_tensors; i++)
+        if (strcmp(m->tensors[i].name, name) == 0) return &m->tensors[i];
+    return NULL;
+}
+
+static const void *tdata(const orc_model_t *m, const orc_tensor_t *t) {
+    if (!t || t->offset + t->size > m->fsize) return NULL;
+    return m->base + t->offset;
+}
+
+static int parse_gguf(orc_model_t *m) {
+    rd_t r = {m->base, 0, m->fsize, 0};
+    if (rd_u32(&r) != 0x46554747u) return -1;
+    uint32_t ver = rd_u32(&r);
+    if (ver < 2 || ver > 3) return -1;
+    uint64_t n_tensors = rd_u64(&r);
+    uint64_t n_kv = rd_u64(&r);
+    for (uint64_t i = 0; i < n_kv; i++) {
+        uint64_t kl;
+        const char *k = rd_str(&r, &kl);
+        if (!k) return -1;
+        uint32_t vt = rd_u32(&r);
+        if (key_is(k, kl, "general.architecture") && vt == 8) {
+            uint64_t sl;
+            const char *s = rd_str(&r, &sl);
+            if (!s) return -1;
+            size_t c = sl < sizeof(m->arch) - 1 ? sl : sizeof(m->arch) - 1;
+            memcpy(m->arch, s, c);
+            m->arch[c] = 0;
+        } else if (key_ends(k, kl, ".embedding_length") && vt == 4) {
+            m->d = rd_u32(&r);
+        } else if (key_ends(k, kl, ".attention.head_count_kv") && vt == 4) {
+            m->n_kv_heads = rd_u32(&r);
+        } else if (key_ends(k, kl, ".attention.head_count") && vt == 4) {
+            m->n_heads = rd_u32(&r);
+        } else if (key_ends(k, kl, ".context_length") && vt == 4) {
+            m->ctx_len = rd_u32(&r);
+        } else if (key_ends(k, kl, ".feed_forward_length") && vt == 4) {
+            m->ffn = rd_u32(&r);
+        } else if (key_ends(k, kl, ".block_count") && vt == 4) {
+            m->n_layers = rd_u32(&r);
+        } else if (key_ends(k, kl, ".vocab_size") && vt == 4) {
+            m->vocab_meta = rd_u32(&r);
+        } else if (key_ends(k, kl, ".rope.freq_base") && vt == 6) {
+            m->theta = rd_f32(&r);
+        } else if (key_ends(k, kl, ".attention.layer_norm_rms_epsilon") && vt == 6) {
+            m->eps = rd_f32(&r);
+        } else if (key_ends(k, kl, ".attention.key_length") && vt == 4) {
+            m->key_len = rd_u32(&r);
+        } else if (key_ends(k, kl, ".rope.dimension_count") && vt == 4) {
+            m->rope_dim_meta = rd_u32(&r);
+        } else if (key_is(k, kl, "tokenizer.ggml.tokens") && vt == 9) {
+            uint32_t at = rd_u32(&r);
+            uint64_t n = rd_u64(&r);
+            if (at == 8 && n > 0) m->vocab_meta = (uint32_t)n;
+            for (uint64_t v = 0; v < n && !r.bad; v++) rd_skip(&r, at);
+        } else {
+            rd_skip(&r, vt);
+        }
+        if (r.bad) return -1;
+    }
+    if (m->eps == 0.0f) m->eps = 1e-5f;                       /* gguf_loader.c:370 */
+    if (m->theta == 0.0f) m->theta = strstr(m->arch, "qwen") ? 1000000.0f : 10000.0f;
+    if (m->ctx_len == 0) m->ctx_len = 2048;
+
+    m->n_tensors = n_tensors;
+    m->tensors = (orc_tensor_t *)calloc(n_tensors ? n_tensors : 1, sizeof(orc_tensor_t));
+    if (!m->tensors) return -1;
+    for (uint64_t i = 0; i < n_tensors; i++) {
+        orc_tensor_t *t = &m->tensors[i];
+        uint64_t nl;
+        const char *nm = rd_str(&r, &nl);
+        if (!nm) return -1;
+        size_t c = nl < 255 ? nl : 255;
+        memcpy(t->name, nm, c);
+        t->name[c] = 0;
+        t->n_dims = rd_u32(&r);
+        if (t->n_dims > 4) return -1;
+        for (uint32_t dd = 0; dd < t->n_dims; dd++) t->dims[dd] = rd_u64(&r);
+        t->type = (int32_t)rd_u32(&r);
+        t->offset = rd_u64(&r);
+        if (r.bad) return -1;
+        if (m->vocab_meta == 0 && strcmp(t->name, "token_embd.weight") == 0 && t->n_dims == 2)
+            m->vocab_meta = (uint32_t)t->dims[1];
+        uint64_t ne = 1;
+        for (uint32_t dd = 0; dd < t->n_dims; dd++) ne *= t->dims[dd];
+        uint32_t bs = type_block(t->type);
+        t->size = bs == 1 ? ne * type_size(t->type) : (ne / bs) * type_size(t->type);
+        t->layer = parse_layer(t->name);
+    }
+    uint64_t data_off = (r.pos + 31) & ~(uint64_t)31;      /* gguf_loader.c:426 */
+    for (uint64_t i = 0; i < n_tensors; i++) m->tensors[i].offset += data_off;
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Scheduler: layer_scheduler.c:129-244, 291-567, 571-936                    */
+/* ------------------------------------------------------------------------ */
+
+void orc_model_close(orc_model_t *m) {
+    if (!m) return;
+    free(m->tensors);
+    free(m->layers);
+    free(m->kq); free(m->vq); free(m->ks); free(m->vs); free(m->kh); free(m->vh);
+    free(m->hidden); free(m->residual); free(m->attn_out); free(m->ffn_buf);
+    free(m->ffn_gate); free(m->q); free(m->k); free(m->v); free(m->logits);
+    if (m->base && m->base != MAP_FAILED) munmap(m->base, m->fsize);
+    if (m->fd >= 0) close(m->fd);
+    free(m);
+}
+
+static int matrix_ok(const orc_tensor_t *t, uint64_t rows, uint64_t cols) {
+    return t && t->n_dims == 2 && t->dims[0] == cols && t->dims[1] == rows &&
+           (t->type == ORC_Q4_0 || t->type == ORC_Q8_0 || t->type == ORC_F32 || t->type == ORC_F16);
+}
+static int vector_ok(const orc_tensor_t *t, uint64_t n) {
+    return t && t->type == ORC_F32 && t->dims[0] == n;
+}
+
+orc_model_t *orc_model_open(const char *path, int32_t max_seq, int32_t kv_mode) {
+    if (!path) return NULL;
+    orc_model_t *m = (orc_model_t *)calloc(1, sizeof(orc_model_t));
+    if (!m) return NULL;
+    m->fd = open(path, O_RDONLY);
+    if (m->fd < 0) { free(m); return NULL; }
+    struct stat st;
+    if (fstat(m->fd, &st) < 0) { close(m->fd); free(m); return NULL; }
+    m->fsize = (uint64_t)st.st_size;
+    m->base = (uint8_t *)mmap(NULL, m->fsize, PROT_READ, MAP_SHARED, m->fd, 0);
+    if (m->base == MAP_FAILED) { m->base = NULL; orc_model_close(m); return NULL; }
+    if (parse_gguf(m) != 0) { orc_model_close(m); return NULL; }
+
+    if (strstr(m->arch, "qwen") || strstr(m->arch, "falcon") || strstr(m->arch, "phi") ||
+        strstr(m->arch, "deepseek") || strstr(m->arch, "gemma")) {
+        orc_model_close(m);   /* non-llama branches are not restated */
+        return NULL;
+    }
+    if (m->n_kv_heads == 0) m->n_kv_heads = m->n_heads;
+    if (m->n_layers == 0 || m->d == 0 || m->n_heads == 0) { orc_model_close(m); return NULL; }
+
+    /* head_dim derivation, layer_scheduler.c:161-181 */
+    int32_t hd = 0;
+    if (m->key_len > 0) {
+        hd = (int32_t)m->key_len;
+    } else {
+        const orc_tensor_t *wq0 = find_global(m, "blk.0.attn_q.weight");
+        if (wq0) hd = (int32_t)(wq0->dims[1] / m->n_heads);
+    }
+    if (hd == 0) hd = (int32_t)(m->d / m->n_heads);
+    m->hd = hd;
+    m->rope_dim = m->rope_dim_meta > 0 ? (int32_t)m->rope_dim_meta : hd;
+
+    /* vocab clamp, layer_scheduler.c:185-197 */
+    int32_t vocab = (int32_t)m->vocab_meta;
+    for (uint64_t i = 0; i < m->n_tensors; i++) {
+        const orc_tensor_t *t = &m->tensors[i];
+        if ((strcmp(t->name, "output.weight") == 0 || strcmp(t->name, "token_embd.weight") == 0) &&
+            t->n_dims == 2 && (int32_t)t->dims[1] < vocab)
+            vocab = (int32_t)t->dims[1];
+    }
+    m->vocab = vocab;
+    m->max_seq = max_seq > 0 ? max_seq : (int32_t)m->ctx_len;
+    m->kv_mode = kv_mode;
+    m->kv_dim = (int32_t)m->n_kv_heads * hd;
+
+    int32_t L = (int32_t)m->n_layers, d = (int32_t)m->d, ffn = (int32_t)m->ffn;
+    int32_t qdim = (int32_t)m->n_heads * hd;
+    m->embd = find_global(m, "token_embd.weight");
+    m->out_norm = find_global(m, "output_norm.weight");
+    m->out = find_global(m, "output.weight");
+    if (!m->out) m->out = m->embd;                            /* tied, :652-655 */
+    if (!m->embd || !matrix_ok(m->embd, m->embd->dims[1], (uint64_t)d) || !m->out ||
+        !matrix_ok(m->out, m->out->dims[1], (uint64_t)d) || (m->out_norm && !vector_ok(m->out_norm, d))) {
+        orc_model_close(m);
+        return NULL;
+    }
+    m->layers = (orc_layer_t *)calloc((size_t)L, sizeof(orc_layer_t));
+    if (!m->layers) { orc_model_close(m); return NULL; }
+    for (int32_t l = 0; l < L; l++) {
+        orc_layer_t *ly = &m->layers[l];
+        ly->attn_norm = find_suffix(m, l, "attn_norm.weight");
+        ly->wq = find_suffix(m, l, "attn_q.weight");
+        ly->wk = find_suffix(m, l, "attn_k.weight");
+        ly->wv = find_suffix(m, l, "attn_v.weight");
+        ly->wo = find_suffix(m, l, "attn_output.weight");
+        ly->ffn_norm = find_suffix(m, l, "ffn_norm.weight");
+        ly->wg = find_suffix(m, l, "ffn_gate.weight");
+        ly->wu = find_suffix(m, l, "ffn_up.weight");
+        ly->wd = find_suffix(m, l, "ffn_down.weight");
+        if (!vector_ok(ly->attn_norm, d) || !matrix_ok(ly->wq, qdim, d) ||
+            !matrix_ok(ly->wk, m->kv_dim, d) || !matrix_ok(ly->wv, m->kv_dim, d) ||
+            !matrix_ok(ly->wo, d, qdim) || !vector_ok(ly->ffn_norm, d) ||
+            !matrix_ok(ly->wg, ffn, d) || !matrix_ok(ly->wu, ffn, d) || !matrix_ok(ly->wd, d, ffn) ||
+            find_suffix(m, l, "attn_q.bias") || find_suffix(m, l, "attn_qkv.weight")) {
+            orc_model_close(m);
+            return NULL;
+        }
+    }
+
+    size_t vecs = (size_t)L * m->max_seq;
+    size_t elems = vecs * m->kv_dim;
+    if (kv_mode == ORC_KV_INT8) {
+        m->kq = (int8_t *)calloc(elems, 1);
+        m->vq = (int8_t *)calloc(elems, 1);
+        m->ks = (float *)calloc(vecs, sizeof(float));
+        m->vs = (float *)calloc(vecs, sizeof(float));
+        if (!m->kq || !m->vq || !m->ks || !m->vs) { orc_model_close(m); return NULL; }
+    } else {
+        m->kh = (uint16_t *)calloc(elems, 2);
+        m->vh = (uint16_t *)calloc(elems, 2);
+        if (!m->kh || !m->vh) { orc_model_close(m); return NULL; }
+    }
+    m->hidden = (float *)calloc((size_t)d, 4);
+    m->residual = (float *)calloc((size_t)d, 4);
+    m->attn_out = (float *)calloc((size_t)(qdim > d ? qdim : d), 4);
+    m->ffn_buf = (float *)calloc((size_t)ffn, 4);
+    m->ffn_gate = (float *)calloc((size_t)ffn, 4);
+    m->q = (float *)calloc((size_t)qdim, 4);
+    m->k = (float *)calloc((size_t)m->kv_dim, 4);
+    m->v = (float *)calloc((size_t)m->kv_dim, 4);
+    m->logits = (float *)calloc((size_t)vocab, 4);
+    if (!m->hidden || !m->residual || !m->attn_out || !m->ffn_buf || !m->ffn_gate || !m->q ||
+        !m->k || !m->v || !m->logits) {
+        orc_model_close(m);
+        return NULL;
+    }
+    return m;
+}
+
+void orc_model_dims(const orc_model_t *m, int32_t *o) {
+    o[0] = (int32_t)m->n_layers; o[1] = (int32_t)m->d; o[2] = (int32_t)m->n_heads;
+    o[3] = (int32_t)m->n_kv_heads; o[4] = m->hd; o[5] = (int32_t)m->ffn; o[6] = m->vocab;
+    o[7] = m->max_seq;
+}
+float orc_model_eps(const orc_model_t *m) { return m->eps; }
+float orc_model_theta(const orc_model_t *m) { return m->theta; }
+const float *orc_hidden(const orc_model_t *m) { return m->hidden; }
+
+static void matvec_t(orc_model_t *m, float *out, const orc_tensor_t *t, const float *x) {
+    orc_dequant_matvec(out, tdata(m, t), x, (int32_t)t->dims[1], (int32_t)t->dims[0], t->type);
+}
+
+/* KV row (layer, pos) -> fp32, head slice [head*hd, head*hd+hd) */
+static void kv_read(const orc_model_t *m, int is_v, int32_t layer, int32_t t, int32_t head, float *dst) {
+    size_t vi = (size_t)layer * m->max_seq + t;
+    size_t off = vi * m->kv_dim + (size_t)head * m->hd;
+    if (m->kv_mode == ORC_KV_INT8) {
+        const int8_t *q = (is_v ? m->vq : m->kq) + off;
+        float s = (is_v ? m->vs : m->ks)[vi];
+        for (int32_t i = 0; i < m->hd; i++) dst[i] = (float)q[i] * s;   /* :120-125 */
+    } else {
+        const uint16_t *h = (is_v ? m->vh : m->kh) + off;
+        for (int32_t i = 0; i < m->hd; i++) dst[i] = orc_f16_to_f32(h[i]);
+    }
+}
+
+static void kv_store(orc_model_t *m, int32_t layer, int32_t pos, const float *k, const float *v) {
+    size_t vi = (size_t)layer * m->max_seq + pos;
+    size_t off = vi * m->kv_dim;
+    if (m->kv_mode == ORC_KV_INT8) {                                 /* :409-413 */
+        orc_kv_int8_encode(k, m->kq + off, &m->ks[vi], m->kv_dim);
+        orc_kv_int8_encode(v, m->vq + off, &m->vs[vi], m->kv_dim);
+    } else {
+        for (int32_t i = 0; i < m->kv_dim; i++) {
+            m->kh[off + i] = orc_f32_to_f16(k[i]);
+            m->vh[off + i] = orc_f32_to_f16(v[i]);
+        }
+    }
+}
+
+typedef struct {
+    orc_model_t *m;
+    int32_t layer, seq_len, heads_per_kv;
+    float scale;
+} attn_job_t;
+
+/* layer_scheduler.c:424-468, one query head per task */
+static void attn_head(void *arg, int32_t h) {
+    attn_job_t *j = (attn_job_t *)arg;
+    orc_model_t *m = j->m;
+    int32_t hd = m->hd;
+    const float *q = m->q + (size_t)h * hd;
+    int32_t kvh = h / j->heads_per_kv;
+    float *scores = (float *)malloc((size_t)j->seq_len * sizeof(float));
+    float *tmp = (float *)malloc((size_t)hd * sizeof(float));
+    for (int32_t t = 0; t < j->seq_len; t++) {
+        kv_read(m, 0, j->layer, t, kvh, tmp);
+        scores[t] = orc_dot(q, tmp, hd) * j->scale;
+    }
+    orc_softmax(scores, j->seq_len);
+    float *dst = m->attn_out + (size_t)h * hd;
+    memset(dst, 0, (size_t)hd * sizeof(float));
+    for (int32_t t = 0; t < j->seq_len; t++) {
+        kv_read(m, 1, j->layer, t, kvh, tmp);
+        float w = scores[t];
+        for (int32_t i = 0; i < hd; i++) dst[i] = w * tmp[i] + dst[i];
+    }
+    free(tmp);
+    free(scores);
+}
+
+/* layer_scheduler.c:291-567 (llama branch) */
+static void process_layer(orc_model_t *m, int32_t l, int32_t pos) {
+    const orc_layer_t *ly = &m->layers[l];
+    int32_t d = (int32_t)m->d, ffn = (int32_t)m->ffn;
+    memcpy(m->residual, m->hidden, (size_t)d * 4);
+    orc_rmsnorm(m->hidden, m->residual, (const float *)tdata(m, ly->attn_norm), d, m->eps);
+    matvec_t(m, m->q, ly->wq, m->hidden);
+    matvec_t(m, m->k, ly->wk, m->hidden);
+    matvec_t(m, m->v, ly->wv, m->hidden);
+    orc_rope(m->q, m->k, (int32_t)m->n_heads, (int32_t)m->n_kv_heads, m->hd, m->rope_dim, pos,
+             m->theta, 0);
+    kv_store(m, l, pos, m->k, m->v);
+
+    attn_job_t j = {m, l, pos + 1, (int32_t)(m->n_heads / m->n_kv_heads),
+                    1.0f / sqrtf((float)m->hd)};
+    memset(m->attn_out, 0, (size_t)d * 4);
+    pool_run(attn_head, &j, (int32_t)m->n_heads);
+
+    matvec_t(m, m->hidden, ly->wo, m->attn_out);
+    for (int32_t i = 0; i < d; i++) m->hidden[i] = m->hidden[i] + m->residual[i];   /* :484 */
+
+    memcpy(m->residual, m->hidden, (size_t)d * 4);
+    orc_rmsnorm(m->hidden, m->residual, (const float *)tdata(m, ly->ffn_norm), d, m->eps);
+    matvec_t(m, m->ffn_gate, ly->wg, m->hidden);
+    matvec_t(m, m->ffn_buf, ly->wu, m->hidden);
+    for (int32_t i = 0; i < ffn; i++) m->ffn_buf[i] = orc_silu_mul(m->ffn_gate[i], m->ffn_buf[i]);
+    matvec_t(m, m->hidden, ly->wd, m->ffn_buf);
+    for (int32_t i = 0; i < d; i++) m->hidden[i] = m->hidden[i] + m->residual[i];   /* :566 */
+}
+
+static void embed_row(orc_model_t *m, int32_t token, float *dst) {   /* :584-595 */
+    size_t rb = orc_row_bytes((int32_t)m->d, m->embd->type);
+    const uint8_t *row = (const uint8_t *)tdata(m, m->embd) + (size_t)token * rb;
+    orc_dequantize(row, dst, (int32_t)m->d, m->embd->type);
+}
+
+static void head(orc_model_t *m) {                                   /* :634-662 */
+    if (m->out_norm)
+        orc_rmsnorm(m->hidden, m->hidden, (const float *)tdata(m, m->out_norm), (int32_t)m->d, m->eps);
+    orc_dequant_matvec(m->logits, tdata(m, m->out), m->hidden, m->vocab, (int32_t)m->d, m->out->type);
+}
+
+const float *orc_forward(orc_model_t *m, int32_t token, int32_t pos) {
+    if (!m || pos < 0 || pos >= m->max_seq || token < 0 || (uint64_t)token >= m->embd->dims[1])
+        return NULL;
+    embed_row(m, token, m->hidden);
+    for (int32_t l = 0; l < (int32_t)m->n_layers; l++) process_layer(m, l, pos);
+    head(m);
+    return m->logits;
+}
+
+const float *orc_prefill(orc_model_t *m, const int32_t *tokens, int32_t n, int32_t start_pos) {
+    if (!m || n <= 0 || start_pos < 0 || start_pos + n > m->max_seq) return NULL;
+    int32_t d = (int32_t)m->d;
+    float *batch = (float *)malloc((size_t)n * d * 4);
+    if (!batch) return NULL;
+    for (int32_t i = 0; i < n; i++) {
+        if (tokens[i] < 0 || (uint64_t)tokens[i] >= m->embd->dims[1]) { free(batch); return NULL; }
+        embed_row(m, tokens[i], batch + (size_t)i * d);
+    }
+    for (int32_t l = 0; l < (int32_t)m->n_layers; l++)               /* layer-major, :721-755 */
+        for (int32_t i = 0; i < n; i++) {
+            memcpy(m->hidden, batch + (size_t)i * d, (size_t)d * 4);
+            process_layer(m, l, start_pos + i);
+            memcpy(batch + (size_t)i * d, m->hidden, (size_t)d * 4);
+        }
+    memcpy(m->hidden, batch + (size_t)(n - 1) * d, (size_t)d * 4);
+    free(batch);
+    head(m);
+    return m->logits;
+}
+
+/* layer_scheduler.c:805-915: positions 0..n-1, final norm on every token,
+ * mean pool, L2 normalise. */
+int32_t orc_embed(orc_model_t *m, const int32_t *tokens, int32_t n, float *out) {
+    if (!m || n <= 0 || n > m->max_seq) return -1;
+    int32_t d = (int32_t)m->d;
+    float *batch = (float *)malloc((size_t)n * d * 4);
+    if (!batch) return -1;
+    for (int32_t i = 0; i < n; i++) {
+        if (tokens[i] < 0 || (uint64_t)tokens[i] >= m->embd->dims[1]) { free(batch); return -1; }
+        embed_row(m, tokens[i], batch + (size_t)i * d);
+    }
+    for (int32_t l = 0; l < (int32_t)m->n_layers; l++)
+        for (int32_t i = 0; i < n; i++) {
+            memcpy(m->hidden, batch + (size_t)i * d, (size_t)d * 4);
+            process_layer(m, l, i);
+            memcpy(batch + (size_t)i * d, m->hidden, (size_t)d * 4);
+        }
+    if (m->out_norm)
+        for (int32_t i = 0; i < n; i++)
+            orc_rmsnorm(batch + (size_t)i * d, batch + (size_t)i * d,
+                        (const float *)tdata(m, m->out_norm), d, m->eps);
+    memset(out, 0, (size_t)d * 4);
+    for (int32_t i = 0; i < n; i++)
+        for (int32_t j = 0; j < d; j++) out[j] += batch[(size_t)i * d + j];
+    float inv = 1.0f / (float)n, l2 = 0.0f;
+    for (int32_t j = 0; j < d; j++) {
+        out[j] *= inv;
+        l2 += out[j] * out[j];
+    }
+    float s = 1.0f / (sqrtf(l2) + 1e-12f);
+    for (int32_t j = 0; j < d; j++) out[j] *= s;
+    free(batch);
+    return 0;
+}
+
+void orc_reset(orc_model_t *m) {                                     /* :917-936 */
+    if (!m) return;
+    size_t vecs = (size_t)m->n_layers * m->max_seq, elems = vecs * m->kv_dim;
+    if (m->kv_mode == ORC_KV_INT8) {
+        memset(m->kq, 0, elems); memset(m->vq, 0, elems);
+        memset(m->ks, 0, vecs * 4); memset(m->vs, 0, vecs * 4);
+    } else {
+        memset(m->kh, 0, elems * 2); memset(m->vh, 0, elems * 2);
+    }
+    memset(m->hidden, 0, (size_t)m->d * 4);
+}
+
+int32_t orc_kv_write(orc_model_t *m, int32_t layer, int32_t pos, const uint16_t *k_f16,
+                     const uint16_t *v_f16) {
+    if (!m || layer < 0 || layer >= (int32_t)m->n_layers || pos < 0 || pos >= m->max_seq) return -1;
+    if (m->kv_mode == ORC_KV_F16) {
+        size_t off = ((size_t)layer * m->max_seq + pos) * m->kv_dim;
+        memcpy(m->kh + off, k_f16, (size_t)m->kv_dim * 2);
+        memcpy(m->vh + off, v_f16, (size_t)m->kv_dim * 2);
+        return 0;
+    }
+    float *kf = (float *)malloc((size_t)m->kv_dim * 4), *vf = (float *)malloc((size_t)m->kv_dim * 4);
+    for (int32_t i = 0; i < m->kv_dim; i++) {
+        kf[i] = orc_f16_to_f32(k_f16[i]);
+        vf[i] = orc_f16_to_f32(v_f16[i]);
+    }
+    kv_store(m, layer, pos, kf, vf);
+    free(kf);
+    free(vf);
+    return 0;
+}

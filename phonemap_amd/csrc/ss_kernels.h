@@ -1,0 +1,88 @@
+// ss_kernels.h - launch interface of the gfx950 kernels (internal, C++).
+// The C-ABI in ss_hip.hip is the only user.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ssk {
+
+// Matvec epilogues.
+enum Epi : int {
+  EPI_STORE = 0,   // y[r] = W x
+  EPI_ADD = 1,     // y[r] = W x + y[r]          (residual, layer_scheduler.c:484,566)
+  EPI_SWIGLU = 2,  // y[r] = u * silu(g)          (layer_scheduler.c:533-549), W = gate, W2 = up
+  EPI_QKV = 3,     // rows of [Wq;Wk;Wv]: RoPE on q/k pairs, K/V appended to the cache
+  EPI_LOGITS = 4,  // y[r] = W x, then the first-max argmax over all rows
+};
+
+// A packed Q4_0/Q8_0 matrix on the device: code plane then scale plane.
+struct PackedMat {
+  const uint8_t* qs;
+  const uint16_t* ds;
+};
+
+struct GemvArgs {
+  PackedMat w, w2;           // w2: up projection for EPI_SWIGLU
+  const float* x;            // input vector [cols]
+  const float* nw;           // RMSNorm weight [cols] or nullptr
+  float eps;
+  float* y;                  // output [rows]
+  int rows, cols, type, chunk_blocks;
+  // EPI_QKV
+  int qdim, kvdim, head_dim, rope_dim, max_seq, kv_type;
+  const float* rope_cs;      // [max_seq][rope_dim/2][2]
+  const int* dpos;           // device position
+  void* kcache;              // this layer: [kvh][max_seq][head_dim] fp16 (kv_type 0)
+  void* vcache;
+  float* kv_f32;             // kv_type 1: fp32 K,V staging [2*kvdim]
+  // EPI_LOGITS
+  float2* part;              // per-workgroup (value, index bits)
+  unsigned* counter;
+  int* out_idx;              // argmax result
+  int* tokens;               // if non-null: tokens[pos+1] = argmax and ++*pos (device-side greedy)
+  int* dpos_mut;
+};
+
+struct AttnArgs {
+  const float* q;            // [n_heads][hd]
+  const void* kc;            // this layer: [kvh][max_seq][hd] fp16 or int8
+  const void* vc;
+  const float* ks;           // int8: this layer's per-position scales [max_seq]
+  const float* vs;
+  const int* dpos;           // ctx = *dpos + 1 when set, else seq_len
+  int seq_len, max_seq, ns, n_kv_heads;
+  float scale;
+  float* out;                // [n_heads][hd]
+  float* part_o;             // [kvh][ns][G][hd]
+  float* part_ml;            // [kvh][ns][G][2]
+  unsigned* counter;         // [kvh]
+};
+
+int gemv_rows_per_wave(int epi);
+hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t s);
+int gemv_grid(int epi, int rows);
+hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, hipStream_t s);
+bool attention_supported(int head_dim, int group);
+
+hipError_t launch_pack(int type, const uint8_t* src, uint8_t* qs, uint16_t* ds, int64_t nblocks,
+                       int64_t blk_offset, hipStream_t s);
+hipError_t launch_embed(int type, PackedMat t, int cols, const int* tokens, const int* dpos,
+                        int token, float* out, hipStream_t s);
+hipError_t launch_rmsnorm(float* out, const float* x, const float* w, int n, float eps,
+                          hipStream_t s);
+hipError_t launch_rope(float* q, float* k, int n_heads, int n_kv_heads, int head_dim,
+                       int rope_dim, const float* cs_row, int is_neox, hipStream_t s);
+hipError_t launch_kv_append(void* kc, void* vc, float* ksc, float* vsc, const float* k,
+                            const float* v, int n_kv_heads, int head_dim, int max_seq,
+                            const int* dpos, int pos, int kv_type, hipStream_t s);
+hipError_t launch_swiglu(float* out, const float* g, const float* u, int n, hipStream_t s);
+hipError_t launch_argmax(int* out, const float* x, int n, float2* part, unsigned* counter,
+                         hipStream_t s);
+hipError_t launch_set_state(int* dpos, int* tokens, int pos, int token, hipStream_t s);
+hipError_t launch_advance(int* dpos, hipStream_t s);
+
+constexpr int kArgmaxMaxBlocks = 1024;
+constexpr int kGemvMaxChunkBlocks = 448;   // 448 blocks * 144 B of LDS = 63 KiB
+
+}  // namespace ssk
