@@ -1,0 +1,1120 @@
+// ss_hip.hip - the C-ABI of include/ss_hip.h over the gfx950 kernels.
+//
+// Replaces the reference's Metal backend (src/backends/metal_backend.{h,m})
+// and the per-token CPU sweep of src/core/layer_scheduler.c:291-679. The
+// whole token (embedding, every layer, output norm, LM head, argmax) is
+// enqueued on one stream with no host synchronisation; by default it is
+// captured once into a HIP graph and replayed per token, with the token and
+// position read from device memory so that greedy decoding can run many
+// tokens back to back without the host.
+
+#include "ss_hip.h"
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <mutex>
+#include <unordered_map>
+#include <vector>
+
+#include "ss_kernels.h"
+
+namespace {
+
+constexpr int32_t kErrParams = -5;   // SS_ERROR_INVALID_PARAMS
+constexpr int32_t kErrOom = -3;      // SS_ERROR_OUT_OF_MEMORY
+constexpr int32_t kErrBackend = -7;  // SS_ERROR_BACKEND
+constexpr int32_t kErrCancel = -6;   // SS_ERROR_CANCELLED
+
+thread_local char g_err[512] = "";
+
+int32_t fail(int32_t code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+#define HIP_TRY(expr)                                                                   \
+  do {                                                                                  \
+    hipError_t e_ = (expr);                                                             \
+    if (e_ != hipSuccess)                                                               \
+      return fail(kErrBackend, "%s failed: %s (%s:%d)", #expr, hipGetErrorString(e_),   \
+                  __FILE__, __LINE__);                                                  \
+  } while (0)
+
+size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
+
+int code_bytes(int type) { return type == SS_HIP_Q4_0 ? 16 : type == SS_HIP_Q8_0 ? 32 : 0; }
+int gguf_block_bytes(int type) { return type == SS_HIP_Q4_0 ? 18 : type == SS_HIP_Q8_0 ? 34 : 0; }
+
+bool quant_type_ok(int type) { return type == SS_HIP_Q4_0 || type == SS_HIP_Q8_0; }
+
+ssk::PackedMat view(const void* base, int type, int64_t rows, int cols) {
+  const size_t nblk = (size_t)rows * (cols / 32);
+  ssk::PackedMat m;
+  m.qs = static_cast<const uint8_t*>(base);
+  m.ds = reinterpret_cast<const uint16_t*>(m.qs + align256(nblk * code_bytes(type)));
+  return m;
+}
+
+// Algorithmic HBM bytes of one matvec launch: packed weights (18 or 34 bytes
+// per 32 weights) + x + y.
+double matvec_bytes(int type, int64_t rows, int cols, int nmat) {
+  return (double)nmat * rows * (cols / 32) * gguf_block_bytes(type) + 4.0 * cols + 4.0 * rows;
+}
+
+}  // namespace
+
+struct ss_hip_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  int n_cu = 0;
+  // scratch for the single-op entry points
+  void* staging = nullptr;
+  size_t staging_bytes = 0;
+  float2* am_part = nullptr;
+  unsigned* am_counter = nullptr;
+  float* rope_row = nullptr;
+  int rope_row_len = 0;
+  float* att_o = nullptr;
+  float* att_ml = nullptr;
+  unsigned* att_counter = nullptr;
+  size_t att_o_floats = 0, att_ml_floats = 0;
+  int att_counter_n = 0;
+  // host-pointer plug (metal_backend.m:190-235 registry)
+  std::unordered_map<const void*, void*> registry;
+  float* plug_x = nullptr;
+  float* plug_y = nullptr;
+  size_t plug_x_n = 0, plug_y_n = 0;
+};
+
+namespace {
+
+int32_t ensure(ss_hip_ctx* c, void** p, size_t* have, size_t need, bool zero) {
+  if (*have >= need && *p) return 0;
+  if (*p) hipFree(*p);
+  *p = nullptr;
+  *have = 0;
+  HIP_TRY(hipMalloc(p, need));
+  if (zero) HIP_TRY(hipMemset(*p, 0, need));
+  *have = need;
+  (void)c;
+  return 0;
+}
+
+hipStream_t pick(ss_hip_ctx* c, void* stream) {
+  return stream ? static_cast<hipStream_t>(stream) : c->stream;
+}
+
+int32_t set_device(ss_hip_ctx* c) {
+  HIP_TRY(hipSetDevice(c->device));
+  return 0;
+}
+
+// Pack rows [row_off, row_off+rows) of a combined [total_rows x cols]
+// matrix from host GGUF blocks, in chunks through the context's staging buffer.
+int32_t pack_rows(ss_hip_ctx* c, void* dst, int64_t total_rows, int64_t row_off,
+                  const void* src, int type, int64_t rows, int cols) {
+  const int nb = cols / 32;
+  const size_t row_bytes = (size_t)nb * gguf_block_bytes(type);
+  const size_t chunk_target = 64u << 20;
+  int64_t chunk_rows = (int64_t)(chunk_target / row_bytes);
+  if (chunk_rows < 1) chunk_rows = 1;
+  if (chunk_rows > rows) chunk_rows = rows;
+  int32_t rc = ensure(c, &c->staging, &c->staging_bytes, (size_t)chunk_rows * row_bytes, false);
+  if (rc) return rc;
+  ssk::PackedMat v = view(dst, type, total_rows, cols);
+  for (int64_t r = 0; r < rows; r += chunk_rows) {
+    const int64_t n = rows - r < chunk_rows ? rows - r : chunk_rows;
+    HIP_TRY(hipMemcpyAsync(c->staging, static_cast<const uint8_t*>(src) + (size_t)r * row_bytes,
+                           (size_t)n * row_bytes, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(ssk::launch_pack(type, static_cast<const uint8_t*>(c->staging),
+                             const_cast<uint8_t*>(v.qs), const_cast<uint16_t*>(v.ds),
+                             n * nb, (row_off + r) * nb, c->stream));
+  }
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+// (cos, sin) of tensor.c:250-254 for one position, rope_dim/2 pairs.
+void rope_row(float* cs, int rope_dim, int pos, float theta) {
+  for (int i = 0; i < rope_dim; i += 2) {
+    const float freq = 1.0f / powf(theta, (float)i / (float)rope_dim);
+    const float angle = (float)pos * freq;
+    cs[i] = cosf(angle);
+    cs[i + 1] = sinf(angle);
+  }
+}
+
+int attn_splits(int n_kv_heads, int max_seq) {
+  int ns = 512 / n_kv_heads;
+  const int by_len = (max_seq + 63) / 64;
+  if (ns > by_len) ns = by_len;
+  if (ns > 64) ns = 64;
+  if (ns < 1) ns = 1;
+  return ns;
+}
+
+}  // namespace
+
+// ============================================================== context
+extern "C" {
+
+const char* ss_hip_last_error(void) { return g_err; }
+
+int32_t ss_hip_device_count(void) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+  return n;
+}
+
+int32_t ss_hip_device_name(int32_t device, char* buf, int32_t len) {
+  hipDeviceProp_t p;
+  HIP_TRY(hipGetDeviceProperties(&p, device));
+  if (buf && len > 0) snprintf(buf, (size_t)len, "%s (%s, %d CUs)", p.name, p.gcnArchName,
+                               p.multiProcessorCount);
+  return 0;
+}
+
+ss_hip_ctx_t* ss_hip_init(int32_t device) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+    fail(kErrBackend, "no HIP device available");
+    return nullptr;
+  }
+  if (device < 0 || device >= n) {
+    fail(kErrParams, "device %d out of range (%d devices)", device, n);
+    return nullptr;
+  }
+  hipDeviceProp_t p;
+  if (hipSetDevice(device) != hipSuccess || hipGetDeviceProperties(&p, device) != hipSuccess) {
+    fail(kErrBackend, "cannot select HIP device %d", device);
+    return nullptr;
+  }
+  if (strncmp(p.gcnArchName, "gfx950", 6) != 0) {
+    fail(kErrBackend, "device %d is %s; this build targets gfx950 only", device, p.gcnArchName);
+    return nullptr;
+  }
+  auto* c = new ss_hip_ctx();
+  c->device = device;
+  c->n_cu = p.multiProcessorCount;
+  if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
+      hipMalloc(&c->am_part, sizeof(float2) * ssk::kArgmaxMaxBlocks) != hipSuccess ||
+      hipMalloc(&c->am_counter, sizeof(unsigned)) != hipSuccess ||
+      hipMemset(c->am_counter, 0, sizeof(unsigned)) != hipSuccess) {
+    fail(kErrBackend, "HIP context set-up failed on device %d", device);
+    ss_hip_free(c);
+    return nullptr;
+  }
+  return c;
+}
+
+void ss_hip_free(ss_hip_ctx_t* c) {
+  if (!c) return;
+  hipSetDevice(c->device);
+  if (c->stream) hipStreamSynchronize(c->stream);
+  for (auto& kv : c->registry) hipFree(kv.second);
+  void* bufs[] = {c->staging, c->am_part, c->am_counter, c->rope_row, c->att_o,
+                  c->att_ml,  c->att_counter, c->plug_x, c->plug_y};
+  for (void* b : bufs)
+    if (b) hipFree(b);
+  if (c->stream) hipStreamDestroy(c->stream);
+  delete c;
+}
+
+void* ss_hip_stream(ss_hip_ctx_t* c) { return c ? (void*)c->stream : nullptr; }
+
+int32_t ss_hip_sync(ss_hip_ctx_t* c) {
+  if (!c) return fail(kErrParams, "null context");
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return 0;
+}
+
+void* ss_hip_malloc(ss_hip_ctx_t* c, size_t bytes) {
+  if (!c || set_device(c)) return nullptr;
+  void* p = nullptr;
+  if (hipMalloc(&p, bytes ? bytes : 1) != hipSuccess) {
+    fail(kErrOom, "hipMalloc(%zu) failed", bytes);
+    return nullptr;
+  }
+  return p;
+}
+
+int32_t ss_hip_mfree(ss_hip_ctx_t* c, void* p) {
+  if (!c) return fail(kErrParams, "null context");
+  if (p) HIP_TRY(hipFree(p));
+  return 0;
+}
+
+int32_t ss_hip_memcpy_h2d(ss_hip_ctx_t* c, void* dev, const void* host, size_t bytes) {
+  if (!c) return fail(kErrParams, "null context");
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  HIP_TRY(hipMemcpy(dev, host, bytes, hipMemcpyHostToDevice));
+  return 0;
+}
+
+int32_t ss_hip_memcpy_d2h(ss_hip_ctx_t* c, void* host, const void* dev, size_t bytes) {
+  if (!c) return fail(kErrParams, "null context");
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  HIP_TRY(hipMemcpy(host, dev, bytes, hipMemcpyDeviceToHost));
+  return 0;
+}
+
+size_t ss_hip_packed_bytes(int32_t type, int32_t rows, int32_t cols) {
+  if (!quant_type_ok(type) || rows <= 0 || cols <= 0 || cols % 32) return 0;
+  const size_t nblk = (size_t)rows * (cols / 32);
+  return align256(nblk * code_bytes(type)) + nblk * 2;
+}
+
+int32_t ss_hip_pack_matrix(ss_hip_ctx_t* c, void* dst, const void* src, int32_t type,
+                           int32_t rows, int32_t cols) {
+  if (!c || !dst || !src) return fail(kErrParams, "null argument");
+  if (!quant_type_ok(type) || rows <= 0 || cols <= 0 || cols % 32)
+    return fail(kErrParams, "pack: unsupported type %d or shape %dx%d", type, rows, cols);
+  if (set_device(c)) return kErrBackend;
+  return pack_rows(c, dst, rows, 0, src, type, rows, cols);
+}
+
+// ============================================================== single ops
+static int32_t check_mv(int32_t rows, int32_t cols, int32_t type) {
+  if (!quant_type_ok(type)) return fail(kErrParams, "matvec: type %d is not Q4_0/Q8_0", type);
+  if (rows <= 0 || cols <= 0 || cols % 32)
+    return fail(kErrParams, "matvec: bad shape %dx%d (cols must be a multiple of 32)", rows, cols);
+  return 0;
+}
+
+static ssk::GemvArgs gemv_args(const void* w, const float* x, float* y, int rows, int cols,
+                               int type) {
+  ssk::GemvArgs a;
+  memset(&a, 0, sizeof(a));
+  a.w = view(w, type, rows, cols);
+  a.x = x;
+  a.y = y;
+  a.rows = rows;
+  a.cols = cols;
+  a.type = type;
+  const int nb = cols / 32;
+  a.chunk_blocks = nb < ssk::kGemvMaxChunkBlocks ? nb : ssk::kGemvMaxChunkBlocks;
+  return a;
+}
+
+int32_t ss_hip_matvec(ss_hip_ctx_t* c, float* y, const void* w, const float* x, int32_t rows,
+                      int32_t cols, int32_t type, void* stream) {
+  return ss_hip_matvec_fused(c, y, w, x, nullptr, 0.f, 0, rows, cols, type, stream);
+}
+
+int32_t ss_hip_matvec_fused(ss_hip_ctx_t* c, float* y, const void* w, const float* x,
+                            const float* nw, float eps, int32_t accumulate, int32_t rows,
+                            int32_t cols, int32_t type, void* stream) {
+  if (!c || !y || !w || !x) return fail(kErrParams, "matvec: null argument");
+  if (int32_t rc = check_mv(rows, cols, type)) return rc;
+  ssk::GemvArgs a = gemv_args(w, x, y, rows, cols, type);
+  a.nw = nw;
+  a.eps = eps;
+  HIP_TRY(ssk::launch_gemv(accumulate ? ssk::EPI_ADD : ssk::EPI_STORE, a, pick(c, stream)));
+  return 0;
+}
+
+int32_t ss_hip_ffn_gate_up(ss_hip_ctx_t* c, float* out, const void* wg, const void* wu,
+                           const float* x, const float* nw, float eps, int32_t rows, int32_t cols,
+                           int32_t type, void* stream) {
+  if (!c || !out || !wg || !wu || !x) return fail(kErrParams, "ffn_gate_up: null argument");
+  if (int32_t rc = check_mv(rows, cols, type)) return rc;
+  ssk::GemvArgs a = gemv_args(wg, x, out, rows, cols, type);
+  a.w2 = view(wu, type, rows, cols);
+  a.nw = nw;
+  a.eps = eps;
+  HIP_TRY(ssk::launch_gemv(ssk::EPI_SWIGLU, a, pick(c, stream)));
+  return 0;
+}
+
+int32_t ss_hip_rmsnorm(ss_hip_ctx_t* c, float* out, const float* x, const float* w, int32_t n,
+                       float eps, void* stream) {
+  if (!c || !out || !x || !w || n <= 0) return fail(kErrParams, "rmsnorm: bad argument");
+  HIP_TRY(ssk::launch_rmsnorm(out, x, w, n, eps, pick(c, stream)));
+  return 0;
+}
+
+int32_t ss_hip_rope(ss_hip_ctx_t* c, float* q, float* k, int32_t n_heads, int32_t n_kv_heads,
+                    int32_t head_dim, int32_t rope_dim, int32_t pos, float theta, int32_t is_neox,
+                    void* stream) {
+  if (!c || !q || !k || n_heads <= 0 || n_kv_heads <= 0 || rope_dim <= 0 || rope_dim % 2 ||
+      rope_dim > head_dim || pos < 0)
+    return fail(kErrParams, "rope: bad argument");
+  std::vector<float> cs((size_t)rope_dim);
+  rope_row(cs.data(), rope_dim, pos, theta);
+  if (c->rope_row_len < rope_dim) {
+    if (c->rope_row) hipFree(c->rope_row);
+    c->rope_row = nullptr;
+    HIP_TRY(hipMalloc(&c->rope_row, sizeof(float) * rope_dim));
+    c->rope_row_len = rope_dim;
+  }
+  hipStream_t s = pick(c, stream);
+  HIP_TRY(hipStreamSynchronize(s));
+  HIP_TRY(hipMemcpy(c->rope_row, cs.data(), sizeof(float) * rope_dim, hipMemcpyHostToDevice));
+  HIP_TRY(ssk::launch_rope(q, k, n_heads, n_kv_heads, head_dim, rope_dim, c->rope_row, is_neox, s));
+  return 0;
+}
+
+int32_t ss_hip_kv_append(ss_hip_ctx_t* c, void* kc, void* vc, float* ksc, float* vsc,
+                         const float* k, const float* v, int32_t n_kv_heads, int32_t head_dim,
+                         int32_t max_seq, int32_t pos, int32_t kv_type, void* stream) {
+  if (!c || !kc || !vc || !k || !v || n_kv_heads <= 0 || head_dim <= 0 || pos < 0 ||
+      pos >= max_seq || (kv_type != 0 && kv_type != 1) || (kv_type == 1 && (!ksc || !vsc)))
+    return fail(kErrParams, "kv_append: bad argument");
+  HIP_TRY(ssk::launch_kv_append(kc, vc, ksc, vsc, k, v, n_kv_heads, head_dim, max_seq, nullptr,
+                                pos, kv_type, pick(c, stream)));
+  return 0;
+}
+
+int32_t ss_hip_attention(ss_hip_ctx_t* c, float* out, const float* q, const void* kc,
+                         const void* vc, const float* ksc, const float* vsc, int32_t n_heads,
+                         int32_t n_kv_heads, int32_t head_dim, int32_t max_seq, int32_t seq_len,
+                         int32_t kv_type, void* stream) {
+  if (!c || !out || !q || !kc || !vc || n_kv_heads <= 0 || n_heads % n_kv_heads ||
+      seq_len <= 0 || seq_len > max_seq || (kv_type != 0 && kv_type != 1) ||
+      (kv_type == 1 && (!ksc || !vsc)))
+    return fail(kErrParams, "attention: bad argument");
+  const int group = n_heads / n_kv_heads;
+  if (!ssk::attention_supported(head_dim, group))
+    return fail(kErrParams, "attention: head_dim %d / group %d not supported", head_dim, group);
+  const int ns = attn_splits(n_kv_heads, max_seq);
+  int32_t rc = ensure(c, (void**)&c->att_o, &c->att_o_floats,
+                      sizeof(float) * (size_t)n_kv_heads * ns * group * head_dim, false);
+  if (!rc) rc = ensure(c, (void**)&c->att_ml, &c->att_ml_floats,
+                       sizeof(float) * (size_t)n_kv_heads * ns * group * 2, false);
+  if (rc) return rc;
+  if (c->att_counter_n < n_kv_heads) {
+    if (c->att_counter) hipFree(c->att_counter);
+    c->att_counter = nullptr;
+    HIP_TRY(hipMalloc(&c->att_counter, sizeof(unsigned) * n_kv_heads));
+    HIP_TRY(hipMemset(c->att_counter, 0, sizeof(unsigned) * n_kv_heads));
+    c->att_counter_n = n_kv_heads;
+  }
+  ssk::AttnArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = q;
+  a.kc = kc;
+  a.vc = vc;
+  a.ks = ksc;
+  a.vs = vsc;
+  a.seq_len = seq_len;
+  a.max_seq = max_seq;
+  a.ns = ns;
+  a.n_kv_heads = n_kv_heads;
+  a.scale = 1.0f / sqrtf((float)head_dim);
+  a.out = out;
+  a.part_o = c->att_o;
+  a.part_ml = c->att_ml;
+  a.counter = c->att_counter;
+  HIP_TRY(ssk::launch_attention(head_dim, group, kv_type, a, pick(c, stream)));
+  return 0;
+}
+
+int32_t ss_hip_swiglu(ss_hip_ctx_t* c, float* out, const float* g, const float* u, int32_t n,
+                      void* stream) {
+  if (!c || !out || !g || !u || n <= 0) return fail(kErrParams, "swiglu: bad argument");
+  HIP_TRY(ssk::launch_swiglu(out, g, u, n, pick(c, stream)));
+  return 0;
+}
+
+int32_t ss_hip_argmax(ss_hip_ctx_t* c, int32_t* out, const float* x, int32_t n, void* stream) {
+  if (!c || !out || !x || n <= 0) return fail(kErrParams, "argmax: bad argument");
+  HIP_TRY(ssk::launch_argmax(out, x, n, c->am_part, c->am_counter, pick(c, stream)));
+  return 0;
+}
+
+int32_t ss_hip_embed_row(ss_hip_ctx_t* c, float* out, const void* table, int32_t type,
+                         int32_t rows, int32_t cols, int32_t token, void* stream) {
+  if (!c || !out || !table || token < 0 || token >= rows) return fail(kErrParams, "embed: bad argument");
+  if (int32_t rc = check_mv(rows, cols, type)) return rc;
+  HIP_TRY(ssk::launch_embed(type, view(table, type, rows, cols), cols, nullptr, nullptr, token, out,
+                            pick(c, stream)));
+  return 0;
+}
+
+// ---- Metal-shaped host plug (metal_backend.h:27-58) ----
+int32_t ss_hip_should_use_gpu(int32_t rows, int32_t cols) {   // metal_backend.m:336-340
+  return (int64_t)rows * cols > 1024;
+}
+
+int32_t ss_hip_matvec_host(ss_hip_ctx_t* c, float* out, const void* mat, const float* vec,
+                           int32_t rows, int32_t cols, int32_t type) {
+  if (!c || !out || !mat || !vec || check_mv(rows, cols, type)) return 0;
+  if (set_device(c)) return 0;
+  void* dev = nullptr;
+  auto it = c->registry.find(mat);
+  if (it != c->registry.end()) {
+    dev = it->second;
+  } else {
+    if (hipMalloc(&dev, ss_hip_packed_bytes(type, rows, cols)) != hipSuccess) return 0;
+    if (pack_rows(c, dev, rows, 0, mat, type, rows, cols)) {
+      hipFree(dev);
+      return 0;
+    }
+    c->registry[mat] = dev;
+  }
+  if (ensure(c, (void**)&c->plug_x, &c->plug_x_n, sizeof(float) * cols, false) ||
+      ensure(c, (void**)&c->plug_y, &c->plug_y_n, sizeof(float) * rows, false))
+    return 0;
+  if (hipMemcpyAsync(c->plug_x, vec, sizeof(float) * cols, hipMemcpyHostToDevice, c->stream) !=
+      hipSuccess)
+    return 0;
+  if (ss_hip_matvec(c, c->plug_y, dev, c->plug_x, rows, cols, type, nullptr)) return 0;
+  if (hipMemcpyAsync(out, c->plug_y, sizeof(float) * rows, hipMemcpyDeviceToHost, c->stream) !=
+          hipSuccess ||
+      hipStreamSynchronize(c->stream) != hipSuccess)
+    return 0;
+  return 1;
+}
+
+}  // extern "C"
+
+// ============================================================== model
+namespace {
+
+struct DevLayer {
+  float* attn_norm = nullptr;
+  float* ffn_norm = nullptr;
+  void* wqkv = nullptr;   // packed [Wq;Wk;Wv]
+  void* wo = nullptr;
+  void* wg = nullptr;
+  void* wu = nullptr;
+  void* wd = nullptr;
+  int t_qkv = 0, t_o = 0, t_gu = 0, t_d = 0;
+};
+
+enum ProfClass { PC_Q4 = 0, PC_Q8 = 1, PC_ATTN = 2, PC_OTHER = 3, PC_N = 4 };
+
+struct ProfRec {
+  int cls;
+  double bytes;
+  hipEvent_t a, b;
+};
+
+}  // namespace
+
+struct ss_hip_model {
+  ss_hip_ctx* ctx = nullptr;
+  int L = 0, d = 0, H = 0, KVH = 0, hd = 0, rope_dim = 0, ffn = 0, vocab = 0, max_seq = 0;
+  int qdim = 0, kvdim = 0, group = 0, ns = 0, embd_rows = 0;
+  float eps = 1e-5f, theta = 10000.f;
+  int kv_type = 0;
+  bool use_graph = true;
+  std::vector<DevLayer> layers;
+  void* embd = nullptr;
+  int t_embd = 0;
+  void* out = nullptr;   // == embd when tied
+  int t_out = 0;
+  float* out_norm = nullptr;
+  // KV cache: [L][KVH][max_seq][hd] (+ [L][max_seq] scales for int8)
+  void* kc = nullptr;
+  void* vc = nullptr;
+  float* ks = nullptr;
+  float* vs = nullptr;
+  size_t kv_layer_elems = 0;
+  // activations
+  float *hidden = nullptr, *q = nullptr, *attn = nullptr, *ffn_act = nullptr, *logits = nullptr;
+  float *kv_f32 = nullptr, *rope_cs = nullptr, *dbg = nullptr;
+  int* dpos = nullptr;
+  int* tokens = nullptr;   // [max_seq + 1]
+  int* argmax = nullptr;
+  float2* lm_part = nullptr;
+  unsigned* lm_counter = nullptr;
+  float *att_o = nullptr, *att_ml = nullptr;
+  unsigned* att_counter = nullptr;
+  int* h_io = nullptr;   // pinned host scratch
+  hipGraphExec_t g_full = nullptr, g_nohead = nullptr;
+  int host_pos = -1;     // position of the last evaluated token (-1 = none)
+  const volatile int32_t* cancel = nullptr;
+  uint64_t bytes = 0;
+  // profiling (eager launches bracketed by events)
+  bool prof = false;
+  std::vector<ProfRec> prof_recs;
+  std::vector<hipEvent_t> ev_pool;
+  size_t ev_used = 0;
+  std::vector<void*> allocs;
+};
+
+namespace {
+
+int32_t m_alloc(ss_hip_model* m, void** p, size_t bytes, bool zero = true) {
+  *p = nullptr;
+  hipError_t e = hipMalloc(p, bytes ? bytes : 1);
+  if (e != hipSuccess)
+    return fail(kErrOom, "hipMalloc(%zu) failed: %s", bytes, hipGetErrorString(e));
+  m->allocs.push_back(*p);
+  m->bytes += bytes;
+  if (zero) HIP_TRY(hipMemset(*p, 0, bytes ? bytes : 1));
+  return 0;
+}
+
+int32_t upload_vec(ss_hip_model* m, float** dst, const ss_hip_tensor_t& t, int n, const char* what) {
+  if (!t.data) return fail(kErrParams, "model: missing %s", what);
+  if (t.type != SS_HIP_F32 && t.type != SS_HIP_F16)
+    return fail(kErrParams, "model: %s has type %d (F32/F16 expected)", what, t.type);
+  if ((int64_t)t.rows * t.cols != n) return fail(kErrParams, "model: %s has %d x %d elements, %d expected", what, t.rows, t.cols, n);
+  std::vector<float> h((size_t)n);
+  if (t.type == SS_HIP_F32) {
+    memcpy(h.data(), t.data, sizeof(float) * n);
+  } else {
+    // exact binary16 widening (quantize.c:20-56)
+    const uint16_t* s = static_cast<const uint16_t*>(t.data);
+    for (int i = 0; i < n; i++) {
+      const uint32_t hv = s[i];
+      const uint32_t sign = (hv & 0x8000u) << 16;
+      uint32_t e = (hv >> 10) & 0x1F, mant = hv & 0x3FF, bits;
+      if (e == 0) {
+        if (mant == 0) {
+          bits = sign;
+        } else {
+          e = 1;
+          while (!(mant & 0x400)) { mant <<= 1; e--; }
+          bits = sign | ((e + 112) << 23) | ((mant & 0x3FF) << 13);
+        }
+      } else if (e == 31) {
+        bits = sign | 0x7F800000u | (mant << 13);
+      } else {
+        bits = sign | ((e + 112) << 23) | (mant << 13);
+      }
+      memcpy(&h[i], &bits, 4);
+    }
+  }
+  if (int32_t rc = m_alloc(m, (void**)dst, sizeof(float) * n, false)) return rc;
+  HIP_TRY(hipMemcpy(*dst, h.data(), sizeof(float) * n, hipMemcpyHostToDevice));
+  return 0;
+}
+
+int32_t upload_mat(ss_hip_model* m, void** dst, const ss_hip_tensor_t* parts, int nparts, int rows_expect_total,
+                   int cols, int* type_out, const char* what) {
+  int type = parts[0].type;
+  int64_t total = 0;
+  for (int i = 0; i < nparts; i++) {
+    if (!parts[i].data) return fail(kErrParams, "model: missing %s", what);
+    if (parts[i].type != type)
+      return fail(kErrParams, "model: %s parts have mixed types (%d vs %d)", what, type, parts[i].type);
+    if (parts[i].cols != cols) return fail(kErrParams, "model: %s has %d columns, %d expected", what, parts[i].cols, cols);
+    total += parts[i].rows;
+  }
+  if (!quant_type_ok(type)) return fail(kErrParams, "model: %s has type %d; Q4_0 and Q8_0 are supported", what, type);
+  if (total != rows_expect_total) return fail(kErrParams, "model: %s has %lld rows, %d expected", what, (long long)total, rows_expect_total);
+  if (cols % 32) return fail(kErrParams, "model: %s columns %d not a multiple of 32", what, cols);
+  if (int32_t rc = m_alloc(m, dst, ss_hip_packed_bytes(type, (int)total, cols), false)) return rc;
+  int64_t off = 0;
+  for (int i = 0; i < nparts; i++) {
+    if (int32_t rc = pack_rows(m->ctx, *dst, total, off, parts[i].data, type, parts[i].rows, cols)) return rc;
+    off += parts[i].rows;
+  }
+  *type_out = type;
+  return 0;
+}
+
+hipEvent_t next_event(ss_hip_model* m) {
+  if (m->ev_used == m->ev_pool.size()) {
+    hipEvent_t e;
+    hipEventCreate(&e);
+    m->ev_pool.push_back(e);
+  }
+  return m->ev_pool[m->ev_used++];
+}
+
+// Launch with optional event bracketing (profiling mode only; never inside a capture).
+template <class F>
+hipError_t timed(ss_hip_model* m, int cls, double bytes, F&& launch) {
+  if (!m->prof) return launch();
+  ProfRec r{cls, bytes, next_event(m), next_event(m)};
+  hipEventRecord(r.a, m->ctx->stream);
+  hipError_t e = launch();
+  hipEventRecord(r.b, m->ctx->stream);
+  m->prof_recs.push_back(r);
+  return e;
+}
+
+int q_class(int type) { return type == SS_HIP_Q4_0 ? PC_Q4 : PC_Q8; }
+
+// Enqueue one token on the model stream. The token is tokens[*dpos]. With
+// the head, the last workgroup of the LM-head matvec writes the argmax to
+// tokens[*dpos + 1] and advances *dpos; without it, k_advance does.
+int32_t enqueue_token(ss_hip_model* m, bool with_head) {
+  hipStream_t s = m->ctx->stream;
+  const int nbd = m->d / 32;
+  HIP_TRY(timed(m, PC_OTHER, 0, [&] {
+    return ssk::launch_embed(m->t_embd, view(m->embd, m->t_embd, m->embd_rows, m->d), m->d,
+                             m->tokens, m->dpos, 0, m->hidden, s);
+  }));
+  for (int l = 0; l < m->L; l++) {
+    if (m->cancel && *m->cancel && !m->prof) return fail(kErrCancel, "cancelled");
+    const DevLayer& ly = m->layers[l];
+    char* kc = static_cast<char*>(m->kc) + (size_t)l * m->kv_layer_elems * (m->kv_type ? 1 : 2);
+    char* vc = static_cast<char*>(m->vc) + (size_t)l * m->kv_layer_elems * (m->kv_type ? 1 : 2);
+    float* ksl = m->ks ? m->ks + (size_t)l * m->max_seq : nullptr;
+    float* vsl = m->vs ? m->vs + (size_t)l * m->max_seq : nullptr;
+
+    // 1. rmsnorm(attn_norm) -> [Wq;Wk;Wv] -> RoPE -> KV append   (layer_scheduler.c:320-413)
+    ssk::GemvArgs a = gemv_args(ly.wqkv, m->hidden, m->q, m->qdim + 2 * m->kvdim, m->d, ly.t_qkv);
+    a.nw = ly.attn_norm;
+    a.eps = m->eps;
+    a.qdim = m->qdim;
+    a.kvdim = m->kvdim;
+    a.head_dim = m->hd;
+    a.rope_dim = m->rope_dim;
+    a.max_seq = m->max_seq;
+    a.kv_type = m->kv_type;
+    a.rope_cs = m->rope_cs;
+    a.dpos = m->dpos;
+    a.kcache = kc;
+    a.vcache = vc;
+    a.kv_f32 = m->kv_f32;
+    HIP_TRY(timed(m, q_class(ly.t_qkv), matvec_bytes(ly.t_qkv, a.rows, m->d, 1),
+                  [&] { return ssk::launch_gemv(ssk::EPI_QKV, a, s); }));
+    if (m->kv_type == 1)
+      HIP_TRY(timed(m, PC_OTHER, 0, [&] {
+        return ssk::launch_kv_append(kc, vc, ksl, vsl, m->kv_f32, m->kv_f32 + m->kvdim, m->KVH,
+                                     m->hd, m->max_seq, m->dpos, 0, 1, s);
+      }));
+
+    // 2. attention over positions 0..pos                          (:415-468)
+    ssk::AttnArgs at;
+    memset(&at, 0, sizeof(at));
+    at.q = m->q;
+    at.kc = kc;
+    at.vc = vc;
+    at.ks = ksl;
+    at.vs = vsl;
+    at.dpos = m->dpos;
+    at.max_seq = m->max_seq;
+    at.ns = m->ns;
+    at.n_kv_heads = m->KVH;
+    at.scale = 1.0f / sqrtf((float)m->hd);
+    at.out = m->attn;
+    at.part_o = m->att_o;
+    at.part_ml = m->att_ml;
+    at.counter = m->att_counter;
+    HIP_TRY(timed(m, PC_ATTN, 0, [&] { return ssk::launch_attention(m->hd, m->group, m->kv_type, at, s); }));
+
+    // 3. hidden += Wo attn                                         (:470-484)
+    ssk::GemvArgs o = gemv_args(ly.wo, m->attn, m->hidden, m->d, m->qdim, ly.t_o);
+    HIP_TRY(timed(m, q_class(ly.t_o), matvec_bytes(ly.t_o, m->d, m->qdim, 1),
+                  [&] { return ssk::launch_gemv(ssk::EPI_ADD, o, s); }));
+
+    // 4. rmsnorm(ffn_norm) -> gate, up -> silu(gate) * up           (:486-550)
+    ssk::GemvArgs gu = gemv_args(ly.wg, m->hidden, m->ffn_act, m->ffn, m->d, ly.t_gu);
+    gu.w2 = view(ly.wu, ly.t_gu, m->ffn, m->d);
+    gu.nw = ly.ffn_norm;
+    gu.eps = m->eps;
+    HIP_TRY(timed(m, q_class(ly.t_gu), matvec_bytes(ly.t_gu, m->ffn, m->d, 2),
+                  [&] { return ssk::launch_gemv(ssk::EPI_SWIGLU, gu, s); }));
+
+    // 5. hidden += Wdown act                                       (:552-566)
+    ssk::GemvArgs dn = gemv_args(ly.wd, m->ffn_act, m->hidden, m->d, m->ffn, ly.t_d);
+    HIP_TRY(timed(m, q_class(ly.t_d), matvec_bytes(ly.t_d, m->d, m->ffn, 1),
+                  [&] { return ssk::launch_gemv(ssk::EPI_ADD, dn, s); }));
+  }
+  if (with_head) {
+    // output_norm + LM head + first-max argmax                    (:634-662, tensor.c:318-328)
+    ssk::GemvArgs h = gemv_args(m->out, m->hidden, m->logits, m->vocab, m->d, m->t_out);
+    h.nw = m->out_norm;
+    h.eps = m->eps;
+    h.part = m->lm_part;
+    h.counter = m->lm_counter;
+    h.out_idx = m->argmax;
+    h.tokens = m->tokens;
+    h.dpos_mut = m->dpos;
+    HIP_TRY(timed(m, q_class(m->t_out), matvec_bytes(m->t_out, m->vocab, m->d, 1),
+                  [&] { return ssk::launch_gemv(ssk::EPI_LOGITS, h, s); }));
+  } else {
+    HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_advance(m->dpos, s); }));
+  }
+  (void)nbd;
+  return 0;
+}
+
+int32_t capture(ss_hip_model* m, bool with_head, hipGraphExec_t* out) {
+  hipStream_t s = m->ctx->stream;
+  HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+  int32_t rc = enqueue_token(m, with_head);
+  hipGraph_t g = nullptr;
+  hipError_t e = hipStreamEndCapture(s, &g);
+  if (rc) {
+    if (g) hipGraphDestroy(g);
+    return rc;
+  }
+  if (e != hipSuccess) return fail(kErrBackend, "graph capture failed: %s", hipGetErrorString(e));
+  e = hipGraphInstantiate(out, g, nullptr, nullptr, 0);
+  hipGraphDestroy(g);
+  if (e != hipSuccess) return fail(kErrBackend, "graph instantiate failed: %s", hipGetErrorString(e));
+  return 0;
+}
+
+int32_t run_token(ss_hip_model* m, bool with_head) {
+  if (m->use_graph && !m->prof) {
+    HIP_TRY(hipGraphLaunch(with_head ? m->g_full : m->g_nohead, m->ctx->stream));
+    return 0;
+  }
+  return enqueue_token(m, with_head);
+}
+
+void model_release(ss_hip_model* m) {
+  if (!m) return;
+  hipSetDevice(m->ctx->device);
+  hipStreamSynchronize(m->ctx->stream);
+  if (m->g_full) hipGraphExecDestroy(m->g_full);
+  if (m->g_nohead) hipGraphExecDestroy(m->g_nohead);
+  for (void* p : m->allocs) hipFree(p);
+  for (hipEvent_t e : m->ev_pool) hipEventDestroy(e);
+  if (m->h_io) hipHostFree(m->h_io);
+  delete m;
+}
+
+}  // namespace
+
+extern "C" {
+
+ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* d) {
+  if (!c || !d || !d->layers) {
+    fail(kErrParams, "model: null argument");
+    return nullptr;
+  }
+  if (set_device(c)) return nullptr;
+  if (d->n_layers <= 0 || d->hidden <= 0 || d->n_heads <= 0 || d->n_kv_heads <= 0 ||
+      d->head_dim <= 0 || d->ffn <= 0 || d->vocab <= 0 || d->max_seq <= 0 ||
+      d->n_heads % d->n_kv_heads || d->rope_dim <= 0 || d->rope_dim > d->head_dim ||
+      d->rope_dim % 2 || d->hidden % 32 || d->ffn % 32 || (d->n_heads * d->head_dim) % 32 ||
+      (d->kv_type != 0 && d->kv_type != 1)) {
+    fail(kErrParams, "model: unsupported shape (L=%d d=%d H=%d KVH=%d hd=%d rope=%d ffn=%d V=%d ctx=%d kv=%d)",
+         d->n_layers, d->hidden, d->n_heads, d->n_kv_heads, d->head_dim, d->rope_dim, d->ffn,
+         d->vocab, d->max_seq, d->kv_type);
+    return nullptr;
+  }
+  const int group = d->n_heads / d->n_kv_heads;
+  if (!ssk::attention_supported(d->head_dim, group)) {
+    fail(kErrParams, "model: head_dim %d with %d query heads per KV head is not supported",
+         d->head_dim, group);
+    return nullptr;
+  }
+  auto* m = new ss_hip_model();
+  m->ctx = c;
+  m->L = d->n_layers;
+  m->d = d->hidden;
+  m->H = d->n_heads;
+  m->KVH = d->n_kv_heads;
+  m->hd = d->head_dim;
+  m->rope_dim = d->rope_dim;
+  m->ffn = d->ffn;
+  m->vocab = d->vocab;
+  m->max_seq = d->max_seq;
+  m->eps = d->rms_eps;
+  m->theta = d->rope_theta;
+  m->kv_type = d->kv_type;
+  m->use_graph = d->use_graph != 0;
+  m->qdim = m->H * m->hd;
+  m->kvdim = m->KVH * m->hd;
+  m->group = group;
+  m->ns = attn_splits(m->KVH, m->max_seq);
+
+  auto bail = [&](void) -> ss_hip_model_t* {
+    model_release(m);
+    return nullptr;
+  };
+
+  // weights
+  if (!d->token_embd.data || d->token_embd.cols != m->d || d->token_embd.rows < m->vocab) {
+    fail(kErrParams, "model: token_embd must be [>= vocab x hidden]");
+    return bail();
+  }
+  m->embd_rows = d->token_embd.rows;
+  if (upload_mat(m, &m->embd, &d->token_embd, 1, m->embd_rows, m->d, &m->t_embd, "token_embd"))
+    return bail();
+  if (d->output.data && d->output.data != d->token_embd.data) {
+    if (d->output.rows < m->vocab) {
+      fail(kErrParams, "model: output has %d rows < vocab %d", d->output.rows, m->vocab);
+      return bail();
+    }
+    ss_hip_tensor_t o = d->output;
+    o.rows = m->vocab;   // rows beyond the vocab clamp are never read (layer_scheduler.c:660)
+    if (upload_mat(m, &m->out, &o, 1, m->vocab, m->d, &m->t_out, "output")) return bail();
+  } else {
+    m->out = m->embd;   // tied embeddings, layer_scheduler.c:652-655
+    m->t_out = m->t_embd;
+  }
+  if (d->output_norm.data && upload_vec(m, &m->out_norm, d->output_norm, m->d, "output_norm"))
+    return bail();
+  m->layers.resize(m->L);
+  for (int l = 0; l < m->L; l++) {
+    const ss_hip_tensor_t* t = d->layers + (size_t)l * SS_HIP_LAYER_TENSORS;
+    DevLayer& ly = m->layers[l];
+    char what[64];
+    snprintf(what, sizeof(what), "blk.%d attn_norm", l);
+    if (upload_vec(m, &ly.attn_norm, t[SS_HIP_ATTN_NORM], m->d, what)) return bail();
+    snprintf(what, sizeof(what), "blk.%d ffn_norm", l);
+    if (upload_vec(m, &ly.ffn_norm, t[SS_HIP_FFN_NORM], m->d, what)) return bail();
+    snprintf(what, sizeof(what), "blk.%d attn_q/k/v", l);
+    if (upload_mat(m, &ly.wqkv, t + SS_HIP_WQ, 3, m->qdim + 2 * m->kvdim, m->d, &ly.t_qkv, what))
+      return bail();
+    if (t[SS_HIP_WQ].rows != m->qdim || t[SS_HIP_WK].rows != m->kvdim) {
+      fail(kErrParams, "model: blk.%d q/k/v row counts do not match the head shape", l);
+      return bail();
+    }
+    snprintf(what, sizeof(what), "blk.%d attn_output", l);
+    if (upload_mat(m, &ly.wo, t + SS_HIP_WO, 1, m->d, m->qdim, &ly.t_o, what)) return bail();
+    snprintf(what, sizeof(what), "blk.%d ffn_gate", l);
+    int tu = 0;
+    if (upload_mat(m, &ly.wg, t + SS_HIP_W_GATE, 1, m->ffn, m->d, &ly.t_gu, what)) return bail();
+    snprintf(what, sizeof(what), "blk.%d ffn_up", l);
+    if (upload_mat(m, &ly.wu, t + SS_HIP_W_UP, 1, m->ffn, m->d, &tu, what)) return bail();
+    if (tu != ly.t_gu) {
+      fail(kErrParams, "model: blk.%d ffn_gate and ffn_up types differ", l);
+      return bail();
+    }
+    snprintf(what, sizeof(what), "blk.%d ffn_down", l);
+    if (upload_mat(m, &ly.wd, t + SS_HIP_W_DOWN, 1, m->d, m->ffn, &ly.t_d, what)) return bail();
+  }
+
+  // KV cache and working state
+  const size_t esz = m->kv_type ? 1 : 2;
+  m->kv_layer_elems = (size_t)m->KVH * m->max_seq * m->hd;
+  if (m_alloc(m, &m->kc, m->kv_layer_elems * m->L * esz) ||
+      m_alloc(m, &m->vc, m->kv_layer_elems * m->L * esz))
+    return bail();
+  if (m->kv_type == 1 && (m_alloc(m, (void**)&m->ks, sizeof(float) * m->L * m->max_seq) ||
+                          m_alloc(m, (void**)&m->vs, sizeof(float) * m->L * m->max_seq)))
+    return bail();
+  const int lm_grid = ssk::gemv_grid(ssk::EPI_LOGITS, m->vocab);
+  if (m_alloc(m, (void**)&m->hidden, sizeof(float) * m->d) ||
+      m_alloc(m, (void**)&m->q, sizeof(float) * m->qdim) ||
+      m_alloc(m, (void**)&m->attn, sizeof(float) * m->qdim) ||
+      m_alloc(m, (void**)&m->ffn_act, sizeof(float) * m->ffn) ||
+      m_alloc(m, (void**)&m->logits, sizeof(float) * m->vocab) ||
+      m_alloc(m, (void**)&m->kv_f32, sizeof(float) * 2 * m->kvdim) ||
+      m_alloc(m, (void**)&m->dbg, sizeof(float) * m->d) ||
+      m_alloc(m, (void**)&m->dpos, sizeof(int) * 4) ||
+      m_alloc(m, (void**)&m->tokens, sizeof(int) * (m->max_seq + 1)) ||
+      m_alloc(m, (void**)&m->argmax, sizeof(int) * 4) ||
+      m_alloc(m, (void**)&m->lm_part, sizeof(float2) * lm_grid) ||
+      m_alloc(m, (void**)&m->lm_counter, sizeof(unsigned) * 4) ||
+      m_alloc(m, (void**)&m->att_o, sizeof(float) * (size_t)m->KVH * m->ns * m->group * m->hd) ||
+      m_alloc(m, (void**)&m->att_ml, sizeof(float) * (size_t)m->KVH * m->ns * m->group * 2) ||
+      m_alloc(m, (void**)&m->att_counter, sizeof(unsigned) * m->KVH))
+    return bail();
+  // RoPE (cos, sin) table for every position, computed with the host libm
+  // exactly as tensor.c:250-254 computes each pair.
+  {
+    std::vector<float> cs((size_t)m->max_seq * m->rope_dim);
+    for (int p = 0; p < m->max_seq; p++) rope_row(cs.data() + (size_t)p * m->rope_dim, m->rope_dim, p, m->theta);
+    if (m_alloc(m, (void**)&m->rope_cs, sizeof(float) * cs.size(), false)) return bail();
+    if (hipMemcpy(m->rope_cs, cs.data(), sizeof(float) * cs.size(), hipMemcpyHostToDevice) != hipSuccess) {
+      fail(kErrBackend, "rope table upload failed");
+      return bail();
+    }
+  }
+  if (hipHostMalloc((void**)&m->h_io, 64 * sizeof(int), hipHostMallocDefault) != hipSuccess) {
+    fail(kErrBackend, "pinned host buffer allocation failed");
+    return bail();
+  }
+  if (hipDeviceSynchronize() != hipSuccess) {
+    fail(kErrBackend, "model upload failed");
+    return bail();
+  }
+  if (m->use_graph && (capture(m, true, &m->g_full) || capture(m, false, &m->g_nohead))) return bail();
+  return m;
+}
+
+void ss_hip_model_free(ss_hip_model_t* m) { model_release(m); }
+
+uint64_t ss_hip_model_bytes(const ss_hip_model_t* m) { return m ? m->bytes : 0; }
+
+void ss_hip_set_cancel_flag(ss_hip_model_t* m, const volatile int32_t* flag) {
+  if (m) m->cancel = flag;
+}
+
+static int32_t finish_eval(ss_hip_model_t* m, float* logits_host, int32_t* argmax_out) {
+  hipStream_t s = m->ctx->stream;
+  if (argmax_out) HIP_TRY(hipMemcpyAsync(m->h_io, m->argmax, sizeof(int), hipMemcpyDeviceToHost, s));
+  if (logits_host)
+    HIP_TRY(hipMemcpyAsync(logits_host, m->logits, sizeof(float) * m->vocab, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  if (argmax_out) *argmax_out = m->h_io[0];
+  return 0;
+}
+
+int32_t ss_hip_eval_token(ss_hip_model_t* m, int32_t token, int32_t pos, float* logits_host,
+                          int32_t* argmax_out) {
+  if (!m) return fail(kErrParams, "null model");
+  if (pos < 0 || pos >= m->max_seq) return fail(kErrParams, "pos %d outside [0, %d)", pos, m->max_seq);
+  if (token < 0 || token >= m->embd_rows) return fail(kErrParams, "token %d outside [0, %d)", token, m->embd_rows);
+  if (set_device(m->ctx)) return kErrBackend;
+  if (m->cancel && *m->cancel) return fail(kErrCancel, "cancelled");
+  HIP_TRY(ssk::launch_set_state(m->dpos, m->tokens, pos, token, m->ctx->stream));
+  if (int32_t rc = run_token(m, true)) return rc;
+  m->host_pos = pos;
+  return finish_eval(m, logits_host, argmax_out);
+}
+
+int32_t ss_hip_eval_prompt(ss_hip_model_t* m, const int32_t* tokens, int32_t n, int32_t start,
+                           float* logits_host, int32_t* argmax_out) {
+  if (!m || !tokens || n <= 0) return fail(kErrParams, "eval_prompt: bad argument");
+  if (start < 0 || start + n > m->max_seq)
+    return fail(kErrParams, "prompt [%d, %d) exceeds the context of %d", start, start + n, m->max_seq);
+  for (int i = 0; i < n; i++)
+    if (tokens[i] < 0 || tokens[i] >= m->embd_rows)
+      return fail(kErrParams, "prompt token %d = %d outside [0, %d)", i, tokens[i], m->embd_rows);
+  if (set_device(m->ctx)) return kErrBackend;
+  hipStream_t s = m->ctx->stream;
+  HIP_TRY(hipStreamSynchronize(s));
+  HIP_TRY(hipMemcpy(m->tokens + start, tokens, sizeof(int) * n, hipMemcpyHostToDevice));
+  HIP_TRY(ssk::launch_set_state(m->dpos, m->tokens, start, tokens[0], s));
+  for (int i = 0; i < n; i++) {
+    if (m->cancel && *m->cancel) {
+      hipStreamSynchronize(s);
+      return fail(kErrCancel, "cancelled");
+    }
+    if (int32_t rc = run_token(m, i == n - 1)) return rc;
+  }
+  m->host_pos = start + n - 1;
+  return finish_eval(m, logits_host, argmax_out);
+}
+
+int32_t ss_hip_decode_greedy(ss_hip_model_t* m, int32_t n_steps, int32_t* tokens_out) {
+  if (!m || n_steps < 0) return fail(kErrParams, "decode_greedy: bad argument");
+  if (m->host_pos < 0) return fail(kErrParams, "decode_greedy: evaluate a token or prompt first");
+  if (m->host_pos + n_steps >= m->max_seq)
+    return fail(kErrParams, "decode_greedy: %d steps from position %d exceed the context of %d",
+                n_steps, m->host_pos, m->max_seq);
+  if (n_steps == 0) return 0;
+  if (set_device(m->ctx)) return kErrBackend;
+  hipStream_t s = m->ctx->stream;
+  for (int i = 0; i < n_steps; i++) {
+    if (m->cancel && *m->cancel) {
+      hipStreamSynchronize(s);
+      return fail(kErrCancel, "cancelled");
+    }
+    if (int32_t rc = run_token(m, true)) return rc;
+  }
+  const int p0 = m->host_pos;
+  m->host_pos += n_steps;
+  if (tokens_out)
+    HIP_TRY(hipMemcpyAsync(tokens_out, m->tokens + p0 + 2, sizeof(int) * n_steps,
+                           hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return 0;
+}
+
+int32_t ss_hip_kv_reset(ss_hip_model_t* m) {
+  if (!m) return fail(kErrParams, "null model");
+  if (set_device(m->ctx)) return kErrBackend;
+  hipStream_t s = m->ctx->stream;
+  const size_t esz = m->kv_type ? 1 : 2;
+  HIP_TRY(hipMemsetAsync(m->kc, 0, m->kv_layer_elems * m->L * esz, s));
+  HIP_TRY(hipMemsetAsync(m->vc, 0, m->kv_layer_elems * m->L * esz, s));
+  if (m->ks) HIP_TRY(hipMemsetAsync(m->ks, 0, sizeof(float) * m->L * m->max_seq, s));
+  if (m->vs) HIP_TRY(hipMemsetAsync(m->vs, 0, sizeof(float) * m->L * m->max_seq, s));
+  HIP_TRY(hipMemsetAsync(m->hidden, 0, sizeof(float) * m->d, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  m->host_pos = -1;
+  return 0;
+}
+
+int32_t ss_hip_kv_write(ss_hip_model_t* m, int32_t layer, int32_t pos0, int32_t n_pos,
+                        const uint16_t* k, const uint16_t* v) {
+  if (!m || !k || !v || layer < 0 || layer >= m->L || pos0 < 0 || n_pos <= 0 ||
+      pos0 + n_pos > m->max_seq)
+    return fail(kErrParams, "kv_write: bad argument");
+  if (set_device(m->ctx)) return kErrBackend;
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  const size_t esz = m->kv_type ? 1 : 2;
+  char* kc = static_cast<char*>(m->kc) + (size_t)layer * m->kv_layer_elems * esz;
+  char* vc = static_cast<char*>(m->vc) + (size_t)layer * m->kv_layer_elems * esz;
+  if (m->kv_type == 0) {
+    for (int g = 0; g < m->KVH; g++) {
+      const size_t dst = ((size_t)g * m->max_seq + pos0) * m->hd * 2;
+      HIP_TRY(hipMemcpy2D(kc + dst, (size_t)m->hd * 2, k + (size_t)g * m->hd, (size_t)m->kvdim * 2,
+                          (size_t)m->hd * 2, n_pos, hipMemcpyHostToDevice));
+      HIP_TRY(hipMemcpy2D(vc + dst, (size_t)m->hd * 2, v + (size_t)g * m->hd, (size_t)m->kvdim * 2,
+                          (size_t)m->hd * 2, n_pos, hipMemcpyHostToDevice));
+    }
+    return 0;
+  }
+  // int8 mode: widen to fp32 and encode as layer_scheduler.c:101-118 does
+  std::vector<int8_t> qk((size_t)n_pos * m->kvdim), qv((size_t)n_pos * m->kvdim);
+  std::vector<float> sk(n_pos), sv(n_pos), f(m->kvdim);
+  for (int which = 0; which < 2; which++) {
+    const uint16_t* src = which ? v : k;
+    std::vector<int8_t>& q = which ? qv : qk;
+    std::vector<float>& sc = which ? sv : sk;
+    for (int p = 0; p < n_pos; p++) {
+      float amax = 0.f;
+      for (int i = 0; i < m->kvdim; i++) {
+        const uint16_t h = src[(size_t)p * m->kvdim + i];
+        const _Float16 hf = __builtin_bit_cast(_Float16, h);
+        f[i] = (float)hf;
+        if (fabsf(f[i]) > amax) amax = fabsf(f[i]);
+      }
+      const float s = amax / 127.0f;
+      const float inv = s > 0.0f ? 1.0f / s : 0.0f;
+      sc[p] = s;
+      for (int i = 0; i < m->kvdim; i++) q[(size_t)p * m->kvdim + i] = (int8_t)roundf(f[i] * inv);
+    }
+  }
+  for (int g = 0; g < m->KVH; g++) {
+    const size_t dst = ((size_t)g * m->max_seq + pos0) * m->hd;
+    HIP_TRY(hipMemcpy2D(kc + dst, (size_t)m->hd, qk.data() + (size_t)g * m->hd, (size_t)m->kvdim,
+                        (size_t)m->hd, n_pos, hipMemcpyHostToDevice));
+    HIP_TRY(hipMemcpy2D(vc + dst, (size_t)m->hd, qv.data() + (size_t)g * m->hd, (size_t)m->kvdim,
+                        (size_t)m->hd, n_pos, hipMemcpyHostToDevice));
+  }
+  HIP_TRY(hipMemcpy(m->ks + (size_t)layer * m->max_seq + pos0, sk.data(), sizeof(float) * n_pos,
+                    hipMemcpyHostToDevice));
+  HIP_TRY(hipMemcpy(m->vs + (size_t)layer * m->max_seq + pos0, sv.data(), sizeof(float) * n_pos,
+                    hipMemcpyHostToDevice));
+  return 0;
+}
+
+int32_t ss_hip_hidden(ss_hip_model_t* m, float* host_out) {
+  if (!m || !host_out) return fail(kErrParams, "hidden: bad argument");
+  if (set_device(m->ctx)) return kErrBackend;
+  hipStream_t s = m->ctx->stream;
+  if (m->out_norm)
+    HIP_TRY(ssk::launch_rmsnorm(m->dbg, m->hidden, m->out_norm, m->d, m->eps, s));
+  else
+    HIP_TRY(hipMemcpyAsync(m->dbg, m->hidden, sizeof(float) * m->d, hipMemcpyDeviceToDevice, s));
+  HIP_TRY(hipMemcpyAsync(host_out, m->dbg, sizeof(float) * m->d, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return 0;
+}
+
+int32_t ss_hip_profile_begin(ss_hip_model_t* m) {
+  if (!m) return fail(kErrParams, "null model");
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  m->prof = true;
+  m->prof_recs.clear();
+  m->ev_used = 0;
+  return 0;
+}
+
+// ms_out receives, per class (0 = Q4_0 matvec, 1 = Q8_0 matvec,
+// 2 = attention, 3 = other), three doubles: total ms, launches, algorithmic
+// bytes; n is the capacity in doubles (12 for all classes).
+int32_t ss_hip_profile_end(ss_hip_model_t* m, double* out, int32_t n) {
+  if (!m) return fail(kErrParams, "null model");
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  double acc[PC_N * 3] = {0};
+  for (const ProfRec& r : m->prof_recs) {
+    float ms = 0.f;
+    HIP_TRY(hipEventElapsedTime(&ms, r.a, r.b));
+    acc[r.cls * 3] += ms;
+    acc[r.cls * 3 + 1] += 1;
+    acc[r.cls * 3 + 2] += r.bytes;
+  }
+  for (int i = 0; i < n && i < PC_N * 3; i++) out[i] = acc[i];
+  m->prof = false;
+  m->prof_recs.clear();
+  m->ev_used = 0;
+  return 0;
+}
+
+}  // extern "C"
