@@ -1,0 +1,46 @@
+/*
+ * ss_synth.h - seeded synthetic Llama-architecture GGUF writer.
+ *
+ * Produces benchmark and test models with random-initialised weights in the
+ * layout the reference loader reads (SlipStream/src/core/gguf_loader.c:282-361:
+ * UINT32/FLOAT32 metadata, a 32-byte-aligned data section, dims[0] = columns,
+ * dims[1] = rows). No counterpart in the reference; it stands in for the
+ * checkpoints that cannot be downloaded.
+ *
+ * Distributions: Q4_0 blocks have d = fp16(|N(0, scale_sigma)|) and uniform
+ * random nibbles; Q8_0 blocks have d = fp16(|N(0, scale_sigma)|) and int8 codes
+ * uniform in [-127, 127]; norm weights are fp32 1 + N(0, norm_sigma).
+ * The bytes depend only on the spec (seed included), not on n_threads.
+ */
+#ifndef SS_SYNTH_H
+#define SS_SYNTH_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct {
+    int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, context_length;
+    float rope_theta, rms_eps;
+    int32_t layer_type;   /* ggml type of the layer matrices: 2 (Q4_0) or 8 (Q8_0) */
+    int32_t embd_type;    /* token_embd.weight */
+    int32_t out_type;     /* output.weight; -1 = tied to token_embd (no output.weight) */
+    uint64_t seed;
+    float scale_sigma;    /* 0 = 0.02 */
+    float norm_sigma;     /* 0 = 0.01 */
+    int32_t with_vocab;   /* write tokenizer.ggml.tokens/scores (SentencePiece-style) */
+    int32_t n_threads;    /* 0 = hardware concurrency */
+} ss_synth_spec_t;
+
+/* Returns 0, or a negative ss_error_t value (-5 bad spec, -1 cannot write). */
+int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *spec);
+
+/* Vocabulary string i of the synthetic tokenizer (for tests); NULL if i is out of range. */
+const char *ss_synth_vocab_string(int32_t vocab, int32_t i, char *buf, int32_t len);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

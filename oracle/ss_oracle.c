@@ -313,11 +313,11 @@ static void pool_drain(orc_task_fn fn, void *arg, int32_t count) {
     }
 }
 
-static void *pool_worker(void *unused) {
-    (void)unused;
-    unsigned seen = 0;
+/* arg: the job generation current when the worker was created, so a job
+ * posted before the worker first takes the mutex is still seen as new. */
+static void *pool_worker(void *arg) {
+    unsigned seen = (unsigned)(uintptr_t)arg;
     pthread_mutex_lock(&g_pool.mu);
-    seen = g_pool.gen;
     for (;;) {
         while (g_pool.gen == seen && !g_pool.stop) pthread_cond_wait(&g_pool.cv_go, &g_pool.mu);
         if (g_pool.stop) break;
@@ -358,7 +358,9 @@ void orc_set_threads(int32_t n) {
     g_pool.nthreads = n;
     int started = 0;
     for (int i = 0; i < n - 1; i++)
-        if (pthread_create(&g_pool.th[started], NULL, pool_worker, NULL) == 0) started++;
+        if (pthread_create(&g_pool.th[started], NULL, pool_worker,
+                           (void *)(uintptr_t)g_pool.gen) == 0)
+            started++;
     g_pool.nworkers = started;
     g_pool.nthreads = started + 1;
     pthread_mutex_unlock(&g_pool.mu);

@@ -1,0 +1,336 @@
+/*
+ * ss_synth.c - seeded synthetic Llama GGUF writer (see include/ss_synth.h).
+ *
+ * Tensor bytes are generated in independent chunks, each from its own
+ * xoshiro256** stream seeded from (seed, tensor, chunk), and written with
+ * pwrite by a small thread pool, so a 40 GB file is produced at disk speed
+ * and the bytes do not depend on the thread count.
+ */
+#define _GNU_SOURCE
+#include "ss_synth.h"
+
+#include <fcntl.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+#define T_F32 0
+#define T_Q4_0 2
+#define T_Q8_0 8
+#define CHUNK_BLOCKS (1u << 18)   /* 256 Ki blocks per work item */
+
+typedef struct {
+    char name[64];
+    uint32_t n_dims;
+    uint64_t dims[2];
+    int32_t type;
+    uint64_t offset;   /* relative to the data section */
+    uint64_t bytes;
+    int norm;
+} syn_tensor_t;
+
+/* ---- random numbers ---- */
+static uint64_t splitmix64(uint64_t *s) {
+    uint64_t z = (*s += 0x9E3779B97F4A7C15ull);
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+typedef struct { uint64_t s[4]; } xo_t;
+static uint64_t rotl(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+static uint64_t xo_next(xo_t *x) {
+    uint64_t r = rotl(x->s[1] * 5, 7) * 9, t = x->s[1] << 17;
+    x->s[2] ^= x->s[0]; x->s[3] ^= x->s[1]; x->s[1] ^= x->s[2]; x->s[0] ^= x->s[3];
+    x->s[2] ^= t; x->s[3] = rotl(x->s[3], 45);
+    return r;
+}
+static void xo_seed(xo_t *x, uint64_t seed, uint64_t a, uint64_t b) {
+    uint64_t s = seed ^ (a * 0xD1B54A32D192ED03ull) ^ (b * 0x8CB92BA72F3D8DD7ull);
+    for (int i = 0; i < 4; i++) x->s[i] = splitmix64(&s);
+}
+static double xo_unit(xo_t *x) { return ((xo_next(x) >> 11) + 0.5) * (1.0 / 9007199254740992.0); }
+static double xo_normal(xo_t *x) {   /* Box-Muller */
+    double u1 = xo_unit(x), u2 = xo_unit(x);
+    return sqrt(-2.0 * log(u1)) * cos(6.283185307179586 * u2);
+}
+
+static uint16_t to_f16(float f) {    /* IEEE binary16, round to nearest even */
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    uint32_t sign = (x >> 16) & 0x8000u, ax = x & 0x7FFFFFFFu;
+    if (ax >= 0x477FF000u) return (uint16_t)(sign | (ax > 0x7F800000u ? 0x7E00u : 0x7C00u));
+    uint32_t e = ax >> 23;
+    if (e >= 113) {
+        uint32_t m = ax & 0x7FFFFFu, h = ((e - 112) << 10) | (m >> 13), rem = m & 0x1FFFu;
+        if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) h++;
+        return (uint16_t)(sign | h);
+    }
+    if (e < 102) return (uint16_t)sign;
+    uint32_t m = (ax & 0x7FFFFFu) | 0x800000u, sh = 126 - e, h = m >> sh;
+    uint32_t rem = m & ((1u << sh) - 1u), half = 1u << (sh - 1);
+    if (rem > half || (rem == half && (h & 1u))) h++;
+    return (uint16_t)(sign | h);
+}
+
+/* ---- synthetic SentencePiece-style vocabulary ---- */
+static void word_of(uint64_t n, char *out) {   /* bijective base-26: a..z, aa, ab, ... */
+    char tmp[16];
+    int k = 0;
+    n += 1;
+    while (n > 0 && k < 15) { n -= 1; tmp[k++] = (char)('a' + n % 26); n /= 26; }
+    for (int i = 0; i < k; i++) out[i] = tmp[k - 1 - i];
+    out[k] = 0;
+}
+
+const char *ss_synth_vocab_string(int32_t vocab, int32_t i, char *buf, int32_t len) {
+    if (i < 0 || i >= vocab || !buf || len < 32) return NULL;
+    if (i == 0) { snprintf(buf, len, "<unk>"); return buf; }
+    if (i == 1) { snprintf(buf, len, "<s>"); return buf; }
+    if (i == 2) { snprintf(buf, len, "</s>"); return buf; }
+    if (i < 259) { snprintf(buf, len, "<0x%02X>", i - 3); return buf; }
+    if (i == 259) { snprintf(buf, len, "\xE2\x96\x81"); return buf; }   /* U+2581 */
+    if (i < 259 + 1 + 94) { buf[0] = (char)(0x21 + (i - 260)); buf[1] = 0; return buf; }
+    uint64_t k = (uint64_t)(i - 354);
+    char w[16];
+    word_of(k / 2, w);
+    if (k % 2 == 0) snprintf(buf, len, "\xE2\x96\x81%s", w);
+    else snprintf(buf, len, "%s", w);
+    return buf;
+}
+
+/* ---- GGUF serialisation ---- */
+typedef struct { uint8_t *p; size_t n, cap; int bad; } wbuf_t;
+static void wb_put(wbuf_t *b, const void *d, size_t n) {
+    if (b->bad) return;
+    if (b->n + n > b->cap) {
+        size_t c = b->cap ? b->cap * 2 : 1 << 16;
+        while (c < b->n + n) c *= 2;
+        uint8_t *q = (uint8_t *)realloc(b->p, c);
+        if (!q) { b->bad = 1; return; }
+        b->p = q;
+        b->cap = c;
+    }
+    memcpy(b->p + b->n, d, n);
+    b->n += n;
+}
+static void wb_u32(wbuf_t *b, uint32_t v) { wb_put(b, &v, 4); }
+static void wb_u64(wbuf_t *b, uint64_t v) { wb_put(b, &v, 8); }
+static void wb_f32(wbuf_t *b, float v) { wb_put(b, &v, 4); }
+static void wb_str(wbuf_t *b, const char *s) { uint64_t n = strlen(s); wb_u64(b, n); wb_put(b, s, n); }
+static void kv_u32(wbuf_t *b, const char *k, uint32_t v) { wb_str(b, k); wb_u32(b, 4); wb_u32(b, v); }
+static void kv_f32(wbuf_t *b, const char *k, float v) { wb_str(b, k); wb_u32(b, 6); wb_f32(b, v); }
+static void kv_str(wbuf_t *b, const char *k, const char *v) { wb_str(b, k); wb_u32(b, 8); wb_str(b, v); }
+
+typedef struct {
+    int fd;
+    uint64_t data_off, seed;
+    float scale_sigma, norm_sigma;
+    syn_tensor_t *t;
+    int nt;
+    /* work items: (tensor, chunk) flattened */
+    uint64_t *item_tensor, *item_chunk;
+    uint64_t n_items, next;
+    int failed;
+} job_t;
+
+static uint64_t tensor_blocks(const syn_tensor_t *t) { return t->dims[0] * t->dims[1] / 32; }
+
+static void gen_item(job_t *j, uint64_t it, uint8_t *buf) {
+    const syn_tensor_t *t = &j->t[j->item_tensor[it]];
+    uint64_t chunk = j->item_chunk[it];
+    xo_t x;
+    xo_seed(&x, j->seed, j->item_tensor[it] + 1, chunk);
+    size_t n = 0;
+    uint64_t off = 0;
+    if (t->type == T_F32) {
+        uint64_t ne = t->dims[0] * (t->n_dims > 1 ? t->dims[1] : 1);
+        float *f = (float *)buf;
+        for (uint64_t i = 0; i < ne; i++) f[i] = (float)(1.0 + j->norm_sigma * xo_normal(&x));
+        n = ne * 4;
+    } else {
+        uint64_t nb = tensor_blocks(t), b0 = chunk * CHUNK_BLOCKS;
+        uint64_t b1 = b0 + CHUNK_BLOCKS < nb ? b0 + CHUNK_BLOCKS : nb;
+        size_t bb = t->type == T_Q4_0 ? 18 : 34;
+        for (uint64_t b = b0; b < b1; b++) {
+            uint8_t *p = buf + (b - b0) * bb;
+            uint16_t d = to_f16((float)fabs(j->scale_sigma * xo_normal(&x)));
+            memcpy(p, &d, 2);
+            if (t->type == T_Q4_0) {
+                uint64_t r0 = xo_next(&x), r1 = xo_next(&x);
+                memcpy(p + 2, &r0, 8);
+                memcpy(p + 10, &r1, 8);
+            } else {
+                for (int i = 0; i < 32; i++) {
+                    uint32_t r = (uint32_t)(xo_next(&x) >> 32);
+                    p[2 + i] = (uint8_t)(int8_t)((int)(((uint64_t)r * 255u) >> 32) - 127);
+                }
+            }
+        }
+        n = (b1 - b0) * bb;
+        off = b0 * bb;
+    }
+    if (pwrite(j->fd, buf, n, (off_t)(j->data_off + t->offset + off)) != (ssize_t)n)
+        __atomic_store_n(&j->failed, 1, __ATOMIC_RELAXED);
+}
+
+static void *worker(void *arg) {
+    job_t *j = (job_t *)arg;
+    uint8_t *buf = (uint8_t *)malloc((size_t)CHUNK_BLOCKS * 34 + (1u << 20));
+    uint64_t max_vec = 0;
+    for (int i = 0; i < j->nt; i++)
+        if (j->t[i].type == T_F32 && j->t[i].bytes > max_vec) max_vec = j->t[i].bytes;
+    uint8_t *vbuf = max_vec > (size_t)CHUNK_BLOCKS * 34 ? (uint8_t *)malloc(max_vec) : NULL;
+    if (!buf) { __atomic_store_n(&j->failed, 1, __ATOMIC_RELAXED); return NULL; }
+    for (;;) {
+        uint64_t it = __atomic_fetch_add(&j->next, 1, __ATOMIC_RELAXED);
+        if (it >= j->n_items || __atomic_load_n(&j->failed, __ATOMIC_RELAXED)) break;
+        gen_item(j, it, (vbuf && j->t[j->item_tensor[it]].type == T_F32) ? vbuf : buf);
+    }
+    free(vbuf);
+    free(buf);
+    return NULL;
+}
+
+int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
+    if (!path || !s) return -5;
+    if (s->n_layers <= 0 || s->hidden <= 0 || s->n_heads <= 0 || s->n_kv_heads <= 0 ||
+        s->head_dim <= 0 || s->ffn <= 0 || s->vocab <= 3 || s->hidden % 32 || s->ffn % 32 ||
+        (s->n_heads * s->head_dim) % 32 || (s->n_kv_heads * s->head_dim) % 32 ||
+        (s->layer_type != T_Q4_0 && s->layer_type != T_Q8_0) ||
+        (s->embd_type != T_Q4_0 && s->embd_type != T_Q8_0) ||
+        (s->out_type != -1 && s->out_type != T_Q4_0 && s->out_type != T_Q8_0))
+        return -5;
+    const int L = s->n_layers;
+    const uint64_t d = (uint64_t)s->hidden, q = (uint64_t)s->n_heads * s->head_dim,
+                   kv = (uint64_t)s->n_kv_heads * s->head_dim, f = (uint64_t)s->ffn;
+    int nt = 1 + 9 * L + 1 + (s->out_type >= 0 ? 1 : 0);
+    syn_tensor_t *t = (syn_tensor_t *)calloc((size_t)nt, sizeof(syn_tensor_t));
+    if (!t) return -3;
+    int k = 0;
+#define ADD(nm, type_, cols, rows, isnorm)                                           \
+    do {                                                                             \
+        snprintf(t[k].name, sizeof(t[k].name), "%s", nm);                           \
+        t[k].type = (type_);                                                         \
+        t[k].dims[0] = (cols);                                                       \
+        t[k].dims[1] = (rows);                                                       \
+        t[k].n_dims = (isnorm) ? 1 : 2;                                              \
+        t[k].norm = (isnorm);                                                        \
+        t[k].bytes = (isnorm) ? (uint64_t)(cols) * 4                                 \
+                              : (uint64_t)(cols) * (rows) / 32 * ((type_) == T_Q4_0 ? 18 : 34); \
+        k++;                                                                         \
+    } while (0)
+    ADD("token_embd.weight", s->embd_type, d, (uint64_t)s->vocab, 0);
+    char nm[64];
+    for (int l = 0; l < L; l++) {
+        snprintf(nm, sizeof(nm), "blk.%d.attn_norm.weight", l); ADD(nm, T_F32, d, 1, 1);
+        snprintf(nm, sizeof(nm), "blk.%d.attn_q.weight", l); ADD(nm, s->layer_type, d, q, 0);
+        snprintf(nm, sizeof(nm), "blk.%d.attn_k.weight", l); ADD(nm, s->layer_type, d, kv, 0);
+        snprintf(nm, sizeof(nm), "blk.%d.attn_v.weight", l); ADD(nm, s->layer_type, d, kv, 0);
+        snprintf(nm, sizeof(nm), "blk.%d.attn_output.weight", l); ADD(nm, s->layer_type, q, d, 0);
+        snprintf(nm, sizeof(nm), "blk.%d.ffn_norm.weight", l); ADD(nm, T_F32, d, 1, 1);
+        snprintf(nm, sizeof(nm), "blk.%d.ffn_gate.weight", l); ADD(nm, s->layer_type, d, f, 0);
+        snprintf(nm, sizeof(nm), "blk.%d.ffn_up.weight", l); ADD(nm, s->layer_type, d, f, 0);
+        snprintf(nm, sizeof(nm), "blk.%d.ffn_down.weight", l); ADD(nm, s->layer_type, f, d, 0);
+    }
+    ADD("output_norm.weight", T_F32, d, 1, 1);
+    if (s->out_type >= 0) ADD("output.weight", s->out_type, d, (uint64_t)s->vocab, 0);
+#undef ADD
+    uint64_t off = 0;
+    for (int i = 0; i < nt; i++) {
+        t[i].offset = off;
+        off = (off + t[i].bytes + 31) & ~(uint64_t)31;
+    }
+    const uint64_t data_bytes = off;
+
+    wbuf_t b = {0};
+    const uint32_t n_kv = 12 + (s->with_vocab ? 3 : 0);
+    wb_u32(&b, 0x46554747u);
+    wb_u32(&b, 3);
+    wb_u64(&b, (uint64_t)nt);
+    wb_u64(&b, n_kv);
+    kv_str(&b, "general.architecture", "llama");
+    kv_str(&b, "general.name", "synthetic-llama");
+    kv_u32(&b, "general.alignment", 32);
+    kv_u32(&b, "llama.block_count", (uint32_t)L);
+    kv_u32(&b, "llama.context_length", (uint32_t)(s->context_length > 0 ? s->context_length : 2048));
+    kv_u32(&b, "llama.embedding_length", (uint32_t)d);
+    kv_u32(&b, "llama.feed_forward_length", (uint32_t)f);
+    kv_u32(&b, "llama.attention.head_count", (uint32_t)s->n_heads);
+    kv_u32(&b, "llama.attention.head_count_kv", (uint32_t)s->n_kv_heads);
+    kv_u32(&b, "llama.rope.dimension_count", (uint32_t)s->head_dim);
+    kv_f32(&b, "llama.rope.freq_base", s->rope_theta > 0 ? s->rope_theta : 10000.0f);
+    kv_f32(&b, "llama.attention.layer_norm_rms_epsilon", s->rms_eps > 0 ? s->rms_eps : 1e-5f);
+    if (s->with_vocab) {
+        char vb[64];
+        kv_str(&b, "tokenizer.ggml.model", "llama");
+        wb_str(&b, "tokenizer.ggml.tokens");
+        wb_u32(&b, 9);
+        wb_u32(&b, 8);
+        wb_u64(&b, (uint64_t)s->vocab);
+        for (int i = 0; i < s->vocab; i++) wb_str(&b, ss_synth_vocab_string(s->vocab, i, vb, sizeof(vb)));
+        wb_str(&b, "tokenizer.ggml.scores");
+        wb_u32(&b, 9);
+        wb_u32(&b, 6);
+        wb_u64(&b, (uint64_t)s->vocab);
+        for (int i = 0; i < s->vocab; i++) wb_f32(&b, i < 259 ? 0.0f : -(float)(i - 259) * 0.01f);
+    }
+    for (int i = 0; i < nt; i++) {
+        wb_str(&b, t[i].name);
+        wb_u32(&b, t[i].n_dims);
+        for (uint32_t dd = 0; dd < t[i].n_dims; dd++) wb_u64(&b, t[i].dims[dd]);
+        wb_u32(&b, (uint32_t)t[i].type);
+        wb_u64(&b, t[i].offset);
+    }
+    if (b.bad) { free(b.p); free(t); return -3; }
+    const uint64_t data_off = (b.n + 31) & ~(uint64_t)31;
+    while (b.n < data_off) { uint8_t z = 0; wb_put(&b, &z, 1); }
+
+    int fd = open(path, O_WRONLY | O_CREAT | O_TRUNC, 0644);
+    if (fd < 0) { free(b.p); free(t); return -1; }
+    int32_t rc = 0;
+    if (ftruncate(fd, (off_t)(data_off + data_bytes)) != 0 ||
+        pwrite(fd, b.p, b.n, 0) != (ssize_t)b.n)
+        rc = -1;
+    free(b.p);
+
+    job_t j = {0};
+    j.fd = fd;
+    j.data_off = data_off;
+    j.seed = s->seed;
+    j.scale_sigma = s->scale_sigma > 0 ? s->scale_sigma : 0.02f;
+    j.norm_sigma = s->norm_sigma > 0 ? s->norm_sigma : 0.01f;
+    j.t = t;
+    j.nt = nt;
+    uint64_t items = 0;
+    for (int i = 0; i < nt; i++)
+        items += t[i].type == T_F32 ? 1 : (tensor_blocks(&t[i]) + CHUNK_BLOCKS - 1) / CHUNK_BLOCKS;
+    j.item_tensor = (uint64_t *)malloc(items * 8);
+    j.item_chunk = (uint64_t *)malloc(items * 8);
+    if (!j.item_tensor || !j.item_chunk) rc = -3;
+    uint64_t it = 0;
+    for (int i = 0; rc == 0 && i < nt; i++) {
+        uint64_t nc = t[i].type == T_F32 ? 1 : (tensor_blocks(&t[i]) + CHUNK_BLOCKS - 1) / CHUNK_BLOCKS;
+        for (uint64_t c = 0; c < nc; c++) { j.item_tensor[it] = (uint64_t)i; j.item_chunk[it] = c; it++; }
+    }
+    j.n_items = items;
+    if (rc == 0) {
+        int nth = s->n_threads > 0 ? s->n_threads : (int)sysconf(_SC_NPROCESSORS_ONLN);
+        if (nth < 1) nth = 1;
+        if (nth > 64) nth = 64;
+        pthread_t th[64];
+        int started = 0;
+        for (int i = 0; i < nth; i++)
+            if (pthread_create(&th[started], NULL, worker, &j) == 0) started++;
+        if (started == 0) worker(&j);
+        for (int i = 0; i < started; i++) pthread_join(th[i], NULL);
+        if (j.failed) rc = -1;
+    }
+    free(j.item_tensor);
+    free(j.item_chunk);
+    free(t);
+    if (close(fd) != 0) rc = -1;
+    return rc;
+}

@@ -1,0 +1,259 @@
+"""Per-kernel parity of the HIP path against the CPU oracle, through the C-ABI.
+
+Tolerance (fp32 accumulation on both sides, different summation order):
+max |gpu - oracle| / max |oracle| <= 1e-3 for every floating-point output;
+bit-exact for integer results (argmax, int8 codes) and for pure
+dequantisation (one fp32 multiply per weight on both sides).
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.util import Q4_0, Q8_0, make_blocks, rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+vp = C.c_void_p
+
+
+def _matvec_case(hip, qtype, rows, cols, seed):
+    rng = np.random.default_rng(seed)
+    w = make_blocks(qtype, rows, cols, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    want = oracle.matvec(w, x, rows, cols, qtype)
+    W = hip.packed(w, qtype, rows, cols)
+    X = hip.upload(x)
+    Y = hip.buf(4 * rows)
+    rc = hip.L.ss_hip_matvec(hip.ctx, Y.ptr, W.ptr, X.ptr, rows, cols, qtype, None)
+    assert rc == 0, hip.err()
+    got = Y.read(np.float32, rows)
+    for b in (W, X, Y):
+        b.free()
+    return got, want
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("rows,cols", [(4096, 4096), (1, 32), (7, 64), (257, 2048), (33, 11008),
+                                       (17, 14336), (9, 28672), (5, 14368)])
+def test_matvec(hip, qtype, rows, cols):
+    print("matvec", qtype, rows, cols, flush=True)
+    got, want = _matvec_case(hip, qtype, rows, cols, seed=rows * 7 + cols)
+    assert np.all(np.isfinite(got))
+    assert rel_err(got, want) <= TOL
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_matvec_fused_norm_residual(hip, qtype):
+    rows, cols, eps = 300, 4096, 1e-5
+    rng = np.random.default_rng(11)
+    w = make_blocks(qtype, rows, cols, rng)
+    x = (3.0 * rng.standard_normal(cols)).astype(np.float32)
+    nw = (1.0 + 0.01 * rng.standard_normal(cols)).astype(np.float32)
+    res = rng.standard_normal(rows).astype(np.float32)
+    want = oracle.matvec(w, oracle.rmsnorm(x, nw, eps), rows, cols, qtype) + res
+    W, X, NW, Y = hip.packed(w, qtype, rows, cols), hip.upload(x), hip.upload(nw), hip.upload(res)
+    rc = hip.L.ss_hip_matvec_fused(hip.ctx, Y.ptr, W.ptr, X.ptr, NW.ptr, eps, 1, rows, cols, qtype, None)
+    assert rc == 0, hip.err()
+    assert rel_err(Y.read(np.float32, rows), want) <= TOL
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_ffn_gate_up(hip, qtype):
+    rows, cols, eps = 1100, 2048, 1e-5
+    rng = np.random.default_rng(5)
+    wg = make_blocks(qtype, rows, cols, rng)
+    wu = make_blocks(qtype, rows, cols, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    nw = (1.0 + 0.01 * rng.standard_normal(cols)).astype(np.float32)
+    xn = oracle.rmsnorm(x, nw, eps)
+    g = oracle.matvec(wg, xn, rows, cols, qtype)
+    u = oracle.matvec(wu, xn, rows, cols, qtype)
+    lib = oracle.lib()
+    want = np.array([lib.orc_silu_mul(float(a), float(b)) for a, b in zip(g, u)], np.float32)
+    WG, WU = hip.packed(wg, qtype, rows, cols), hip.packed(wu, qtype, rows, cols)
+    X, NW, Y = hip.upload(x), hip.upload(nw), hip.buf(4 * rows)
+    rc = hip.L.ss_hip_ffn_gate_up(hip.ctx, Y.ptr, WG.ptr, WU.ptr, X.ptr, NW.ptr, eps, rows, cols, qtype, None)
+    assert rc == 0, hip.err()
+    assert rel_err(Y.read(np.float32, rows), want) <= TOL
+
+
+@pytest.mark.parametrize("n", [4, 2048, 8192, 5000])
+def test_rmsnorm(hip, n):
+    rng = np.random.default_rng(n)
+    x = (10 * rng.standard_normal(n)).astype(np.float32)
+    w = (1 + 0.01 * rng.standard_normal(n)).astype(np.float32)
+    X, W, Y = hip.upload(x), hip.upload(w), hip.buf(4 * n)
+    assert hip.L.ss_hip_rmsnorm(hip.ctx, Y.ptr, X.ptr, W.ptr, n, 1e-5, None) == 0, hip.err()
+    assert rel_err(Y.read(np.float32, n), oracle.rmsnorm(x, w, 1e-5)) <= TOL
+
+
+@pytest.mark.parametrize("neox", [False, True])
+@pytest.mark.parametrize("pos,theta,hd,rd", [(0, 1e4, 64, 64), (37, 1e4, 128, 128), (4100, 5e5, 128, 128),
+                                             (1000, 1e4, 128, 64)])
+def test_rope(hip, neox, pos, theta, hd, rd):
+    H, KVH = 8, 2
+    rng = np.random.default_rng(pos)
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    k = rng.standard_normal(KVH * hd).astype(np.float32)
+    wq, wk = oracle.rope(q, k, H, KVH, hd, rd, pos, theta, neox)
+    Q, K = hip.upload(q), hip.upload(k)
+    rc = hip.L.ss_hip_rope(hip.ctx, Q.ptr, K.ptr, H, KVH, hd, rd, pos, theta, int(neox), None)
+    assert rc == 0, hip.err()
+    # same host libm (cos, sin) on both sides, one rotation each: ~1 ulp
+    np.testing.assert_allclose(Q.read(np.float32, H * hd), wq, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(K.read(np.float32, KVH * hd), wk, rtol=1e-5, atol=1e-5)
+
+
+def test_kv_append_int8_bit_exact(hip):
+    KVH, hd, max_seq, pos = 8, 128, 16, 5
+    rng = np.random.default_rng(3)
+    k = (4 * rng.standard_normal(KVH * hd)).astype(np.float32)
+    v = (4 * rng.standard_normal(KVH * hd)).astype(np.float32)
+    k[7] = 0.0
+    n = KVH * max_seq * hd
+    KC, VC, KS, VS = hip.upload(np.zeros(n, np.int8)), hip.upload(np.zeros(n, np.int8)), \
+        hip.upload(np.zeros(max_seq, np.float32)), hip.upload(np.zeros(max_seq, np.float32))
+    K, V = hip.upload(k), hip.upload(v)
+    rc = hip.L.ss_hip_kv_append(hip.ctx, KC.ptr, VC.ptr, KS.ptr, VS.ptr, K.ptr, V.ptr, KVH, hd, max_seq, pos, 1, None)
+    assert rc == 0, hip.err()
+    kc = KC.read(np.int8, n).reshape(KVH, max_seq, hd)
+    ks = KS.read(np.float32, max_seq)
+    qk, sk = oracle.kv_int8_encode(k)
+    assert ks[pos] == np.float32(sk)
+    np.testing.assert_array_equal(kc[:, pos, :].reshape(-1), qk)
+    assert not kc[:, pos + 1, :].any() and not kc[:, pos - 1, :].any()
+
+
+def test_kv_append_int8_zero_vector(hip):
+    KVH, hd, max_seq = 2, 64, 4
+    n = KVH * max_seq * hd
+    z = np.zeros(KVH * hd, np.float32)
+    KC, VC, KS, VS = hip.upload(np.zeros(n, np.int8)), hip.upload(np.zeros(n, np.int8)), \
+        hip.upload(np.ones(max_seq, np.float32)), hip.upload(np.ones(max_seq, np.float32))
+    Z = hip.upload(z)
+    assert hip.L.ss_hip_kv_append(hip.ctx, KC.ptr, VC.ptr, KS.ptr, VS.ptr, Z.ptr, Z.ptr, KVH, hd, max_seq, 1, 1, None) == 0
+    assert KS.read(np.float32, max_seq)[1] == 0.0     # s = 0 -> codes 0 (layer_scheduler.c:114)
+    assert not KC.read(np.int8, n).any()
+
+
+def _attn_ref(q, kc, vc, H, KVH, hd, seq, ks=None, vs=None):
+    G = H // KVH
+    out = np.zeros(H * hd, np.float32)
+    for h in range(H):
+        g = h // G
+        kk = kc[g, :seq].astype(np.float32)
+        vv = vc[g, :seq].astype(np.float32)
+        if ks is not None:
+            kk = kk * ks[:seq, None]
+            vv = vv * vs[:seq, None]
+        out[h * hd:(h + 1) * hd] = oracle.attention_head(q[h * hd:(h + 1) * hd], kk, vv)
+    return out
+
+
+@pytest.mark.parametrize("kv_type", [0, 1])
+@pytest.mark.parametrize("H,KVH,hd,seq,max_seq", [(32, 32, 128, 640, 768), (32, 4, 64, 160, 160),
+                                                   (32, 8, 128, 4224, 4352), (8, 8, 128, 1, 8),
+                                                   (16, 8, 64, 65, 100), (64, 8, 128, 1030, 1088)])
+def test_attention(hip, kv_type, H, KVH, hd, seq, max_seq):
+    print("attention", kv_type, H, KVH, hd, seq, flush=True)
+    rng = np.random.default_rng(seq)
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    if kv_type == 0:
+        kc = rng.standard_normal((KVH, max_seq, hd)).astype(np.float16)
+        vc = rng.standard_normal((KVH, max_seq, hd)).astype(np.float16)
+        ks = vs = None
+        KS = VS = None
+    else:
+        kc = rng.integers(-127, 128, (KVH, max_seq, hd)).astype(np.int8)
+        vc = rng.integers(-127, 128, (KVH, max_seq, hd)).astype(np.int8)
+        ks = (rng.random(max_seq) * 0.03).astype(np.float32)
+        vs = (rng.random(max_seq) * 0.03).astype(np.float32)
+    want = _attn_ref(q, kc, vc, H, KVH, hd, seq, ks, vs)
+    Q, KC, VC, O = hip.upload(q), hip.upload(kc), hip.upload(vc), hip.buf(4 * H * hd)
+    KS = hip.upload(ks) if ks is not None else None
+    VS = hip.upload(vs) if vs is not None else None
+    rc = hip.L.ss_hip_attention(hip.ctx, O.ptr, Q.ptr, KC.ptr, VC.ptr, KS.ptr if KS else None,
+                                VS.ptr if VS else None, H, KVH, hd, max_seq, seq, kv_type, None)
+    assert rc == 0, hip.err()
+    got = O.read(np.float32, H * hd)
+    assert rel_err(got, want) <= TOL
+    # run twice: the split counters must have been reset by the merging workgroup
+    rc = hip.L.ss_hip_attention(hip.ctx, O.ptr, Q.ptr, KC.ptr, VC.ptr, KS.ptr if KS else None,
+                                VS.ptr if VS else None, H, KVH, hd, max_seq, seq, kv_type, None)
+    assert rc == 0
+    assert np.array_equal(O.read(np.float32, H * hd), got)
+
+
+def test_attention_single_position_is_v0(hip):
+    H, KVH, hd, max_seq = 4, 4, 64, 8
+    rng = np.random.default_rng(1)
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    kc = rng.standard_normal((KVH, max_seq, hd)).astype(np.float16)
+    vc = rng.standard_normal((KVH, max_seq, hd)).astype(np.float16)
+    Q, KC, VC, O = hip.upload(q), hip.upload(kc), hip.upload(vc), hip.buf(4 * H * hd)
+    assert hip.L.ss_hip_attention(hip.ctx, O.ptr, Q.ptr, KC.ptr, VC.ptr, None, None, H, KVH, hd, max_seq, 1, 0, None) == 0
+    np.testing.assert_allclose(O.read(np.float32, H * hd), vc[:, 0, :].astype(np.float32).reshape(-1), rtol=1e-6)
+
+
+@pytest.mark.parametrize("n", [5, 32000, 128256, 300000])
+def test_argmax(hip, n):
+    rng = np.random.default_rng(n)
+    x = rng.standard_normal(n).astype(np.float32)
+    if n > 10:
+        x[n // 3] = x[n - 2] = 9.0          # tie: first index wins
+    X, O = hip.upload(x), hip.buf(16)
+    for _ in range(2):
+        assert hip.L.ss_hip_argmax(hip.ctx, O.ptr, X.ptr, n, None) == 0, hip.err()
+        assert int(O.read(np.int32, 1)[0]) == oracle.argmax(x)
+
+
+def test_argmax_reference_known_answer(hip):
+    x = np.array([1.0, 3.0, 2.0, 5.0, 4.0], np.float32)   # test_tensor_ops.c:116-119
+    X, O = hip.upload(x), hip.buf(16)
+    assert hip.L.ss_hip_argmax(hip.ctx, O.ptr, X.ptr, 5, None) == 0
+    assert int(O.read(np.int32, 1)[0]) == 3
+    x = np.array([np.nan, 1.0, 7.0], np.float32)             # x[0] NaN -> 0
+    X2 = hip.upload(x)
+    assert hip.L.ss_hip_argmax(hip.ctx, O.ptr, X2.ptr, 3, None) == 0
+    assert int(O.read(np.int32, 1)[0]) == oracle.argmax(x) == 0
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_embed_row_bit_exact(hip, qtype):
+    rows, cols = 50, 4096
+    rng = np.random.default_rng(9)
+    w = make_blocks(qtype, rows, cols, rng)
+    bpr = (cols // 32) * (18 if qtype == Q4_0 else 34)
+    T, O = hip.packed(w, qtype, rows, cols), hip.buf(4 * cols)
+    for tok in (0, 17, 49):
+        assert hip.L.ss_hip_embed_row(hip.ctx, O.ptr, T.ptr, qtype, rows, cols, tok, None) == 0
+        want = oracle.dequantize(w[tok * bpr:(tok + 1) * bpr], cols, qtype)
+        assert np.array_equal(O.read(np.float32, cols), want)
+
+
+def test_swiglu(hip):
+    n = 11008
+    rng = np.random.default_rng(2)
+    g = (5 * rng.standard_normal(n)).astype(np.float32)
+    u = rng.standard_normal(n).astype(np.float32)
+    G, U, O = hip.upload(g), hip.upload(u), hip.buf(4 * n)
+    assert hip.L.ss_hip_swiglu(hip.ctx, O.ptr, G.ptr, U.ptr, n, None) == 0
+    lib = oracle.lib()
+    want = np.array([lib.orc_silu_mul(float(a), float(b)) for a, b in zip(g, u)], np.float32)
+    np.testing.assert_allclose(O.read(np.float32, n), want, rtol=2e-6, atol=1e-7)
+
+
+def test_matvec_host_plug(hip):
+    rows, cols = 64, 256
+    rng = np.random.default_rng(4)
+    w = make_blocks(Q4_0, rows, cols, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    out = np.zeros(rows, np.float32)
+    fp = C.POINTER(C.c_float)
+    for _ in range(2):   # second call hits the registry
+        ok = hip.L.ss_hip_matvec_host(hip.ctx, out.ctypes.data_as(fp), w.ctypes.data_as(vp),
+                                      x.ctypes.data_as(fp), rows, cols, Q4_0)
+        assert ok == 1
+        assert rel_err(out, oracle.matvec(w, x, rows, cols, Q4_0)) <= TOL
