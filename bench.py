@@ -1,0 +1,200 @@
+"""Batch-1 decode benchmark of the SlipStream token loop on one MI355X.
+
+Default workload: Llama-2-7B-shape decoder with random-init weights (32
+layers, d 4096, 32 heads = 32 KV heads of dim 128, FFN 11008, vocab 32000),
+Q4_0 layer matrices with Q8_0 token_embd/output, a 512-token random prompt,
+then greedy decode at batch 1 with an fp16 KV cache. A "step" is one decode
+token: embedding, 32 layers, output norm, LM head, argmax.
+
+Prints one JSON line. `value` is decode tokens/s over exactly --steps decode
+steps (after --warmup untimed ones), with the weights resident in HBM. The
+roofline object is for the dominant kernel class (the Q4_0 matvecs),
+measured with HIP events on the model stream in a profiled replay of the
+same decode steps; cpu_baseline is the CPU oracle (the reference path
+restated in C) on the same GGUF, timed on this host on a bounded sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+import numpy as np  # noqa: E402
+
+METRIC = "batch-1 decode tokens/sec (7B Q4_0); matvec achieved HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+
+CONFIGS = {
+    "llama2-7b": dict(spec=dict(n_layers=32, hidden=4096, n_heads=32, n_kv_heads=32, head_dim=128,
+                                ffn=11008, vocab=32000, context_length=4096, layer_type=2, embd_type=8,
+                                out_type=8, seed=7), prompt=512, steps=256,
+                      name="llama2-7b-shape, Q4_0 layers + Q8_0 token_embd/output"),
+    "tinyllama": dict(spec=dict(n_layers=22, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=64,
+                                ffn=5632, vocab=32000, context_length=2048, layer_type=2, embd_type=2,
+                                out_type=2, seed=1001), prompt=32, steps=128,
+                      name="tinyllama-1.1b-shape, all Q4_0"),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def token_bytes(spec, ctx):
+    """Algorithmic HBM bytes of one decode token at context length ctx."""
+    L, d, H, KVH, hd, F, V = (spec[k] for k in ("n_layers", "hidden", "n_heads", "n_kv_heads",
+                                                 "head_dim", "ffn", "vocab"))
+    bpw = {2: 18 / 32, 8: 34 / 32}
+    lt = bpw[spec["layer_type"]]
+    layer_w = (H * hd * d + 2 * KVH * hd * d + d * H * hd + 3 * F * d) * lt
+    head = V * d * bpw[spec["out_type"] if spec["out_type"] >= 0 else spec["embd_type"]]
+    kv_read = 2 * L * ctx * KVH * hd * 2
+    kv_write = 2 * L * KVH * hd * 2
+    norms = (2 * L + 1) * d * 4
+    embd_row = d * bpw[spec["embd_type"]]
+    return L * layer_w + head + kv_read + kv_write + norms + embd_row
+
+
+def cpu_baseline(path, spec, prompt_len, budget_s=20.0, max_steps=8):
+    """The oracle (reference CPU path restated in C) on the same file: KV for
+    positions 0..prompt_len-1 pre-filled with fp16 values, then decode steps
+    at positions prompt_len.. until the time budget is spent."""
+    import oracle
+    om = oracle.Model(path, prompt_len + max_steps + 1, "f16")
+    rng = np.random.default_rng(0)
+    kvdim = spec["n_kv_heads"] * spec["head_dim"]
+    for layer in range(spec["n_layers"]):
+        k = rng.standard_normal((prompt_len, kvdim)).astype(np.float16).view(np.uint16)
+        for p in range(prompt_len):
+            om.kv_write(layer, p, k[p], k[p])
+    tok = 11
+    om.forward(tok, prompt_len)   # untimed: pages the weights in
+    t0 = time.perf_counter()
+    n = 0
+    while n < max_steps and (time.perf_counter() - t0) < budget_s:
+        tok = oracle.argmax(om.forward(tok, prompt_len + 1 + n))
+        n += 1
+    dt = time.perf_counter() - t0
+    threads = oracle.lib().orc_get_threads()
+    om.close()
+    return {"value": n / dt, "unit": "tok/s", "cores": int(threads), "kind": "port",
+            "sample": "%d decode steps at context %d (KV pre-filled), same GGUF, %d threads, %.1f s"
+                      % (n, prompt_len + 1, threads, dt)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--config", default="llama2-7b", choices=sorted(CONFIGS))
+    ap.add_argument("--kv", default="f16", choices=["f16", "int8"])
+    ap.add_argument("--model-dir", default=os.environ.get("SS_BENCH_DIR", "/tmp"))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-steps", type=int, default=16)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (--gpus %d requested)"
+              % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    from phonemap_amd import api
+    cfg = CONFIGS[args.config]
+    spec = cfg["spec"]
+    steps = args.steps if args.steps is not None else cfg["steps"]
+    warm = args.warmup
+    prompt_len = cfg["prompt"]
+    path = os.path.join(args.model_dir, "ss_bench_%s_s%d.gguf" % (args.config, spec["seed"]))
+    if not os.path.exists(path):
+        t = time.perf_counter()
+        api.write_synthetic_gguf(path + ".part", api.SynthSpec(**spec))
+        os.replace(path + ".part", path)
+        log("wrote %s (%.2f GB) in %.1f s" % (path, os.path.getsize(path) / 1e9, time.perf_counter() - t))
+    max_ctx = prompt_len + warm + steps + args.profile_steps + 2
+    t = time.perf_counter()
+    m = api.Model(path, max_context=max_ctx, kv=args.kv)
+    log("loaded in %.1f s" % (time.perf_counter() - t))
+    L = api._lib()
+    rng = np.random.default_rng(1234)
+    prompt = rng.integers(3, spec["vocab"], prompt_len).tolist()
+
+    m.reset()
+    t = time.perf_counter()
+    m.eval_prompt(prompt, 0, want_logits=False)
+    prefill_s = time.perf_counter() - t
+    log("prefill %d tokens: %.3f s" % (prompt_len, prefill_s))
+    if warm:
+        m.decode_greedy(warm)
+    t0 = time.perf_counter()
+    toks = m.decode_greedy(steps)       # returns after a stream synchronise
+    dt = time.perf_counter() - t0
+    tps = steps / dt
+    log("decode %d steps: %.3f s, %.1f tok/s" % (steps, dt, tps))
+
+    # profiled replay (eager launches bracketed by HIP events on the model stream)
+    roof = None
+    try:
+        roof = profile_classes(m, args.profile_steps)
+    except Exception as e:   # profiling is optional for the headline number
+        log("profiling failed: %s" % e)
+
+    avg_ctx = prompt_len + warm + (steps + 1) / 2.0
+    tb = token_bytes(spec, avg_ctx)
+    out = {
+        "metric": METRIC, "value": round(tps, 2), "unit": "tok/s", "n_gpus": 1, "steps": steps,
+        "warmup": warm, "ms_per_step": round(1000.0 * dt / steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "%s, %d-token random prompt, then %d greedy decode steps at batch 1, %s KV"
+                               % (cfg["name"], prompt_len, steps, args.kv),
+                   "global_batch": 1, "seq_len": prompt_len + warm + steps, "parallelism": "none",
+                   "prefill_tok_s": round(prompt_len / prefill_s, 2),
+                   "token_bytes_GB": round(tb / 1e9, 4),
+                   "sweep_GBs": round(tb * tps / 1e9, 1),
+                   "sweep_frac": round(tb * tps / 1e9 / HBM_PEAK_GBS, 4),
+                   "first_tokens": toks[:8]},
+        "roofline": roof,
+        "cpu_baseline": None,
+    }
+    m.close()
+    if not args.no_cpu_baseline:
+        try:
+            out["cpu_baseline"] = cpu_baseline(path, spec, prompt_len)
+        except Exception as e:
+            log("cpu baseline failed: %s" % e)
+    print(json.dumps(out), flush=True)
+
+
+def profile_classes(m, n_steps):
+    """Per-kernel-class device time over n_steps decode steps."""
+    import ctypes as C
+    from phonemap_amd import lib
+    from phonemap_amd.api import SlipStreamError
+    L = lib()
+    hm = L.ss_model_hip(m.h)
+    if not hm:
+        raise SlipStreamError("no HIP model handle")
+    if L.ss_hip_profile_begin(hm) != 0:
+        raise SlipStreamError("profile_begin failed")
+    m.decode_greedy(n_steps)
+    out = np.zeros(12, np.float64)
+    if L.ss_hip_profile_end(hm, out.ctypes.data_as(C.POINTER(C.c_double)), 12) != 0:
+        raise SlipStreamError("profile_end failed")
+    ms, cnt, byt = out[0], out[1], out[2]
+    if cnt <= 0:
+        raise SlipStreamError("no Q4_0 launches recorded")
+    avg_s = ms / 1e3 / cnt
+    ach = byt / cnt / avg_s / 1e9
+    return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "k_gemv Q4_0 (all epilogues)", "launches": int(cnt),
+            "avg_us": round(avg_s * 1e6, 3), "bytes_per_launch": round(byt / cnt, 1),
+            "classes_ms": {"q4_0_matvec": round(out[0], 3), "q8_0_matvec": round(out[3], 3),
+                           "attention": round(out[6], 3), "other": round(out[9], 3)},
+            "profiled_steps": n_steps}
+
+
+if __name__ == "__main__":
+    main()

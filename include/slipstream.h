@@ -206,6 +206,10 @@ ss_error_t ss_decode_greedy(ss_model_t *model, int32_t n_steps, int32_t *tokens_
 ss_error_t ss_kv_write(ss_model_t *model, int32_t layer, int32_t pos0, int32_t n_pos,
                        const uint16_t *k_f16, const uint16_t *v_f16);
 
+/* The backend handle of a loaded model (an ss_hip_model_t*, include/ss_hip.h),
+ * for callers that use the backend C-ABI directly (profiling, tests). */
+void *ss_model_hip(ss_model_t *model);
+
 /* tensor.h:115 and :121-123 (host-side, no device involved) */
 int32_t ss_argmax(const float *x, int32_t size);
 int32_t ss_sample(const float *logits, int32_t vocab_size, float temperature, float top_p,

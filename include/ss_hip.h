@@ -49,6 +49,8 @@ void ss_hip_free(ss_hip_ctx_t *ctx);
 const char *ss_hip_last_error(void);
 int32_t ss_hip_device_count(void);
 int32_t ss_hip_device_name(int32_t device, char *buf, int32_t len);
+/* compute units and HBM bytes of a device (for ss_get_device_info) */
+int32_t ss_hip_device_info(int32_t device, int32_t *n_cu, uint64_t *hbm_bytes);
 void *ss_hip_stream(ss_hip_ctx_t *ctx);          /* the context's hipStream_t */
 int32_t ss_hip_sync(ss_hip_ctx_t *ctx);
 

@@ -181,6 +181,14 @@ int32_t ss_hip_device_name(int32_t device, char* buf, int32_t len) {
   return 0;
 }
 
+int32_t ss_hip_device_info(int32_t device, int32_t* n_cu, uint64_t* hbm_bytes) {
+  hipDeviceProp_t p;
+  HIP_TRY(hipGetDeviceProperties(&p, device));
+  if (n_cu) *n_cu = p.multiProcessorCount;
+  if (hbm_bytes) *hbm_bytes = (uint64_t)p.totalGlobalMem;
+  return 0;
+}
+
 ss_hip_ctx_t* ss_hip_init(int32_t device) {
   int n = 0;
   if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {

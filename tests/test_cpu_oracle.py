@@ -1,0 +1,279 @@
+"""Pins the CPU oracle before it is trusted as the checker.
+
+Each oracle function is checked against (a) the known answers in the
+reference's own unit tests (tests/golden/reference_known_answers.json),
+(b) oracle/_ref/libssref.so, the reference's cpu_neon.c built from its own
+source, where that covers it, and (c) closed forms, invariants and
+independent float64 brute force chosen so a dropped term, wrong sign or
+transposed operand fails.
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.util import Q4_0, Q8_0, dequant_np, make_blocks, rel_err
+
+GOLD = json.load(open(os.path.join(os.path.dirname(__file__), "golden", "reference_known_answers.json")))
+L = oracle.lib()
+REF = oracle.ref()
+needs_ref = pytest.mark.skipif(REF is None, reason="oracle/_ref not built (reference tree absent)")
+
+
+def p(a):
+    return oracle._ptr(a)
+
+
+# ---------------------------------------------------------------- f16
+def test_f16_known_answers():
+    for h, v, tol in GOLD["f16_to_f32"]["cases"]:
+        assert abs(L.orc_f16_to_f32(h) - v) < tol
+
+
+def test_f16_to_f32_exhaustive_matches_ieee():
+    bits = np.arange(65536, dtype=np.uint16)
+    want = bits.view(np.float16).astype(np.float32)
+    got = np.array([L.orc_f16_to_f32(int(b)) for b in bits], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_f32_to_f16_round_to_nearest_even():
+    rng = np.random.default_rng(0)
+    xs = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 20000),
+        np.array([0.0, -0.0, 65504.0, 65519.0, 65520.0, 1e9, -1e9, 6.1e-5, 5.96e-8, 2.98e-8, 2.99e-8,
+                  1.0 + 2 ** -11, 1.0 + 3 * 2 ** -11, np.inf, -np.inf], np.float32)])
+    want = xs.astype(np.float16).view(np.uint16)
+    got = np.array([L.orc_f32_to_f16(float(x)) for x in xs], np.uint16)
+    assert np.array_equal(got, want)
+
+
+# ---------------------------------------------------------------- dequant
+def test_dequant_known_answers():
+    g = GOLD["dequant_f32"]
+    out = oracle.dequantize(np.array(g["src"], np.float32), 4, 0)
+    assert np.allclose(out, g["out"], atol=g["tol"])
+    g = GOLD["dequant_f16"]
+    out = oracle.dequantize(np.array(g["src"], np.uint16), 4, 1)
+    assert np.allclose(out, g["out"], atol=g["tol"])
+
+
+def test_q4_0_hand_built_block():
+    # d = 1.0; byte j = j | (15 - j) << 4  ->  w[j] = j - 8, w[j + 16] = 7 - j
+    blk = np.zeros(18, np.uint8)
+    blk[0:2] = np.array([0x3C00], np.uint16).view(np.uint8)
+    blk[2:] = [j | ((15 - j) << 4) for j in range(16)]
+    out = oracle.dequantize(blk, 32, Q4_0)
+    assert out[:16].tolist() == [j - 8 for j in range(16)]
+    assert out[16:].tolist() == [7 - j for j in range(16)]
+    # d = -2.0 (0xC000) and a subnormal d = 2^-24 (0x0001)
+    blk[0:2] = np.array([0xC000], np.uint16).view(np.uint8)
+    assert oracle.dequantize(blk, 32, Q4_0)[0] == 16.0
+    blk[0:2] = np.array([0x0001], np.uint16).view(np.uint8)
+    assert oracle.dequantize(blk, 32, Q4_0)[0] == np.float32(-8 * 2.0 ** -24)
+
+
+def test_q8_0_hand_built_block():
+    blk = np.zeros(34, np.uint8)
+    blk[0:2] = np.array([0x3800], np.uint16).view(np.uint8)   # 0.5
+    codes = np.array([127, -127, 0, 1, -1] + list(range(-13, 14)), np.int8)[:32]
+    blk[2:] = codes.view(np.uint8)
+    assert np.array_equal(oracle.dequantize(blk, 32, Q8_0), codes.astype(np.float32) * 0.5)
+
+
+def test_matvec_known_answer_orientation():
+    """test_tensor_ops.c:66-78 encoded exactly as Q8_0 (d = 1): [[1,2,3],[4,5,6]] @ [1,2,3]."""
+    g = GOLD["matvec"]
+    rows, cols = 2, 32
+    blocks = np.zeros((rows, 34), np.uint8)
+    for r in range(rows):
+        blocks[r, 0:2] = np.array([0x3C00], np.uint16).view(np.uint8)
+        codes = np.zeros(32, np.int8)
+        codes[:3] = g["mat"][r]
+        blocks[r, 2:] = codes.view(np.uint8)
+    x = np.zeros(cols, np.float32)
+    x[:3] = g["vec"]
+    assert oracle.matvec(blocks.reshape(-1), x, rows, cols, Q8_0).tolist() == g["out"]
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("rows,cols", [(1, 32), (37, 256), (300, 4096)])
+def test_matvec_vs_float64_brute_force(qtype, rows, cols):
+    rng = np.random.default_rng(rows + cols)
+    w = make_blocks(qtype, rows, cols, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    want = dequant_np(w, rows, cols, qtype) @ x.astype(np.float64)
+    assert rel_err(oracle.matvec(w, x, rows, cols, qtype), want) < 2e-6
+
+
+@needs_ref
+def test_dot_and_matvec_vs_reference_cpu_neon():
+    rng = np.random.default_rng(3)
+    a = rng.standard_normal(1000).astype(np.float32)
+    b = rng.standard_normal(1000).astype(np.float32)
+    ref = REF.ss_neon_dot(p(a), p(b), 1000)
+    assert abs(L.orc_dot(p(a), p(b), 1000) - ref) <= 1e-5 * max(1.0, abs(ref))
+    # F32 matvec known answer through the reference's own ss_neon_matvec
+    mat = np.array([1, 2, 3, 4, 5, 6], np.float32)
+    vec = np.array([1, 2, 3], np.float32)
+    out = np.zeros(2, np.float32)
+    REF.ss_neon_matvec(p(out), p(mat), p(vec), 2, 3)
+    assert out.tolist() == GOLD["matvec"]["out"]
+
+
+# ---------------------------------------------------------------- norms / activations
+def test_rmsnorm_known_answer():
+    g = GOLD["rmsnorm"]
+    out = oracle.rmsnorm(g["x"], g["w"], g["eps"])
+    s = 1.0 / math.sqrt(g["rms_sq"])
+    assert abs(out[0] - 1 * s) < g["tol"] and abs(out[1] - 2 * s) < g["tol"]
+
+
+@needs_ref
+@pytest.mark.parametrize("n", [4, 2048, 4096, 8192])
+def test_rmsnorm_bit_exact_vs_reference(n):
+    rng = np.random.default_rng(n)
+    x = (5 * rng.standard_normal(n)).astype(np.float32)
+    w = (1 + 0.01 * rng.standard_normal(n)).astype(np.float32)
+    ref = np.zeros(n, np.float32)
+    REF.ss_neon_rmsnorm(p(ref), p(x), p(w), n, 1e-5)
+    assert np.array_equal(oracle.rmsnorm(x, w, 1e-5), ref)
+
+
+def test_silu_known_answers():
+    for g, want in GOLD["silu"]["cases"]:
+        assert abs(L.orc_silu_mul(g, 1.0) - want) < GOLD["silu"]["tol"]
+
+
+@needs_ref
+def test_silu_bit_exact_vs_reference():
+    rng = np.random.default_rng(1)
+    g = (8 * rng.standard_normal(4099)).astype(np.float32)
+    ref = g.copy()
+    REF.ss_neon_silu(p(ref), ref.size)
+    got = np.array([L.orc_silu_mul(float(v), 1.0) for v in g], np.float32)
+    assert np.array_equal(got, ref)
+
+
+def test_softmax_known_answers():
+    g = GOLD["softmax_uniform"]
+    assert np.allclose(oracle.softmax(g["x"]), g["out"], atol=g["tol"])
+    g = GOLD["softmax_sums_to_one"]
+    assert abs(float(np.sum(oracle.softmax(g["x"]))) - g["sum"]) < g["tol"]
+    x = np.array([1000.0, 999.0, -1e30], np.float32)        # max subtraction keeps it finite
+    s = oracle.softmax(x)
+    assert np.all(np.isfinite(s)) and abs(s[0] / s[1] - math.e) < 1e-5
+
+
+def test_argmax_known_answers_and_tie_rule():
+    assert oracle.argmax(GOLD["argmax"]["x"]) == GOLD["argmax"]["out"]
+    assert oracle.argmax([2.0, 5.0, 5.0, 1.0]) == 1            # first maximum
+    assert oracle.argmax([float("nan"), 3.0]) == 0              # starts from x[0]
+    assert oracle.argmax([1.0, float("nan"), 3.0]) == 2
+
+
+# ---------------------------------------------------------------- RoPE
+def test_rope_position_zero_is_identity():
+    rng = np.random.default_rng(2)
+    q = rng.standard_normal(4 * 64).astype(np.float32)
+    k = rng.standard_normal(2 * 64).astype(np.float32)
+    for neox in (False, True):
+        q2, k2 = oracle.rope(q, k, 4, 2, 64, 64, 0, 10000.0, neox)
+        assert np.array_equal(q2, q) and np.array_equal(k2, k)
+
+
+@pytest.mark.parametrize("neox", [False, True])
+def test_rope_closed_form_and_norms(neox):
+    hd, pos, theta = 64, 37, 10000.0
+    rng = np.random.default_rng(4)
+    q = rng.standard_normal(hd).astype(np.float32)
+    k = rng.standard_normal(hd).astype(np.float32)
+    q2, _ = oracle.rope(q, k, 1, 1, hd, hd, pos, theta, neox)
+    half = hd // 2
+    for i in range(half):
+        a, b = (i, i + half) if neox else (2 * i, 2 * i + 1)
+        ang = pos * theta ** (-(2.0 * i) / hd)
+        ca, sa = math.cos(ang), math.sin(ang)
+        assert abs(q2[a] - (q[a] * ca - q[b] * sa)) < 2e-5
+        assert abs(q2[b] - (q[a] * sa + q[b] * ca)) < 2e-5
+        assert abs(math.hypot(q2[a], q2[b]) - math.hypot(q[a], q[b])) < 1e-5
+
+
+def test_rope_partial_dim_leaves_tail():
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal(128).astype(np.float32)
+    q2, _ = oracle.rope(q, q[:128].copy(), 1, 1, 128, 64, 99, 10000.0, False)
+    assert np.array_equal(q2[64:], q[64:]) and not np.array_equal(q2[:64], q[:64])
+
+
+def test_rope_table_matches_rope():
+    rd, npos = 64, 50
+    cs = np.zeros(npos * rd, np.float32)
+    L.orc_rope_table(p(cs), rd, npos, 10000.0)
+    q = np.zeros(rd, np.float32)
+    q[0::2] = 1.0
+    for pos in (0, 7, 49):
+        q2, _ = oracle.rope(q, q.copy(), 1, 1, rd, rd, pos, 10000.0, False)
+        assert np.array_equal(q2[0::2], cs[pos * rd:(pos + 1) * rd][0::2])   # cos
+        assert np.array_equal(q2[1::2], cs[pos * rd:(pos + 1) * rd][1::2])   # sin
+
+
+# ---------------------------------------------------------------- KV int8
+def test_kv_int8_closed_form():
+    rng = np.random.default_rng(6)
+    x = (3 * rng.standard_normal(1024)).astype(np.float32)
+    q, s = oracle.kv_int8_encode(x)
+    amax = np.max(np.abs(x))
+    assert s == np.float32(amax) / np.float32(127.0)
+    assert q.min() >= -127 and q.max() <= 127 and 127 in np.abs(q)
+    assert np.max(np.abs(q.astype(np.float32) * s - x)) <= s / 2 * (1 + 1e-5)
+    want = np.round(x.astype(np.float64) * (1.0 / np.float64(np.float32(s)))).astype(np.int8)
+    assert np.mean(q == want) > 0.999
+    qz, sz = oracle.kv_int8_encode(np.zeros(64, np.float32))
+    assert sz == 0.0 and not qz.any()
+
+
+# ---------------------------------------------------------------- attention
+def test_attention_single_position_is_v0():
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal(64).astype(np.float32)
+    k = rng.standard_normal((1, 64)).astype(np.float32)
+    v = rng.standard_normal((1, 64)).astype(np.float32)
+    assert np.array_equal(oracle.attention_head(q, k, v), v[0])
+
+
+def test_attention_identical_keys_average_values():
+    rng = np.random.default_rng(8)
+    q = rng.standard_normal(64).astype(np.float32)
+    k = np.repeat(rng.standard_normal((1, 64)).astype(np.float32), 10, axis=0)
+    v = rng.standard_normal((10, 64)).astype(np.float32)
+    assert np.allclose(oracle.attention_head(q, k, v), v.mean(axis=0), atol=1e-6)
+
+
+def test_attention_vs_float64():
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal(128).astype(np.float32)
+    k = rng.standard_normal((300, 128)).astype(np.float32)
+    v = rng.standard_normal((300, 128)).astype(np.float32)
+    s = (k.astype(np.float64) @ q) / math.sqrt(128)
+    pr = np.exp(s - s.max())
+    pr /= pr.sum()
+    assert rel_err(oracle.attention_head(q, k, v), pr @ v.astype(np.float64)) < 1e-5
+
+
+def test_thread_count_does_not_change_results():
+    rng = np.random.default_rng(10)
+    w = make_blocks(Q4_0, 333, 2048, rng)
+    x = rng.standard_normal(2048).astype(np.float32)
+    n0 = L.orc_get_threads()
+    outs = []
+    for n in (1, 3, 8):
+        L.orc_set_threads(n)
+        outs.append(oracle.matvec(w, x, 333, 2048, Q4_0))
+    L.orc_set_threads(n0)
+    assert all(np.array_equal(outs[0], o) for o in outs[1:])
