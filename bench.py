@@ -94,6 +94,8 @@ def main():
     ap.add_argument("--kv", default="f16", choices=["f16", "int8"])
     ap.add_argument("--model-dir", default=os.environ.get("SS_BENCH_DIR", "/tmp"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="launch kernels eagerly instead of replaying the per-token HIP graph")
     ap.add_argument("--profile-steps", type=int, default=16)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -115,7 +117,7 @@ def main():
         log("wrote %s (%.2f GB) in %.1f s" % (path, os.path.getsize(path) / 1e9, time.perf_counter() - t))
     max_ctx = prompt_len + warm + steps + args.profile_steps + 2
     t = time.perf_counter()
-    m = api.Model(path, max_context=max_ctx, kv=args.kv)
+    m = api.Model(path, max_context=max_ctx, kv=args.kv, use_graph=not args.no_graph)
     log("loaded in %.1f s" % (time.perf_counter() - t))
     L = api._lib()
     rng = np.random.default_rng(1234)

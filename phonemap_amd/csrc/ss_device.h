@@ -1,0 +1,82 @@
+// ss_device.h - device helpers shared by the gfx950 kernels (internal).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ssk {
+
+constexpr int kWave = 64;
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+
+// Sum over 8 consecutive lanes (all 8 must be active), result in every lane.
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp<0xb1>(v);   // quad_perm [1,0,3,2]
+  v += dpp<0x4e>(v);   // quad_perm [2,3,0,1]
+  v += dpp<0x141>(v);  // row_half_mirror
+  return v;
+}
+
+// Sum over the whole wave, result in every lane.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = sum8(v);
+  v += dpp<0x140>(v);  // row_mirror: 16-lane rows
+  v += __shfl_xor(v, 16, kWave);
+  v += __shfl_xor(v, 32, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<0xb1>(v));
+  v = fmaxf(v, dpp<0x4e>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  v = fmaxf(v, __shfl_xor(v, 16, kWave));
+  v = fmaxf(v, __shfl_xor(v, 32, kWave));
+  return v;
+}
+
+__device__ __forceinline__ float h2f(uint16_t h) {
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+__device__ __forceinline__ uint16_t f2h(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);   // round to nearest even
+}
+
+// "b beats a" for the first-maximum argmax of tensor.c:318-328: larger
+// value, or equal value at a smaller index. NaN never beats anything.
+__device__ __forceinline__ bool beats(float bv, int bi, float av, int ai) {
+  return bv > av || (bv == av && bi < ai);
+}
+
+// Best (value, index) over the wave, in every lane.
+__device__ __forceinline__ void wave_best(float& bv, int& bi) {
+  for (int off = 32; off > 0; off >>= 1) {
+    const float ov = __shfl_xor(bv, off, kWave);
+    const int oi = __shfl_xor(bi, off, kWave);
+    if (beats(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+}
+
+template <int QT>
+struct QTraits;
+template <>
+struct QTraits<2> {            // Q4_0
+  static constexpr int kQB = 16;         // code bytes per block
+  static constexpr int kGgufBytes = 18;  // GGUF block bytes
+};
+template <>
+struct QTraits<8> {            // Q8_0
+  static constexpr int kQB = 32;
+  static constexpr int kGgufBytes = 34;
+};
+
+}  // namespace ssk

@@ -30,6 +30,8 @@ constexpr int32_t kErrBackend = -7;  // SS_ERROR_BACKEND
 constexpr int32_t kErrCancel = -6;   // SS_ERROR_CANCELLED
 
 thread_local char g_err[512] = "";
+// compute units of the device the last context was created on (sizes matvec grids)
+int g_n_cu = 0;
 
 int32_t fail(int32_t code, const char* fmt, ...) {
   va_list ap;
@@ -55,11 +57,7 @@ int gguf_block_bytes(int type) { return type == SS_HIP_Q4_0 ? 18 : type == SS_HI
 bool quant_type_ok(int type) { return type == SS_HIP_Q4_0 || type == SS_HIP_Q8_0; }
 
 ssk::PackedMat view(const void* base, int type, int64_t rows, int cols) {
-  const size_t nblk = (size_t)rows * (cols / 32);
-  ssk::PackedMat m;
-  m.qs = static_cast<const uint8_t*>(base);
-  m.ds = reinterpret_cast<const uint16_t*>(m.qs + align256(nblk * code_bytes(type)));
-  return m;
+  return ssk::packed_view(base, type, rows, cols);
 }
 
 // Algorithmic HBM bytes of one matvec launch: packed weights (18 or 34 bytes
@@ -78,14 +76,14 @@ struct ss_hip_ctx {
   void* staging = nullptr;
   size_t staging_bytes = 0;
   float2* am_part = nullptr;
-  unsigned* am_counter = nullptr;
+
   float* rope_row = nullptr;
   int rope_row_len = 0;
   float* att_o = nullptr;
   float* att_ml = nullptr;
-  unsigned* att_counter = nullptr;
+
   size_t att_o_floats = 0, att_ml_floats = 0;
-  int att_counter_n = 0;
+
   // host-pointer plug (metal_backend.m:190-235 registry)
   std::unordered_map<const void*, void*> registry;
   float* plug_x = nullptr;
@@ -135,7 +133,7 @@ int32_t pack_rows(ss_hip_ctx* c, void* dst, int64_t total_rows, int64_t row_off,
                            (size_t)n * row_bytes, hipMemcpyHostToDevice, c->stream));
     HIP_TRY(ssk::launch_pack(type, static_cast<const uint8_t*>(c->staging),
                              const_cast<uint8_t*>(v.qs), const_cast<uint16_t*>(v.ds),
-                             n * nb, (row_off + r) * nb, c->stream));
+                             n * nb, nb, row_off + r, c->stream));
   }
   HIP_TRY(hipStreamSynchronize(c->stream));
   return 0;
@@ -211,10 +209,9 @@ ss_hip_ctx_t* ss_hip_init(int32_t device) {
   auto* c = new ss_hip_ctx();
   c->device = device;
   c->n_cu = p.multiProcessorCount;
+  g_n_cu = c->n_cu;
   if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
-      hipMalloc(&c->am_part, sizeof(float2) * ssk::kArgmaxMaxBlocks) != hipSuccess ||
-      hipMalloc(&c->am_counter, sizeof(unsigned)) != hipSuccess ||
-      hipMemset(c->am_counter, 0, sizeof(unsigned)) != hipSuccess) {
+      hipMalloc(&c->am_part, sizeof(float2) * ssk::kArgmaxMaxBlocks) != hipSuccess) {
     fail(kErrBackend, "HIP context set-up failed on device %d", device);
     ss_hip_free(c);
     return nullptr;
@@ -227,8 +224,8 @@ void ss_hip_free(ss_hip_ctx_t* c) {
   hipSetDevice(c->device);
   if (c->stream) hipStreamSynchronize(c->stream);
   for (auto& kv : c->registry) hipFree(kv.second);
-  void* bufs[] = {c->staging, c->am_part, c->am_counter, c->rope_row, c->att_o,
-                  c->att_ml,  c->att_counter, c->plug_x, c->plug_y};
+  void* bufs[] = {c->staging, c->am_part, c->rope_row, c->att_o,
+                  c->att_ml, c->plug_x, c->plug_y};
   for (void* b : bufs)
     if (b) hipFree(b);
   if (c->stream) hipStreamDestroy(c->stream);
@@ -275,8 +272,7 @@ int32_t ss_hip_memcpy_d2h(ss_hip_ctx_t* c, void* host, const void* dev, size_t b
 
 size_t ss_hip_packed_bytes(int32_t type, int32_t rows, int32_t cols) {
   if (!quant_type_ok(type) || rows <= 0 || cols <= 0 || cols % 32) return 0;
-  const size_t nblk = (size_t)rows * (cols / 32);
-  return align256(nblk * code_bytes(type)) + nblk * 2;
+  return ssk::packed_bytes(type, rows, cols);
 }
 
 int32_t ss_hip_pack_matrix(ss_hip_ctx_t* c, void* dst, const void* src, int32_t type,
@@ -285,6 +281,8 @@ int32_t ss_hip_pack_matrix(ss_hip_ctx_t* c, void* dst, const void* src, int32_t 
   if (!quant_type_ok(type) || rows <= 0 || cols <= 0 || cols % 32)
     return fail(kErrParams, "pack: unsupported type %d or shape %dx%d", type, rows, cols);
   if (set_device(c)) return kErrBackend;
+  // rows are padded to a multiple of 64 with zero codes and zero scales
+  HIP_TRY(hipMemsetAsync(dst, 0, ssk::packed_bytes(type, rows, cols), c->stream));
   return pack_rows(c, dst, rows, 0, src, type, rows, cols);
 }
 
@@ -306,8 +304,7 @@ static ssk::GemvArgs gemv_args(const void* w, const float* x, float* y, int rows
   a.rows = rows;
   a.cols = cols;
   a.type = type;
-  const int nb = cols / 32;
-  a.chunk_blocks = nb < ssk::kGemvMaxChunkBlocks ? nb : ssk::kGemvMaxChunkBlocks;
+  a.n_cu = g_n_cu;
   return a;
 }
 
@@ -397,13 +394,6 @@ int32_t ss_hip_attention(ss_hip_ctx_t* c, float* out, const float* q, const void
   if (!rc) rc = ensure(c, (void**)&c->att_ml, &c->att_ml_floats,
                        sizeof(float) * (size_t)n_kv_heads * ns * group * 2, false);
   if (rc) return rc;
-  if (c->att_counter_n < n_kv_heads) {
-    if (c->att_counter) hipFree(c->att_counter);
-    c->att_counter = nullptr;
-    HIP_TRY(hipMalloc(&c->att_counter, sizeof(unsigned) * n_kv_heads));
-    HIP_TRY(hipMemset(c->att_counter, 0, sizeof(unsigned) * n_kv_heads));
-    c->att_counter_n = n_kv_heads;
-  }
   ssk::AttnArgs a;
   memset(&a, 0, sizeof(a));
   a.q = q;
@@ -419,7 +409,6 @@ int32_t ss_hip_attention(ss_hip_ctx_t* c, float* out, const float* q, const void
   a.out = out;
   a.part_o = c->att_o;
   a.part_ml = c->att_ml;
-  a.counter = c->att_counter;
   HIP_TRY(ssk::launch_attention(head_dim, group, kv_type, a, pick(c, stream)));
   return 0;
 }
@@ -433,7 +422,7 @@ int32_t ss_hip_swiglu(ss_hip_ctx_t* c, float* out, const float* g, const float* 
 
 int32_t ss_hip_argmax(ss_hip_ctx_t* c, int32_t* out, const float* x, int32_t n, void* stream) {
   if (!c || !out || !x || n <= 0) return fail(kErrParams, "argmax: bad argument");
-  HIP_TRY(ssk::launch_argmax(out, x, n, c->am_part, c->am_counter, pick(c, stream)));
+  HIP_TRY(ssk::launch_argmax(out, x, n, c->am_part, pick(c, stream)));
   return 0;
 }
 
@@ -461,6 +450,10 @@ int32_t ss_hip_matvec_host(ss_hip_ctx_t* c, float* out, const void* mat, const f
     dev = it->second;
   } else {
     if (hipMalloc(&dev, ss_hip_packed_bytes(type, rows, cols)) != hipSuccess) return 0;
+    if (hipMemset(dev, 0, ss_hip_packed_bytes(type, rows, cols)) != hipSuccess) {
+      hipFree(dev);
+      return 0;
+    }
     if (pack_rows(c, dev, rows, 0, mat, type, rows, cols)) {
       hipFree(dev);
       return 0;
@@ -533,9 +526,9 @@ struct ss_hip_model {
   int* tokens = nullptr;   // [max_seq + 1]
   int* argmax = nullptr;
   float2* lm_part = nullptr;
-  unsigned* lm_counter = nullptr;
+  int lm_grid = 0;
   float *att_o = nullptr, *att_ml = nullptr;
-  unsigned* att_counter = nullptr;
+
   int* h_io = nullptr;   // pinned host scratch
   hipGraphExec_t g_full = nullptr, g_nohead = nullptr;
   int host_pos = -1;     // position of the last evaluated token (-1 = none)
@@ -612,7 +605,8 @@ int32_t upload_mat(ss_hip_model* m, void** dst, const ss_hip_tensor_t* parts, in
   if (!quant_type_ok(type)) return fail(kErrParams, "model: %s has type %d; Q4_0 and Q8_0 are supported", what, type);
   if (total != rows_expect_total) return fail(kErrParams, "model: %s has %lld rows, %d expected", what, (long long)total, rows_expect_total);
   if (cols % 32) return fail(kErrParams, "model: %s columns %d not a multiple of 32", what, cols);
-  if (int32_t rc = m_alloc(m, dst, ss_hip_packed_bytes(type, (int)total, cols), false)) return rc;
+  // zero-filled: rows are padded to a multiple of 64 with zero codes and scales
+  if (int32_t rc = m_alloc(m, dst, ss_hip_packed_bytes(type, (int)total, cols), true)) return rc;
   int64_t off = 0;
   for (int i = 0; i < nparts; i++) {
     if (int32_t rc = pack_rows(m->ctx, *dst, total, off, parts[i].data, type, parts[i].rows, cols)) return rc;
@@ -702,7 +696,6 @@ int32_t enqueue_token(ss_hip_model* m, bool with_head) {
     at.out = m->attn;
     at.part_o = m->att_o;
     at.part_ml = m->att_ml;
-    at.counter = m->att_counter;
     HIP_TRY(timed(m, PC_ATTN, 0, [&] { return ssk::launch_attention(m->hd, m->group, m->kv_type, at, s); }));
 
     // 3. hidden += Wo attn                                         (:470-484)
@@ -729,12 +722,13 @@ int32_t enqueue_token(ss_hip_model* m, bool with_head) {
     h.nw = m->out_norm;
     h.eps = m->eps;
     h.part = m->lm_part;
-    h.counter = m->lm_counter;
-    h.out_idx = m->argmax;
-    h.tokens = m->tokens;
-    h.dpos_mut = m->dpos;
     HIP_TRY(timed(m, q_class(m->t_out), matvec_bytes(m->t_out, m->vocab, m->d, 1),
                   [&] { return ssk::launch_gemv(ssk::EPI_LOGITS, h, s); }));
+    // pick the winner, append it at tokens[pos+1], advance pos
+    HIP_TRY(timed(m, PC_OTHER, 0, [&] {
+      return ssk::launch_argmax_merge(m->lm_part, m->lm_grid, m->logits, m->argmax, m->tokens,
+                                      m->dpos, s);
+    }));
   } else {
     HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_advance(m->dpos, s); }));
   }
@@ -892,7 +886,8 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
   if (m->kv_type == 1 && (m_alloc(m, (void**)&m->ks, sizeof(float) * m->L * m->max_seq) ||
                           m_alloc(m, (void**)&m->vs, sizeof(float) * m->L * m->max_seq)))
     return bail();
-  const int lm_grid = ssk::gemv_grid(ssk::EPI_LOGITS, m->vocab);
+  m->lm_grid = ssk::gemv_plan(m->vocab, m->d, c->n_cu, 1).grid;
+  const int lm_grid = m->lm_grid;
   if (m_alloc(m, (void**)&m->hidden, sizeof(float) * m->d) ||
       m_alloc(m, (void**)&m->q, sizeof(float) * m->qdim) ||
       m_alloc(m, (void**)&m->attn, sizeof(float) * m->qdim) ||
@@ -904,10 +899,8 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
       m_alloc(m, (void**)&m->tokens, sizeof(int) * (m->max_seq + 1)) ||
       m_alloc(m, (void**)&m->argmax, sizeof(int) * 4) ||
       m_alloc(m, (void**)&m->lm_part, sizeof(float2) * lm_grid) ||
-      m_alloc(m, (void**)&m->lm_counter, sizeof(unsigned) * 4) ||
       m_alloc(m, (void**)&m->att_o, sizeof(float) * (size_t)m->KVH * m->ns * m->group * m->hd) ||
-      m_alloc(m, (void**)&m->att_ml, sizeof(float) * (size_t)m->KVH * m->ns * m->group * 2) ||
-      m_alloc(m, (void**)&m->att_counter, sizeof(unsigned) * m->KVH))
+      m_alloc(m, (void**)&m->att_ml, sizeof(float) * (size_t)m->KVH * m->ns * m->group * 2))
     return bail();
   // RoPE (cos, sin) table for every position, computed with the host libm
   // exactly as tensor.c:250-254 computes each pair.

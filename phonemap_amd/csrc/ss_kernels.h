@@ -13,7 +13,7 @@ enum Epi : int {
   EPI_ADD = 1,     // y[r] = W x + y[r]          (residual, layer_scheduler.c:484,566)
   EPI_SWIGLU = 2,  // y[r] = u * silu(g)          (layer_scheduler.c:533-549), W = gate, W2 = up
   EPI_QKV = 3,     // rows of [Wq;Wk;Wv]: RoPE on q/k pairs, K/V appended to the cache
-  EPI_LOGITS = 4,  // y[r] = W x, then the first-max argmax over all rows
+  EPI_LOGITS = 4,  // y[r] = W x, plus one first-max argmax candidate per workgroup in part[]
 };
 
 // A packed Q4_0/Q8_0 matrix on the device: code plane then scale plane.
@@ -28,7 +28,9 @@ struct GemvArgs {
   const float* nw;           // RMSNorm weight [cols] or nullptr
   float eps;
   float* y;                  // output [rows]
-  int rows, cols, type, chunk_blocks;
+  int rows, cols, type;
+  int n_cu;                  // compute units (sizes the grid)
+  int chunk_blocks;          // blocks of x staged per pass (set by the launcher)
   // EPI_QKV
   int qdim, kvdim, head_dim, rope_dim, max_seq, kv_type;
   const float* rope_cs;      // [max_seq][rope_dim/2][2]
@@ -37,11 +39,7 @@ struct GemvArgs {
   void* vcache;
   float* kv_f32;             // kv_type 1: fp32 K,V staging [2*kvdim]
   // EPI_LOGITS
-  float2* part;              // per-workgroup (value, index bits)
-  unsigned* counter;
-  int* out_idx;              // argmax result
-  int* tokens;               // if non-null: tokens[pos+1] = argmax and ++*pos (device-side greedy)
-  int* dpos_mut;
+  float2* part;              // one (value, index bits) candidate per workgroup
 };
 
 struct AttnArgs {
@@ -56,17 +54,24 @@ struct AttnArgs {
   float* out;                // [n_heads][hd]
   float* part_o;             // [kvh][ns][G][hd]
   float* part_ml;            // [kvh][ns][G][2]
-  unsigned* counter;         // [kvh]
 };
 
-int gemv_rows_per_wave(int epi);
+struct GemvPlan {
+  int grid, threads, chunk_blocks;
+  size_t lds_bytes;
+};
+GemvPlan gemv_plan(int rows, int cols, int n_cu, int nmat);
+// bytes and plane views of a packed matrix (64-row tiles, see ss_gemv.hip)
+size_t packed_bytes(int type, int64_t rows, int cols);
+PackedMat packed_view(const void* base, int type, int64_t rows, int cols);
 hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t s);
-int gemv_grid(int epi, int rows);
+hipError_t launch_argmax_merge(const float2* part, int n, const float* y, int* out_idx, int* tokens,
+                               int* dpos, hipStream_t s);
 hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, hipStream_t s);
 bool attention_supported(int head_dim, int group);
 
 hipError_t launch_pack(int type, const uint8_t* src, uint8_t* qs, uint16_t* ds, int64_t nblocks,
-                       int64_t blk_offset, hipStream_t s);
+                       int nb, int64_t row_off, hipStream_t s);
 hipError_t launch_embed(int type, PackedMat t, int cols, const int* tokens, const int* dpos,
                         int token, float* out, hipStream_t s);
 hipError_t launch_rmsnorm(float* out, const float* x, const float* w, int n, float eps,
@@ -77,12 +82,13 @@ hipError_t launch_kv_append(void* kc, void* vc, float* ksc, float* vsc, const fl
                             const float* v, int n_kv_heads, int head_dim, int max_seq,
                             const int* dpos, int pos, int kv_type, hipStream_t s);
 hipError_t launch_swiglu(float* out, const float* g, const float* u, int n, hipStream_t s);
-hipError_t launch_argmax(int* out, const float* x, int n, float2* part, unsigned* counter,
-                         hipStream_t s);
+hipError_t launch_argmax(int* out, const float* x, int n, float2* part, hipStream_t s);
 hipError_t launch_set_state(int* dpos, int* tokens, int pos, int token, hipStream_t s);
 hipError_t launch_advance(int* dpos, hipStream_t s);
 
 constexpr int kArgmaxMaxBlocks = 1024;
-constexpr int kGemvMaxChunkBlocks = 448;   // 448 blocks * 144 B of LDS = 63 KiB
+constexpr int kGemvMaxChunkBlocks = 384;   // 384 blocks * 144 B of LDS = 54 KiB of x per pass
+constexpr int kGemvMaxSplit = 16;          // waves per matvec workgroup
+constexpr int kMaxSplits = 64;             // attention splits per KV head
 
 }  // namespace ssk
