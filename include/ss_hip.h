@@ -15,10 +15,14 @@
  * context's own stream. One context is used by one thread at a time.
  *
  * Device weight layout: a GGUF Q4_0/Q8_0 matrix of R rows and C columns
- * (R*C/32 blocks of fp16 d + 16/32 code bytes) is stored on the device as
- * two planes, codes first: code bytes [R][C/32][16 or 32] then, at the next
- * 256-byte boundary, scales [R][C/32] as binary16. ss_hip_pack_matrix makes
- * it; ss_hip_packed_bytes gives its size. Bytes per weight are unchanged.
+ * (R*C/32 blocks of fp16 d + 16/32 code bytes) is stored on the device in
+ * tiles of 16 rows x 4 blocks. Tile (g, t) holds rows 16g..16g+15, blocks
+ * 4t..4t+3; the block chunk of (row r, block b) is entry
+ * (g*T + t)*64 + (b%4)*16 + r%16, T = ceil(C/128). Two planes, codes first
+ * (16 or 32 bytes per entry), then at the next 256-byte boundary the
+ * binary16 scales with the same index. R is padded to a multiple of 16 and
+ * C/32 to a multiple of 4 with zero entries. ss_hip_pack_matrix makes it;
+ * ss_hip_packed_bytes gives its size.
  */
 #ifndef SS_HIP_H
 #define SS_HIP_H

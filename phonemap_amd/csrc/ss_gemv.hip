@@ -1,19 +1,22 @@
 // ss_gemv.hip - block-quantized matrix-vector kernels for gfx950.
 //
-// Device weight layout (made by k_pack from GGUF blocks): rows are taken in
-// groups of 64 (padded with zero rows); for row group g and 32-column block
-// b, the 64 rows' code chunks are contiguous - code[(g*nb + b)*64 + lane]
-// of 16 (Q4_0) or 32 (Q8_0) bytes - and the binary16 scales follow in a
-// second plane with the same index. A wave therefore loads one block of 64
-// different rows as one contiguous 1 KiB (Q4_0) read, one row per lane.
+// Device weight layout (made by k_pack from GGUF blocks): a tile is 16 rows
+// x 4 consecutive 32-column blocks = 64 block chunks, one per lane; chunk
+// (row, block) sits at lane (block % 4) * 16 + row % 16 of tile
+// (row / 16, block / 4), tiles of a row group being consecutive:
+// code[((g * ntk + t) * 64 + lane] of 16 (Q4_0) or 32 (Q8_0) bytes, then the
+// binary16 scales in a second plane with the same index. Rows are padded to a
+// multiple of 16 and blocks to a multiple of 4 with zero codes and scales.
+// A wave loads a tile as one contiguous 1 KiB (Q4_0) read.
 //
-// k_gemv3: workgroup = S waves x one row group. Lane l owns row 64g + l;
-// wave s walks blocks [s*nb/S, (s+1)*nb/S) of it, dequantising in registers
-// with fp32 accumulation, double-buffering batches of blocks. x (times the
-// RMSNorm weight when there is one) is staged once per workgroup in LDS and
-// read with broadcast loads. The S partial sums of each row are added in LDS
-// in wave order, so results do not depend on timing. There is no cross-lane
-// reduction per row and no data handed between workgroups.
+// k_gemv: workgroup = S waves x one 16-row group. Wave s walks a contiguous
+// share of the group's tiles; each lane dequantises its chunk in registers
+// and accumulates in fp32 (double-buffered batches of tiles). x, times the
+// RMSNorm weight when there is one, is staged once per workgroup in LDS and
+// read with broadcast loads (4 distinct blocks per read). Per row, the 4
+// lanes holding it are added with two shuffles and the S waves in LDS in wave
+// order, so results do not depend on timing; no data passes between
+// workgroups. 16-row groups give >= 256 workgroups for every 7B-shape matrix.
 
 #include <math.h>
 
@@ -23,86 +26,166 @@
 namespace ssk {
 namespace {
 
-// floats of LDS per 32-column block of x: 32 values, their sum, 3 pad
-constexpr int kXBlk = 36;
+// x in LDS, per 32-column block: the staged values v_j (x_j times the RMSNorm
+// weight) as three int8 levels, v_j ~= s3 * X_j with
+// X_j = 16384*q1_j + 128*q2_j + q3_j (q1 = v/s1 rounded, q2 and q3 the
+// rounded remainders at 1/128 and 1/16384 of s1 = max|v|/127). The error is
+// at most s3/2 = max|v| * 2.4e-7 per value, the size of fp32 rounding, so
+// dot products become exact integer sums (v_dot4) plus one fp32 rounding per
+// block. Words: [0,8) q1, [8,16) q2, [16,24) q3 (4 codes per word, column
+// order), [24] 8 * sum_j X_j (the Q4_0 offset term), [25] s3 (fp32 bits).
+constexpr int kXW = 28;   // words per block (7 x 16 B)
+
+__device__ __forceinline__ int sdot4(uint32_t a, int b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, b, c, false);
+}
 
 // Q4_0 block (quantize.c:60-72): byte j holds weight j (low nibble) and
 // weight j+16 (high nibble), value = d * (nibble - 8). Returns
-// sum_j (nibble_j - 8) * x_j; the caller multiplies by d. The -8 offset is
-// folded through the block sum of x staged at xb[32]; high nibbles are used
-// in place (x16) and rescaled by 1/16 exactly.
-__device__ __forceinline__ float q4_block(const uint4 q, const float* __restrict__ xb) {
-  const float4* x4 = reinterpret_cast<const float4*>(xb);
+// sum_j (nibble_j - 8) * X_j exactly; the caller multiplies by d * s3. The -8
+// offset is applied through the staged 8 * sum_j X_j. |sum_j nibble_j X_j|
+// <= 32 * 15 * 127 * 16513 < 2^31.
+__device__ __forceinline__ float q4_block(const uint4 q, const int* __restrict__ xb) {
   const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-  float slo = 0.f, shi = 0.f;
+  uint32_t lo[4], hi[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const uint32_t lo = w[k] & 0x0F0F0F0Fu;
-    const uint32_t hi = w[k] & 0xF0F0F0F0u;
-    const float4 xl = x4[k];
-    const float4 xh = x4[4 + k];
-    slo = fmaf((float)(lo & 0xffu), xl.x, slo);
-    slo = fmaf((float)((lo >> 8) & 0xffu), xl.y, slo);
-    slo = fmaf((float)((lo >> 16) & 0xffu), xl.z, slo);
-    slo = fmaf((float)(lo >> 24), xl.w, slo);
-    shi = fmaf((float)(hi & 0xffu), xh.x, shi);
-    shi = fmaf((float)((hi >> 8) & 0xffu), xh.y, shi);
-    shi = fmaf((float)((hi >> 16) & 0xffu), xh.z, shi);
-    shi = fmaf((float)(hi >> 24), xh.w, shi);
+    lo[k] = w[k] & 0x0F0F0F0Fu;
+    hi[k] = (w[k] >> 4) & 0x0F0F0F0Fu;
   }
-  return fmaf(shi, 0.0625f, slo) - 8.0f * xb[32];
-}
-
-// Q8_0 block (quantize.c:139-149): 32 int8 codes, value = d * code.
-__device__ __forceinline__ float q8_block(const uint4 a, const uint4 b, const float* __restrict__ xb) {
-  const float4* x4 = reinterpret_cast<const float4*>(xb);
-  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  float s0 = 0.f, s1 = 0.f;
+  int acc = 0;
 #pragma unroll
-  for (int k = 0; k < 8; k += 2) {
-    const float4 xa = x4[k];
-    const float4 xc = x4[k + 1];
-    s0 = fmaf((float)(int8_t)(w[k] & 0xffu), xa.x, s0);
-    s0 = fmaf((float)(int8_t)((w[k] >> 8) & 0xffu), xa.y, s0);
-    s0 = fmaf((float)(int8_t)((w[k] >> 16) & 0xffu), xa.z, s0);
-    s0 = fmaf((float)(int8_t)(w[k] >> 24), xa.w, s0);
-    s1 = fmaf((float)(int8_t)(w[k + 1] & 0xffu), xc.x, s1);
-    s1 = fmaf((float)(int8_t)((w[k + 1] >> 8) & 0xffu), xc.y, s1);
-    s1 = fmaf((float)(int8_t)((w[k + 1] >> 16) & 0xffu), xc.z, s1);
-    s1 = fmaf((float)(int8_t)(w[k + 1] >> 24), xc.w, s1);
+  for (int l = 0; l < 3; ++l) {
+    if (l) acc <<= 7;
+    const int4 xa = *reinterpret_cast<const int4*>(xb + 8 * l);
+    const int4 xc = *reinterpret_cast<const int4*>(xb + 8 * l + 4);
+    acc = sdot4(lo[0], xa.x, acc);
+    acc = sdot4(lo[1], xa.y, acc);
+    acc = sdot4(lo[2], xa.z, acc);
+    acc = sdot4(lo[3], xa.w, acc);
+    acc = sdot4(hi[0], xc.x, acc);
+    acc = sdot4(hi[1], xc.y, acc);
+    acc = sdot4(hi[2], xc.z, acc);
+    acc = sdot4(hi[3], xc.w, acc);
   }
-  return s0 + s1;
+  return (float)(acc - xb[24]);
 }
 
-__device__ __forceinline__ size_t tile_idx(int g, int nb, int b, int lane) {
-  return ((size_t)g * nb + b) * kWave + lane;
+// Q8_0 block (quantize.c:139-149): 32 int8 codes, value = d * code. Returns
+// sum_j code_j * X_j; levels 1-2 and level 3 are summed apart to stay in
+// int32, and joined in fp32.
+__device__ __forceinline__ float q8_block(const uint4 a, const uint4 b, const int* __restrict__ xb) {
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+  int acc = 0, acc3 = 0;
+#pragma unroll
+  for (int l = 0; l < 3; ++l) {
+    const int4 xa = *reinterpret_cast<const int4*>(xb + 8 * l);
+    const int4 xc = *reinterpret_cast<const int4*>(xb + 8 * l + 4);
+    int s = l == 1 ? acc << 7 : 0;
+    s = sdot4(w[0], xa.x, s);
+    s = sdot4(w[1], xa.y, s);
+    s = sdot4(w[2], xa.z, s);
+    s = sdot4(w[3], xa.w, s);
+    s = sdot4(w[4], xc.x, s);
+    s = sdot4(w[5], xc.y, s);
+    s = sdot4(w[6], xc.z, s);
+    s = sdot4(w[7], xc.w, s);
+    if (l < 2) acc = s; else acc3 = s;
+  }
+  return fmaf((float)acc, 128.0f, (float)acc3);
+}
+
+__device__ __forceinline__ size_t tile_idx(int g, int ntk, int t, int lane) {
+  return ((size_t)g * ntk + t) * kWave + lane;
+}
+
+// lane of a tile that holds block b of row r
+__device__ __forceinline__ int tile_lane(int r, int b) { return (b % kTB) * kRG + r % kRG; }
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+
+__device__ __forceinline__ int q8c(float f) {   // round to nearest even, then clamp to int8
+  return (int)fminf(fmaxf(rintf(f), -127.f), 127.f);
+}
+
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+         ((uint32_t)d << 24);
+}
+
+// Encode one group of 4 staged values (8 lanes per block, all active).
+__device__ __forceinline__ void encode4(int* xb, int sub, float4 v) {
+  float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+  m = fmaxf(m, dpp<0xb1>(m));
+  m = fmaxf(m, dpp<0x4e>(m));
+  m = fmaxf(m, dpp<0x141>(m));
+  const float s3 = m * (1.0f / (127.0f * 16384.0f));
+  const float s1 = s3 * 16384.0f, s2 = s3 * 128.0f;
+  const float i1 = m > 0.f ? 127.0f / m : 0.f;   // 1 / s1
+  const float f[4] = {v.x, v.y, v.z, v.w};
+  int q1[4], q2[4], q3[4], X = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    q1[k] = q8c(f[k] * i1);
+    const float r1 = fmaf((float)-q1[k], s1, f[k]);
+    q2[k] = q8c(r1 * (i1 * 128.0f));
+    const float r2 = fmaf((float)-q2[k], s2, r1);
+    q3[k] = q8c(r2 * (i1 * 16384.0f));
+    X += q1[k] * 16384 + q2[k] * 128 + q3[k];
+  }
+  X += dpp_i<0xb1>(X);
+  X += dpp_i<0x4e>(X);
+  X += dpp_i<0x141>(X);
+  xb[sub] = (int)pack4(q1[0], q1[1], q1[2], q1[3]);
+  xb[8 + sub] = (int)pack4(q2[0], q2[1], q2[2], q2[3]);
+  xb[16 + sub] = (int)pack4(q3[0], q3[1], q3[2], q3[3]);
+  if (sub == 0) {
+    xb[24] = 8 * X;
+    xb[25] = __float_as_int(m == m && m < INFINITY ? s3 : m);   // non-finite x stays non-finite
+  }
 }
 
 // Stage blocks [cb, cb+nblk) of x into LDS, times the RMSNorm weight nw when
-// set (the x*w of cpu_neon.c:114; the 1/rms factor is applied to the row sums),
-// with each block's sum at slot 32. Returns this thread's share of sum(x^2).
-__device__ float stage_x(float* xs, const float* __restrict__ x, const float* __restrict__ nw,
-                         int cb, int nblk) {
+// set (the x*w of cpu_neon.c:114; the 1/rms factor is applied to the row sums);
+// blocks at or past nb (tile padding) are zero. Loads are issued U groups at
+// a time before any is used. Returns this thread's share of sum(x^2).
+__device__ float stage_x(int* xs, const float* __restrict__ x, const float* __restrict__ nw,
+                         int cb, int nblk, int nb) {
+  constexpr int U = 4;
   float ss = 0.f;
-  const int ngroups = nblk * 8;
-  for (int g = threadIdx.x; g < ngroups; g += blockDim.x) {
-    const int blk = g >> 3, sub = g & 7;
-    const int col = (cb + blk) * 32 + sub * 4;
-    float4 v = *reinterpret_cast<const float4*>(x + col);
-    if (nw) {
-      ss = fmaf(v.x, v.x, ss);
-      ss = fmaf(v.y, v.y, ss);
-      ss = fmaf(v.z, v.z, ss);
-      ss = fmaf(v.w, v.w, ss);
-      const float4 w = *reinterpret_cast<const float4*>(nw + col);
-      v.x *= w.x;
-      v.y *= w.y;
-      v.z *= w.z;
-      v.w *= w.w;
+  const int ngroups = nblk * 8;   // a multiple of 8: groups of 8 lanes stay whole
+  for (int base = threadIdx.x; base < ngroups; base += U * blockDim.x) {
+    float4 v[U], w[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = base + u * blockDim.x;
+      v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      w[u] = make_float4(1.f, 1.f, 1.f, 1.f);
+      if (i < ngroups && cb + (i >> 3) < nb) {
+        const int col = (cb + (i >> 3)) * 32 + (i & 7) * 4;
+        v[u] = *reinterpret_cast<const float4*>(x + col);
+        if (nw) w[u] = *reinterpret_cast<const float4*>(nw + col);
+      }
     }
-    *reinterpret_cast<float4*>(xs + blk * kXBlk + sub * 4) = v;
-    const float s = sum8((v.x + v.y) + (v.z + v.w));
-    if (sub == 0) xs[blk * kXBlk + 32] = s;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int i = base + u * blockDim.x;
+      if (i < ngroups) {
+        float4 t = v[u];
+        ss = fmaf(t.x, t.x, ss);
+        ss = fmaf(t.y, t.y, ss);
+        ss = fmaf(t.z, t.z, ss);
+        ss = fmaf(t.w, t.w, ss);
+        t.x *= w[u].x;
+        t.y *= w[u].y;
+        t.z *= w[u].z;
+        t.w *= w[u].w;
+        encode4(xs + (i >> 3) * kXW, i & 7, t);
+      }
+    }
   }
   return ss;
 }
@@ -114,9 +197,10 @@ struct Batch {
   float d[NMAT][NB];
 };
 
+// Tiles [t, min(t+NB, lim)) of row group g, this lane's chunk of each.
 template <int QT, int NB, int NMAT>
-__device__ __forceinline__ void load_batch(Batch<QT, NB, NMAT>& f, const GemvArgs& a, int g, int nb,
-                                           int b, int lim, int lane) {
+__device__ __forceinline__ void load_batch(Batch<QT, NB, NMAT>& f, const GemvArgs& a, int g, int ntk,
+                                           int t, int lim, int lane) {
   constexpr int kQB = QTraits<QT>::kQB;
   constexpr int kNV = kQB / 16;
 #pragma unroll
@@ -124,8 +208,8 @@ __device__ __forceinline__ void load_batch(Batch<QT, NB, NMAT>& f, const GemvArg
     const PackedMat& w = m == 0 ? a.w : a.w2;
 #pragma unroll
     for (int k = 0; k < NB; ++k) {
-      if (b + k < lim) {
-        const size_t i = tile_idx(g, nb, b + k, lane);
+      if (t + k < lim) {
+        const size_t i = tile_idx(g, ntk, t + k, lane);
         const uint4* src = reinterpret_cast<const uint4*>(w.qs + i * kQB);
 #pragma unroll
         for (int v = 0; v < kNV; ++v) f.q[m][k][v] = src[v];
@@ -135,13 +219,15 @@ __device__ __forceinline__ void load_batch(Batch<QT, NB, NMAT>& f, const GemvArg
   }
 }
 
+// xs holds the staged tiles from ct on; kb is this lane's block within a tile.
 template <int QT, int NB, int NMAT>
 __device__ __forceinline__ void fma_batch(float (&acc)[NMAT], const Batch<QT, NB, NMAT>& f,
-                                          const float* xs, int b, int lim, int cb) {
+                                          const int* xs, int t, int lim, int ct, int kb) {
 #pragma unroll
   for (int k = 0; k < NB; ++k) {
-    if (b + k < lim) {
-      const float* xb = xs + (b + k - cb) * kXBlk;
+    if (t + k < lim) {
+      const int* xb = xs + ((t + k - ct) * kTB + kb) * kXW;
+      const float s3 = __int_as_float(xb[25]);
 #pragma unroll
       for (int m = 0; m < NMAT; ++m) {
         float s;
@@ -149,16 +235,17 @@ __device__ __forceinline__ void fma_batch(float (&acc)[NMAT], const Batch<QT, NB
           s = q4_block(f.q[m][k][0], xb);
         else
           s = q8_block(f.q[m][k][0], f.q[m][k][1], xb);
-        acc[m] = fmaf(f.d[m][k], s, acc[m]);
+        acc[m] = fmaf(f.d[m][k] * s3, s, acc[m]);
       }
     }
   }
 }
 
-// Per-lane epilogue of wave 0: v[] holds row `row`'s final value(s).
+// Epilogue in wave 0: every lane holds row `row`'s final value(s) v[]; lanes
+// with `own` set (one per row) write.
 template <int EPI, int NMAT>
-__device__ __forceinline__ void epilogue(const GemvArgs& a, int row, const float (&v)[NMAT]) {
-  const bool valid = row < a.rows;
+__device__ __forceinline__ void epilogue(const GemvArgs& a, int row, bool own, const float (&v)[NMAT]) {
+  const bool valid = own && row < a.rows;
   if constexpr (EPI == EPI_STORE || EPI == EPI_ADD) {
     if (valid) a.y[row] = EPI == EPI_ADD ? v[0] + a.y[row] : v[0];   // layer_scheduler.c:484,566
   } else if constexpr (EPI == EPI_SWIGLU) {
@@ -207,62 +294,74 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int row, const float
 }
 
 template <int QT, int NMAT, int EPI>
-__global__ void __launch_bounds__(1024) k_gemv3(const GemvArgs a) {
-  constexpr int NB = (QT == 2 ? 4 : 2) / NMAT;   // blocks per batch and buffer (4 KiB per wave)
+__global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
+  constexpr int NB = (QT == 2 ? 4 : 2) / NMAT;   // tiles per batch (4 KiB per wave); two in flight
   extern __shared__ float4 smem4[];
-  float* xs = reinterpret_cast<float*>(smem4);
-  float* red = xs + a.chunk_blocks * kXBlk;      // [NMAT][S][64] partial sums, then [S] sum(x^2)
+  int* xs = reinterpret_cast<int*>(smem4);
+  float* red = reinterpret_cast<float*>(xs + a.chunk_tiles * kTB * kXW);   // [NMAT][S][16], then [S]
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int S = blockDim.x >> 6;
+  const int kb = lane / kRG;
   const int g = blockIdx.x;
   const int nb = a.cols >> 5;
-  const int b0 = wave * nb / S, b1 = (wave + 1) * nb / S;
+  const int ntk = (nb + kTB - 1) / kTB;
 
   float acc[NMAT];
 #pragma unroll
   for (int m = 0; m < NMAT; ++m) acc[m] = 0.f;
   float ssq = 0.f;
-  Batch<QT, NB, NMAT> cur, nxt;
+  Batch<QT, NB, NMAT> bA, bB;
 
-  for (int cb = 0; cb < nb; cb += a.chunk_blocks) {
-    const int ce = min(nb, cb + a.chunk_blocks);
-    const int lo = max(b0, cb), hi = min(b1, ce);
-    if (lo < hi) load_batch<QT, NB, NMAT>(cur, a, g, nb, lo, hi, lane);   // in flight during staging
-    if (cb) __syncthreads();   // everyone is done with the previous chunk of x
-    ssq += stage_x(xs, a.x, a.nw, cb, ce - cb);
+  for (int ct = 0; ct < ntk; ct += a.chunk_tiles) {
+    const int n = min(a.chunk_tiles, ntk - ct);
+    const int lo = ct + wave * n / S, hi = ct + (wave + 1) * n / S;
+    // the first two batches are in flight during staging
+    if (lo < hi) load_batch<QT, NB, NMAT>(bA, a, g, ntk, lo, hi, lane);
+    if (lo + NB < hi) load_batch<QT, NB, NMAT>(bB, a, g, ntk, lo + NB, hi, lane);
+    if (ct) __syncthreads();   // everyone is done with the previous chunk of x
+    ssq += stage_x(xs, a.x, a.nw, ct * kTB, n * kTB, nb);
     __syncthreads();
-    for (int b = lo; b < hi; b += NB) {
-      if (b + NB < hi) load_batch<QT, NB, NMAT>(nxt, a, g, nb, b + NB, hi, lane);
-      fma_batch<QT, NB, NMAT>(acc, cur, xs, b, hi, cb);
-      cur = nxt;
+    for (int t = lo; t < hi; t += 2 * NB) {
+      fma_batch<QT, NB, NMAT>(acc, bA, xs, t, hi, ct, kb);
+      if (t + 2 * NB < hi) load_batch<QT, NB, NMAT>(bA, a, g, ntk, t + 2 * NB, hi, lane);
+      if (t + NB < hi) {
+        fma_batch<QT, NB, NMAT>(acc, bB, xs, t + NB, hi, ct, kb);
+        if (t + 3 * NB < hi) load_batch<QT, NB, NMAT>(bB, a, g, ntk, t + 3 * NB, hi, lane);
+      }
     }
   }
 
+  // lanes r, r+16, r+32, r+48 hold row r's four block columns
 #pragma unroll
-  for (int m = 0; m < NMAT; ++m) red[(m * S + wave) * kWave + lane] = acc[m];
+  for (int m = 0; m < NMAT; ++m) {
+    acc[m] += __shfl_xor(acc[m], 16, kWave);
+    acc[m] += __shfl_xor(acc[m], 32, kWave);
+    if (lane < kRG) red[(m * S + wave) * kRG + lane] = acc[m];
+  }
   if (a.nw) {
     const float w = wave_sum(ssq);
-    if (lane == 0) red[NMAT * S * kWave + wave] = w;
+    if (lane == 0) red[NMAT * S * kRG + wave] = w;
   }
   __syncthreads();
   if (wave != 0) return;
+  const int r = lane % kRG;
   float v[NMAT];
 #pragma unroll
   for (int m = 0; m < NMAT; ++m) {
     float s = 0.f;
-    for (int w = 0; w < S; ++w) s += red[(m * S + w) * kWave + lane];
+    for (int w = 0; w < S; ++w) s += red[(m * S + w) * kRG + r];
     v[m] = s;
   }
   if (a.nw) {   // RMSNorm scale of tensor.c:114-131: 1 / sqrt(mean(x^2) + eps)
     float t = 0.f;
-    for (int w = 0; w < S; ++w) t += red[NMAT * S * kWave + w];
+    for (int w = 0; w < S; ++w) t += red[NMAT * S * kRG + w];
     const float scale = 1.0f / sqrtf(t / (float)a.cols + a.eps);
 #pragma unroll
     for (int m = 0; m < NMAT; ++m) v[m] *= scale;
   }
-  epilogue<EPI, NMAT>(a, g * kWave + lane, v);
+  epilogue<EPI, NMAT>(a, g * kRG + r, lane < kRG, v);
 }
 
 // GGUF blocks -> tiled planes. Source block i of a [rows x nb] tensor whose
@@ -275,7 +374,7 @@ __global__ void k_pack(const uint8_t* __restrict__ src, uint8_t* __restrict__ qs
   if (i >= nblocks) return;
   const int64_t row = row_off + i / nb;
   const int b = (int)(i % nb);
-  const size_t o = tile_idx((int)(row >> 6), nb, b, (int)(row & 63));
+  const size_t o = tile_idx((int)(row / kRG), (nb + kTB - 1) / kTB, b / kTB, tile_lane((int)(row % kRG), b));
   const uint8_t* s = src + i * kBytes;
   ds[o] = (uint16_t)(s[0] | (s[1] << 8));
   uint4* dst = reinterpret_cast<uint4*>(qs + o * kQB);
@@ -299,8 +398,9 @@ __global__ void k_embed(PackedMat t, int cols, const int* tokens, const int* dpo
   constexpr int kQB = QTraits<QT>::kQB;
   const int tok = tokens ? tokens[*dpos] : token;
   const int nb = cols >> 5;
+  const int ntk = (nb + kTB - 1) / kTB;
   for (int b = threadIdx.x; b < nb; b += blockDim.x) {
-    const size_t i = tile_idx(tok >> 6, nb, b, tok & 63);
+    const size_t i = tile_idx(tok / kRG, ntk, b / kTB, tile_lane(tok % kRG, b));
     const float d = h2f(t.ds[i]);
     const uint8_t* q = t.qs + i * kQB;
     float* o = out + b * 32;
@@ -353,8 +453,8 @@ template <int QT, int NMAT, int EPI>
 hipError_t launch_t(const GemvArgs& a, hipStream_t s) {
   GemvPlan p = gemv_plan(a.rows, a.cols, a.n_cu, NMAT);
   GemvArgs b = a;
-  b.chunk_blocks = p.chunk_blocks;
-  hipLaunchKernelGGL((k_gemv3<QT, NMAT, EPI>), dim3(p.grid), dim3(p.threads), p.lds_bytes, s, b);
+  b.chunk_tiles = p.chunk_tiles;
+  hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI>), dim3(p.grid), dim3(p.threads), p.lds_bytes, s, b);
   return hipGetLastError();
 }
 
@@ -372,36 +472,41 @@ hipError_t launch_q(int epi, const GemvArgs& a, hipStream_t s) {
 
 }  // namespace
 
-// One workgroup per 64-row group with S waves splitting the columns; S is the
-// power of two (<= 16) that brings the launch closest to 8 waves per CU.
+// One workgroup per 16-row group with S waves splitting its tiles. S is the
+// largest power of two (<= 16) that keeps the launch within 16 waves per CU
+// and gives every wave at least two tiles.
 GemvPlan gemv_plan(int rows, int cols, int n_cu, int nmat) {
   GemvPlan p;
-  const int groups = (rows + 63) / 64;
-  const int nb = cols / 32;
-  const int want = (n_cu > 0 ? n_cu : 256) * 8;
+  const int groups = (rows + kRG - 1) / kRG;
+  const int ntk = (cols / 32 + kTB - 1) / kTB;
+  const int want = (n_cu > 0 ? n_cu : 256) * 16;
   int S = 1;
-  while (S < kGemvMaxSplit && groups * S * 2 <= want && S * 2 <= (nb + 3) / 4) S *= 2;
+  while (S < kGemvMaxSplit && groups * S * 2 <= want && S * 2 <= ntk / 2) S *= 2;
   p.grid = groups;
   p.threads = S * kWave;
-  p.chunk_blocks = nb < kGemvMaxChunkBlocks ? nb : kGemvMaxChunkBlocks;
-  p.lds_bytes = (size_t)p.chunk_blocks * kXBlk * sizeof(float) +
-                (size_t)(nmat * S * kWave + S) * sizeof(float);
+  p.chunk_tiles = ntk < kGemvMaxChunkTiles ? ntk : kGemvMaxChunkTiles;
+  p.lds_bytes = (size_t)p.chunk_tiles * kTB * kXW * sizeof(int) +
+                (size_t)(nmat * S * kRG + S) * sizeof(float);
   return p;
+}
+
+// chunks (one per lane of a tile) of a packed [rows x cols] matrix
+static size_t packed_chunks(int64_t rows, int cols) {
+  return (size_t)((rows + kRG - 1) / kRG) * ((cols / 32 + kTB - 1) / kTB) * kWave;
 }
 
 size_t packed_bytes(int type, int64_t rows, int cols) {
   const int kqb = type == 2 ? 16 : type == 8 ? 32 : 0;
-  const size_t tiles = (size_t)((rows + 63) / 64) * 64 * (cols / 32);
-  const size_t code = (tiles * kqb + 255) & ~(size_t)255;
-  return code + tiles * 2;
+  const size_t n = packed_chunks(rows, cols);
+  return ((n * kqb + 255) & ~(size_t)255) + n * 2;
 }
 
 PackedMat packed_view(const void* base, int type, int64_t rows, int cols) {
   const int kqb = type == 2 ? 16 : 32;
-  const size_t tiles = (size_t)((rows + 63) / 64) * 64 * (cols / 32);
+  const size_t n = packed_chunks(rows, cols);
   PackedMat m;
   m.qs = static_cast<const uint8_t*>(base);
-  m.ds = reinterpret_cast<const uint16_t*>(m.qs + ((tiles * kqb + 255) & ~(size_t)255));
+  m.ds = reinterpret_cast<const uint16_t*>(m.qs + ((n * kqb + 255) & ~(size_t)255));
   return m;
 }
 

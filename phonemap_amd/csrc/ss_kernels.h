@@ -30,7 +30,7 @@ struct GemvArgs {
   float* y;                  // output [rows]
   int rows, cols, type;
   int n_cu;                  // compute units (sizes the grid)
-  int chunk_blocks;          // blocks of x staged per pass (set by the launcher)
+  int chunk_tiles;           // tiles (4 blocks) of x staged per pass (set by the launcher)
   // EPI_QKV
   int qdim, kvdim, head_dim, rope_dim, max_seq, kv_type;
   const float* rope_cs;      // [max_seq][rope_dim/2][2]
@@ -57,11 +57,11 @@ struct AttnArgs {
 };
 
 struct GemvPlan {
-  int grid, threads, chunk_blocks;
+  int grid, threads, chunk_tiles;
   size_t lds_bytes;
 };
 GemvPlan gemv_plan(int rows, int cols, int n_cu, int nmat);
-// bytes and plane views of a packed matrix (64-row tiles, see ss_gemv.hip)
+// bytes and plane views of a packed matrix (16-row x 4-block tiles, see ss_gemv.hip)
 size_t packed_bytes(int type, int64_t rows, int cols);
 PackedMat packed_view(const void* base, int type, int64_t rows, int cols);
 hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t s);
@@ -87,7 +87,9 @@ hipError_t launch_set_state(int* dpos, int* tokens, int pos, int token, hipStrea
 hipError_t launch_advance(int* dpos, hipStream_t s);
 
 constexpr int kArgmaxMaxBlocks = 1024;
-constexpr int kGemvMaxChunkBlocks = 384;   // 384 blocks * 144 B of LDS = 54 KiB of x per pass
+constexpr int kRG = 16;                    // rows per packed row group
+constexpr int kTB = 4;                     // 32-column blocks per tile (kRG * kTB = 64 lanes)
+constexpr int kGemvMaxChunkTiles = 96;     // 384 blocks * 144 B of LDS = 54 KiB of x per pass
 constexpr int kGemvMaxSplit = 16;          // waves per matvec workgroup
 constexpr int kMaxSplits = 64;             // attention splits per KV head
 
