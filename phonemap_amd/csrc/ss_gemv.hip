@@ -102,6 +102,13 @@ __device__ __forceinline__ size_t tile_idx(int g, int ntk, int t, int lane) {
 // lane of a tile that holds block b of row r
 __device__ __forceinline__ int tile_lane(int r, int b) { return (b % kTB) * kRG + r % kRG; }
 
+// binary16 index of the scale of (tile t, lane) of row group g: each lane's
+// scales of a unit of 8 tiles are 16 contiguous bytes
+__device__ __forceinline__ size_t scale_idx(int g, int ntk, int t, int lane) {
+  const int nu = (ntk + kUT - 1) / kUT;
+  return (((size_t)g * nu + t / kUT) * kWave + lane) * kUT + t % kUT;
+}
+
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
   return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
@@ -148,85 +155,109 @@ __device__ __forceinline__ void encode4(int* xb, int sub, float4 v) {
   }
 }
 
-// Stage blocks [cb, cb+nblk) of x into LDS, times the RMSNorm weight nw when
-// set (the x*w of cpu_neon.c:114; the 1/rms factor is applied to the row sums);
-// blocks at or past nb (tile padding) are zero. Loads are issued U groups at
-// a time before any is used. Returns this thread's share of sum(x^2).
-__device__ float stage_x(int* xs, const float* __restrict__ x, const float* __restrict__ nw,
-                         int cb, int nblk, int nb) {
-  constexpr int U = 4;
-  float ss = 0.f;
+// Staging of blocks [cb, cb+nblk) of x into LDS, times the RMSNorm weight nw
+// when set (the x*w of cpu_neon.c:114; the 1/rms factor is applied to the row
+// sums); blocks at or past nb (tile padding) are zero. A pass covers
+// kStageU * blockDim groups of 4 values: xfetch issues its loads, xput
+// encodes and stores them, so weight loads can be issued in between - vector
+// loads complete in issue order, and x must not queue behind the weights.
+constexpr int kStageU = 4;
+
+struct XPass {
+  float4 v[kStageU], w[kStageU];
+};
+
+__device__ __forceinline__ void xfetch(XPass& p, const float* __restrict__ x, const float* __restrict__ nw,
+                                       int cb, int nblk, int nb, int base) {
+  // branch-free: out-of-range groups read a valid address and are zeroed in
+  // xput, so the compiler can count the loads in flight exactly
+  const int ngroups = nblk * 8;
+  const float* wp = nw ? nw : x;
+#pragma unroll
+  for (int u = 0; u < kStageU; ++u) {
+    const int i = min(base + u * (int)blockDim.x, ngroups - 1);
+    const int col = min(cb + (i >> 3), nb - 1) * 32 + (i & 7) * 4;
+    p.v[u] = *reinterpret_cast<const float4*>(x + col);
+    p.w[u] = *reinterpret_cast<const float4*>(wp + col);
+  }
+}
+
+// Returns this thread's share of sum(x^2) over the pass.
+__device__ __forceinline__ float xput(const XPass& p, int* xs, const float* nw, int cb, int nblk, int nb,
+                                      int base) {
   const int ngroups = nblk * 8;   // a multiple of 8: groups of 8 lanes stay whole
-  for (int base = threadIdx.x; base < ngroups; base += U * blockDim.x) {
-    float4 v[U], w[U];
+  float ss = 0.f;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = base + u * blockDim.x;
-      v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-      w[u] = make_float4(1.f, 1.f, 1.f, 1.f);
-      if (i < ngroups && cb + (i >> 3) < nb) {
-        const int col = (cb + (i >> 3)) * 32 + (i & 7) * 4;
-        v[u] = *reinterpret_cast<const float4*>(x + col);
-        if (nw) w[u] = *reinterpret_cast<const float4*>(nw + col);
+  for (int u = 0; u < kStageU; ++u) {
+    const int i = base + u * (int)blockDim.x;
+    if (i < ngroups) {
+      const bool in = cb + (i >> 3) < nb;
+      float4 t = in ? p.v[u] : make_float4(0.f, 0.f, 0.f, 0.f);
+      ss = fmaf(t.x, t.x, ss);
+      ss = fmaf(t.y, t.y, ss);
+      ss = fmaf(t.z, t.z, ss);
+      ss = fmaf(t.w, t.w, ss);
+      if (nw) {
+        t.x *= p.w[u].x;
+        t.y *= p.w[u].y;
+        t.z *= p.w[u].z;
+        t.w *= p.w[u].w;
       }
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int i = base + u * blockDim.x;
-      if (i < ngroups) {
-        float4 t = v[u];
-        ss = fmaf(t.x, t.x, ss);
-        ss = fmaf(t.y, t.y, ss);
-        ss = fmaf(t.z, t.z, ss);
-        ss = fmaf(t.w, t.w, ss);
-        t.x *= w[u].x;
-        t.y *= w[u].y;
-        t.z *= w[u].z;
-        t.w *= w[u].w;
-        encode4(xs + (i >> 3) * kXW, i & 7, t);
-      }
+      encode4(xs + (i >> 3) * kXW, i & 7, t);
     }
   }
   return ss;
 }
 
-template <int QT, int NB, int NMAT>
-struct Batch {
+// One wave's share per round: a unit of UT (2, 4 or 8) consecutive tiles
+// (those < ntk), every chunk of it requested before any is used. A unit lies
+// inside one 8-tile scale group, whose 16 bytes per lane it reads UT/2 words of.
+template <int QT, int NMAT, int UT>
+struct Round {
   static constexpr int kNV = QTraits<QT>::kQB / 16;
-  uint4 q[NMAT][NB][kNV];
-  float d[NMAT][NB];
+  uint4 q[NMAT][UT][kNV];
+  uint32_t sc[NMAT][UT / 2];   // the unit's binary16 scales, tile order
 };
 
-// Tiles [t, min(t+NB, lim)) of row group g, this lane's chunk of each.
-template <int QT, int NB, int NMAT>
-__device__ __forceinline__ void load_batch(Batch<QT, NB, NMAT>& f, const GemvArgs& a, int g, int ntk,
-                                           int t, int lim, int lane) {
+template <int QT, int NMAT, int UT>
+__device__ __forceinline__ void load_round(Round<QT, NMAT, UT>& f, const GemvArgs& a, int g, int ntk,
+                                           int u, int lane) {
   constexpr int kQB = QTraits<QT>::kQB;
   constexpr int kNV = kQB / 16;
+  const int t0 = u * UT;
 #pragma unroll
   for (int m = 0; m < NMAT; ++m) {
     const PackedMat& w = m == 0 ? a.w : a.w2;
+    const uint32_t* sp = reinterpret_cast<const uint32_t*>(w.ds + scale_idx(g, ntk, t0, lane));
+    if constexpr (UT == 8) {
+      const uint4 v = *reinterpret_cast<const uint4*>(sp);
+      f.sc[m][0] = v.x; f.sc[m][1] = v.y; f.sc[m][2] = v.z; f.sc[m][3] = v.w;
+    } else if constexpr (UT == 4) {
+      const uint2 v = *reinterpret_cast<const uint2*>(sp);
+      f.sc[m][0] = v.x; f.sc[m][1] = v.y;
+    } else {
+      f.sc[m][0] = *sp;
+    }
 #pragma unroll
-    for (int k = 0; k < NB; ++k) {
-      if (t + k < lim) {
-        const size_t i = tile_idx(g, ntk, t + k, lane);
-        const uint4* src = reinterpret_cast<const uint4*>(w.qs + i * kQB);
+    for (int k = 0; k < UT; ++k) {
+      // tiles past the row (last unit) reload the last tile and are skipped in fma_round
+      const int t = min(t0 + k, ntk - 1);
+      const uint4* src = reinterpret_cast<const uint4*>(w.qs + tile_idx(g, ntk, t, lane) * kQB);
 #pragma unroll
-        for (int v = 0; v < kNV; ++v) f.q[m][k][v] = src[v];
-        f.d[m][k] = h2f(w.ds[i]);
-      }
+      for (int v = 0; v < kNV; ++v) f.q[m][k][v] = src[v];
     }
   }
 }
 
-// xs holds the staged tiles from ct on; kb is this lane's block within a tile.
-template <int QT, int NB, int NMAT>
-__device__ __forceinline__ void fma_batch(float (&acc)[NMAT], const Batch<QT, NB, NMAT>& f,
-                                          const int* xs, int t, int lim, int ct, int kb) {
+// xs holds the staged tiles from t0 on; kb is this lane's block within a tile.
+template <int QT, int NMAT, int UT>
+__device__ __forceinline__ void fma_round(float (&acc)[NMAT], const Round<QT, NMAT, UT>& f, const int* xs,
+                                          int u, int ntk, int t0, int kb) {
 #pragma unroll
-  for (int k = 0; k < NB; ++k) {
-    if (t + k < lim) {
-      const int* xb = xs + ((t + k - ct) * kTB + kb) * kXW;
+  for (int k = 0; k < UT; ++k) {
+    const int t = u * UT + k;
+    if (t < ntk) {
+      const int* xb = xs + ((t - t0) * kTB + kb) * kXW;
       const float s3 = __int_as_float(xb[25]);
 #pragma unroll
       for (int m = 0; m < NMAT; ++m) {
@@ -235,7 +266,9 @@ __device__ __forceinline__ void fma_batch(float (&acc)[NMAT], const Batch<QT, NB
           s = q4_block(f.q[m][k][0], xb);
         else
           s = q8_block(f.q[m][k][0], f.q[m][k][1], xb);
-        acc[m] = fmaf(f.d[m][k] * s3, s, acc[m]);
+        const uint32_t sw = f.sc[m][k / 2];
+        const float d = h2f((uint16_t)(k & 1 ? sw >> 16 : sw & 0xffffu));
+        acc[m] = fmaf(d * s3, s, acc[m]);
       }
     }
   }
@@ -293,9 +326,13 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int row, bool own, c
   }
 }
 
-template <int QT, int NMAT, int EPI>
-__global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
-  constexpr int NB = (QT == 2 ? 4 : 2) / NMAT;   // tiles per batch (4 KiB per wave); two in flight
+// Q8_0 and two-matrix rounds hold 64 VGPRs of codes: at most 8 waves, so
+// 256 VGPRs are available to them.
+template <int QT, int NMAT>
+constexpr int gemv_max_waves() { return QT == 8 || NMAT == 2 ? 8 : 16; }
+
+template <int QT, int NMAT, int EPI, int UT>
+__global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(const GemvArgs a) {
   extern __shared__ float4 smem4[];
   int* xs = reinterpret_cast<int*>(smem4);
   float* red = reinterpret_cast<float*>(xs + a.chunk_tiles * kTB * kXW);   // [NMAT][S][16], then [S]
@@ -307,29 +344,36 @@ __global__ void __launch_bounds__(1024) k_gemv(const GemvArgs a) {
   const int g = blockIdx.x;
   const int nb = a.cols >> 5;
   const int ntk = (nb + kTB - 1) / kTB;
+  const int nu = (ntk + UT - 1) / UT;
+  const int chunk_units = a.chunk_tiles / UT;
 
   float acc[NMAT];
 #pragma unroll
   for (int m = 0; m < NMAT; ++m) acc[m] = 0.f;
   float ssq = 0.f;
-  Batch<QT, NB, NMAT> bA, bB;
+  Round<QT, NMAT, UT> rd;
 
-  for (int ct = 0; ct < ntk; ct += a.chunk_tiles) {
-    const int n = min(a.chunk_tiles, ntk - ct);
-    const int lo = ct + wave * n / S, hi = ct + (wave + 1) * n / S;
-    // the first two batches are in flight during staging
-    if (lo < hi) load_batch<QT, NB, NMAT>(bA, a, g, ntk, lo, hi, lane);
-    if (lo + NB < hi) load_batch<QT, NB, NMAT>(bB, a, g, ntk, lo + NB, hi, lane);
-    if (ct) __syncthreads();   // everyone is done with the previous chunk of x
-    ssq += stage_x(xs, a.x, a.nw, ct * kTB, n * kTB, nb);
+  // units of a chunk go to waves round robin; a wave's first unit is in
+  // flight while the chunk of x is staged
+  for (int cu = 0; cu < nu; cu += chunk_units) {
+    const int ce = min(nu, cu + chunk_units);
+    const int t0 = cu * UT, t1 = min(ntk, ce * UT);
+    const int nblk = (t1 - t0) * kTB;
+    XPass xp;
+    xfetch(xp, a.x, a.nw, t0 * kTB, nblk, nb, threadIdx.x);
+    int u = cu + wave;
+    load_round<QT, NMAT, UT>(rd, a, g, ntk, min(u, ce - 1), lane);
+    if (cu) __syncthreads();   // everyone is done with the previous chunk of x
+    ssq += xput(xp, xs, a.nw, t0 * kTB, nblk, nb, threadIdx.x);
+    for (int base = (int)(threadIdx.x + kStageU * blockDim.x); base < nblk * 8; base += kStageU * (int)blockDim.x) {
+      xfetch(xp, a.x, a.nw, t0 * kTB, nblk, nb, base);
+      ssq += xput(xp, xs, a.nw, t0 * kTB, nblk, nb, base);
+    }
     __syncthreads();
-    for (int t = lo; t < hi; t += 2 * NB) {
-      fma_batch<QT, NB, NMAT>(acc, bA, xs, t, hi, ct, kb);
-      if (t + 2 * NB < hi) load_batch<QT, NB, NMAT>(bA, a, g, ntk, t + 2 * NB, hi, lane);
-      if (t + NB < hi) {
-        fma_batch<QT, NB, NMAT>(acc, bB, xs, t + NB, hi, ct, kb);
-        if (t + 3 * NB < hi) load_batch<QT, NB, NMAT>(bB, a, g, ntk, t + 3 * NB, hi, lane);
-      }
+    if (u < ce) fma_round<QT, NMAT, UT>(acc, rd, xs, u, ntk, t0, kb);
+    for (u += S; u < ce; u += S) {   // rows wider than S units
+      load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
+      fma_round<QT, NMAT, UT>(acc, rd, xs, u, ntk, t0, kb);
     }
   }
 
@@ -374,9 +418,10 @@ __global__ void k_pack(const uint8_t* __restrict__ src, uint8_t* __restrict__ qs
   if (i >= nblocks) return;
   const int64_t row = row_off + i / nb;
   const int b = (int)(i % nb);
-  const size_t o = tile_idx((int)(row / kRG), (nb + kTB - 1) / kTB, b / kTB, tile_lane((int)(row % kRG), b));
+  const int ntk = (nb + kTB - 1) / kTB, g = (int)(row / kRG), l = tile_lane((int)(row % kRG), b);
+  const size_t o = tile_idx(g, ntk, b / kTB, l);
   const uint8_t* s = src + i * kBytes;
-  ds[o] = (uint16_t)(s[0] | (s[1] << 8));
+  ds[scale_idx(g, ntk, b / kTB, l)] = (uint16_t)(s[0] | (s[1] << 8));
   uint4* dst = reinterpret_cast<uint4*>(qs + o * kQB);
 #pragma unroll
   for (int v = 0; v < kQB / 16; ++v) {
@@ -400,8 +445,9 @@ __global__ void k_embed(PackedMat t, int cols, const int* tokens, const int* dpo
   const int nb = cols >> 5;
   const int ntk = (nb + kTB - 1) / kTB;
   for (int b = threadIdx.x; b < nb; b += blockDim.x) {
-    const size_t i = tile_idx(tok / kRG, ntk, b / kTB, tile_lane(tok % kRG, b));
-    const float d = h2f(t.ds[i]);
+    const int l = tile_lane(tok % kRG, b);
+    const size_t i = tile_idx(tok / kRG, ntk, b / kTB, l);
+    const float d = h2f(t.ds[scale_idx(tok / kRG, ntk, b / kTB, l)]);
     const uint8_t* q = t.qs + i * kQB;
     float* o = out + b * 32;
     if constexpr (QT == 2) {
@@ -451,10 +497,15 @@ __global__ void k_argmax_merge(const float2* part, int n, const float* y, int* o
 
 template <int QT, int NMAT, int EPI>
 hipError_t launch_t(const GemvArgs& a, hipStream_t s) {
-  GemvPlan p = gemv_plan(a.rows, a.cols, a.n_cu, NMAT);
+  GemvPlan p = gemv_plan(a.rows, a.cols, QT, NMAT);
   GemvArgs b = a;
   b.chunk_tiles = p.chunk_tiles;
-  hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI>), dim3(p.grid), dim3(p.threads), p.lds_bytes, s, b);
+  if (p.unit == 2)
+    hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, 2>), dim3(p.grid), dim3(p.threads), p.lds_bytes, s, b);
+  else if (p.unit == 4)
+    hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, 4>), dim3(p.grid), dim3(p.threads), p.lds_bytes, s, b);
+  else
+    hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, 8>), dim3(p.grid), dim3(p.threads), p.lds_bytes, s, b);
   return hipGetLastError();
 }
 
@@ -472,41 +523,58 @@ hipError_t launch_q(int epi, const GemvArgs& a, hipStream_t s) {
 
 }  // namespace
 
-// One workgroup per 16-row group with S waves splitting its tiles. S is the
-// largest power of two (<= 16) that keeps the launch within 16 waves per CU
-// and gives every wave at least two tiles.
-GemvPlan gemv_plan(int rows, int cols, int n_cu, int nmat) {
+// One workgroup per 16-row group; one wave per unit of UT tiles of the row,
+// up to 16 (Q4_0, one matrix) or 8 waves; rows wider than that take several
+// rounds per wave. UT is the largest of 8, 4, 2 that still gives the launch
+// kGemvWantWaves waves (smaller units shorten the work left after the last
+// load lands); x is staged in chunks of up to kGemvMaxChunkTiles tiles.
+GemvPlan gemv_plan(int rows, int cols, int type, int nmat) {
   GemvPlan p;
   const int groups = (rows + kRG - 1) / kRG;
   const int ntk = (cols / 32 + kTB - 1) / kTB;
-  const int want = (n_cu > 0 ? n_cu : 256) * 16;
-  int S = 1;
-  while (S < kGemvMaxSplit && groups * S * 2 <= want && S * 2 <= ntk / 2) S *= 2;
+  const int smax = type == 8 || nmat == 2 ? gemv_max_waves<8, 1>() : gemv_max_waves<2, 1>();
+  int ut = 8;
+  while (ut > 2) {
+    const int nu = (ntk + ut - 1) / ut;
+    const long waves = (long)groups * (nu < smax ? nu : smax);
+    const int nu2 = (ntk + ut / 2 - 1) / (ut / 2);
+    if (waves >= kGemvWantWaves || nu2 > smax) break;
+    ut /= 2;
+  }
+  const int nu = (ntk + ut - 1) / ut;
+  const int S = nu < smax ? nu : smax;
+  p.unit = ut;
   p.grid = groups;
   p.threads = S * kWave;
-  p.chunk_tiles = ntk < kGemvMaxChunkTiles ? ntk : kGemvMaxChunkTiles;
+  const int ct = nu * ut;
+  p.chunk_tiles = ct < kGemvMaxChunkTiles ? ct : kGemvMaxChunkTiles;
   p.lds_bytes = (size_t)p.chunk_tiles * kTB * kXW * sizeof(int) +
                 (size_t)(nmat * S * kRG + S) * sizeof(float);
   return p;
 }
 
-// chunks (one per lane of a tile) of a packed [rows x cols] matrix
-static size_t packed_chunks(int64_t rows, int cols) {
-  return (size_t)((rows + kRG - 1) / kRG) * ((cols / 32 + kTB - 1) / kTB) * kWave;
+// code and scale bytes of a packed [rows x cols] matrix
+static void packed_sizes(int type, int64_t rows, int cols, size_t* code, size_t* scales) {
+  const size_t groups = (size_t)((rows + kRG - 1) / kRG);
+  const int ntk = (cols / 32 + kTB - 1) / kTB;
+  const int nu = (ntk + kUT - 1) / kUT;
+  const int kqb = type == 2 ? 16 : type == 8 ? 32 : 0;
+  *code = ((groups * ntk * kWave * kqb) + 255) & ~(size_t)255;
+  *scales = groups * nu * kWave * kUT * 2;
 }
 
 size_t packed_bytes(int type, int64_t rows, int cols) {
-  const int kqb = type == 2 ? 16 : type == 8 ? 32 : 0;
-  const size_t n = packed_chunks(rows, cols);
-  return ((n * kqb + 255) & ~(size_t)255) + n * 2;
+  size_t c, sc;
+  packed_sizes(type, rows, cols, &c, &sc);
+  return c + sc;
 }
 
 PackedMat packed_view(const void* base, int type, int64_t rows, int cols) {
-  const int kqb = type == 2 ? 16 : 32;
-  const size_t n = packed_chunks(rows, cols);
+  size_t c, sc;
+  packed_sizes(type, rows, cols, &c, &sc);
   PackedMat m;
   m.qs = static_cast<const uint8_t*>(base);
-  m.ds = reinterpret_cast<const uint16_t*>(m.qs + ((n * kqb + 255) & ~(size_t)255));
+  m.ds = reinterpret_cast<const uint16_t*>(m.qs + c);
   return m;
 }
 

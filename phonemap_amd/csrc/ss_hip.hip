@@ -886,7 +886,7 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
   if (m->kv_type == 1 && (m_alloc(m, (void**)&m->ks, sizeof(float) * m->L * m->max_seq) ||
                           m_alloc(m, (void**)&m->vs, sizeof(float) * m->L * m->max_seq)))
     return bail();
-  m->lm_grid = ssk::gemv_plan(m->vocab, m->d, c->n_cu, 1).grid;
+  m->lm_grid = ssk::gemv_plan(m->vocab, m->d, m->t_out, 1).grid;
   const int lm_grid = m->lm_grid;
   if (m_alloc(m, (void**)&m->hidden, sizeof(float) * m->d) ||
       m_alloc(m, (void**)&m->q, sizeof(float) * m->qdim) ||

@@ -57,10 +57,10 @@ struct AttnArgs {
 };
 
 struct GemvPlan {
-  int grid, threads, chunk_tiles;
+  int grid, threads, chunk_tiles, unit;
   size_t lds_bytes;
 };
-GemvPlan gemv_plan(int rows, int cols, int n_cu, int nmat);
+GemvPlan gemv_plan(int rows, int cols, int type, int nmat);
 // bytes and plane views of a packed matrix (16-row x 4-block tiles, see ss_gemv.hip)
 size_t packed_bytes(int type, int64_t rows, int cols);
 PackedMat packed_view(const void* base, int type, int64_t rows, int cols);
@@ -89,7 +89,9 @@ hipError_t launch_advance(int* dpos, hipStream_t s);
 constexpr int kArgmaxMaxBlocks = 1024;
 constexpr int kRG = 16;                    // rows per packed row group
 constexpr int kTB = 4;                     // 32-column blocks per tile (kRG * kTB = 64 lanes)
-constexpr int kGemvMaxChunkTiles = 96;     // 384 blocks * 144 B of LDS = 54 KiB of x per pass
+constexpr int kUT = 8;                     // tiles per scale group (16 B of scales per lane)
+constexpr int kGemvWantWaves = 4096;       // waves per matvec launch the unit size aims for
+constexpr int kGemvMaxChunkTiles = 96;     // a multiple of kUT: 384 blocks * 112 B = 42 KiB of x per pass
 constexpr int kGemvMaxSplit = 16;          // waves per matvec workgroup
 constexpr int kMaxSplits = 64;             // attention splits per KV head
 
