@@ -58,7 +58,7 @@ def token_bytes(spec, ctx):
     return L * layer_w + head + kv_read + kv_write + norms + embd_row
 
 
-def cpu_baseline(path, spec, prompt_len, budget_s=20.0, max_steps=8):
+def cpu_baseline(path, spec, prompt_len, budget_s=15.0, max_steps=160):
     """The oracle (reference CPU path restated in C) on the same file: KV for
     positions 0..prompt_len-1 pre-filled with fp16 values, then decode steps
     at positions prompt_len.. until the time budget is spent."""

@@ -21,6 +21,12 @@
  *    fp32 KV structure of layer_scheduler.c.orig:289-342.
  *  - Only the llama block is restated (no fused qkv, biases, Gemma or NeoX
  *    branches); orc_model_open rejects files that need them.
+ *
+ * Parity unpinned: the summation order of Apple vDSP_dotpr / cblas_saxpy
+ * (system frameworks, no version pin; orc_dot's order is checked against the
+ * reference's own portable ss_neon_dot instead), and end-to-end logits, for
+ * which the reference holds no fixture (the model functions are pinned only
+ * through their pinned parts).
  */
 #define _GNU_SOURCE
 #include "ss_oracle.h"
