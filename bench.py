@@ -85,6 +85,22 @@ def cpu_baseline(path, spec, prompt_len, budget_s=15.0, max_steps=160):
                       % (n, prompt_len + 1, threads, dt)}
 
 
+def copy_calibration(mib):
+    """20 device-to-device copies of mib MiB (torch is only the allocator here)."""
+    import torch
+    n = mib << 20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda")
+    b = torch.empty(n, dtype=torch.uint8, device="cuda")
+    a.fill_(1)
+    torch.cuda.synchronize()
+    t = time.perf_counter()
+    for _ in range(20):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t) / 20
+    log("copy %d MiB: %.1f us, %.0f GB/s read+write" % (mib, dt * 1e6, 2 * n / dt / 1e9))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -97,7 +113,15 @@ def main():
     ap.add_argument("--no-graph", action="store_true",
                     help="launch kernels eagerly instead of replaying the per-token HIP graph")
     ap.add_argument("--profile-steps", type=int, default=16)
+    ap.add_argument("--prompt-len", type=int, default=None,
+                    help="override the prompt length (counter runs use a short prompt)")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run 20 device-to-device copies of MIB MiB (the known-size kernel that "
+                         "scales the FETCH_SIZE/WRITE_SIZE counters) and exit")
     args = ap.parse_args()
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (--gpus %d requested)"
               % args.gpus, file=sys.stderr)
@@ -108,7 +132,7 @@ def main():
     spec = cfg["spec"]
     steps = args.steps if args.steps is not None else cfg["steps"]
     warm = args.warmup
-    prompt_len = cfg["prompt"]
+    prompt_len = args.prompt_len if args.prompt_len is not None else cfg["prompt"]
     path = os.path.join(args.model_dir, "ss_bench_%s_s%d.gguf" % (args.config, spec["seed"]))
     if not os.path.exists(path):
         t = time.perf_counter()
@@ -140,6 +164,8 @@ def main():
     roof = None
     try:
         roof = profile_classes(m, args.profile_steps)
+        if args.config == "llama2-7b":   # the counter runs were made on this workload
+            roof["traffic"] = measured_traffic()
     except Exception as e:   # profiling is optional for the headline number
         log("profiling failed: %s" % e)
 
@@ -167,6 +193,22 @@ def main():
         except Exception as e:
             log("cpu baseline failed: %s" % e)
     print(json.dumps(out), flush=True)
+
+
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "traffic_llama2-7b_q4_0_matvec.md")
+
+
+def measured_traffic():
+    """HBM bytes per Q4_0 matvec launch from the committed FETCH_SIZE/WRITE_SIZE
+    counter runs (scaled by a copy kernel of known size), or None."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def profile_classes(m, n_steps):
