@@ -4,18 +4,19 @@
 // x 4 consecutive 32-column blocks = 64 block chunks, one per lane; chunk
 // (row, block) sits at lane (block % 4) * 16 + row % 16 of tile
 // (row / 16, block / 4), tiles of a row group being consecutive:
-// code[((g * ntk + t) * 64 + lane] of 16 (Q4_0) or 32 (Q8_0) bytes, then the
-// binary16 scales in a second plane with the same index. Rows are padded to a
-// multiple of 16 and blocks to a multiple of 4 with zero codes and scales.
-// A wave loads a tile as one contiguous 1 KiB (Q4_0) read.
+// code[(g * ntk + t) * 64 + lane] of 16 (Q4_0) or 32 (Q8_0) bytes. The
+// binary16 scales follow in a second plane, each lane's scales of 8
+// consecutive tiles in 16 contiguous bytes. Rows are padded to a multiple of
+// 16 and blocks to a multiple of 4 with zero codes and scales. A wave loads a
+// tile as one contiguous 1 KiB (Q4_0) read.
 //
-// k_gemv: workgroup = S waves x one 16-row group. Wave s walks a contiguous
-// share of the group's tiles; each lane dequantises its chunk in registers
-// and accumulates in fp32 (double-buffered batches of tiles). x, times the
-// RMSNorm weight when there is one, is staged once per workgroup in LDS and
-// read with broadcast loads (4 distinct blocks per read). Per row, the 4
-// lanes holding it are added with two shuffles and the S waves in LDS in wave
-// order, so results do not depend on timing; no data passes between
+// k_gemv: workgroup = one 16-row group; wave s takes units (UT consecutive
+// tiles) s, s+S, ... of it. A wave requests its x slice, then every chunk and
+// scale of its unit, before using any; it encodes its own slice of x into its
+// own LDS region (no workgroup barrier before the dot products) and
+// accumulates exact integer block dot products scaled in fp32. Per row, the
+// 4 lanes holding it are added with two shuffles and the S waves in LDS in
+// wave order, so results do not depend on timing; no data passes between
 // workgroups. 16-row groups give >= 256 workgroups for every 7B-shape matrix.
 
 #include <math.h>
@@ -155,56 +156,63 @@ __device__ __forceinline__ void encode4(int* xb, int sub, float4 v) {
   }
 }
 
-// Staging of blocks [cb, cb+nblk) of x into LDS, times the RMSNorm weight nw
-// when set (the x*w of cpu_neon.c:114; the 1/rms factor is applied to the row
-// sums); blocks at or past nb (tile padding) are zero. A pass covers
-// kStageU * blockDim groups of 4 values: xfetch issues its loads, xput
-// encodes and stores them, so weight loads can be issued in between - vector
-// loads complete in issue order, and x must not queue behind the weights.
-constexpr int kStageU = 4;
-
-struct XPass {
-  float4 v[kStageU], w[kStageU];
+// A wave stages only the x slice of its own unit (UT*4 blocks of 32 values),
+// times the RMSNorm weight nw when set (the x*w of cpu_neon.c:114; the 1/rms
+// factor is applied to the row sums), into its own LDS region: the waves of a
+// workgroup cover disjoint columns, so no barrier precedes the dot products.
+// Blocks at or past nb (tile padding) are zero. Lane l handles groups of 4
+// values j*64 + l (eight lanes per block). xfetch issues the loads and xput
+// encodes them, so the weight loads can be issued in between: vector loads
+// complete in issue order, and x must not queue behind the weights.
+template <int UT>
+struct XSlice {
+  float4 v[UT / 2], w[UT / 2];
 };
 
-__device__ __forceinline__ void xfetch(XPass& p, const float* __restrict__ x, const float* __restrict__ nw,
-                                       int cb, int nblk, int nb, int base) {
-  // branch-free: out-of-range groups read a valid address and are zeroed in
-  // xput, so the compiler can count the loads in flight exactly
-  const int ngroups = nblk * 8;
-  const float* wp = nw ? nw : x;
+template <int UT>
+__device__ __forceinline__ void xfetch(XSlice<UT>& p, const float* __restrict__ x, const float* __restrict__ nw,
+                                       int u, int nb, int lane) {
+  const float* wp = nw ? nw : x;   // branch-free: the loads are counted exactly
 #pragma unroll
-  for (int u = 0; u < kStageU; ++u) {
-    const int i = min(base + u * (int)blockDim.x, ngroups - 1);
-    const int col = min(cb + (i >> 3), nb - 1) * 32 + (i & 7) * 4;
-    p.v[u] = *reinterpret_cast<const float4*>(x + col);
-    p.w[u] = *reinterpret_cast<const float4*>(wp + col);
+  for (int j = 0; j < UT / 2; ++j) {
+    const int gi = j * kWave + lane;
+    const int col = min(u * UT * kTB + (gi >> 3), nb - 1) * 32 + (gi & 7) * 4;
+    p.v[j] = *reinterpret_cast<const float4*>(x + col);
+    p.w[j] = *reinterpret_cast<const float4*>(wp + col);
   }
 }
 
-// Returns this thread's share of sum(x^2) over the pass.
-__device__ __forceinline__ float xput(const XPass& p, int* xs, const float* nw, int cb, int nblk, int nb,
-                                      int base) {
-  const int ngroups = nblk * 8;   // a multiple of 8: groups of 8 lanes stay whole
+// Ties the x registers to this point of the program, so the compiler cannot
+// sink their loads below the weight loads (xput only uses them under a mask).
+__device__ __forceinline__ void pin(float4& v) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+}
+
+// Returns this lane's share of sum(x^2) over the slice.
+template <int UT>
+__device__ __forceinline__ float xput(XSlice<UT>& p, int* xw, const float* nw, int u, int nb, int lane) {
   float ss = 0.f;
 #pragma unroll
-  for (int u = 0; u < kStageU; ++u) {
-    const int i = base + u * (int)blockDim.x;
-    if (i < ngroups) {
-      const bool in = cb + (i >> 3) < nb;
-      float4 t = in ? p.v[u] : make_float4(0.f, 0.f, 0.f, 0.f);
-      ss = fmaf(t.x, t.x, ss);
-      ss = fmaf(t.y, t.y, ss);
-      ss = fmaf(t.z, t.z, ss);
-      ss = fmaf(t.w, t.w, ss);
-      if (nw) {
-        t.x *= p.w[u].x;
-        t.y *= p.w[u].y;
-        t.z *= p.w[u].z;
-        t.w *= p.w[u].w;
-      }
-      encode4(xs + (i >> 3) * kXW, i & 7, t);
+  for (int j = 0; j < UT / 2; ++j) {
+    pin(p.v[j]);
+    pin(p.w[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < UT / 2; ++j) {
+    const int gi = j * kWave + lane;
+    const bool in = u * UT * kTB + (gi >> 3) < nb;
+    float4 t = in ? p.v[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+    ss = fmaf(t.x, t.x, ss);
+    ss = fmaf(t.y, t.y, ss);
+    ss = fmaf(t.z, t.z, ss);
+    ss = fmaf(t.w, t.w, ss);
+    if (nw) {
+      t.x *= p.w[j].x;
+      t.y *= p.w[j].y;
+      t.z *= p.w[j].z;
+      t.w *= p.w[j].w;
     }
+    encode4(xw + (gi >> 3) * kXW, gi & 7, t);
   }
   return ss;
 }
@@ -249,15 +257,16 @@ __device__ __forceinline__ void load_round(Round<QT, NMAT, UT>& f, const GemvArg
   }
 }
 
-// xs holds the staged tiles from t0 on; kb is this lane's block within a tile.
+// xs holds the unit's staged x; kb is this lane's block within a tile. Tiles
+// past the row (last unit) meet an all-zero x slice (s3 = 0) and add exactly
+// 0, so every tile is processed and the loads have no conditional use.
 template <int QT, int NMAT, int UT>
 __device__ __forceinline__ void fma_round(float (&acc)[NMAT], const Round<QT, NMAT, UT>& f, const int* xs,
-                                          int u, int ntk, int t0, int kb) {
+                                          int kb) {
 #pragma unroll
   for (int k = 0; k < UT; ++k) {
-    const int t = u * UT + k;
-    if (t < ntk) {
-      const int* xb = xs + ((t - t0) * kTB + kb) * kXW;
+    {
+      const int* xb = xs + (k * kTB + kb) * kXW;
       const float s3 = __int_as_float(xb[25]);
 #pragma unroll
       for (int m = 0; m < NMAT; ++m) {
@@ -335,7 +344,6 @@ template <int QT, int NMAT, int EPI, int UT>
 __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(const GemvArgs a) {
   extern __shared__ float4 smem4[];
   int* xs = reinterpret_cast<int*>(smem4);
-  float* red = reinterpret_cast<float*>(xs + a.chunk_tiles * kTB * kXW);   // [NMAT][S][16], then [S]
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -345,7 +353,8 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
   const int nb = a.cols >> 5;
   const int ntk = (nb + kTB - 1) / kTB;
   const int nu = (ntk + UT - 1) / UT;
-  const int chunk_units = a.chunk_tiles / UT;
+  int* xw = xs + wave * (UT * kTB * kXW);                          // this wave's x slice
+  float* red = reinterpret_cast<float*>(xs + S * UT * kTB * kXW);   // [NMAT][S][16], then [S]
 
   float acc[NMAT];
 #pragma unroll
@@ -353,28 +362,17 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
   float ssq = 0.f;
   Round<QT, NMAT, UT> rd;
 
-  // units of a chunk go to waves round robin; a wave's first unit is in
-  // flight while the chunk of x is staged
-  for (int cu = 0; cu < nu; cu += chunk_units) {
-    const int ce = min(nu, cu + chunk_units);
-    const int t0 = cu * UT, t1 = min(ntk, ce * UT);
-    const int nblk = (t1 - t0) * kTB;
-    XPass xp;
-    xfetch(xp, a.x, a.nw, t0 * kTB, nblk, nb, threadIdx.x);
-    int u = cu + wave;
-    load_round<QT, NMAT, UT>(rd, a, g, ntk, min(u, ce - 1), lane);
-    if (cu) __syncthreads();   // everyone is done with the previous chunk of x
-    ssq += xput(xp, xs, a.nw, t0 * kTB, nblk, nb, threadIdx.x);
-    for (int base = (int)(threadIdx.x + kStageU * blockDim.x); base < nblk * 8; base += kStageU * (int)blockDim.x) {
-      xfetch(xp, a.x, a.nw, t0 * kTB, nblk, nb, base);
-      ssq += xput(xp, xs, a.nw, t0 * kTB, nblk, nb, base);
-    }
-    __syncthreads();
-    if (u < ce) fma_round<QT, NMAT, UT>(acc, rd, xs, u, ntk, t0, kb);
-    for (u += S; u < ce; u += S) {   // rows wider than S units
-      load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
-      fma_round<QT, NMAT, UT>(acc, rd, xs, u, ntk, t0, kb);
-    }
+  // units go to waves round robin (one round for rows of up to S units)
+  for (int u = wave; u < nu; u += S) {
+    XSlice<UT> xp;
+    xfetch<UT>(xp, a.x, a.nw, u, nb, lane);
+    load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
+    ssq += xput<UT>(xp, xw, a.nw, u, nb, lane);
+    // the slice is written and read by this wave only: LDS operations of a
+    // wave complete in order, the fence keeps the compiler from reordering
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    fma_round<QT, NMAT, UT>(acc, rd, xw, kb);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   }
 
   // lanes r, r+16, r+32, r+48 hold row r's four block columns
@@ -498,14 +496,7 @@ __global__ void k_argmax_merge(const float2* part, int n, const float* y, int* o
 template <int QT, int NMAT, int EPI>
 hipError_t launch_t(const GemvArgs& a, hipStream_t s) {
   GemvPlan p = gemv_plan(a.rows, a.cols, QT, NMAT);
-  GemvArgs b = a;
-  b.chunk_tiles = p.chunk_tiles;
-  if (p.unit == 2)
-    hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, 2>), dim3(p.grid), dim3(p.threads), p.lds_bytes, s, b);
-  else if (p.unit == 4)
-    hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, 4>), dim3(p.grid), dim3(p.threads), p.lds_bytes, s, b);
-  else
-    hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, 8>), dim3(p.grid), dim3(p.threads), p.lds_bytes, s, b);
+  hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, kGemvUnit>), dim3(p.grid), dim3(p.threads), p.lds_bytes, s, a);
   return hipGetLastError();
 }
 
@@ -523,33 +514,22 @@ hipError_t launch_q(int epi, const GemvArgs& a, hipStream_t s) {
 
 }  // namespace
 
-// One workgroup per 16-row group; one wave per unit of UT tiles of the row,
-// up to 16 (Q4_0, one matrix) or 8 waves; rows wider than that take several
-// rounds per wave. UT is the largest of 8, 4, 2 that still gives the launch
-// kGemvWantWaves waves (smaller units shorten the work left after the last
-// load lands); x is staged in chunks of up to kGemvMaxChunkTiles tiles.
+// One workgroup per 16-row group; one wave per unit of kGemvUnit tiles of the
+// row, up to 16 (Q4_0, one matrix) or 8 waves; rows wider than that take
+// several rounds per wave. Two-tile units measured fastest for every 7B shape
+// (fewest registers, most waves resident, shortest work after the last load).
 GemvPlan gemv_plan(int rows, int cols, int type, int nmat) {
   GemvPlan p;
   const int groups = (rows + kRG - 1) / kRG;
   const int ntk = (cols / 32 + kTB - 1) / kTB;
   const int smax = type == 8 || nmat == 2 ? gemv_max_waves<8, 1>() : gemv_max_waves<2, 1>();
-  int ut = 8;
-  while (ut > 2) {
-    const int nu = (ntk + ut - 1) / ut;
-    const long waves = (long)groups * (nu < smax ? nu : smax);
-    const int nu2 = (ntk + ut / 2 - 1) / (ut / 2);
-    if (waves >= kGemvWantWaves || nu2 > smax) break;
-    ut /= 2;
-  }
+  const int ut = kGemvUnit;
   const int nu = (ntk + ut - 1) / ut;
   const int S = nu < smax ? nu : smax;
   p.unit = ut;
   p.grid = groups;
   p.threads = S * kWave;
-  const int ct = nu * ut;
-  p.chunk_tiles = ct < kGemvMaxChunkTiles ? ct : kGemvMaxChunkTiles;
-  p.lds_bytes = (size_t)p.chunk_tiles * kTB * kXW * sizeof(int) +
-                (size_t)(nmat * S * kRG + S) * sizeof(float);
+  p.lds_bytes = (size_t)S * ut * kTB * kXW * sizeof(int) + (size_t)(nmat * S * kRG + S) * sizeof(float);
   return p;
 }
 

@@ -149,11 +149,12 @@ void rope_row(float* cs, int rope_dim, int pos, float theta) {
   }
 }
 
-int attn_splits(int n_kv_heads, int max_seq) {
-  int ns = 512 / n_kv_heads;
-  const int by_len = (max_seq + 63) / 64;
-  if (ns > by_len) ns = by_len;
-  if (ns > 64) ns = 64;
+// Splits per KV head: enough that a split of the longest context is one round
+// of k_attn loads, at most kMaxSplits.
+int attn_splits(int head_dim, int group, int max_seq) {
+  const int round = ssk::attn_round_positions(head_dim, group);
+  int ns = (max_seq + round - 1) / round;
+  if (ns > ssk::kMaxSplits) ns = ssk::kMaxSplits;
   if (ns < 1) ns = 1;
   return ns;
 }
@@ -388,7 +389,7 @@ int32_t ss_hip_attention(ss_hip_ctx_t* c, float* out, const float* q, const void
   const int group = n_heads / n_kv_heads;
   if (!ssk::attention_supported(head_dim, group))
     return fail(kErrParams, "attention: head_dim %d / group %d not supported", head_dim, group);
-  const int ns = attn_splits(n_kv_heads, max_seq);
+  const int ns = attn_splits(head_dim, group, max_seq);
   int32_t rc = ensure(c, (void**)&c->att_o, &c->att_o_floats,
                       sizeof(float) * (size_t)n_kv_heads * ns * group * head_dim, false);
   if (!rc) rc = ensure(c, (void**)&c->att_ml, &c->att_ml_floats,
@@ -817,7 +818,7 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
   m->qdim = m->H * m->hd;
   m->kvdim = m->KVH * m->hd;
   m->group = group;
-  m->ns = attn_splits(m->KVH, m->max_seq);
+  m->ns = attn_splits(m->hd, m->group, m->max_seq);
 
   auto bail = [&](void) -> ss_hip_model_t* {
     model_release(m);

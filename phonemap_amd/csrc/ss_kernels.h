@@ -30,7 +30,6 @@ struct GemvArgs {
   float* y;                  // output [rows]
   int rows, cols, type;
   int n_cu;                  // compute units (sizes the grid)
-  int chunk_tiles;           // tiles (4 blocks) of x staged per pass (set by the launcher)
   // EPI_QKV
   int qdim, kvdim, head_dim, rope_dim, max_seq, kv_type;
   const float* rope_cs;      // [max_seq][rope_dim/2][2]
@@ -57,7 +56,7 @@ struct AttnArgs {
 };
 
 struct GemvPlan {
-  int grid, threads, chunk_tiles, unit;
+  int grid, threads, unit;
   size_t lds_bytes;
 };
 GemvPlan gemv_plan(int rows, int cols, int type, int nmat);
@@ -69,6 +68,8 @@ hipError_t launch_argmax_merge(const float2* part, int n, const float* y, int* o
                                int* dpos, hipStream_t s);
 hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, hipStream_t s);
 bool attention_supported(int head_dim, int group);
+// positions one k_attn workgroup covers in one round of loads
+int attn_round_positions(int head_dim, int group);
 
 hipError_t launch_pack(int type, const uint8_t* src, uint8_t* qs, uint16_t* ds, int64_t nblocks,
                        int nb, int64_t row_off, hipStream_t s);
@@ -90,8 +91,7 @@ constexpr int kArgmaxMaxBlocks = 1024;
 constexpr int kRG = 16;                    // rows per packed row group
 constexpr int kTB = 4;                     // 32-column blocks per tile (kRG * kTB = 64 lanes)
 constexpr int kUT = 8;                     // tiles per scale group (16 B of scales per lane)
-constexpr int kGemvWantWaves = 4096;       // waves per matvec launch the unit size aims for
-constexpr int kGemvMaxChunkTiles = 96;     // a multiple of kUT: 384 blocks * 112 B = 42 KiB of x per pass
+constexpr int kGemvUnit = 2;               // tiles per wave per round (2, 4 or 8)
 constexpr int kGemvMaxSplit = 16;          // waves per matvec workgroup
 constexpr int kMaxSplits = 64;             // attention splits per KV head
 

@@ -14,183 +14,199 @@ namespace {
 
 // ------------------------------------------------------------ attention
 // Single-query GQA attention (layer_scheduler.c:415-468) with the sequence
-// split over gridDim.x workgroups (flash-decoding): workgroup (s, g) runs an
-// online softmax over its slice of positions for the G query heads that
-// share KV head g, staging 64-position K and V tiles in LDS, and writes a
-// partial (max, sum, unnormalised output); k_attn_merge combines them.
+// split over gridDim.x workgroups (flash-decoding); k_attn_merge combines the
+// splits. In workgroup (s, g), serving the G query heads that share KV head
+// g, lane l of wave w holds 8 consecutive elements (column chunk l % LPR) of
+// the K and V rows (l / LPR) + RPI*w + ... of its positions; a round of
+// positions is requested at once, straight into registers. Scores are summed
+// over the LPR lanes of a row with DPP, each wave keeps its own online
+// softmax, and the 4 waves are combined once at the end.
 template <int KVT>
 struct KvElem;
 template <>
-struct KvElem<0> {
-  using T = uint16_t;
-  static __device__ __forceinline__ float get(T v, float) { return h2f(v); }
+struct KvElem<0> {   // binary16, 8 elements = 16 bytes
+  using Chunk = uint4;
+  static __device__ __forceinline__ void get(const Chunk& c, float s, float (&v)[8]) {
+    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = h2f((uint16_t)(w[i] & 0xffffu));
+      v[2 * i + 1] = h2f((uint16_t)(w[i] >> 16));
+    }
+    (void)s;
+  }
 };
 template <>
-struct KvElem<1> {
-  using T = int8_t;
-  static __device__ __forceinline__ float get(T v, float s) { return (float)v * s; }
+struct KvElem<1> {   // int8 codes times the position's scale (layer_scheduler.c:120-125)
+  using Chunk = uint2;
+  static __device__ __forceinline__ void get(const Chunk& c, float s, float (&v)[8]) {
+    const uint32_t w[2] = {c.x, c.y};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (float)(int8_t)((w[i / 4] >> (8 * (i % 4))) & 0xffu) * s;
+  }
 };
 
 __device__ __forceinline__ void attn_split(const AttnArgs& a, int& ctx, int& chunk, int& active) {
   ctx = a.dpos ? *a.dpos + 1 : a.seq_len;
   chunk = (ctx + a.ns - 1) / a.ns;
-  if (chunk < 64) chunk = 64;
+  if (chunk < 32) chunk = 32;
   active = (ctx + chunk - 1) / chunk;
 }
 
+// Sum over aligned groups of N (4, 8 or 16) lanes, result in every lane.
+template <int N>
+__device__ __forceinline__ float sum_lanes(float v) {
+  v += dpp<0xb1>(v);                           // quad_perm [1,0,3,2]
+  v += dpp<0x4e>(v);                           // quad_perm [2,3,0,1]
+  if constexpr (N >= 8) v += dpp<0x141>(v);    // row_half_mirror
+  if constexpr (N >= 16) v += dpp<0x140>(v);   // row_mirror
+  return v;
+}
+
+constexpr int kAttnWaves = 4;
+// rows of K and V per lane per round: 64 positions per round at hd 128, G <= 2
+__host__ __device__ constexpr int attn_rows_per_lane(int group) {
+  return group >= 8 ? 1 : group >= 4 ? 2 : 4;
+}
+
 template <int HD, int G, int KVT>
-__global__ void __launch_bounds__(256) k_attn(const AttnArgs a) {
-  using E = typename KvElem<KVT>::T;
-  constexpr int kT = 64;                         // positions per tile
-  constexpr int kChunkBytes = 16;
-  constexpr int kRowBytes = HD * (int)sizeof(E);
-  constexpr int kCpr = kRowBytes / kChunkBytes;  // 16-byte chunks per row
-  constexpr int kEpc = kChunkBytes / (int)sizeof(E);
-  constexpr int kStride = HD + kEpc;             // padded LDS row, elements
-  // score phase: NG head groups x SPLIT threads per (position, head)
-  constexpr int kNG = G >= 4 ? 4 : G;
-  constexpr int kHPT = G >= 4 ? G / 4 : 1;
-  constexpr int kSplit = 4 / kNG;
-  constexpr int kCps = kCpr / kSplit;            // chunks per split
-  // value phase: OPT outputs per thread, TPO threads (position phases) per output
-  constexpr int kNPV = G * HD;
-  constexpr int kOPT = kNPV >= 256 ? kNPV / 256 : 1;
-  constexpr int kTPO = kNPV >= 256 ? 1 : 256 / kNPV;
-  constexpr int kOThreads = 256 / kTPO;
+__global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
+  using KE = KvElem<KVT>;
+  using Chunk = typename KE::Chunk;
+  constexpr int kLpr = HD / 8;                  // lanes per row
+  constexpr int kRpi = kWave / kLpr;            // rows per wave and load
+  constexpr int kK = attn_rows_per_lane(G);     // rows per lane per round
+  constexpr int kRound = kK * kAttnWaves * kRpi;    // positions per round
+  constexpr int kEb = KVT == 0 ? 2 : 1;          // bytes per element
 
-  __shared__ __attribute__((aligned(16))) E kt[kT * kStride];
-  __shared__ __attribute__((aligned(16))) E vt[kT * kStride];
-  __shared__ __attribute__((aligned(16))) float qsh[G][HD + 4];
-  __shared__ float st[G][kT];
-  __shared__ float ksc[kT], vsc[kT];
-  __shared__ float m_run[G], l_run[G], corr[G];
-  __shared__ float red[kTPO > 1 ? kTPO * 256 : 1];
+  __shared__ float wm[kAttnWaves][G], wl[kAttnWaves][G];
+  __shared__ float wo[kAttnWaves][G][HD];
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kvh = blockIdx.y;
   int ctx, chunk, active;
   attn_split(a, ctx, chunk, active);
-  if ((int)blockIdx.x >= active) return;
+  if ((int)blockIdx.x >= active) return;   // whole workgroup
   const int t0 = blockIdx.x * chunk;
   const int t1 = min(ctx, t0 + chunk);
+  const int c = lane % kLpr, rsub = lane / kLpr;
 
   const size_t head_base = (size_t)kvh * a.max_seq;
-  const E* kbase = reinterpret_cast<const E*>(a.kc) + head_base * HD;
-  const E* vbase = reinterpret_cast<const E*>(a.vc) + head_base * HD;
+  const uint8_t* kb = static_cast<const uint8_t*>(a.kc) + (head_base * HD + c * 8) * kEb;
+  const uint8_t* vb = static_cast<const uint8_t*>(a.vc) + (head_base * HD + c * 8) * kEb;
 
-  for (int i = tid; i < G * HD; i += 256) qsh[i / HD][i % HD] = a.q[(size_t)kvh * G * HD + i];
-  if (tid < G) {
-    m_run[tid] = -INFINITY;
-    l_run[tid] = 0.f;
+  float q[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float4* qp = reinterpret_cast<const float4*>(a.q + ((size_t)kvh * G + g) * HD + c * 8);
+    const float4 x0 = qp[0], x1 = qp[1];
+    q[g][0] = x0.x; q[g][1] = x0.y; q[g][2] = x0.z; q[g][3] = x0.w;
+    q[g][4] = x1.x; q[g][5] = x1.y; q[g][6] = x1.z; q[g][7] = x1.w;
+  }
+  float m[G], l[G], o[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
   }
 
-  // value-phase ownership
-  const int vphase = tid / kOThreads;
-  const int o0 = (tid % kOThreads) * kOPT;
-  const int vg = o0 / HD, vd = o0 % HD;
-  float acc[kOPT];
+  for (int r0 = t0; r0 < t1; r0 += kRound) {
+    Chunk kr[kK], vr[kK];
+    float ks[kK], vs[kK];
 #pragma unroll
-  for (int j = 0; j < kOPT; ++j) acc[j] = 0.f;
-
-  // score-phase ownership
-  const int sp = (tid / kSplit) % kT;        // position in tile
-  const int sg = tid / (kT * kSplit);        // head group
-  const int ss = tid % kSplit;               // split index
-
-  for (int tile = t0; tile < t1; tile += kT) {
-    const int nv = min(kT, t1 - tile);
-    __syncthreads();   // previous tile fully consumed (and q/m/l initialised)
-    for (int c = tid; c < nv * kCpr; c += 256) {
-      const int row = c / kCpr, part = c % kCpr;
-      const size_t go = (size_t)(tile + row) * HD + part * kEpc;
-      *reinterpret_cast<uint4*>(kt + row * kStride + part * kEpc) =
-          *reinterpret_cast<const uint4*>(kbase + go);
-      *reinterpret_cast<uint4*>(vt + row * kStride + part * kEpc) =
-          *reinterpret_cast<const uint4*>(vbase + go);
-    }
-    if constexpr (KVT == 1) {
-      if (tid < nv) {
-        ksc[tid] = a.ks[tile + tid];
-        vsc[tid] = a.vs[tile + tid];
+    for (int k = 0; k < kK; ++k) {   // branch-free: positions past t1 reload t1-1 and are masked
+      const int p = min(r0 + (k * kAttnWaves + wave) * kRpi + rsub, t1 - 1);
+      kr[k] = *reinterpret_cast<const Chunk*>(kb + (size_t)p * HD * kEb);
+      vr[k] = *reinterpret_cast<const Chunk*>(vb + (size_t)p * HD * kEb);
+      if constexpr (KVT == 1) {
+        ks[k] = a.ks[p];
+        vs[k] = a.vs[p];
+      } else {
+        ks[k] = vs[k] = 1.f;
       }
     }
-    __syncthreads();
-
-    // scores s[g][p] = (q_g . k_p) * scale
+    float sc[G][kK];
 #pragma unroll
-    for (int hh = 0; hh < kHPT; ++hh) {
-      const int g = sg * kHPT + hh;
-      float dot = 0.f;
-      if (sp < nv) {
-        const float kscale = KVT == 1 ? ksc[sp] : 1.f;
-        const E* krow = kt + sp * kStride;
+    for (int k = 0; k < kK; ++k) {
+      float kv[8];
+      KE::get(kr[k], ks[k], kv);
+      const bool live = r0 + (k * kAttnWaves + wave) * kRpi + rsub < t1;
 #pragma unroll
-        for (int cc = 0; cc < kCps; ++cc) {
-          const int chunk_i = cc * kSplit + ss;
-          const E* kp = krow + chunk_i * kEpc;
-          const float* qp = &qsh[g][chunk_i * kEpc];
+      for (int g = 0; g < G; ++g) {
+        float d = 0.f;
 #pragma unroll
-          for (int e = 0; e < kEpc; ++e) dot = fmaf(qp[e], KvElem<KVT>::get(kp[e], kscale), dot);
-        }
-      }
-      if constexpr (kSplit >= 2) dot += __shfl_xor(dot, 1, kWave);
-      if constexpr (kSplit >= 4) dot += __shfl_xor(dot, 2, kWave);
-      if (ss == 0) st[g][sp] = sp < nv ? dot * a.scale : -INFINITY;
-    }
-    __syncthreads();
-
-    // online softmax update, one wave per head
-    for (int g = wave; g < G; g += 4) {
-      const float sv = st[g][lane];
-      const float mt = wave_max(sv);
-      const float mo = m_run[g];
-      const float mn = fmaxf(mo, mt);
-      const float p = expf(sv - mn);
-      st[g][lane] = p;
-      const float lt = wave_sum(p);
-      if (lane == 0) {
-        const float c = expf(mo - mn);
-        corr[g] = c;
-        l_run[g] = l_run[g] * c + lt;
-        m_run[g] = mn;
+        for (int e = 0; e < 8; ++e) d = fmaf(q[g][e], kv[e], d);
+        d = sum_lanes<kLpr>(d) * a.scale;        // (q . k) * (1/sqrt(hd)), layer_scheduler.c:442-446
+        sc[g][k] = live ? d : -INFINITY;
       }
     }
-    __syncthreads();
-
-    // acc = acc * corr + sum_p p[g][p] * v[p]
-    const float c = corr[vg];
 #pragma unroll
-    for (int j = 0; j < kOPT; ++j) acc[j] *= c;
-    for (int p = vphase; p < nv; p += kTPO) {
-      const float w = st[vg][p];
-      const float vscale = KVT == 1 ? vsc[p] : 1.f;
-      const E* vrow = vt + p * kStride + vd;
+    for (int g = 0; g < G; ++g) {
+      float mt = sc[g][0];
 #pragma unroll
-      for (int j = 0; j < kOPT; ++j) acc[j] = fmaf(w, KvElem<KVT>::get(vrow[j], vscale), acc[j]);
+      for (int k = 1; k < kK; ++k) mt = fmaxf(mt, sc[g][k]);
+      mt = wave_max(mt);
+      const float mn = fmaxf(m[g], mt);
+      const float mref = mn == -INFINITY ? 0.f : mn;   // nothing live yet: all weights 0
+      const float corr = expf(m[g] - mref);
+      float ps = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] *= corr;
+#pragma unroll
+      for (int k = 0; k < kK; ++k) {
+        const float p = expf(sc[g][k] - mref);
+        ps += p;
+        float vv[8];
+        KE::get(vr[k], vs[k], vv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[g][e] = fmaf(p, vv[e], o[g][e]);
+      }
+      l[g] = l[g] * corr + wave_sum(c == 0 ? ps : 0.f);
+      m[g] = mn;
     }
   }
 
-  // merge the position phases
-  if constexpr (kTPO > 1) {
-    __syncthreads();
-    red[vphase * kOThreads + (tid % kOThreads)] = acc[0];
-    __syncthreads();
-    if (vphase == 0) {
-      float s = acc[0];
-      for (int ph = 1; ph < kTPO; ++ph) s += red[ph * kOThreads + tid];
-      acc[0] = s;
+  // rows of a wave: lanes with the same column chunk are kLpr apart
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      for (int off = kLpr; off < kWave; off <<= 1) o[g][e] += __shfl_xor(o[g][e], off, kWave);
+  if (rsub == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) wo[wave][g][c * 8 + e] = o[g][e];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      wm[wave][g] = m[g];
+      wl[wave][g] = l[g];
     }
   }
+  __syncthreads();
   float* po = a.part_o + (((size_t)kvh * a.ns + blockIdx.x) * G) * HD;
   float* pml = a.part_ml + (((size_t)kvh * a.ns + blockIdx.x) * G) * 2;
-  if (vphase == 0) {
+  for (int i = tid; i < G * HD; i += kAttnWaves * 64) {
+    const int g = i / HD, d = i % HD;
+    float M = -INFINITY;
 #pragma unroll
-    for (int j = 0; j < kOPT; ++j) po[vg * HD + vd + j] = acc[j];
-  }
-  if (tid < G) {
-    pml[tid * 2] = m_run[tid];
-    pml[tid * 2 + 1] = l_run[tid];
+    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, wm[w][g]);   // finite: wave 0 has position t0
+    float so = 0.f, sl = 0.f;
+#pragma unroll
+    for (int w = 0; w < kAttnWaves; ++w) {
+      const float f = expf(wm[w][g] - M);
+      so = fmaf(f, wo[w][g][d], so);
+      sl = fmaf(f, wl[w][g], sl);
+    }
+    po[g * HD + d] = so;
+    if (d == 0) {
+      pml[g * 2] = M;
+      pml[g * 2 + 1] = sl;
+    }
   }
 }
 
@@ -333,9 +349,9 @@ template <int HD, int G>
 hipError_t launch_attn_t(int kv_type, const AttnArgs& a, hipStream_t s) {
   const dim3 grid(a.ns, a.n_kv_heads);
   if (kv_type == 0)
-    hipLaunchKernelGGL((k_attn<HD, G, 0>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((k_attn<HD, G, 0>), grid, dim3(kAttnWaves * 64), 0, s, a);
   else
-    hipLaunchKernelGGL((k_attn<HD, G, 1>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((k_attn<HD, G, 1>), grid, dim3(kAttnWaves * 64), 0, s, a);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL((k_attn_merge<HD, G>), dim3(a.n_kv_heads), dim3(256), 0, s, a);
@@ -354,6 +370,11 @@ hipError_t launch_attn_hd(int group, int kv_type, const AttnArgs& a, hipStream_t
 }
 
 }  // namespace
+
+int attn_round_positions(int head_dim, int group) {
+  const int rows_per_load = kWave / (head_dim / 8);
+  return attn_rows_per_lane(group) * kAttnWaves * rows_per_load;
+}
 
 bool attention_supported(int head_dim, int group) {
   return (head_dim == 64 || head_dim == 128) &&
