@@ -66,6 +66,15 @@ __device__ __forceinline__ void wave_best(float& bv, int& bi) {
   }
 }
 
+// Attention split of positions 0..ctx-1 over ns workgroups per KV head:
+// chunk positions each (at least 32), `active` of them non-empty. Shared by
+// the attention kernel and the consumers that merge its splits.
+__device__ __forceinline__ void attn_chunks(int ctx, int ns, int& chunk, int& active) {
+  chunk = (ctx + ns - 1) / ns;
+  if (chunk < 32) chunk = 32;
+  active = (ctx + chunk - 1) / chunk;
+}
+
 template <int QT>
 struct QTraits;
 template <>

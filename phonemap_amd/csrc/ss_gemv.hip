@@ -217,6 +217,78 @@ __device__ __forceinline__ float xput(XSlice<UT>& p, int* xw, const float* nw, i
   return ss;
 }
 
+// Merge staging (the k_attn_merge step inside the Wo matvec): x[col] for
+// col in head h = G*kvh + g is sum_s o_s * e^(m_s - M) / sum_s l_s e^(m_s - M)
+// over the active attention splits s of KV head kvh. A lane fetches the
+// (m, l) and 4 o values of all kMergeSplits split slots for its group of 4
+// columns (slots past the active ones reload the last active split and get
+// weight 0) before the weight loads, in one batch.
+template <int UT>
+struct MSlice {
+  float2 ml[UT / 2][kMergeSplits];
+  float4 o[UT / 2][kMergeSplits];
+};
+
+__device__ __forceinline__ int merge_active(const GemvArgs& a) {
+  int chunk, active;
+  attn_chunks(*a.dpos + 1, a.att_ns, chunk, active);
+  return active;
+}
+
+template <int UT>
+__device__ __forceinline__ void mfetch(MSlice<UT>& p, const GemvArgs& a, int u, int active, int lane) {
+  const int hd = a.head_dim, G = a.att_group;
+#pragma unroll
+  for (int j = 0; j < UT / 2; ++j) {
+    const int gi = j * kWave + lane;
+    const int col = min(u * UT * kTB * 32 + (gi >> 3) * 32 + (gi & 7) * 4, a.cols - 4);
+    const int h = col / hd, d = col % hd;
+    const int kvh = h / G, g = h % G;
+#pragma unroll
+    for (int s = 0; s < kMergeSplits; ++s) {
+      const size_t i = ((size_t)kvh * a.att_ns + min(s, active - 1)) * G + g;
+      p.ml[j][s] = *reinterpret_cast<const float2*>(a.att_ml + i * 2);
+      p.o[j][s] = *reinterpret_cast<const float4*>(a.att_o + i * hd + d);
+    }
+  }
+}
+
+// Same arithmetic order as k_attn_merge.
+template <int UT>
+__device__ __forceinline__ void mput(MSlice<UT>& p, int* xw, int u, int nb, int active, int lane) {
+#pragma unroll
+  for (int j = 0; j < UT / 2; ++j)
+#pragma unroll
+    for (int s = 0; s < kMergeSplits; ++s) {
+      asm volatile("" : "+v"(p.ml[j][s].x), "+v"(p.ml[j][s].y));
+      pin(p.o[j][s]);
+    }
+#pragma unroll
+  for (int j = 0; j < UT / 2; ++j) {
+    const int gi = j * kWave + lane;
+    float M = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < kMergeSplits; ++s)
+      if (s < active) M = fmaxf(M, p.ml[j][s].x);
+    float L = 0.f;
+#pragma unroll
+    for (int s = 0; s < kMergeSplits; ++s)
+      if (s < active) L += p.ml[j][s].y * expf(p.ml[j][s].x - M);
+    const float inv = 1.0f / L;
+    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int s = 0; s < kMergeSplits; ++s) {
+      const float w = s < active ? expf(p.ml[j][s].x - M) * inv : 0.f;
+      t.x = fmaf(p.o[j][s].x, w, t.x);
+      t.y = fmaf(p.o[j][s].y, w, t.y);
+      t.z = fmaf(p.o[j][s].z, w, t.z);
+      t.w = fmaf(p.o[j][s].w, w, t.w);
+    }
+    if (u * UT * kTB + (gi >> 3) >= nb) t = make_float4(0.f, 0.f, 0.f, 0.f);
+    encode4(xw + (gi >> 3) * kXW, gi & 7, t);
+  }
+}
+
 // One wave's share per round: a unit of UT (2, 4 or 8) consecutive tiles
 // (those < ntk), every chunk of it requested before any is used. A unit lies
 // inside one 8-tile scale group, whose 16 bytes per lane it reads UT/2 words of.
@@ -340,7 +412,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int row, bool own, c
 template <int QT, int NMAT>
 constexpr int gemv_max_waves() { return QT == 8 || NMAT == 2 ? 8 : 16; }
 
-template <int QT, int NMAT, int EPI, int UT>
+template <int QT, int NMAT, int EPI, int UT, bool MERGE>
 __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(const GemvArgs a) {
   extern __shared__ float4 smem4[];
   int* xs = reinterpret_cast<int*>(smem4);
@@ -363,11 +435,19 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
   Round<QT, NMAT, UT> rd;
 
   // units go to waves round robin (one round for rows of up to S units)
+  const int active = MERGE ? merge_active(a) : 0;
   for (int u = wave; u < nu; u += S) {
-    XSlice<UT> xp;
-    xfetch<UT>(xp, a.x, a.nw, u, nb, lane);
-    load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
-    ssq += xput<UT>(xp, xw, a.nw, u, nb, lane);
+    if constexpr (MERGE) {
+      MSlice<UT> mp;
+      mfetch<UT>(mp, a, u, active, lane);
+      load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
+      mput<UT>(mp, xw, u, nb, active, lane);
+    } else {
+      XSlice<UT> xp;
+      xfetch<UT>(xp, a.x, a.nw, u, nb, lane);
+      load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
+      ssq += xput<UT>(xp, xw, a.nw, u, nb, lane);
+    }
     // the slice is written and read by this wave only: LDS operations of a
     // wave complete in order, the fence keeps the compiler from reordering
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -493,10 +573,11 @@ __global__ void k_argmax_merge(const float2* part, int n, const float* y, int* o
   }
 }
 
-template <int QT, int NMAT, int EPI>
+template <int QT, int NMAT, int EPI, bool MERGE = false>
 hipError_t launch_t(const GemvArgs& a, hipStream_t s) {
   GemvPlan p = gemv_plan(a.rows, a.cols, QT, NMAT);
-  hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, kGemvUnit>), dim3(p.grid), dim3(p.threads), p.lds_bytes, s, a);
+  hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, kGemvUnit, MERGE>), dim3(p.grid), dim3(p.threads), p.lds_bytes,
+                     s, a);
   return hipGetLastError();
 }
 
@@ -504,7 +585,7 @@ template <int QT>
 hipError_t launch_q(int epi, const GemvArgs& a, hipStream_t s) {
   switch (epi) {
     case EPI_STORE: return launch_t<QT, 1, EPI_STORE>(a, s);
-    case EPI_ADD: return launch_t<QT, 1, EPI_ADD>(a, s);
+    case EPI_ADD: return a.att_o ? launch_t<QT, 1, EPI_ADD, true>(a, s) : launch_t<QT, 1, EPI_ADD>(a, s);
     case EPI_SWIGLU: return launch_t<QT, 2, EPI_SWIGLU>(a, s);
     case EPI_QKV: return launch_t<QT, 1, EPI_QKV>(a, s);
     case EPI_LOGITS: return launch_t<QT, 1, EPI_LOGITS>(a, s);
@@ -559,6 +640,9 @@ PackedMat packed_view(const void* base, int type, int64_t rows, int cols) {
 }
 
 hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t s) {
+  if (a.att_o && (epi != EPI_ADD || !a.att_ml || !a.dpos || a.att_ns < 1 || a.att_ns > kMergeSplits ||
+                  a.att_group < 1 || a.head_dim < 32 || a.head_dim % 32 || a.cols % a.head_dim))
+    return hipErrorInvalidValue;
   if (a.type == 2) return launch_q<2>(epi, a, s);
   if (a.type == 8) return launch_q<8>(epi, a, s);
   return hipErrorInvalidValue;

@@ -410,7 +410,7 @@ int32_t ss_hip_attention(ss_hip_ctx_t* c, float* out, const float* q, const void
   a.out = out;
   a.part_o = c->att_o;
   a.part_ml = c->att_ml;
-  HIP_TRY(ssk::launch_attention(head_dim, group, kv_type, a, pick(c, stream)));
+  HIP_TRY(ssk::launch_attention(head_dim, group, kv_type, a, true, pick(c, stream)));
   return 0;
 }
 
@@ -697,10 +697,22 @@ int32_t enqueue_token(ss_hip_model* m, bool with_head) {
     at.out = m->attn;
     at.part_o = m->att_o;
     at.part_ml = m->att_ml;
-    HIP_TRY(timed(m, PC_ATTN, 0, [&] { return ssk::launch_attention(m->hd, m->group, m->kv_type, at, s); }));
+    // with few splits the Wo matvec merges them itself (no merge launch)
+    const bool fused = m->ns <= ssk::kMergeSplits;
+    HIP_TRY(timed(m, PC_ATTN, 0, [&] {
+      return ssk::launch_attention(m->hd, m->group, m->kv_type, at, !fused, s);
+    }));
 
     // 3. hidden += Wo attn                                         (:470-484)
     ssk::GemvArgs o = gemv_args(ly.wo, m->attn, m->hidden, m->d, m->qdim, ly.t_o);
+    if (fused) {
+      o.att_o = m->att_o;
+      o.att_ml = m->att_ml;
+      o.att_ns = m->ns;
+      o.att_group = m->group;
+      o.head_dim = m->hd;
+      o.dpos = m->dpos;
+    }
     HIP_TRY(timed(m, q_class(ly.t_o), matvec_bytes(ly.t_o, m->d, m->qdim, 1),
                   [&] { return ssk::launch_gemv(ssk::EPI_ADD, o, s); }));
 

@@ -20,7 +20,7 @@ namespace {
 // the K and V rows (l / LPR) + RPI*w + ... of its positions; a round of
 // positions is requested at once, straight into registers. Scores are summed
 // over the LPR lanes of a row with DPP, each wave keeps its own online
-// softmax, and the 4 waves are combined once at the end.
+// softmax, and the 8 waves are combined once at the end.
 template <int KVT>
 struct KvElem;
 template <>
@@ -48,9 +48,7 @@ struct KvElem<1> {   // int8 codes times the position's scale (layer_scheduler.c
 
 __device__ __forceinline__ void attn_split(const AttnArgs& a, int& ctx, int& chunk, int& active) {
   ctx = a.dpos ? *a.dpos + 1 : a.seq_len;
-  chunk = (ctx + a.ns - 1) / a.ns;
-  if (chunk < 32) chunk = 32;
-  active = (ctx + chunk - 1) / chunk;
+  attn_chunks(ctx, a.ns, chunk, active);
 }
 
 // Sum over aligned groups of N (4, 8 or 16) lanes, result in every lane.
@@ -63,8 +61,8 @@ __device__ __forceinline__ float sum_lanes(float v) {
   return v;
 }
 
-constexpr int kAttnWaves = 4;
-// rows of K and V per lane per round: 64 positions per round at hd 128, G <= 2
+constexpr int kAttnWaves = 8;
+// rows of K and V per lane per round: 128 positions per round at hd 128, G <= 2
 __host__ __device__ constexpr int attn_rows_per_lane(int group) {
   return group >= 8 ? 1 : group >= 4 ? 2 : 4;
 }
@@ -346,25 +344,25 @@ __global__ void k_advance(int* dpos) { *dpos += 1; }
 
 // ------------------------------------------------------------ launchers
 template <int HD, int G>
-hipError_t launch_attn_t(int kv_type, const AttnArgs& a, hipStream_t s) {
+hipError_t launch_attn_t(int kv_type, const AttnArgs& a, bool merge, hipStream_t s) {
   const dim3 grid(a.ns, a.n_kv_heads);
   if (kv_type == 0)
     hipLaunchKernelGGL((k_attn<HD, G, 0>), grid, dim3(kAttnWaves * 64), 0, s, a);
   else
     hipLaunchKernelGGL((k_attn<HD, G, 1>), grid, dim3(kAttnWaves * 64), 0, s, a);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (e != hipSuccess || !merge) return e;
   hipLaunchKernelGGL((k_attn_merge<HD, G>), dim3(a.n_kv_heads), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
 template <int HD>
-hipError_t launch_attn_hd(int group, int kv_type, const AttnArgs& a, hipStream_t s) {
+hipError_t launch_attn_hd(int group, int kv_type, const AttnArgs& a, bool merge, hipStream_t s) {
   switch (group) {
-    case 1: return launch_attn_t<HD, 1>(kv_type, a, s);
-    case 2: return launch_attn_t<HD, 2>(kv_type, a, s);
-    case 4: return launch_attn_t<HD, 4>(kv_type, a, s);
-    case 8: return launch_attn_t<HD, 8>(kv_type, a, s);
+    case 1: return launch_attn_t<HD, 1>(kv_type, a, merge, s);
+    case 2: return launch_attn_t<HD, 2>(kv_type, a, merge, s);
+    case 4: return launch_attn_t<HD, 4>(kv_type, a, merge, s);
+    case 8: return launch_attn_t<HD, 8>(kv_type, a, merge, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -381,11 +379,11 @@ bool attention_supported(int head_dim, int group) {
          (group == 1 || group == 2 || group == 4 || group == 8);
 }
 
-hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a,
+hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, bool merge,
                             hipStream_t s) {
-  if (a.ns > 64) return hipErrorInvalidValue;   // k_attn_merge holds 64 split weights per head
-  if (head_dim == 64) return launch_attn_hd<64>(group, kv_type, a, s);
-  if (head_dim == 128) return launch_attn_hd<128>(group, kv_type, a, s);
+  if (a.ns > kMaxSplits) return hipErrorInvalidValue;   // k_attn_merge holds 64 split weights per head
+  if (head_dim == 64) return launch_attn_hd<64>(group, kv_type, a, merge, s);
+  if (head_dim == 128) return launch_attn_hd<128>(group, kv_type, a, merge, s);
   return hipErrorInvalidValue;
 }
 

@@ -70,6 +70,29 @@ def test_greedy_and_logits(spec, kv, graph):
 
 
 @pytest.mark.parametrize("kv", ["f16", "int8"])
+def test_long_context_split_merge_path(kv):
+    """A context of 1024 gives 16 attention splits per KV head: more than the
+    Wo matvec merges itself, so the separate merge kernel runs."""
+    path = _model_file("gqa8", **GQA8)
+    rng = np.random.default_rng(9)
+    prompt = rng.integers(3, GQA8["vocab"], 40).tolist()
+    om = oracle.Model(path, 1024, kv)
+    tol = TOL if kv == "f16" else TOL_INT8
+    with api.Model(path, max_context=1024, kv=kv) as m:
+        lg, am = m.eval_prompt(prompt, 0)
+        olg = om.prefill(prompt, 0)
+        assert rel_err(lg, olg) <= tol
+        tok, pos = am, len(prompt)
+        for _ in range(16):
+            lg, am = m.eval_token(tok, pos)
+            olg = om.forward(tok, pos)
+            assert rel_err(lg, olg) <= tol, pos
+            assert am == oracle.argmax(olg)
+            tok, pos = am, pos + 1
+    om.close()
+
+
+@pytest.mark.parametrize("kv", ["f16", "int8"])
 def test_device_greedy_equals_host_loop(kv):
     path = _model_file("gqa8", **GQA8)
     prompt = list(range(5, 37))
