@@ -8,9 +8,12 @@ token: embedding, 32 layers, output norm, LM head, argmax.
 
 Prints one JSON line. `value` is decode tokens/s over exactly --steps decode
 steps (after --warmup untimed ones), with the weights resident in HBM. The
-roofline object is for the dominant kernel class (the Q4_0 matvecs),
-measured with HIP events on the model stream in a profiled replay of the
-same decode steps; cpu_baseline is the CPU oracle (the reference path
+roofline object is for the dominant kernel: with the default launch mode
+(one persistent launch per token) that is the whole-token kernel, whose
+algorithmic bytes are every weight byte of the token once plus the KV cache
+read; with per-kernel launches it is the Q4_0 matvec class. It is measured
+with HIP events on the model stream around each launch in a profiled replay
+of further decode steps. cpu_baseline is the CPU oracle (the reference path
 restated in C) on the same GGUF, timed on this host on a bounded sample.
 """
 import argparse
@@ -110,8 +113,9 @@ def main():
     ap.add_argument("--kv", default="f16", choices=["f16", "int8"])
     ap.add_argument("--model-dir", default=os.environ.get("SS_BENCH_DIR", "/tmp"))
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--no-graph", action="store_true",
-                    help="launch kernels eagerly instead of replaying the per-token HIP graph")
+    ap.add_argument("--launch", default="graph", choices=["graph", "sweep", "eager"],
+                    help="per-kernel launches replayed from a HIP graph (default), one persistent "
+                         "launch per token, or per-kernel launches issued eagerly")
     ap.add_argument("--profile-steps", type=int, default=16)
     ap.add_argument("--prompt-len", type=int, default=None,
                     help="override the prompt length (counter runs use a short prompt)")
@@ -141,7 +145,7 @@ def main():
         log("wrote %s (%.2f GB) in %.1f s" % (path, os.path.getsize(path) / 1e9, time.perf_counter() - t))
     max_ctx = prompt_len + warm + steps + args.profile_steps + 2
     t = time.perf_counter()
-    m = api.Model(path, max_context=max_ctx, kv=args.kv, use_graph=not args.no_graph)
+    m = api.Model(path, max_context=max_ctx, kv=args.kv, launch=args.launch)
     log("loaded in %.1f s" % (time.perf_counter() - t))
     L = api._lib()
     rng = np.random.default_rng(1234)
@@ -164,8 +168,8 @@ def main():
     roof = None
     try:
         roof = profile_classes(m, args.profile_steps)
-        if args.config == "llama2-7b":   # the counter runs were made on this workload
-            roof["traffic"] = measured_traffic()
+        if args.config == "llama2-7b" and args.kv == "f16" and args.prompt_len is None:
+            roof["traffic"] = measured_traffic(roof["kernel_id"])   # counter runs of this workload
     except Exception as e:   # profiling is optional for the headline number
         log("profiling failed: %s" % e)
 
@@ -195,15 +199,16 @@ def main():
     print(json.dumps(out), flush=True)
 
 
-TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                            "traffic_llama2-7b_q4_0_matvec.md")
+TRAFFIC_FILES = {"sweep": "traffic_llama2-7b_sweep.md", "q4_0": "traffic_llama2-7b_q4_0_matvec.md"}
 
 
-def measured_traffic():
-    """HBM bytes per Q4_0 matvec launch from the committed FETCH_SIZE/WRITE_SIZE
-    counter runs (scaled by a copy kernel of known size), or None."""
+def measured_traffic(kernel_id):
+    """HBM bytes per launch of the dominant kernel from the committed
+    FETCH_SIZE/WRITE_SIZE counter runs (scaled by a copy kernel of known
+    size), or None."""
+    path = os.path.join(ROOT, "profiles", TRAFFIC_FILES[kernel_id])
     try:
-        for line in open(TRAFFIC_FILE):
+        for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
                 return int(line.split(":")[1])
     except OSError:
@@ -223,20 +228,26 @@ def profile_classes(m, n_steps):
     if L.ss_hip_profile_begin(hm) != 0:
         raise SlipStreamError("profile_begin failed")
     m.decode_greedy(n_steps)
-    out = np.zeros(12, np.float64)
-    if L.ss_hip_profile_end(hm, out.ctypes.data_as(C.POINTER(C.c_double)), 12) != 0:
+    out = np.zeros(15, np.float64)
+    if L.ss_hip_profile_end(hm, out.ctypes.data_as(C.POINTER(C.c_double)), 15) != 0:
         raise SlipStreamError("profile_end failed")
-    ms, cnt, byt = out[0], out[1], out[2]
+    if out[13] > 0:      # persistent launches: the whole token is the kernel
+        ms, cnt, byt = out[12], out[13], out[14]
+        kernel, kid = "k_sweep (whole token: embedding, all layers, LM head, argmax)", "sweep"
+    else:
+        ms, cnt, byt = out[0], out[1], out[2]
+        kernel, kid = "k_gemv Q4_0 (all epilogues)", "q4_0"
     if cnt <= 0:
-        raise SlipStreamError("no Q4_0 launches recorded")
+        raise SlipStreamError("no launches of the dominant kernel recorded")
     avg_s = ms / 1e3 / cnt
     ach = byt / cnt / avg_s / 1e9
     return {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
-            "kernel": "k_gemv Q4_0 (all epilogues)", "launches": int(cnt),
+            "kernel": kernel, "kernel_id": kid, "launches": int(cnt),
             "avg_us": round(avg_s * 1e6, 3), "bytes_per_launch": round(byt / cnt, 1),
             "classes_ms": {"q4_0_matvec": round(out[0], 3), "q8_0_matvec": round(out[3], 3),
-                           "attention": round(out[6], 3), "other": round(out[9], 3)},
+                           "attention": round(out[6], 3), "other": round(out[9], 3),
+                           "sweep": round(out[12], 3)},
             "profiled_steps": n_steps}
 
 

@@ -160,8 +160,14 @@ typedef struct {
     int32_t device;         /* HIP device ordinal, default 0 */
     uint32_t max_context;   /* 0 = config->context_size, else model default; no 512 cap */
     uint32_t streaming;     /* 0 = weights resident in HBM */
-    uint32_t use_graph;     /* 1 (default) = replay the per-token sweep as a HIP graph */
+    uint32_t launch;        /* SS_LAUNCH_* below, default SS_LAUNCH_GRAPH */
 } ss_model_ext_t;
+
+/* How a token is launched on the GPU. SWEEP: one persistent launch per
+ * token (fp16 KV; other cases use GRAPH). GRAPH: one kernel per step, the
+ * token's kernels replayed from a HIP graph. EAGER: one kernel per step,
+ * launched one by one. */
+enum { SS_LAUNCH_EAGER = 0, SS_LAUNCH_GRAPH = 1, SS_LAUNCH_SWEEP = 2 };
 
 ss_model_ext_t ss_default_ext(void);
 ss_model_t *ss_model_load_ex(const char *path, const ss_model_config_t *config,

@@ -43,6 +43,13 @@ typedef struct ss_hip_model ss_hip_model_t;
 #define SS_HIP_Q4_0 2
 #define SS_HIP_Q8_0 8
 
+/* token launch modes (match SS_LAUNCH_* in slipstream.h): per-kernel eager,
+ * per-kernel replayed from a HIP graph, or one persistent launch per token
+ * (fp16 KV cache; falls back to GRAPH for shapes it does not cover) */
+#define SS_HIP_LAUNCH_EAGER 0
+#define SS_HIP_LAUNCH_GRAPH 1
+#define SS_HIP_LAUNCH_SWEEP 2
+
 /* KV cache types (match ss_kv_type_t in slipstream.h) */
 #define SS_HIP_KV_F16 0
 #define SS_HIP_KV_INT8 1
@@ -157,7 +164,7 @@ typedef struct {
     int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, rope_dim, ffn, vocab, max_seq;
     float rms_eps, rope_theta;
     int32_t kv_type;     /* SS_HIP_KV_* */
-    int32_t use_graph;   /* replay the token sweep as one HIP graph */
+    int32_t launch;      /* SS_HIP_LAUNCH_* */
     ss_hip_tensor_t token_embd, output_norm, output;
     const ss_hip_tensor_t *layers;   /* n_layers * SS_HIP_LAYER_TENSORS */
 } ss_hip_model_desc_t;
@@ -185,10 +192,26 @@ int32_t ss_hip_hidden(ss_hip_model_t *m, float *host_out);
 void ss_hip_set_cancel_flag(ss_hip_model_t *m, const volatile int32_t *flag);
 /* bytes of device memory held by the model (weights, KV, buffers) */
 uint64_t ss_hip_model_bytes(const ss_hip_model_t *m);
+/* the launch mode in effect (SS_HIP_LAUNCH_*; SWEEP may have been
+ * replaced by GRAPH for a shape the persistent launch does not cover) */
+int32_t ss_hip_model_launch(const ss_hip_model_t *m);
+
+/* Phase timing of the persistent launch: with tracing on, every launch
+ * records per workgroup its start and, for each phase p = 0 .. 5L (layer l:
+ * 5l + 0 QKV, +1 attention, +2 Wo, +3 gate/up, +4 down; 5L the LM head),
+ * four 100 MHz wall-clock stamps: compute done, own results published, wait
+ * for the other workgroups done, next input staged. Layout per workgroup:
+ * 4 header words (word 0 = start), then 4 per phase. trace_read copies the
+ * last launch's stamps and returns the word count (workgroups = count /
+ * (4 + 4 * (5L + 1))). */
+int32_t ss_hip_trace_enable(ss_hip_model_t *m, int32_t on);
+int64_t ss_hip_trace_read(ss_hip_model_t *m, uint64_t *host, size_t n_words);
 
 /* ---- timing support for the benchmark ----
- * Records per-kernel-class device time (HIP events on the launching
- * stream) for the next eval calls; kinds: 0 = all matvecs, 1 = attention. */
+ * Records device time per launch class (HIP events on the launching stream)
+ * for the next eval calls: 0 = Q4_0 matvecs, 1 = Q8_0 matvecs, 2 =
+ * attention, 3 = other kernels, 4 = persistent token launches; per class
+ * three doubles (total ms, launches, algorithmic bytes), 15 in all. */
 int32_t ss_hip_profile_begin(ss_hip_model_t *m);
 int32_t ss_hip_profile_end(ss_hip_model_t *m, double *ms_out, int32_t n);
 

@@ -8,8 +8,10 @@
  * checkpoints that cannot be downloaded.
  *
  * Distributions: Q4_0 blocks have d = fp16(|N(0, scale_sigma)|) and uniform
- * random nibbles; Q8_0 blocks have d = fp16(|N(0, scale_sigma)|) and int8 codes
- * uniform in [-127, 127]; norm weights are fp32 1 + N(0, norm_sigma).
+ * random nibbles; Q8_0 blocks have d = fp16(|N(0, scale_sigma / 16)|) and int8
+ * codes uniform in [-127, 127] (the codes' spread is 16 times the nibbles', so
+ * both types give weights of the same spread); norm weights are fp32
+ * 1 + N(0, norm_sigma).
  * The bytes depend only on the spec (seed included), not on n_threads.
  */
 #ifndef SS_SYNTH_H

@@ -11,6 +11,7 @@ _u16p = C.POINTER(C.c_uint16)
 
 SS_BACKEND_AUTO, SS_BACKEND_CPU, SS_BACKEND_METAL, SS_BACKEND_HIP = 0, 1, 2, 3
 SS_KV_F16, SS_KV_INT8 = 0, 1
+LAUNCH = {"eager": 0, "graph": 1, "sweep": 2}   # SS_LAUNCH_*
 ERRORS = {0: "SS_OK", -1: "SS_ERROR_FILE_NOT_FOUND", -2: "SS_ERROR_INVALID_MODEL",
           -3: "SS_ERROR_OUT_OF_MEMORY", -4: "SS_ERROR_MMAP_FAILED", -5: "SS_ERROR_INVALID_PARAMS",
           -6: "SS_ERROR_CANCELLED", -7: "SS_ERROR_BACKEND", -8: "SS_ERROR_TOKENIZER", -99: "SS_ERROR_UNKNOWN"}
@@ -28,7 +29,7 @@ class GenerateParams(C.Structure):    # slipstream.h:98-106
 
 class ModelExt(C.Structure):
     _fields_ = [("kv_type", _i32), ("device", _i32), ("max_context", _u32), ("streaming", _u32),
-                ("use_graph", _u32)]
+                ("launch", _u32)]
 
 
 class ModelInfo(C.Structure):         # slipstream.h:65-79
@@ -141,7 +142,7 @@ def _ptr(a, t):
 class Model:
     """A loaded model on the HIP backend (ss_model_load_ex)."""
 
-    def __init__(self, path, max_context=0, kv="f16", device=0, use_graph=True, backend=SS_BACKEND_HIP):
+    def __init__(self, path, max_context=0, kv="f16", device=0, launch="graph", backend=SS_BACKEND_HIP):
         L = _lib()
         cfg = L.ss_default_config()
         cfg.backend = backend
@@ -149,7 +150,7 @@ class Model:
         ext.kv_type = SS_KV_F16 if kv == "f16" else SS_KV_INT8
         ext.device = device
         ext.max_context = max_context
-        ext.use_graph = 1 if use_graph else 0
+        ext.launch = LAUNCH[launch]
         self.h = L.ss_model_load_ex(path.encode(), C.byref(cfg), C.byref(ext))
         if not self.h:
             raise SlipStreamError("ss_model_load_ex(%s) failed: %s" % (path, ERRORS.get(L.ss_last_error())))

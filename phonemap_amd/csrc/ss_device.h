@@ -75,6 +75,42 @@ __device__ __forceinline__ void attn_chunks(int ctx, int ns, int& chunk, int& ac
   active = (ctx + chunk - 1) / chunk;
 }
 
+// Packed weight tiles: 16 rows x 4 blocks of 32 columns, one block chunk per
+// lane (layout documented in ss_gemv.hip).
+constexpr int kRowsPerTile = 16;
+constexpr int kBlocksPerTile = 4;
+constexpr int kTilesPerScaleGroup = 8;
+
+__device__ __forceinline__ size_t tile_idx(int g, int ntk, int t, int lane) {
+  return ((size_t)g * ntk + t) * kWave + lane;
+}
+
+// lane of a tile that holds block b of row r
+__device__ __forceinline__ int tile_lane(int r, int b) {
+  return (b % kBlocksPerTile) * kRowsPerTile + r % kRowsPerTile;
+}
+
+// binary16 index of the scale of (tile t, lane) of row group g: each lane's
+// scales of a unit of 8 tiles are 16 contiguous bytes
+__device__ __forceinline__ size_t scale_idx(int g, int ntk, int t, int lane) {
+  const int nu = (ntk + kTilesPerScaleGroup - 1) / kTilesPerScaleGroup;
+  return (((size_t)g * nu + t / kTilesPerScaleGroup) * kWave + lane) * kTilesPerScaleGroup +
+         t % kTilesPerScaleGroup;
+}
+
+__device__ __forceinline__ int sdot4(uint32_t a, int b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, b, c, false);
+}
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+
+__device__ __forceinline__ int q8c(float f) {   // round to nearest even, then clamp to int8
+  return (int)fminf(fmaxf(rintf(f), -127.f), 127.f);
+}
+
 template <int QT>
 struct QTraits;
 template <>

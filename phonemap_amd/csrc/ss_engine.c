@@ -77,7 +77,7 @@ ss_model_ext_t ss_default_ext(void) {
     ss_model_ext_t e;
     memset(&e, 0, sizeof(e));
     e.kv_type = SS_KV_F16;
-    e.use_graph = 1;
+    e.launch = SS_LAUNCH_GRAPH;
     return e;
 }
 
@@ -200,7 +200,7 @@ ss_model_t *ss_model_load_ex(const char *path, const ss_model_config_t *config,
     desc.rms_eps = g->rms_norm_eps;
     desc.rope_theta = g->rope_theta;
     desc.kv_type = m->ext.kv_type == SS_KV_INT8 ? SS_HIP_KV_INT8 : SS_HIP_KV_F16;
-    desc.use_graph = m->ext.use_graph ? 1 : 0;
+    desc.launch = (int32_t)m->ext.launch;
     fill_tensor(&desc.token_embd, g, ss_gguf_find(g, "token_embd.weight"));
     fill_tensor(&desc.output_norm, g, ss_gguf_find(g, "output_norm.weight"));
     fill_tensor(&desc.output, g, ss_gguf_find(g, "output.weight"));

@@ -37,10 +37,6 @@ namespace {
 // order), [24] 8 * sum_j X_j (the Q4_0 offset term), [25] s3 (fp32 bits).
 constexpr int kXW = 28;   // words per block (7 x 16 B)
 
-__device__ __forceinline__ int sdot4(uint32_t a, int b, int c) {
-  return __builtin_amdgcn_sdot4((int)a, b, c, false);
-}
-
 // Q4_0 block (quantize.c:60-72): byte j holds weight j (low nibble) and
 // weight j+16 (high nibble), value = d * (nibble - 8). Returns
 // sum_j (nibble_j - 8) * X_j exactly; the caller multiplies by d * s3. The -8
@@ -94,29 +90,6 @@ __device__ __forceinline__ float q8_block(const uint4 a, const uint4 b, const in
     if (l < 2) acc = s; else acc3 = s;
   }
   return fmaf((float)acc, 128.0f, (float)acc3);
-}
-
-__device__ __forceinline__ size_t tile_idx(int g, int ntk, int t, int lane) {
-  return ((size_t)g * ntk + t) * kWave + lane;
-}
-
-// lane of a tile that holds block b of row r
-__device__ __forceinline__ int tile_lane(int r, int b) { return (b % kTB) * kRG + r % kRG; }
-
-// binary16 index of the scale of (tile t, lane) of row group g: each lane's
-// scales of a unit of 8 tiles are 16 contiguous bytes
-__device__ __forceinline__ size_t scale_idx(int g, int ntk, int t, int lane) {
-  const int nu = (ntk + kUT - 1) / kUT;
-  return (((size_t)g * nu + t / kUT) * kWave + lane) * kUT + t % kUT;
-}
-
-template <int CTRL>
-__device__ __forceinline__ int dpp_i(int v) {
-  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
-}
-
-__device__ __forceinline__ int q8c(float f) {   // round to nearest even, then clamp to int8
-  return (int)fminf(fmaxf(rintf(f), -127.f), 127.f);
 }
 
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {

@@ -21,6 +21,7 @@
 #include <vector>
 
 #include "ss_kernels.h"
+#include "ss_sweep.h"
 
 namespace {
 
@@ -491,7 +492,7 @@ struct DevLayer {
   int t_qkv = 0, t_o = 0, t_gu = 0, t_d = 0;
 };
 
-enum ProfClass { PC_Q4 = 0, PC_Q8 = 1, PC_ATTN = 2, PC_OTHER = 3, PC_N = 4 };
+enum ProfClass { PC_Q4 = 0, PC_Q8 = 1, PC_ATTN = 2, PC_OTHER = 3, PC_SWEEP = 4, PC_N = 5 };
 
 struct ProfRec {
   int cls;
@@ -507,7 +508,7 @@ struct ss_hip_model {
   int qdim = 0, kvdim = 0, group = 0, ns = 0, embd_rows = 0;
   float eps = 1e-5f, theta = 10000.f;
   int kv_type = 0;
-  bool use_graph = true;
+  int launch = SS_HIP_LAUNCH_SWEEP;   // mode in effect
   std::vector<DevLayer> layers;
   void* embd = nullptr;
   int t_embd = 0;
@@ -541,6 +542,13 @@ struct ss_hip_model {
   std::vector<hipEvent_t> ev_pool;
   size_t ev_used = 0;
   std::vector<void*> allocs;
+  // persistent sweep (launch == SS_HIP_LAUNCH_SWEEP)
+  ssk::SweepArgs sw;                 // host copy of the argument block
+  ssk::SweepArgs* sw_dev = nullptr;  // device copy read by the kernel
+  int sw_type = 0;                   // layer matrix type
+  uint32_t sw_epoch = 0;             // flag value every workgroup holds between launches
+  double sw_bytes = 0;               // algorithmic bytes of one token at the last launch
+  uint64_t* sw_trace = nullptr;      // phase stamps of the last launch (when enabled)
 };
 
 namespace {
@@ -640,11 +648,142 @@ hipError_t timed(ss_hip_model* m, int cls, double bytes, F&& launch) {
 
 int q_class(int type) { return type == SS_HIP_Q4_0 ? PC_Q4 : PC_Q8; }
 
+// Algorithmic HBM bytes of one token at context ctx: every weight byte once
+// (GGUF block sizes), the fp16 K/V read and appended, the norm weights.
+double token_bytes(const ss_hip_model* m, int ctx, bool with_head) {
+  double b = 0;
+  for (const DevLayer& ly : m->layers) {
+    b += matvec_bytes(ly.t_qkv, m->qdim + 2 * m->kvdim, m->d, 1) + matvec_bytes(ly.t_o, m->d, m->qdim, 1) +
+         matvec_bytes(ly.t_gu, m->ffn, m->d, 2) + matvec_bytes(ly.t_d, m->d, m->ffn, 1);
+    b += 2.0 * 2 * ((double)ctx * m->kvdim + m->kvdim) + 2.0 * 4 * m->d;
+  }
+  if (with_head) b += matvec_bytes(m->t_out, m->vocab, m->d, 1) + 4.0 * m->d;
+  b += (double)m->d / 32 * gguf_block_bytes(m->t_embd);
+  return b;
+}
+
+// One persistent launch per token when the shape allows it: fp16 KV, one
+// quantisation type for all layer matrices, a supported head shape, and the
+// workgroups (one per compute unit) co-resident. Otherwise the model keeps
+// the per-kernel launches (graph mode).
+int32_t sweep_setup(ss_hip_model* m) {
+  if (m->kv_type != SS_HIP_KV_F16) return 1;
+  const int lt = m->layers[0].t_qkv;
+  for (const DevLayer& ly : m->layers)
+    if (ly.t_qkv != lt || ly.t_o != lt || ly.t_gu != lt || ly.t_d != lt) return 1;
+  if (!ssk::sweep_supported(m->hd, m->group, lt, m->t_out)) return 1;
+  int nwg = m->ctx->n_cu < ssk::kSweepMaxWg ? m->ctx->n_cu : ssk::kSweepMaxWg;
+  if (m->KVH > nwg) return 1;
+  ssk::SweepArgs& a = m->sw;
+  memset(&a, 0, sizeof(a));
+  a.embd = view(m->embd, m->t_embd, m->embd_rows, m->d);
+  a.out = view(m->out, m->t_out, m->out == m->embd ? m->embd_rows : m->vocab, m->d);
+  a.embd_type = m->t_embd;
+  a.out_norm = m->out_norm;
+  a.rope_cs = m->rope_cs;
+  a.n_layers = m->L;
+  a.d = m->d;
+  a.qdim = m->qdim;
+  a.kvdim = m->kvdim;
+  a.ffn = m->ffn;
+  a.vocab = m->vocab;
+  a.max_seq = m->max_seq;
+  a.rope_dim = m->rope_dim;
+  a.n_kv_heads = m->KVH;
+  a.eps = m->eps;
+  a.attn_scale = 1.0f / sqrtf((float)m->hd);
+  a.timeout_ticks = 200000000ull;   // 2 s at the 100 MHz s_memrealtime clock
+  size_t lds = 0;
+  for (;;) {   // the shared-memory plan depends on the workgroup count
+    a.nwg = nwg;
+    a.ns = nwg / m->KVH;
+    lds = ssk::sweep_lds_bytes(a, m->hd, m->group);
+    if (lds > 160 * 1024) return 1;
+    int max_wg = 0;
+    HIP_TRY(ssk::sweep_max_workgroups(m->hd, m->group, lt, m->t_out, lds, &max_wg));
+    if (max_wg >= nwg) break;
+    if (max_wg < m->KVH || max_wg < 1) return 1;
+    nwg = max_wg;
+  }
+  std::vector<ssk::SweepLayer> ls(m->L);
+  for (int l = 0; l < m->L; l++) {
+    const DevLayer& ly = m->layers[l];
+    ssk::SweepLayer& s = ls[l];
+    s.qkv = view(ly.wqkv, lt, m->qdim + 2 * m->kvdim, m->d);
+    s.o = view(ly.wo, lt, m->d, m->qdim);
+    s.gate = view(ly.wg, lt, m->ffn, m->d);
+    s.up = view(ly.wu, lt, m->ffn, m->d);
+    s.down = view(ly.wd, lt, m->d, m->ffn);
+    s.attn_norm = ly.attn_norm;
+    s.ffn_norm = ly.ffn_norm;
+    s.kc = reinterpret_cast<uint16_t*>(static_cast<char*>(m->kc) + (size_t)l * m->kv_layer_elems * 2);
+    s.vc = reinterpret_cast<uint16_t*>(static_cast<char*>(m->vc) + (size_t)l * m->kv_layer_elems * 2);
+  }
+  void* layers = nullptr;
+  if (int32_t rc = m_alloc(m, &layers, sizeof(ssk::SweepLayer) * m->L, false)) return rc;
+  HIP_TRY(hipMemcpy(layers, ls.data(), sizeof(ssk::SweepLayer) * m->L, hipMemcpyHostToDevice));
+  a.layers = static_cast<const ssk::SweepLayer*>(layers);
+  a.tokens = m->tokens;
+  a.dpos = m->dpos;
+  a.argmax = m->argmax;
+  a.hidden = m->hidden;
+  a.logits = m->logits;
+  const size_t rec = 64;   // bytes per x record of 16 values
+  const size_t L = (size_t)m->L;
+  if (int32_t rc = m_alloc(m, (void**)&a.hrec, rec * (m->d / 16) * 2 * L)) return rc;
+  if (int32_t rc = m_alloc(m, (void**)&a.frec, rec * (m->ffn / 16) * L)) return rc;
+  if (int32_t rc = m_alloc(m, (void**)&a.arec, rec * (m->qdim / 16) * L)) return rc;
+  if (int32_t rc = m_alloc(m, (void**)&a.q, sizeof(float) * m->qdim * L)) return rc;
+  if (int32_t rc = m_alloc(m, (void**)&a.part, sizeof(float) * (size_t)m->KVH * a.ns * m->group * (m->hd + 2) * L))
+    return rc;
+  if (int32_t rc = m_alloc(m, (void**)&a.att_cnt, sizeof(uint32_t) * (size_t)m->L * m->KVH)) return rc;
+  if (int32_t rc = m_alloc(m, (void**)&a.cand, sizeof(float2) * nwg)) return rc;
+  if (int32_t rc = m_alloc(m, (void**)&a.flags, sizeof(uint32_t) * ssk::kSweepFlagWords)) return rc;
+  if (int32_t rc = m_alloc(m, (void**)&m->sw_dev, sizeof(ssk::SweepArgs), false)) return rc;
+  HIP_TRY(hipMemcpy(m->sw_dev, &a, sizeof(a), hipMemcpyHostToDevice));
+  m->sw_type = lt;
+  m->sw_epoch = 0;
+  m->launch = SS_HIP_LAUNCH_SWEEP;
+  return 0;
+}
+
+// Zero the progress flags and split counters (after a launch gave up, or a reset).
+int32_t sweep_clear(ss_hip_model* m) {
+  hipStream_t s = m->ctx->stream;
+  HIP_TRY(hipMemsetAsync(m->sw.flags, 0, sizeof(uint32_t) * ssk::kSweepFlagWords, s));
+  HIP_TRY(hipMemsetAsync(m->sw.att_cnt, 0, sizeof(uint32_t) * (size_t)m->L * m->KVH, s));
+  m->sw_epoch = 0;
+  return 0;
+}
+
+// After the stream has been synchronised: did a launch give up waiting?
+int32_t sweep_check(ss_hip_model* m) {
+  if (m->launch != SS_HIP_LAUNCH_SWEEP) return 0;
+  uint32_t w[2] = {0, 0};
+  HIP_TRY(hipMemcpy(w, m->sw.flags + ssk::kSweepAbort, sizeof(w), hipMemcpyDeviceToHost));
+  if (!w[0]) return 0;
+  sweep_clear(m);
+  hipStreamSynchronize(m->ctx->stream);
+  m->host_pos = -1;
+  return fail(kErrBackend, "token launch abandoned: workgroup %u timed out waiting in phase %u",
+              w[1] & 0xffffu, w[1] >> 16);
+}
+
 // Enqueue one token on the model stream. The token is tokens[*dpos]. With
 // the head, the last workgroup of the LM-head matvec writes the argmax to
 // tokens[*dpos + 1] and advances *dpos; without it, k_advance does.
 int32_t enqueue_token(ss_hip_model* m, bool with_head) {
   hipStream_t s = m->ctx->stream;
+  if (m->launch == SS_HIP_LAUNCH_SWEEP) {
+    ssk::SweepLaunch sl;
+    sl.args = m->sw_dev;
+    sl.epoch0 = m->sw_epoch;
+    sl.with_head = with_head ? 1 : 0;
+    HIP_TRY(timed(m, PC_SWEEP, m->sw_bytes,
+                  [&] { return ssk::launch_sweep(m->sw, sl, m->hd, m->group, m->sw_type, m->t_out, s); }));
+    m->sw_epoch += (uint32_t)ssk::sweep_phases(m->L, with_head);
+    return 0;
+  }
   const int nbd = m->d / 32;
   HIP_TRY(timed(m, PC_OTHER, 0, [&] {
     return ssk::launch_embed(m->t_embd, view(m->embd, m->t_embd, m->embd_rows, m->d), m->d,
@@ -766,8 +905,10 @@ int32_t capture(ss_hip_model* m, bool with_head, hipGraphExec_t* out) {
   return 0;
 }
 
-int32_t run_token(ss_hip_model* m, bool with_head) {
-  if (m->use_graph && !m->prof) {
+// pos: the position of the token (sizes the profiled byte count only)
+int32_t run_token(ss_hip_model* m, bool with_head, int pos) {
+  if (m->prof) m->sw_bytes = token_bytes(m, pos + 1, with_head);
+  if (m->launch == SS_HIP_LAUNCH_GRAPH && !m->prof) {
     HIP_TRY(hipGraphLaunch(with_head ? m->g_full : m->g_nohead, m->ctx->stream));
     return 0;
   }
@@ -826,7 +967,7 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
   m->eps = d->rms_eps;
   m->theta = d->rope_theta;
   m->kv_type = d->kv_type;
-  m->use_graph = d->use_graph != 0;
+  m->launch = d->launch == SS_HIP_LAUNCH_EAGER ? SS_HIP_LAUNCH_EAGER : SS_HIP_LAUNCH_GRAPH;
   m->qdim = m->H * m->hd;
   m->kvdim = m->KVH * m->hd;
   m->group = group;
@@ -934,13 +1075,42 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
     fail(kErrBackend, "model upload failed");
     return bail();
   }
-  if (m->use_graph && (capture(m, true, &m->g_full) || capture(m, false, &m->g_nohead))) return bail();
+  if (d->launch == SS_HIP_LAUNCH_SWEEP && sweep_setup(m) < 0) return bail();
+  if (m->launch == SS_HIP_LAUNCH_GRAPH && (capture(m, true, &m->g_full) || capture(m, false, &m->g_nohead)))
+    return bail();
   return m;
 }
 
 void ss_hip_model_free(ss_hip_model_t* m) { model_release(m); }
 
 uint64_t ss_hip_model_bytes(const ss_hip_model_t* m) { return m ? m->bytes : 0; }
+
+int32_t ss_hip_model_launch(const ss_hip_model_t* m) { return m ? m->launch : -1; }
+
+int32_t ss_hip_trace_enable(ss_hip_model_t* m, int32_t on) {
+  if (!m) return fail(kErrParams, "null model");
+  if (m->launch != SS_HIP_LAUNCH_SWEEP) return fail(kErrParams, "trace: the model does not use the persistent launch");
+  if (set_device(m->ctx)) return kErrBackend;
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  if (on && !m->sw_trace) {
+    const size_t bytes = sizeof(uint64_t) * ssk::sweep_trace_words(m->L, m->sw.nwg);
+    if (int32_t rc = m_alloc(m, (void**)&m->sw_trace, bytes)) return rc;
+  }
+  m->sw.trace = on ? m->sw_trace : nullptr;
+  HIP_TRY(hipMemcpy(m->sw_dev, &m->sw, sizeof(m->sw), hipMemcpyHostToDevice));
+  return 0;
+}
+
+int64_t ss_hip_trace_read(ss_hip_model_t* m, uint64_t* host, size_t n_words) {
+  if (!m || !host) return fail(kErrParams, "trace: bad argument");
+  if (!m->sw_trace) return fail(kErrParams, "trace: not enabled");
+  if (set_device(m->ctx)) return kErrBackend;
+  size_t n = ssk::sweep_trace_words(m->L, m->sw.nwg);
+  if (n > n_words) n = n_words;
+  HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+  HIP_TRY(hipMemcpy(host, m->sw_trace, sizeof(uint64_t) * n, hipMemcpyDeviceToHost));
+  return (int64_t)n;
+}
 
 void ss_hip_set_cancel_flag(ss_hip_model_t* m, const volatile int32_t* flag) {
   if (m) m->cancel = flag;
@@ -952,6 +1122,7 @@ static int32_t finish_eval(ss_hip_model_t* m, float* logits_host, int32_t* argma
   if (logits_host)
     HIP_TRY(hipMemcpyAsync(logits_host, m->logits, sizeof(float) * m->vocab, hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
+  if (int32_t rc = sweep_check(m)) return rc;
   if (argmax_out) *argmax_out = m->h_io[0];
   return 0;
 }
@@ -964,7 +1135,7 @@ int32_t ss_hip_eval_token(ss_hip_model_t* m, int32_t token, int32_t pos, float* 
   if (set_device(m->ctx)) return kErrBackend;
   if (m->cancel && *m->cancel) return fail(kErrCancel, "cancelled");
   HIP_TRY(ssk::launch_set_state(m->dpos, m->tokens, pos, token, m->ctx->stream));
-  if (int32_t rc = run_token(m, true)) return rc;
+  if (int32_t rc = run_token(m, true, pos)) return rc;
   m->host_pos = pos;
   return finish_eval(m, logits_host, argmax_out);
 }
@@ -987,7 +1158,7 @@ int32_t ss_hip_eval_prompt(ss_hip_model_t* m, const int32_t* tokens, int32_t n, 
       hipStreamSynchronize(s);
       return fail(kErrCancel, "cancelled");
     }
-    if (int32_t rc = run_token(m, i == n - 1)) return rc;
+    if (int32_t rc = run_token(m, i == n - 1, start + i)) return rc;
   }
   m->host_pos = start + n - 1;
   return finish_eval(m, logits_host, argmax_out);
@@ -1007,7 +1178,7 @@ int32_t ss_hip_decode_greedy(ss_hip_model_t* m, int32_t n_steps, int32_t* tokens
       hipStreamSynchronize(s);
       return fail(kErrCancel, "cancelled");
     }
-    if (int32_t rc = run_token(m, true)) return rc;
+    if (int32_t rc = run_token(m, true, m->host_pos + 1 + i)) return rc;
   }
   const int p0 = m->host_pos;
   m->host_pos += n_steps;
@@ -1015,7 +1186,7 @@ int32_t ss_hip_decode_greedy(ss_hip_model_t* m, int32_t n_steps, int32_t* tokens
     HIP_TRY(hipMemcpyAsync(tokens_out, m->tokens + p0 + 2, sizeof(int) * n_steps,
                            hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
-  return 0;
+  return sweep_check(m);
 }
 
 int32_t ss_hip_kv_reset(ss_hip_model_t* m) {

@@ -154,9 +154,11 @@ static void gen_item(job_t *j, uint64_t it, uint8_t *buf) {
         uint64_t nb = tensor_blocks(t), b0 = chunk * CHUNK_BLOCKS;
         uint64_t b1 = b0 + CHUNK_BLOCKS < nb ? b0 + CHUNK_BLOCKS : nb;
         size_t bb = t->type == T_Q4_0 ? 18 : 34;
+        /* int8 codes spread 16 times as wide as nibbles: same weight spread */
+        const double sigma = t->type == T_Q4_0 ? j->scale_sigma : j->scale_sigma / 16.0;
         for (uint64_t b = b0; b < b1; b++) {
             uint8_t *p = buf + (b - b0) * bb;
-            uint16_t d = to_f16((float)fabs(j->scale_sigma * xo_normal(&x)));
+            uint16_t d = to_f16((float)fabs(sigma * xo_normal(&x)));
             memcpy(p, &d, 2);
             if (t->type == T_Q4_0) {
                 uint64_t r0 = xo_next(&x), r1 = xo_next(&x);

@@ -37,7 +37,7 @@ def _declared_functions(header):
     return names
 
 
-@pytest.mark.parametrize("header,count", [("slipstream.h", 36), ("ss_hip.h", 38), ("ss_synth.h", 2)])
+@pytest.mark.parametrize("header,count", [("slipstream.h", 36), ("ss_hip.h", 41), ("ss_synth.h", 2)])
 def test_library_exports_every_declared_function(header, count):
     names = _declared_functions(header)
     assert len(names) == count, sorted(names)
@@ -266,8 +266,15 @@ def test_synthetic_weights_follow_spec(tmp_path):
     assert set(np.unique(nib)) == set(range(16))
     name, dims, typ, o = info["output.weight"]
     n = dims[0] * dims[1] // 32
-    q8 = np.frombuffer(raw, np.uint8, n * 34, off + o).reshape(n, 34)[:, 2:].view(np.int8)
+    blk8 = np.frombuffer(raw, np.uint8, n * 34, off + o).reshape(n, 34)
+    q8 = blk8[:, 2:].view(np.int8)
     assert q8.min() >= -127 and q8.max() == 127
+    d8 = blk8[:, :2].copy().view(np.float16).astype(np.float32).ravel()
+    assert (d8 >= 0).all() and 0.005 / 16 < float(d8.mean()) < 0.05 / 16   # |N(0, 0.02 / 16)|
+    # equal weight spread for both types: sigma * std(nibble - 8) vs sigma / 16 * std(code)
+    w4 = d[:, None] * (np.concatenate([blk[:, 2:] & 15, blk[:, 2:] >> 4], axis=1).astype(np.float32) - 8)
+    w8 = d8[:, None] * q8.astype(np.float32)
+    assert 0.8 < float(w8.std()) / float(w4.std()) < 1.25
     name, dims, typ, o = info["blk.1.attn_norm.weight"]
     w = np.frombuffer(raw, np.float32, dims[0], off + o)
     assert abs(float(w.mean()) - 1.0) < 0.01 and 0.003 < float(w.std()) < 0.03

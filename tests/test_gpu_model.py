@@ -1,5 +1,7 @@
 """End-to-end decode parity: the HIP token loop (through the public C API)
-against the CPU oracle on the same synthetic GGUF files.
+against the CPU oracle on the same synthetic GGUF files, for each launch
+mode: the persistent one-launch-per-token sweep (fp16 KV), and the
+per-kernel launches replayed from a HIP graph or launched eagerly.
 
 Bar: identical greedy tokens; per-step logits within
 max |gpu - oracle| / max |oracle| <= 1e-3 (fp32 accumulation on both sides).
@@ -42,19 +44,27 @@ TINYLLAMA = dict(n_layers=22, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=64
                  context_length=2048, seed=1001)
 
 
+def _launch_in_effect(m):
+    L = api._lib()
+    return L.ss_hip_model_launch(L.ss_model_hip(m.h))
+
+
 @pytest.mark.parametrize("kv", ["f16", "int8"])
 @pytest.mark.parametrize("spec", ["tiny", "tiny_q8", "gqa8"])
-@pytest.mark.parametrize("graph", [True, False])
-def test_greedy_and_logits(spec, kv, graph):
+@pytest.mark.parametrize("launch", ["sweep", "graph", "eager"])
+def test_greedy_and_logits(spec, kv, launch):
     kw = {"tiny": TINY, "tiny_q8": TINY_Q8, "gqa8": GQA8}[spec]
     path = _model_file(spec, **kw)
-    print("model", spec, kv, graph, flush=True)
+    print("model", spec, kv, launch, flush=True)
     rng = np.random.default_rng(7)
     prompt = rng.integers(3, kw["vocab"], 12).tolist()
     steps = 24
     om = oracle.Model(path, 128, kv)
     tol = TOL if kv == "f16" else TOL_INT8
-    with api.Model(path, max_context=128, kv=kv, use_graph=graph) as m:
+    with api.Model(path, max_context=128, kv=kv, launch=launch) as m:
+        # the persistent sweep covers the fp16 cache; int8 runs per kernel
+        want = api.LAUNCH["graph"] if launch == "sweep" and kv == "int8" else api.LAUNCH[launch]
+        assert _launch_in_effect(m) == want
         lg, am = m.eval_prompt(prompt, 0)
         olg = om.prefill(prompt, 0)
         assert rel_err(lg, olg) <= tol
