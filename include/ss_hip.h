@@ -165,6 +165,11 @@ typedef struct {
     float rms_eps, rope_theta;
     int32_t kv_type;     /* SS_HIP_KV_* */
     int32_t launch;      /* SS_HIP_LAUNCH_* */
+    int32_t streaming;   /* nonzero: the layer matrices stay in pinned host
+                          * memory and each layer is uploaded (hipMemcpyAsync,
+                          * side stream) into a ring of device slots while the
+                          * previous layers compute; prompts run layer-major.
+                          * Launches are then per kernel (EAGER). */
     ss_hip_tensor_t token_embd, output_norm, output;
     const ss_hip_tensor_t *layers;   /* n_layers * SS_HIP_LAYER_TENSORS */
 } ss_hip_model_desc_t;
@@ -192,6 +197,8 @@ int32_t ss_hip_hidden(ss_hip_model_t *m, float *host_out);
 void ss_hip_set_cancel_flag(ss_hip_model_t *m, const volatile int32_t *flag);
 /* bytes of device memory held by the model (weights, KV, buffers) */
 uint64_t ss_hip_model_bytes(const ss_hip_model_t *m);
+/* bytes of pinned host memory held by the model (streaming mode weights) */
+uint64_t ss_hip_model_host_bytes(const ss_hip_model_t *m);
 /* the launch mode in effect (SS_HIP_LAUNCH_*; SWEEP may have been
  * replaced by GRAPH for a shape the persistent launch does not cover) */
 int32_t ss_hip_model_launch(const ss_hip_model_t *m);

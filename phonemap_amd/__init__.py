@@ -62,6 +62,7 @@ _PROTOS = {
     "ss_hip_hidden": (_i32, [_vp, _fp]),
     "ss_hip_set_cancel_flag": (None, [_vp, _ip]),
     "ss_hip_model_bytes": (_u64, [_vp]),
+    "ss_hip_model_host_bytes": (_u64, [_vp]),
     "ss_hip_model_launch": (_i32, [_vp]),
     "ss_hip_trace_enable": (_i32, [_vp, _i32]),
     "ss_hip_trace_read": (C.c_int64, [_vp, C.POINTER(C.c_uint64), _sz]),

@@ -142,7 +142,8 @@ def _ptr(a, t):
 class Model:
     """A loaded model on the HIP backend (ss_model_load_ex)."""
 
-    def __init__(self, path, max_context=0, kv="f16", device=0, launch="graph", backend=SS_BACKEND_HIP):
+    def __init__(self, path, max_context=0, kv="f16", device=0, launch="graph", backend=SS_BACKEND_HIP,
+                 streaming=False):
         L = _lib()
         cfg = L.ss_default_config()
         cfg.backend = backend
@@ -151,6 +152,7 @@ class Model:
         ext.device = device
         ext.max_context = max_context
         ext.launch = LAUNCH[launch]
+        ext.streaming = 1 if streaming else 0
         self.h = L.ss_model_load_ex(path.encode(), C.byref(cfg), C.byref(ext))
         if not self.h:
             raise SlipStreamError("ss_model_load_ex(%s) failed: %s" % (path, ERRORS.get(L.ss_last_error())))

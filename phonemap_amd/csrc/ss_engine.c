@@ -201,6 +201,7 @@ ss_model_t *ss_model_load_ex(const char *path, const ss_model_config_t *config,
     desc.rope_theta = g->rope_theta;
     desc.kv_type = m->ext.kv_type == SS_KV_INT8 ? SS_HIP_KV_INT8 : SS_HIP_KV_F16;
     desc.launch = (int32_t)m->ext.launch;
+    desc.streaming = m->ext.streaming ? 1 : 0;
     fill_tensor(&desc.token_embd, g, ss_gguf_find(g, "token_embd.weight"));
     fill_tensor(&desc.output_norm, g, ss_gguf_find(g, "output_norm.weight"));
     fill_tensor(&desc.output, g, ss_gguf_find(g, "output.weight"));

@@ -549,6 +549,20 @@ struct ss_hip_model {
   uint32_t sw_epoch = 0;             // flag value every workgroup holds between launches
   double sw_bytes = 0;               // algorithmic bytes of one token at the last launch
   uint64_t* sw_trace = nullptr;      // phase stamps of the last launch (when enabled)
+  // streaming mode: the layer matrices stay in pinned host memory and are
+  // uploaded into a ring of device slots as the layers are evaluated
+  bool streaming = false;
+  int n_slots = 0;
+  std::vector<void*> host_layers;    // pinned, one packed block per layer
+  std::vector<size_t> layer_size;    // bytes of each block
+  std::vector<size_t> layer_off;     // [L][5] offsets of [Wq;Wk;Wv], Wo, gate, up, down in a block
+  std::vector<void*> slots;          // device slots (largest block each)
+  std::vector<hipEvent_t> ev_ready, ev_free;
+  hipStream_t copy_stream = nullptr;
+  uint64_t up_issued = 0, up_used = 0;   // uploads issued / consumed
+  uint64_t host_bytes = 0;           // pinned bytes held
+  int* pos_iota = nullptr;           // device [max_seq]: value i at index i
+  float* hid_all = nullptr;          // device [max_seq][d]: residual streams of a prompt
 };
 
 namespace {
@@ -600,8 +614,9 @@ int32_t upload_vec(ss_hip_model* m, float** dst, const ss_hip_tensor_t& t, int n
   return 0;
 }
 
+// into: null to allocate the packed matrix, else a zeroed device buffer to pack into
 int32_t upload_mat(ss_hip_model* m, void** dst, const ss_hip_tensor_t* parts, int nparts, int rows_expect_total,
-                   int cols, int* type_out, const char* what) {
+                   int cols, int* type_out, const char* what, void* into = nullptr) {
   int type = parts[0].type;
   int64_t total = 0;
   for (int i = 0; i < nparts; i++) {
@@ -615,7 +630,10 @@ int32_t upload_mat(ss_hip_model* m, void** dst, const ss_hip_tensor_t* parts, in
   if (total != rows_expect_total) return fail(kErrParams, "model: %s has %lld rows, %d expected", what, (long long)total, rows_expect_total);
   if (cols % 32) return fail(kErrParams, "model: %s columns %d not a multiple of 32", what, cols);
   // zero-filled: rows are padded to a multiple of 64 with zero codes and scales
-  if (int32_t rc = m_alloc(m, dst, ss_hip_packed_bytes(type, (int)total, cols), true)) return rc;
+  if (into)
+    *dst = into;
+  else if (int32_t rc = m_alloc(m, dst, ss_hip_packed_bytes(type, (int)total, cols), true))
+    return rc;
   int64_t off = 0;
   for (int i = 0; i < nparts; i++) {
     if (int32_t rc = pack_rows(m->ctx, *dst, total, off, parts[i].data, type, parts[i].rows, cols)) return rc;
@@ -769,6 +787,166 @@ int32_t sweep_check(ss_hip_model* m) {
               w[1] & 0xffffu, w[1] >> 16);
 }
 
+// Token embedding of tokens[*dpos] into hidden (layer_scheduler.c:578-595).
+int32_t enqueue_embed(ss_hip_model* m, const int* dpos, float* hidden) {
+  hipStream_t s = m->ctx->stream;
+  HIP_TRY(timed(m, PC_OTHER, 0, [&] {
+    return ssk::launch_embed(m->t_embd, view(m->embd, m->t_embd, m->embd_rows, m->d), m->d, m->tokens,
+                             dpos, 0, hidden, s);
+  }));
+  return 0;
+}
+
+// One decoder layer (process_layer, layer_scheduler.c:291-567) for the token
+// at position *dpos whose residual stream is hidden; ly holds the layer's
+// weights (resident, or the streaming slot it was uploaded to).
+int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden, const int* dpos) {
+  hipStream_t s = m->ctx->stream;
+  int* dp = const_cast<int*>(dpos);
+  char* kc = static_cast<char*>(m->kc) + (size_t)l * m->kv_layer_elems * (m->kv_type ? 1 : 2);
+  char* vc = static_cast<char*>(m->vc) + (size_t)l * m->kv_layer_elems * (m->kv_type ? 1 : 2);
+  float* ksl = m->ks ? m->ks + (size_t)l * m->max_seq : nullptr;
+  float* vsl = m->vs ? m->vs + (size_t)l * m->max_seq : nullptr;
+
+  // 1. rmsnorm(attn_norm) -> [Wq;Wk;Wv] -> RoPE -> KV append   (layer_scheduler.c:320-413)
+  ssk::GemvArgs a = gemv_args(ly.wqkv, hidden, m->q, m->qdim + 2 * m->kvdim, m->d, ly.t_qkv);
+  a.nw = ly.attn_norm;
+  a.eps = m->eps;
+  a.qdim = m->qdim;
+  a.kvdim = m->kvdim;
+  a.head_dim = m->hd;
+  a.rope_dim = m->rope_dim;
+  a.max_seq = m->max_seq;
+  a.kv_type = m->kv_type;
+  a.rope_cs = m->rope_cs;
+  a.dpos = dp;
+  a.kcache = kc;
+  a.vcache = vc;
+  a.kv_f32 = m->kv_f32;
+  HIP_TRY(timed(m, q_class(ly.t_qkv), matvec_bytes(ly.t_qkv, a.rows, m->d, 1),
+                [&] { return ssk::launch_gemv(ssk::EPI_QKV, a, s); }));
+  if (m->kv_type == 1)
+    HIP_TRY(timed(m, PC_OTHER, 0, [&] {
+      return ssk::launch_kv_append(kc, vc, ksl, vsl, m->kv_f32, m->kv_f32 + m->kvdim, m->KVH, m->hd,
+                                   m->max_seq, dp, 0, 1, s);
+    }));
+
+  // 2. attention over positions 0..pos                          (:415-468)
+  ssk::AttnArgs at;
+  memset(&at, 0, sizeof(at));
+  at.q = m->q;
+  at.kc = kc;
+  at.vc = vc;
+  at.ks = ksl;
+  at.vs = vsl;
+  at.dpos = dp;
+  at.max_seq = m->max_seq;
+  at.ns = m->ns;
+  at.n_kv_heads = m->KVH;
+  at.scale = 1.0f / sqrtf((float)m->hd);
+  at.out = m->attn;
+  at.part_o = m->att_o;
+  at.part_ml = m->att_ml;
+  // with few splits the Wo matvec merges them itself (no merge launch)
+  const bool fused = m->ns <= ssk::kMergeSplits;
+  HIP_TRY(timed(m, PC_ATTN, 0, [&] { return ssk::launch_attention(m->hd, m->group, m->kv_type, at, !fused, s); }));
+
+  // 3. hidden += Wo attn                                         (:470-484)
+  ssk::GemvArgs o = gemv_args(ly.wo, m->attn, hidden, m->d, m->qdim, ly.t_o);
+  if (fused) {
+    o.att_o = m->att_o;
+    o.att_ml = m->att_ml;
+    o.att_ns = m->ns;
+    o.att_group = m->group;
+    o.head_dim = m->hd;
+    o.dpos = dp;
+  }
+  HIP_TRY(timed(m, q_class(ly.t_o), matvec_bytes(ly.t_o, m->d, m->qdim, 1),
+                [&] { return ssk::launch_gemv(ssk::EPI_ADD, o, s); }));
+
+  // 4. rmsnorm(ffn_norm) -> gate, up -> silu(gate) * up           (:486-550)
+  ssk::GemvArgs gu = gemv_args(ly.wg, hidden, m->ffn_act, m->ffn, m->d, ly.t_gu);
+  gu.w2 = view(ly.wu, ly.t_gu, m->ffn, m->d);
+  gu.nw = ly.ffn_norm;
+  gu.eps = m->eps;
+  HIP_TRY(timed(m, q_class(ly.t_gu), matvec_bytes(ly.t_gu, m->ffn, m->d, 2),
+                [&] { return ssk::launch_gemv(ssk::EPI_SWIGLU, gu, s); }));
+
+  // 5. hidden += Wdown act                                       (:552-566)
+  ssk::GemvArgs dn = gemv_args(ly.wd, m->ffn_act, hidden, m->d, m->ffn, ly.t_d);
+  HIP_TRY(timed(m, q_class(ly.t_d), matvec_bytes(ly.t_d, m->d, m->ffn, 1),
+                [&] { return ssk::launch_gemv(ssk::EPI_ADD, dn, s); }));
+  return 0;
+}
+
+// output_norm + LM head + first-max argmax (:634-662, tensor.c:318-328) of the
+// token at *m->dpos: the winner goes to tokens[pos + 1] and pos advances.
+int32_t enqueue_head(ss_hip_model* m, const float* hidden) {
+  hipStream_t s = m->ctx->stream;
+  ssk::GemvArgs h = gemv_args(m->out, hidden, m->logits, m->vocab, m->d, m->t_out);
+  h.nw = m->out_norm;
+  h.eps = m->eps;
+  h.part = m->lm_part;
+  HIP_TRY(timed(m, q_class(m->t_out), matvec_bytes(m->t_out, m->vocab, m->d, 1),
+                [&] { return ssk::launch_gemv(ssk::EPI_LOGITS, h, s); }));
+  HIP_TRY(timed(m, PC_OTHER, 0, [&] {
+    return ssk::launch_argmax_merge(m->lm_part, m->lm_grid, m->logits, m->argmax, m->tokens, m->dpos, s);
+  }));
+  return 0;
+}
+
+// ---- streaming mode (layer_scheduler.c:608-616 prefetch, gguf_loader.c:494-507)
+// Layer uploads form one sequence over tokens: upload k carries layer k % L
+// into slot k % n_slots. Upload k starts on the copy stream once the layer
+// that last used its slot has been computed (ev_free), and the compute
+// stream waits for it (ev_ready) before the layer's kernels; up to n_slots
+// uploads are in flight, so the next layers (and the first layers of the
+// next token) copy while the current layer computes.
+int32_t stream_issue(ss_hip_model* m) {
+  const uint64_t k = m->up_issued;
+  const int slot = (int)(k % (uint64_t)m->n_slots), l = (int)(k % (uint64_t)m->L);
+  HIP_TRY(hipStreamWaitEvent(m->copy_stream, m->ev_free[slot], 0));
+  HIP_TRY(hipMemcpyAsync(m->slots[slot], m->host_layers[l], m->layer_size[l], hipMemcpyHostToDevice,
+                         m->copy_stream));
+  HIP_TRY(hipEventRecord(m->ev_ready[slot], m->copy_stream));
+  m->up_issued++;
+  return 0;
+}
+
+// The weights of layer l for the next kernels on the model stream.
+int32_t stream_acquire(ss_hip_model* m, int l, DevLayer* out) {
+  if (m->up_used % (uint64_t)m->L != (uint64_t)l) {
+    // an evaluation stopped part way (cancel, error): drain both streams and
+    // restart the upload sequence at this layer
+    HIP_TRY(hipStreamSynchronize(m->copy_stream));
+    HIP_TRY(hipStreamSynchronize(m->ctx->stream));
+    m->up_used = m->up_issued = (uint64_t)l;
+  }
+  while (m->up_issued < m->up_used + (uint64_t)m->n_slots)
+    if (int32_t rc = stream_issue(m)) return rc;
+  const int slot = (int)(m->up_used % (uint64_t)m->n_slots);
+  HIP_TRY(hipStreamWaitEvent(m->ctx->stream, m->ev_ready[slot], 0));
+  char* base = static_cast<char*>(m->slots[slot]);
+  const size_t* off = &m->layer_off[(size_t)l * 5];
+  *out = m->layers[l];
+  out->wqkv = base + off[0];
+  out->wo = base + off[1];
+  out->wg = base + off[2];
+  out->wu = base + off[3];
+  out->wd = base + off[4];
+  return 0;
+}
+
+// The kernels of the acquired layer are enqueued: its slot may be refilled.
+int32_t stream_release(ss_hip_model* m) {
+  const int slot = (int)(m->up_used % (uint64_t)m->n_slots);
+  HIP_TRY(hipEventRecord(m->ev_free[slot], m->ctx->stream));
+  m->up_used++;
+  while (m->up_issued < m->up_used + (uint64_t)m->n_slots)
+    if (int32_t rc = stream_issue(m)) return rc;
+  return 0;
+}
+
 // Enqueue one token on the model stream. The token is tokens[*dpos]. With
 // the head, the last workgroup of the LM-head matvec writes the argmax to
 // tokens[*dpos + 1] and advances *dpos; without it, k_advance does.
@@ -784,108 +962,43 @@ int32_t enqueue_token(ss_hip_model* m, bool with_head) {
     m->sw_epoch += (uint32_t)ssk::sweep_phases(m->L, with_head);
     return 0;
   }
-  const int nbd = m->d / 32;
-  HIP_TRY(timed(m, PC_OTHER, 0, [&] {
-    return ssk::launch_embed(m->t_embd, view(m->embd, m->t_embd, m->embd_rows, m->d), m->d,
-                             m->tokens, m->dpos, 0, m->hidden, s);
-  }));
+  if (int32_t rc = enqueue_embed(m, m->dpos, m->hidden)) return rc;
   for (int l = 0; l < m->L; l++) {
     if (m->cancel && *m->cancel && !m->prof) return fail(kErrCancel, "cancelled");
-    const DevLayer& ly = m->layers[l];
-    char* kc = static_cast<char*>(m->kc) + (size_t)l * m->kv_layer_elems * (m->kv_type ? 1 : 2);
-    char* vc = static_cast<char*>(m->vc) + (size_t)l * m->kv_layer_elems * (m->kv_type ? 1 : 2);
-    float* ksl = m->ks ? m->ks + (size_t)l * m->max_seq : nullptr;
-    float* vsl = m->vs ? m->vs + (size_t)l * m->max_seq : nullptr;
-
-    // 1. rmsnorm(attn_norm) -> [Wq;Wk;Wv] -> RoPE -> KV append   (layer_scheduler.c:320-413)
-    ssk::GemvArgs a = gemv_args(ly.wqkv, m->hidden, m->q, m->qdim + 2 * m->kvdim, m->d, ly.t_qkv);
-    a.nw = ly.attn_norm;
-    a.eps = m->eps;
-    a.qdim = m->qdim;
-    a.kvdim = m->kvdim;
-    a.head_dim = m->hd;
-    a.rope_dim = m->rope_dim;
-    a.max_seq = m->max_seq;
-    a.kv_type = m->kv_type;
-    a.rope_cs = m->rope_cs;
-    a.dpos = m->dpos;
-    a.kcache = kc;
-    a.vcache = vc;
-    a.kv_f32 = m->kv_f32;
-    HIP_TRY(timed(m, q_class(ly.t_qkv), matvec_bytes(ly.t_qkv, a.rows, m->d, 1),
-                  [&] { return ssk::launch_gemv(ssk::EPI_QKV, a, s); }));
-    if (m->kv_type == 1)
-      HIP_TRY(timed(m, PC_OTHER, 0, [&] {
-        return ssk::launch_kv_append(kc, vc, ksl, vsl, m->kv_f32, m->kv_f32 + m->kvdim, m->KVH,
-                                     m->hd, m->max_seq, m->dpos, 0, 1, s);
-      }));
-
-    // 2. attention over positions 0..pos                          (:415-468)
-    ssk::AttnArgs at;
-    memset(&at, 0, sizeof(at));
-    at.q = m->q;
-    at.kc = kc;
-    at.vc = vc;
-    at.ks = ksl;
-    at.vs = vsl;
-    at.dpos = m->dpos;
-    at.max_seq = m->max_seq;
-    at.ns = m->ns;
-    at.n_kv_heads = m->KVH;
-    at.scale = 1.0f / sqrtf((float)m->hd);
-    at.out = m->attn;
-    at.part_o = m->att_o;
-    at.part_ml = m->att_ml;
-    // with few splits the Wo matvec merges them itself (no merge launch)
-    const bool fused = m->ns <= ssk::kMergeSplits;
-    HIP_TRY(timed(m, PC_ATTN, 0, [&] {
-      return ssk::launch_attention(m->hd, m->group, m->kv_type, at, !fused, s);
-    }));
-
-    // 3. hidden += Wo attn                                         (:470-484)
-    ssk::GemvArgs o = gemv_args(ly.wo, m->attn, m->hidden, m->d, m->qdim, ly.t_o);
-    if (fused) {
-      o.att_o = m->att_o;
-      o.att_ml = m->att_ml;
-      o.att_ns = m->ns;
-      o.att_group = m->group;
-      o.head_dim = m->hd;
-      o.dpos = m->dpos;
+    if (m->streaming) {
+      DevLayer ly;
+      if (int32_t rc = stream_acquire(m, l, &ly)) return rc;
+      if (int32_t rc = enqueue_layer(m, l, ly, m->hidden, m->dpos)) return rc;
+      if (int32_t rc = stream_release(m)) return rc;
+    } else {
+      if (int32_t rc = enqueue_layer(m, l, m->layers[l], m->hidden, m->dpos)) return rc;
     }
-    HIP_TRY(timed(m, q_class(ly.t_o), matvec_bytes(ly.t_o, m->d, m->qdim, 1),
-                  [&] { return ssk::launch_gemv(ssk::EPI_ADD, o, s); }));
-
-    // 4. rmsnorm(ffn_norm) -> gate, up -> silu(gate) * up           (:486-550)
-    ssk::GemvArgs gu = gemv_args(ly.wg, m->hidden, m->ffn_act, m->ffn, m->d, ly.t_gu);
-    gu.w2 = view(ly.wu, ly.t_gu, m->ffn, m->d);
-    gu.nw = ly.ffn_norm;
-    gu.eps = m->eps;
-    HIP_TRY(timed(m, q_class(ly.t_gu), matvec_bytes(ly.t_gu, m->ffn, m->d, 2),
-                  [&] { return ssk::launch_gemv(ssk::EPI_SWIGLU, gu, s); }));
-
-    // 5. hidden += Wdown act                                       (:552-566)
-    ssk::GemvArgs dn = gemv_args(ly.wd, m->ffn_act, m->hidden, m->d, m->ffn, ly.t_d);
-    HIP_TRY(timed(m, q_class(ly.t_d), matvec_bytes(ly.t_d, m->d, m->ffn, 1),
-                  [&] { return ssk::launch_gemv(ssk::EPI_ADD, dn, s); }));
   }
-  if (with_head) {
-    // output_norm + LM head + first-max argmax                    (:634-662, tensor.c:318-328)
-    ssk::GemvArgs h = gemv_args(m->out, m->hidden, m->logits, m->vocab, m->d, m->t_out);
-    h.nw = m->out_norm;
-    h.eps = m->eps;
-    h.part = m->lm_part;
-    HIP_TRY(timed(m, q_class(m->t_out), matvec_bytes(m->t_out, m->vocab, m->d, 1),
-                  [&] { return ssk::launch_gemv(ssk::EPI_LOGITS, h, s); }));
-    // pick the winner, append it at tokens[pos+1], advance pos
-    HIP_TRY(timed(m, PC_OTHER, 0, [&] {
-      return ssk::launch_argmax_merge(m->lm_part, m->lm_grid, m->logits, m->argmax, m->tokens,
-                                      m->dpos, s);
-    }));
-  } else {
-    HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_advance(m->dpos, s); }));
-  }
-  (void)nbd;
+  if (with_head) return enqueue_head(m, m->hidden);
+  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_advance(m->dpos, s); }));
   return 0;
+}
+
+// Streaming mode prompt, layer-major like ss_scheduler_prefill
+// (layer_scheduler.c:681-803): every layer is uploaded once for the whole
+// prompt and applied to each token in order (a token's attention reads the
+// K/V the earlier tokens of the prompt appended to this layer's cache).
+int32_t enqueue_prompt_layer_major(ss_hip_model* m, const int32_t* tokens, int n, int start) {
+  hipStream_t s = m->ctx->stream;
+  for (int i = 0; i < n; i++)
+    if (int32_t rc = enqueue_embed(m, m->pos_iota + start + i, m->hid_all + (size_t)i * m->d)) return rc;
+  for (int l = 0; l < m->L; l++) {
+    if (m->cancel && *m->cancel) return fail(kErrCancel, "cancelled");
+    DevLayer ly;
+    if (int32_t rc = stream_acquire(m, l, &ly)) return rc;
+    for (int i = 0; i < n; i++)
+      if (int32_t rc = enqueue_layer(m, l, ly, m->hid_all + (size_t)i * m->d, m->pos_iota + start + i)) return rc;
+    if (int32_t rc = stream_release(m)) return rc;
+  }
+  HIP_TRY(hipMemcpyAsync(m->hidden, m->hid_all + (size_t)(n - 1) * m->d, sizeof(float) * m->d,
+                         hipMemcpyDeviceToDevice, s));
+  HIP_TRY(ssk::launch_set_state(m->dpos, m->tokens, start + n - 1, tokens[n - 1], s));
+  return enqueue_head(m, m->hidden);
 }
 
 int32_t capture(ss_hip_model* m, bool with_head, hipGraphExec_t* out) {
@@ -915,6 +1028,65 @@ int32_t run_token(ss_hip_model* m, bool with_head, int pos) {
   return enqueue_token(m, with_head);
 }
 
+constexpr int kStreamSlots = 3;
+
+// Streaming mode: block layout of every layer, the device slots, the copy
+// stream and its events.
+int32_t stream_setup(ss_hip_model* m, const ss_hip_model_desc_t* d) {
+  m->n_slots = kStreamSlots;
+  m->layer_off.assign((size_t)m->L * 5, 0);
+  m->layer_size.assign(m->L, 0);
+  m->host_layers.assign(m->L, nullptr);
+  size_t max_block = 0;
+  for (int l = 0; l < m->L; l++) {
+    const ss_hip_tensor_t* t = d->layers + (size_t)l * SS_HIP_LAYER_TENSORS;
+    const int rows[5] = {m->qdim + 2 * m->kvdim, m->d, m->ffn, m->ffn, m->d};
+    const int cols[5] = {m->d, m->qdim, m->d, m->d, m->ffn};
+    const int types[5] = {t[SS_HIP_WQ].type, t[SS_HIP_WO].type, t[SS_HIP_W_GATE].type, t[SS_HIP_W_UP].type,
+                          t[SS_HIP_W_DOWN].type};
+    size_t o = 0;
+    for (int i = 0; i < 5; i++) {
+      if (!quant_type_ok(types[i]))
+        return fail(kErrParams, "model: blk.%d matrix %d has type %d; Q4_0 and Q8_0 are supported", l, i, types[i]);
+      m->layer_off[(size_t)l * 5 + i] = o;
+      o += align256(ss_hip_packed_bytes(types[i], rows[i], cols[i]));
+    }
+    m->layer_size[l] = o;
+    if (o > max_block) max_block = o;
+  }
+  m->slots.assign(m->n_slots, nullptr);
+  for (int i = 0; i < m->n_slots; i++)
+    if (int32_t rc = m_alloc(m, &m->slots[i], max_block, false)) return rc;
+  HIP_TRY(hipStreamCreateWithFlags(&m->copy_stream, hipStreamNonBlocking));
+  m->ev_ready.assign(m->n_slots, nullptr);
+  m->ev_free.assign(m->n_slots, nullptr);
+  for (int i = 0; i < m->n_slots; i++) {
+    HIP_TRY(hipEventCreateWithFlags(&m->ev_ready[i], hipEventDisableTiming));
+    HIP_TRY(hipEventCreateWithFlags(&m->ev_free[i], hipEventDisableTiming));
+    HIP_TRY(hipEventRecord(m->ev_free[i], m->ctx->stream));
+  }
+  if (int32_t rc = m_alloc(m, (void**)&m->pos_iota, sizeof(int) * m->max_seq, false)) return rc;
+  std::vector<int> iota(m->max_seq);
+  for (int i = 0; i < m->max_seq; i++) iota[i] = i;
+  HIP_TRY(hipMemcpy(m->pos_iota, iota.data(), sizeof(int) * m->max_seq, hipMemcpyHostToDevice));
+  return m_alloc(m, (void**)&m->hid_all, sizeof(float) * (size_t)m->max_seq * m->d, false);
+}
+
+// Streaming mode: layer l's matrices were packed into slot 0; keep them in
+// pinned host memory.
+int32_t stream_keep_layer(ss_hip_model* m, int l) {
+  HIP_TRY(hipDeviceSynchronize());
+  void* h = nullptr;
+  if (hipHostMalloc(&h, m->layer_size[l], hipHostMallocDefault) != hipSuccess)
+    return fail(kErrOom, "pinned host allocation of %zu bytes for blk.%d failed", m->layer_size[l], l);
+  m->host_layers[l] = h;
+  m->host_bytes += m->layer_size[l];
+  HIP_TRY(hipMemcpy(h, m->slots[0], m->layer_size[l], hipMemcpyDeviceToHost));
+  DevLayer& ly = m->layers[l];
+  ly.wqkv = ly.wo = ly.wg = ly.wu = ly.wd = nullptr;   // set per use by stream_acquire
+  return 0;
+}
+
 void model_release(ss_hip_model* m) {
   if (!m) return;
   hipSetDevice(m->ctx->device);
@@ -924,6 +1096,14 @@ void model_release(ss_hip_model* m) {
   for (void* p : m->allocs) hipFree(p);
   for (hipEvent_t e : m->ev_pool) hipEventDestroy(e);
   if (m->h_io) hipHostFree(m->h_io);
+  if (m->copy_stream) {
+    hipStreamSynchronize(m->copy_stream);
+    hipStreamDestroy(m->copy_stream);
+  }
+  for (void* p : m->host_layers)
+    if (p) hipHostFree(p);
+  for (hipEvent_t e : m->ev_ready) hipEventDestroy(e);
+  for (hipEvent_t e : m->ev_free) hipEventDestroy(e);
   delete m;
 }
 
@@ -967,7 +1147,9 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
   m->eps = d->rms_eps;
   m->theta = d->rope_theta;
   m->kv_type = d->kv_type;
-  m->launch = d->launch == SS_HIP_LAUNCH_EAGER ? SS_HIP_LAUNCH_EAGER : SS_HIP_LAUNCH_GRAPH;
+  m->streaming = d->streaming != 0;
+  // streaming mode launches per kernel (the slot of a layer changes per token)
+  m->launch = d->launch == SS_HIP_LAUNCH_EAGER || m->streaming ? SS_HIP_LAUNCH_EAGER : SS_HIP_LAUNCH_GRAPH;
   m->qdim = m->H * m->hd;
   m->kvdim = m->KVH * m->hd;
   m->group = group;
@@ -1001,34 +1183,48 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
   if (d->output_norm.data && upload_vec(m, &m->out_norm, d->output_norm, m->d, "output_norm"))
     return bail();
   m->layers.resize(m->L);
+  if (m->streaming && stream_setup(m, d)) return bail();
   for (int l = 0; l < m->L; l++) {
     const ss_hip_tensor_t* t = d->layers + (size_t)l * SS_HIP_LAYER_TENSORS;
     DevLayer& ly = m->layers[l];
+    // streaming: pack into slot 0 at the block offsets, then keep on the host
+    char* blk = m->streaming ? static_cast<char*>(m->slots[0]) : nullptr;
+    const size_t* off = m->streaming ? &m->layer_off[(size_t)l * 5] : nullptr;
+    if (blk && hipMemset(blk, 0, m->layer_size[l]) != hipSuccess) {
+      fail(kErrBackend, "slot clear failed");
+      return bail();
+    }
     char what[64];
     snprintf(what, sizeof(what), "blk.%d attn_norm", l);
     if (upload_vec(m, &ly.attn_norm, t[SS_HIP_ATTN_NORM], m->d, what)) return bail();
     snprintf(what, sizeof(what), "blk.%d ffn_norm", l);
     if (upload_vec(m, &ly.ffn_norm, t[SS_HIP_FFN_NORM], m->d, what)) return bail();
     snprintf(what, sizeof(what), "blk.%d attn_q/k/v", l);
-    if (upload_mat(m, &ly.wqkv, t + SS_HIP_WQ, 3, m->qdim + 2 * m->kvdim, m->d, &ly.t_qkv, what))
+    if (upload_mat(m, &ly.wqkv, t + SS_HIP_WQ, 3, m->qdim + 2 * m->kvdim, m->d, &ly.t_qkv, what,
+                   blk ? blk + off[0] : nullptr))
       return bail();
     if (t[SS_HIP_WQ].rows != m->qdim || t[SS_HIP_WK].rows != m->kvdim) {
       fail(kErrParams, "model: blk.%d q/k/v row counts do not match the head shape", l);
       return bail();
     }
     snprintf(what, sizeof(what), "blk.%d attn_output", l);
-    if (upload_mat(m, &ly.wo, t + SS_HIP_WO, 1, m->d, m->qdim, &ly.t_o, what)) return bail();
+    if (upload_mat(m, &ly.wo, t + SS_HIP_WO, 1, m->d, m->qdim, &ly.t_o, what, blk ? blk + off[1] : nullptr))
+      return bail();
     snprintf(what, sizeof(what), "blk.%d ffn_gate", l);
     int tu = 0;
-    if (upload_mat(m, &ly.wg, t + SS_HIP_W_GATE, 1, m->ffn, m->d, &ly.t_gu, what)) return bail();
+    if (upload_mat(m, &ly.wg, t + SS_HIP_W_GATE, 1, m->ffn, m->d, &ly.t_gu, what, blk ? blk + off[2] : nullptr))
+      return bail();
     snprintf(what, sizeof(what), "blk.%d ffn_up", l);
-    if (upload_mat(m, &ly.wu, t + SS_HIP_W_UP, 1, m->ffn, m->d, &tu, what)) return bail();
+    if (upload_mat(m, &ly.wu, t + SS_HIP_W_UP, 1, m->ffn, m->d, &tu, what, blk ? blk + off[3] : nullptr))
+      return bail();
     if (tu != ly.t_gu) {
       fail(kErrParams, "model: blk.%d ffn_gate and ffn_up types differ", l);
       return bail();
     }
     snprintf(what, sizeof(what), "blk.%d ffn_down", l);
-    if (upload_mat(m, &ly.wd, t + SS_HIP_W_DOWN, 1, m->d, m->ffn, &ly.t_d, what)) return bail();
+    if (upload_mat(m, &ly.wd, t + SS_HIP_W_DOWN, 1, m->d, m->ffn, &ly.t_d, what, blk ? blk + off[4] : nullptr))
+      return bail();
+    if (m->streaming && stream_keep_layer(m, l)) return bail();
   }
 
   // KV cache and working state
@@ -1075,7 +1271,7 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
     fail(kErrBackend, "model upload failed");
     return bail();
   }
-  if (d->launch == SS_HIP_LAUNCH_SWEEP && sweep_setup(m) < 0) return bail();
+  if (d->launch == SS_HIP_LAUNCH_SWEEP && !m->streaming && sweep_setup(m) < 0) return bail();
   if (m->launch == SS_HIP_LAUNCH_GRAPH && (capture(m, true, &m->g_full) || capture(m, false, &m->g_nohead)))
     return bail();
   return m;
@@ -1084,6 +1280,8 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
 void ss_hip_model_free(ss_hip_model_t* m) { model_release(m); }
 
 uint64_t ss_hip_model_bytes(const ss_hip_model_t* m) { return m ? m->bytes : 0; }
+
+uint64_t ss_hip_model_host_bytes(const ss_hip_model_t* m) { return m ? m->host_bytes : 0; }
 
 int32_t ss_hip_model_launch(const ss_hip_model_t* m) { return m ? m->launch : -1; }
 
@@ -1153,6 +1351,14 @@ int32_t ss_hip_eval_prompt(ss_hip_model_t* m, const int32_t* tokens, int32_t n, 
   HIP_TRY(hipStreamSynchronize(s));
   HIP_TRY(hipMemcpy(m->tokens + start, tokens, sizeof(int) * n, hipMemcpyHostToDevice));
   HIP_TRY(ssk::launch_set_state(m->dpos, m->tokens, start, tokens[0], s));
+  if (m->streaming) {
+    if (int32_t rc = enqueue_prompt_layer_major(m, tokens, n, start)) {
+      hipStreamSynchronize(s);
+      return rc;
+    }
+    m->host_pos = start + n - 1;
+    return finish_eval(m, logits_host, argmax_out);
+  }
   for (int i = 0; i < n; i++) {
     if (m->cancel && *m->cancel) {
       hipStreamSynchronize(s);

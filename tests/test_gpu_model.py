@@ -44,6 +44,9 @@ TINYLLAMA = dict(n_layers=22, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=64
                  context_length=2048, seed=1001)
 
 
+TINY7 = dict(TINY, n_layers=7, seed=4)    # more layers than streaming slots, not a multiple of them
+
+
 def _launch_in_effect(m):
     L = api._lib()
     return L.ss_hip_model_launch(L.ss_model_hip(m.h))
@@ -120,6 +123,55 @@ def test_device_greedy_equals_host_loop(kv):
         assert host == toks
     om = oracle.Model(path, 256, kv)
     assert om.greedy(prompt, 40) == (first, toks)
+    om.close()
+
+
+@pytest.mark.parametrize("kv", ["f16", "int8"])
+@pytest.mark.parametrize("spec", ["tiny7", "gqa8"])
+def test_streaming_matches_resident(spec, kv):
+    """Streaming mode (layer matrices in pinned host memory, uploaded per use
+    into a ring of device slots; prompts layer-major as in
+    layer_scheduler.c:681-803) runs the same kernels on the same inputs as
+    the resident model, so every logit must match it bit for bit, and the
+    greedy tokens must match the oracle's."""
+    kw = {"tiny7": TINY7, "gqa8": GQA8}[spec]
+    path = _model_file(spec, **kw)
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(3, kw["vocab"], 20).tolist()
+    L = api._lib()
+    runs = []
+    for streaming in (False, True):
+        print("model", spec, kv, "streaming" if streaming else "resident", flush=True)
+        with api.Model(path, max_context=128, kv=kv, streaming=streaming) as m:
+            hm = L.ss_model_hip(m.h)
+            if streaming:
+                assert L.ss_hip_model_host_bytes(hm) > 0
+                assert _launch_in_effect(m) == api.LAUNCH["eager"]
+            else:
+                assert L.ss_hip_model_host_bytes(hm) == 0
+            out = [m.eval_prompt(prompt, 0)]
+            tok, pos = out[0][1], len(prompt)
+            for _ in range(12):
+                lg, am = m.eval_token(tok, pos)
+                out.append((lg.copy(), am))
+                tok, pos = am, pos + 1
+            m.reset()   # a second prompt, then device-side greedy steps
+            out.append(m.eval_prompt(prompt[:7], 0))
+            toks = m.decode_greedy(9)
+        runs.append((out, list(toks)))
+    (res, res_toks), (stm, stm_toks) = runs
+    for i, ((a, ia), (b, ib)) in enumerate(zip(res, stm)):
+        assert np.array_equal(a, b), i
+        assert ia == ib, i
+    assert res_toks == stm_toks
+    om = oracle.Model(path, 128, kv)
+    olg = om.prefill(prompt, 0)
+    assert rel_err(stm[0][0], olg) <= (TOL if kv == "f16" else TOL_INT8)
+    tok, pos = oracle.argmax(olg), len(prompt)
+    for i in range(12):
+        assert stm[i][1] == tok
+        tok = oracle.argmax(om.forward(tok, pos))
+        pos += 1
     om.close()
 
 
