@@ -111,6 +111,31 @@ __device__ __forceinline__ int q8c(float f) {   // round to nearest even, then c
   return (int)fminf(fmaxf(rintf(f), -127.f), 127.f);
 }
 
+// Coherent exchange between workgroups of one launch: relaxed agent-scope
+// atomic loads and stores (global_load/global_store sc1 on gfx950) reach
+// the device-coherent level without flushing or invalidating the L2; a
+// writer drains its stores (vm_drain) before it signals.
+__device__ __forceinline__ uint32_t cld(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t cld64(const uint64_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void cst(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void cst64(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float cldf(const float* p) {
+  return __uint_as_float(cld(reinterpret_cast<const uint32_t*>(p)));
+}
+__device__ __forceinline__ void cstf(float* p, float v) {
+  cst(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
+}
+// every vector memory operation of this wave has completed
+__device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 template <int QT>
 struct QTraits;
 template <>

@@ -190,7 +190,7 @@ __device__ __forceinline__ float xput(XSlice<UT>& p, int* xw, const float* nw, i
   return ss;
 }
 
-// Merge staging (the k_attn_merge step inside the Wo matvec): x[col] for
+// Merge staging (the attention split merge inside the Wo matvec): x[col] for
 // col in head h = G*kvh + g is sum_s o_s * e^(m_s - M) / sum_s l_s e^(m_s - M)
 // over the active attention splits s of KV head kvh. A lane fetches the
 // (m, l) and 4 o values of all kMergeSplits split slots for its group of 4
@@ -226,7 +226,7 @@ __device__ __forceinline__ void mfetch(MSlice<UT>& p, const GemvArgs& a, int u, 
   }
 }
 
-// Same arithmetic order as k_attn_merge.
+// Same arithmetic order as the merge in k_attn.
 template <int UT>
 __device__ __forceinline__ void mput(MSlice<UT>& p, int* xw, int u, int nb, int active, int lane) {
 #pragma unroll

@@ -82,8 +82,9 @@ struct ss_hip_ctx {
   int rope_row_len = 0;
   float* att_o = nullptr;
   float* att_ml = nullptr;
+  uint32_t* att_cnt = nullptr;
 
-  size_t att_o_floats = 0, att_ml_floats = 0;
+  size_t att_o_floats = 0, att_ml_floats = 0, att_cnt_bytes = 0;
 
   // host-pointer plug (metal_backend.m:190-235 registry)
   std::unordered_map<const void*, void*> registry;
@@ -151,7 +152,7 @@ void rope_row(float* cs, int rope_dim, int pos, float theta) {
 }
 
 // Splits per KV head: enough that a split of the longest context is one round
-// of k_attn loads, at most kMaxSplits.
+// of k_attn loads (one HBM latency per split), at most kMaxSplits.
 int attn_splits(int head_dim, int group, int max_seq) {
   const int round = ssk::attn_round_positions(head_dim, group);
   int ns = (max_seq + round - 1) / round;
@@ -227,7 +228,7 @@ void ss_hip_free(ss_hip_ctx_t* c) {
   if (c->stream) hipStreamSynchronize(c->stream);
   for (auto& kv : c->registry) hipFree(kv.second);
   void* bufs[] = {c->staging, c->am_part, c->rope_row, c->att_o,
-                  c->att_ml, c->plug_x, c->plug_y};
+                  c->att_ml, c->att_cnt, c->plug_x, c->plug_y};
   for (void* b : bufs)
     if (b) hipFree(b);
   if (c->stream) hipStreamDestroy(c->stream);
@@ -395,6 +396,7 @@ int32_t ss_hip_attention(ss_hip_ctx_t* c, float* out, const float* q, const void
                       sizeof(float) * (size_t)n_kv_heads * ns * group * head_dim, false);
   if (!rc) rc = ensure(c, (void**)&c->att_ml, &c->att_ml_floats,
                        sizeof(float) * (size_t)n_kv_heads * ns * group * 2, false);
+  if (!rc) rc = ensure(c, (void**)&c->att_cnt, &c->att_cnt_bytes, sizeof(uint32_t) * (size_t)n_kv_heads, true);
   if (rc) return rc;
   ssk::AttnArgs a;
   memset(&a, 0, sizeof(a));
@@ -411,7 +413,8 @@ int32_t ss_hip_attention(ss_hip_ctx_t* c, float* out, const float* q, const void
   a.out = out;
   a.part_o = c->att_o;
   a.part_ml = c->att_ml;
-  HIP_TRY(ssk::launch_attention(head_dim, group, kv_type, a, true, pick(c, stream)));
+  a.cnt = c->att_cnt;
+  HIP_TRY(ssk::launch_attention(head_dim, group, kv_type, a, pick(c, stream)));
   return 0;
 }
 
@@ -530,6 +533,7 @@ struct ss_hip_model {
   float2* lm_part = nullptr;
   int lm_grid = 0;
   float *att_o = nullptr, *att_ml = nullptr;
+  uint32_t* att_cnt = nullptr;   // [KVH] split arrivals of the attention merge (zero between launches)
 
   int* h_io = nullptr;   // pinned host scratch
   hipGraphExec_t g_full = nullptr, g_nohead = nullptr;
@@ -847,9 +851,11 @@ int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden,
   at.out = m->attn;
   at.part_o = m->att_o;
   at.part_ml = m->att_ml;
-  // with few splits the Wo matvec merges them itself (no merge launch)
+  // with few splits the Wo matvec merges them while staging; with more, the
+  // last split of each KV head to finish merges them
   const bool fused = m->ns <= ssk::kMergeSplits;
-  HIP_TRY(timed(m, PC_ATTN, 0, [&] { return ssk::launch_attention(m->hd, m->group, m->kv_type, at, !fused, s); }));
+  at.cnt = fused ? nullptr : m->att_cnt;
+  HIP_TRY(timed(m, PC_ATTN, 0, [&] { return ssk::launch_attention(m->hd, m->group, m->kv_type, at, s); }));
 
   // 3. hidden += Wo attn                                         (:470-484)
   ssk::GemvArgs o = gemv_args(ly.wo, m->attn, hidden, m->d, m->qdim, ly.t_o);
@@ -1250,7 +1256,8 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
       m_alloc(m, (void**)&m->argmax, sizeof(int) * 4) ||
       m_alloc(m, (void**)&m->lm_part, sizeof(float2) * lm_grid) ||
       m_alloc(m, (void**)&m->att_o, sizeof(float) * (size_t)m->KVH * m->ns * m->group * m->hd) ||
-      m_alloc(m, (void**)&m->att_ml, sizeof(float) * (size_t)m->KVH * m->ns * m->group * 2))
+      m_alloc(m, (void**)&m->att_ml, sizeof(float) * (size_t)m->KVH * m->ns * m->group * 2) ||
+      m_alloc(m, (void**)&m->att_cnt, sizeof(uint32_t) * m->KVH))
     return bail();
   // RoPE (cos, sin) table for every position, computed with the host libm
   // exactly as tensor.c:250-254 computes each pair.

@@ -40,7 +40,7 @@ struct GemvArgs {
   // EPI_LOGITS
   float2* part;              // one (value, index bits) candidate per workgroup
   // x = the attention output merged from its splits while staging (x unused):
-  // the k_attn_merge step folded into the Wo matvec; needs att_ns <= kMergeSplits
+  // the attention split merge folded into the Wo matvec; needs att_ns <= kMergeSplits
   const float* att_o;        // [kvh][ns][G][head_dim] partial outputs, or nullptr
   const float* att_ml;       // [kvh][ns][G][2] partial (max, sum)
   int att_ns, att_group;     // splits per KV head, query heads per KV head
@@ -58,6 +58,9 @@ struct AttnArgs {
   float* out;                // [n_heads][hd]
   float* part_o;             // [kvh][ns][G][hd]
   float* part_ml;            // [kvh][ns][G][2]
+  uint32_t* cnt;             // [n_kv_heads] split arrivals, zero between launches: the last
+                             // split merges into out; nullptr: the splits stay in part_o/part_ml
+                             // for a merging consumer (ns <= kMergeSplits)
 };
 
 struct GemvPlan {
@@ -71,9 +74,7 @@ PackedMat packed_view(const void* base, int type, int64_t rows, int cols);
 hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t s);
 hipError_t launch_argmax_merge(const float2* part, int n, const float* y, int* out_idx, int* tokens,
                                int* dpos, hipStream_t s);
-// merge = false leaves the splits in part_o/part_ml for a merging consumer
-hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, bool merge,
-                            hipStream_t s);
+hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, hipStream_t s);
 bool attention_supported(int head_dim, int group);
 // positions one k_attn workgroup covers in one round of loads
 int attn_round_positions(int head_dim, int group);
@@ -100,7 +101,7 @@ constexpr int kTB = 4;                     // 32-column blocks per tile (kRG * k
 constexpr int kUT = 8;                     // tiles per scale group (16 B of scales per lane)
 constexpr int kGemvUnit = 2;               // tiles per wave per round (2, 4 or 8)
 constexpr int kGemvMaxSplit = 16;          // waves per matvec workgroup
-constexpr int kMaxSplits = 64;             // attention splits per KV head
+constexpr int kMaxSplits = 256;            // attention splits per KV head
 constexpr int kMergeSplits = 8;            // splits the Wo matvec merges itself
 
 }  // namespace ssk

@@ -1,8 +1,9 @@
 // ss_kernels.hip - attention and the small per-token kernels for gfx950.
 //
-// Split results (attention splits, per-workgroup argmax candidates) are
-// merged by a following small kernel, so no workgroup hands data to another
-// workgroup of the same launch and none needs a device-scope fence.
+// Per-workgroup argmax candidates are merged by a following small kernel.
+// Attention splits of one KV head are merged by the last of its workgroups
+// to finish (a device-scope release/acquire around one atomic counter per KV
+// head), or left for the Wo matvec, which merges a few splits while staging.
 
 #include <math.h>
 
@@ -14,8 +15,7 @@ namespace {
 
 // ------------------------------------------------------------ attention
 // Single-query GQA attention (layer_scheduler.c:415-468) with the sequence
-// split over gridDim.x workgroups (flash-decoding); k_attn_merge combines the
-// splits. In workgroup (s, g), serving the G query heads that share KV head
+// split over gridDim.x workgroups (flash-decoding). In workgroup (s, g), serving the G query heads that share KV head
 // g, lane l of wave w holds 8 consecutive elements (column chunk l % LPR) of
 // the K and V rows (l / LPR) + RPI*w + ... of its positions; a round of
 // positions is requested at once, straight into registers. Scores are summed
@@ -45,6 +45,11 @@ struct KvElem<1> {   // int8 codes times the position's scale (layer_scheduler.c
     for (int i = 0; i < 8; ++i) v[i] = (float)(int8_t)((w[i / 4] >> (8 * (i % 4))) & 0xffu) * s;
   }
 };
+
+// Raw buffer view flags (dword 3 of the descriptor) and the sc1 cache
+// policy bit: loads through such a view read the device-coherent level.
+constexpr int kBufferFlags = 0x00020000;
+constexpr int kSc1 = 16;
 
 __device__ __forceinline__ void attn_split(const AttnArgs& a, int& ctx, int& chunk, int& active) {
   ctx = a.dpos ? *a.dpos + 1 : a.seq_len;
@@ -186,9 +191,28 @@ __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
     }
   }
   __syncthreads();
+  constexpr int kThreads = kAttnWaves * 64;
+  if (a.cnt && active == 1) {
+    // the only split: the output directly (the merge below with one split)
+    for (int i = tid; i < G * HD; i += kThreads) {
+      const int g = i / HD, d = i % HD;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, wm[w][g]);
+      float so = 0.f, sl = 0.f;
+#pragma unroll
+      for (int w = 0; w < kAttnWaves; ++w) {
+        const float f = expf(wm[w][g] - M);
+        so = fmaf(f, wo[w][g][d], so);
+        sl = fmaf(f, wl[w][g], sl);
+      }
+      a.out[((size_t)kvh * G + g) * HD + d] = so * (1.0f / sl);
+    }
+    return;
+  }
   float* po = a.part_o + (((size_t)kvh * a.ns + blockIdx.x) * G) * HD;
   float* pml = a.part_ml + (((size_t)kvh * a.ns + blockIdx.x) * G) * 2;
-  for (int i = tid; i < G * HD; i += kAttnWaves * 64) {
+  for (int i = tid; i < G * HD; i += kThreads) {
     const int g = i / HD, d = i % HD;
     float M = -INFINITY;
 #pragma unroll
@@ -200,45 +224,103 @@ __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
       so = fmaf(f, wo[w][g][d], so);
       sl = fmaf(f, wl[w][g], sl);
     }
-    po[g * HD + d] = so;
-    if (d == 0) {
-      pml[g * 2] = M;
-      pml[g * 2 + 1] = sl;
+    if (a.cnt) {   // merged below by another workgroup: coherent stores
+      cstf(po + g * HD + d, so);
+      if (d == 0) {
+        cstf(pml + g * 2, M);
+        cstf(pml + g * 2 + 1, sl);
+      }
+    } else {       // merged by the next kernel
+      po[g * HD + d] = so;
+      if (d == 0) {
+        pml[g * 2] = M;
+        pml[g * 2 + 1] = sl;
+      }
     }
   }
-}
+  if (!a.cnt) return;   // the consumer (the Wo matvec) merges the splits
 
-// out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M) over the active splits
-template <int HD, int G>
-__global__ void __launch_bounds__(256) k_attn_merge(const AttnArgs a) {
-  __shared__ float mg[G], lg[G];
-  __shared__ float wts[64 * G];
-  const int tid = threadIdx.x;
-  const int kvh = blockIdx.x;
-  int ctx, chunk, active;
-  attn_split(a, ctx, chunk, active);
-  const float* ml = a.part_ml + ((size_t)kvh * a.ns * G) * 2;
-  const float* pob = a.part_o + ((size_t)kvh * a.ns * G) * HD;
-  for (int i = tid; i < G; i += 256) {
-    float M = -INFINITY;
-    for (int s = 0; s < active; ++s) M = fmaxf(M, ml[(s * G + i) * 2]);
-    float L = 0.f;
-    for (int s = 0; s < active; ++s) L += ml[(s * G + i) * 2 + 1] * expf(ml[(s * G + i) * 2] - M);
-    mg[i] = M;
-    lg[i] = 1.0f / L;
+  // The last split of this KV head to finish merges all of them:
+  // out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).
+  __shared__ uint32_t last;
+  __shared__ float wts[kMaxSplits * G];
+  vm_drain();        // this wave's partials have reached the coherent level
+  __syncthreads();
+  if (tid == 0)
+    last = __hip_atomic_fetch_add(a.cnt + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           (uint32_t)(active - 1);
+  __syncthreads();
+  if (!last) return;
+  const float* ml = a.part_ml + (size_t)kvh * a.ns * G * 2;
+  const float* pob = a.part_o + (size_t)kvh * a.ns * G * HD;
+  for (int g = wave; g < G; g += kAttnWaves) {
+    float mx = -INFINITY;
+    float mv[kMaxSplits / kWave], lv[kMaxSplits / kWave];
+#pragma unroll
+    for (int k = 0; k < kMaxSplits / kWave; ++k) {
+      const int sp = lane + k * kWave;
+      mv[k] = sp < active ? cldf(ml + (sp * G + g) * 2) : -INFINITY;
+      lv[k] = sp < active ? cldf(ml + (sp * G + g) * 2 + 1) : 0.f;
+    }
+    for (int k = 0; k < kMaxSplits / kWave; ++k) mx = fmaxf(mx, mv[k]);
+    mx = wave_max(mx);
+    float ls = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxSplits / kWave; ++k) ls += lv[k] * expf(mv[k] - mx);
+    const float inv = 1.0f / wave_sum(ls);
+#pragma unroll
+    for (int k = 0; k < kMaxSplits / kWave; ++k) {
+      const int sp = lane + k * kWave;
+      if (sp < active) wts[sp * G + g] = expf(mv[k] - mx) * inv;
+    }
   }
   __syncthreads();
-  for (int i = tid; i < active * G; i += 256) {
-    const int g = i % G;
-    wts[i] = expf(ml[i * 2] - mg[g]) * lg[g];
+  // Thread (sub, quad) sums four consecutive outputs over the splits
+  // sub, sub + kSub, ..., kBatch 16-byte coherent loads in flight at a time
+  // (out-of-range loads of the buffer view read zero); the kSub partial sums
+  // are then added in subset order. The batch is smaller for small groups,
+  // whose registers the main loop does not fill (occupancy).
+  constexpr int kBatch = G >= 4 ? 16 : 8;
+  constexpr int kQuads = G * HD / 4;
+  constexpr int kSub = kThreads / kQuads;
+  static_assert(kThreads % kQuads == 0, "outputs in quads must divide the workgroup");
+  __shared__ float4 red[kThreads];
+  const int qd = tid % kQuads, sub = tid / kQuads;
+  const int g = qd * 4 / HD;
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(pob), (short)0, active * G * HD * 4, kBufferFlags);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int sp0 = sub; sp0 < active; sp0 += kBatch * kSub) {
+    float4 v[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int sp = sp0 + k * kSub;   // past the last split: offset out of range, reads zero
+      // the builtin returns the 16 bytes as four 32-bit integers
+      v[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ro, (sp * kQuads + qd) * 16, 0, kSc1));
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int sp = sp0 + k * kSub;
+      const float w = sp < active ? wts[sp * G + g] : 0.f;
+      acc.x = fmaf(v[k].x, w, acc.x);
+      acc.y = fmaf(v[k].y, w, acc.y);
+      acc.z = fmaf(v[k].z, w, acc.z);
+      acc.w = fmaf(v[k].w, w, acc.w);
+    }
   }
+  red[tid] = acc;
   __syncthreads();
-  for (int o = tid; o < G * HD; o += 256) {
-    const int g = o / HD, d = o % HD;
-    float s = 0.f;
-    for (int si = 0; si < active; ++si) s = fmaf(pob[((size_t)si * G + g) * HD + d], wts[si * G + g], s);
-    a.out[((size_t)kvh * G + g) * HD + d] = s;
+  if (sub == 0) {
+    for (int k = 1; k < kSub; ++k) {
+      const float4 r = red[k * kQuads + qd];
+      acc.x += r.x;
+      acc.y += r.y;
+      acc.z += r.z;
+      acc.w += r.w;
+    }
+    reinterpret_cast<float4*>(a.out + (size_t)kvh * G * HD)[qd] = acc;
   }
+  if (tid == 0) cst(a.cnt + kvh, 0u);   // every split of this launch has arrived: ready for the next
 }
 
 // ------------------------------------------------------------ small kernels
@@ -344,25 +426,22 @@ __global__ void k_advance(int* dpos) { *dpos += 1; }
 
 // ------------------------------------------------------------ launchers
 template <int HD, int G>
-hipError_t launch_attn_t(int kv_type, const AttnArgs& a, bool merge, hipStream_t s) {
+hipError_t launch_attn_t(int kv_type, const AttnArgs& a, hipStream_t s) {
   const dim3 grid(a.ns, a.n_kv_heads);
   if (kv_type == 0)
     hipLaunchKernelGGL((k_attn<HD, G, 0>), grid, dim3(kAttnWaves * 64), 0, s, a);
   else
     hipLaunchKernelGGL((k_attn<HD, G, 1>), grid, dim3(kAttnWaves * 64), 0, s, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || !merge) return e;
-  hipLaunchKernelGGL((k_attn_merge<HD, G>), dim3(a.n_kv_heads), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
 template <int HD>
-hipError_t launch_attn_hd(int group, int kv_type, const AttnArgs& a, bool merge, hipStream_t s) {
+hipError_t launch_attn_hd(int group, int kv_type, const AttnArgs& a, hipStream_t s) {
   switch (group) {
-    case 1: return launch_attn_t<HD, 1>(kv_type, a, merge, s);
-    case 2: return launch_attn_t<HD, 2>(kv_type, a, merge, s);
-    case 4: return launch_attn_t<HD, 4>(kv_type, a, merge, s);
-    case 8: return launch_attn_t<HD, 8>(kv_type, a, merge, s);
+    case 1: return launch_attn_t<HD, 1>(kv_type, a, s);
+    case 2: return launch_attn_t<HD, 2>(kv_type, a, s);
+    case 4: return launch_attn_t<HD, 4>(kv_type, a, s);
+    case 8: return launch_attn_t<HD, 8>(kv_type, a, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -379,11 +458,10 @@ bool attention_supported(int head_dim, int group) {
          (group == 1 || group == 2 || group == 4 || group == 8);
 }
 
-hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, bool merge,
-                            hipStream_t s) {
-  if (a.ns > kMaxSplits) return hipErrorInvalidValue;   // k_attn_merge holds 64 split weights per head
-  if (head_dim == 64) return launch_attn_hd<64>(group, kv_type, a, merge, s);
-  if (head_dim == 128) return launch_attn_hd<128>(group, kv_type, a, merge, s);
+hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, hipStream_t s) {
+  if (a.ns < 1 || a.ns > kMaxSplits) return hipErrorInvalidValue;   // merge weights: kMaxSplits per head
+  if (head_dim == 64) return launch_attn_hd<64>(group, kv_type, a, s);
+  if (head_dim == 128) return launch_attn_hd<128>(group, kv_type, a, s);
   return hipErrorInvalidValue;
 }
 

@@ -117,27 +117,6 @@ __host__ __device__ inline LdsPlan lds_plan(const SweepArgs& a, int hd, int grou
   return p;
 }
 
-// ------------------------------------------------------------ coherent exchange
-__device__ __forceinline__ uint32_t cld(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ uint64_t cld64(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void cst(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void cst64(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float cldf(const float* p) {
-  return __uint_as_float(cld(reinterpret_cast<const uint32_t*>(p)));
-}
-__device__ __forceinline__ void cstf(float* p, float v) {
-  cst(reinterpret_cast<uint32_t*>(p), __float_as_uint(v));
-}
-// every vector memory operation of this wave has completed
-__device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // Progress flags: one word per workgroup, the epoch it last published.
 // Workgroups 16g .. 16g+15 share one 64-byte line, and the lines of
