@@ -561,8 +561,8 @@ struct ss_hip_model {
   std::vector<size_t> layer_size;    // bytes of each block
   std::vector<size_t> layer_off;     // [L][5] offsets of [Wq;Wk;Wv], Wo, gate, up, down in a block
   std::vector<void*> slots;          // device slots (largest block each)
-  std::vector<hipEvent_t> ev_ready, ev_free;
-  hipStream_t copy_stream = nullptr;
+  std::vector<hipEvent_t> ev_ready, ev_free, ev_half;
+  hipStream_t copy_stream = nullptr, copy_stream2 = nullptr;   // each upload is split over both
   uint64_t up_issued = 0, up_used = 0;   // uploads issued / consumed
   uint64_t host_bytes = 0;           // pinned bytes held
   int* pos_iota = nullptr;           // device [max_seq]: value i at index i
@@ -908,12 +908,21 @@ int32_t enqueue_head(ss_hip_model* m, const float* hidden) {
 // stream waits for it (ev_ready) before the layer's kernels; up to n_slots
 // uploads are in flight, so the next layers (and the first layers of the
 // next token) copy while the current layer computes.
+// An upload is split in two halves on two copy streams (two DMA engines):
+// one stream alone leaves the link idle between consecutive uploads.
 int32_t stream_issue(ss_hip_model* m) {
   const uint64_t k = m->up_issued;
   const int slot = (int)(k % (uint64_t)m->n_slots), l = (int)(k % (uint64_t)m->L);
+  const size_t half = (m->layer_size[l] / 2 + 255) & ~(size_t)255;
+  char* dst = static_cast<char*>(m->slots[slot]);
+  const char* src = static_cast<const char*>(m->host_layers[l]);
   HIP_TRY(hipStreamWaitEvent(m->copy_stream, m->ev_free[slot], 0));
-  HIP_TRY(hipMemcpyAsync(m->slots[slot], m->host_layers[l], m->layer_size[l], hipMemcpyHostToDevice,
-                         m->copy_stream));
+  HIP_TRY(hipStreamWaitEvent(m->copy_stream2, m->ev_free[slot], 0));
+  HIP_TRY(hipMemcpyAsync(dst, src, half, hipMemcpyHostToDevice, m->copy_stream));
+  HIP_TRY(hipMemcpyAsync(dst + half, src + half, m->layer_size[l] - half, hipMemcpyHostToDevice,
+                         m->copy_stream2));
+  HIP_TRY(hipEventRecord(m->ev_half[slot], m->copy_stream2));
+  HIP_TRY(hipStreamWaitEvent(m->copy_stream, m->ev_half[slot], 0));
   HIP_TRY(hipEventRecord(m->ev_ready[slot], m->copy_stream));
   m->up_issued++;
   return 0;
@@ -925,6 +934,7 @@ int32_t stream_acquire(ss_hip_model* m, int l, DevLayer* out) {
     // an evaluation stopped part way (cancel, error): drain both streams and
     // restart the upload sequence at this layer
     HIP_TRY(hipStreamSynchronize(m->copy_stream));
+    HIP_TRY(hipStreamSynchronize(m->copy_stream2));
     HIP_TRY(hipStreamSynchronize(m->ctx->stream));
     m->up_used = m->up_issued = (uint64_t)l;
   }
@@ -1064,10 +1074,13 @@ int32_t stream_setup(ss_hip_model* m, const ss_hip_model_desc_t* d) {
   for (int i = 0; i < m->n_slots; i++)
     if (int32_t rc = m_alloc(m, &m->slots[i], max_block, false)) return rc;
   HIP_TRY(hipStreamCreateWithFlags(&m->copy_stream, hipStreamNonBlocking));
+  HIP_TRY(hipStreamCreateWithFlags(&m->copy_stream2, hipStreamNonBlocking));
   m->ev_ready.assign(m->n_slots, nullptr);
   m->ev_free.assign(m->n_slots, nullptr);
+  m->ev_half.assign(m->n_slots, nullptr);
   for (int i = 0; i < m->n_slots; i++) {
     HIP_TRY(hipEventCreateWithFlags(&m->ev_ready[i], hipEventDisableTiming));
+    HIP_TRY(hipEventCreateWithFlags(&m->ev_half[i], hipEventDisableTiming));
     HIP_TRY(hipEventCreateWithFlags(&m->ev_free[i], hipEventDisableTiming));
     HIP_TRY(hipEventRecord(m->ev_free[i], m->ctx->stream));
   }
@@ -1102,14 +1115,16 @@ void model_release(ss_hip_model* m) {
   for (void* p : m->allocs) hipFree(p);
   for (hipEvent_t e : m->ev_pool) hipEventDestroy(e);
   if (m->h_io) hipHostFree(m->h_io);
-  if (m->copy_stream) {
-    hipStreamSynchronize(m->copy_stream);
-    hipStreamDestroy(m->copy_stream);
-  }
+  for (hipStream_t cs : {m->copy_stream, m->copy_stream2})
+    if (cs) {
+      hipStreamSynchronize(cs);
+      hipStreamDestroy(cs);
+    }
   for (void* p : m->host_layers)
     if (p) hipHostFree(p);
   for (hipEvent_t e : m->ev_ready) hipEventDestroy(e);
   for (hipEvent_t e : m->ev_free) hipEventDestroy(e);
+  for (hipEvent_t e : m->ev_half) hipEventDestroy(e);
   delete m;
 }
 
