@@ -11,8 +11,11 @@ steps (after --warmup untimed ones), with the weights resident in HBM. The
 roofline object is for the dominant kernel class: the matvec of the layer
 quantisation type (per-kernel launches, the default) or the whole-token
 kernel (--launch sweep, one persistent launch per token). It is measured
-with HIP events on the model stream around each launch in a profiled eager
-replay of further decode steps. cpu_baseline is the CPU oracle (the
+with HIP events in a profiled eager replay of further decode steps: the
+matvec and attention kernels are launched with hipExtLaunchKernelGGL, whose
+start/stop events the dispatch itself records when the kernel begins and
+ends (kernel execution time, as a kernel trace reports it); other launches
+are bracketed by events on the model stream. cpu_baseline is the CPU oracle (the
 reference path restated in C) on the same GGUF, timed on this host on a
 bounded sample.
 
@@ -213,6 +216,7 @@ def main():
     roof = None
     try:
         roof = profile_classes(m, prof_steps)
+        roof["timed_as"] = "eager replay; start/stop events recorded by each kernel's dispatch" 
         if args.config == "llama2-7b" and args.kv == "f16" and args.prompt_len is None:
             roof["traffic"] = measured_traffic(roof["kernel_id"])   # counter runs of this workload
     except Exception as e:   # profiling is optional for the headline number
@@ -397,7 +401,8 @@ def profile_classes(m, n_steps):
     m.decode_greedy(n_steps)
     out = np.zeros(15, np.float64)
     if L.ss_hip_profile_end(hm, out.ctypes.data_as(C.POINTER(C.c_double)), 15) != 0:
-        raise SlipStreamError("profile_end failed")
+        err = L.ss_hip_last_error()
+        raise SlipStreamError("profile_end failed: %s" % (err.decode() if err else "?"))
     if out[13] > 0:      # persistent launches: the whole token is the kernel
         ms, cnt, byt = out[12], out[13], out[14]
         kernel, kid = "k_sweep (whole token: embedding, all layers, LM head, argmax)", "sweep"

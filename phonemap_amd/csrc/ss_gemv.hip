@@ -21,6 +21,8 @@
 
 #include <math.h>
 
+#include <hip/hip_ext.h>
+
 #include "ss_device.h"
 #include "ss_kernels.h"
 
@@ -549,8 +551,15 @@ __global__ void k_argmax_merge(const float2* part, int n, const float* y, int* o
 template <int QT, int NMAT, int EPI, bool MERGE = false>
 hipError_t launch_t(const GemvArgs& a, hipStream_t s) {
   GemvPlan p = gemv_plan(a.rows, a.cols, QT, NMAT);
-  hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, kGemvUnit, MERGE>), dim3(p.grid), dim3(p.threads), p.lds_bytes,
-                     s, a);
+  KernelEvents& ev = kernel_events();
+  if (ev.start) {
+    hipExtLaunchKernelGGL((k_gemv<QT, NMAT, EPI, kGemvUnit, MERGE>), dim3(p.grid), dim3(p.threads),
+                          p.lds_bytes, s, ev.start, ev.stop, 0, a);
+    ev.used = true;
+  } else {
+    hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, kGemvUnit, MERGE>), dim3(p.grid), dim3(p.threads), p.lds_bytes,
+                       s, a);
+  }
   return hipGetLastError();
 }
 
@@ -567,6 +576,11 @@ hipError_t launch_q(int epi, const GemvArgs& a, hipStream_t s) {
 }
 
 }  // namespace
+
+KernelEvents& kernel_events() {
+  static thread_local KernelEvents ev;
+  return ev;
+}
 
 // One workgroup per 16-row group; one wave per unit of kGemvUnit tiles of the
 // row, up to 16 (Q4_0, one matrix) or 8 waves; rows wider than that take

@@ -656,14 +656,31 @@ hipEvent_t next_event(ss_hip_model* m) {
   return m->ev_pool[m->ev_used++];
 }
 
-// Launch with optional event bracketing (profiling mode only; never inside a capture).
+// Launch with timing events (profiling mode only; never inside a capture):
+// matvec and attention launches hand the events to their dispatch, which
+// records them at kernel start and end; other launches are bracketed by
+// events on the stream.
 template <class F>
 hipError_t timed(ss_hip_model* m, int cls, double bytes, F&& launch) {
   if (!m->prof) return launch();
   ProfRec r{cls, bytes, next_event(m), next_event(m)};
-  hipEventRecord(r.a, m->ctx->stream);
+  ssk::KernelEvents& ke = ssk::kernel_events();
+  if (cls == PC_Q4 || cls == PC_Q8 || cls == PC_ATTN) {
+    ke.start = r.a;
+    ke.stop = r.b;
+    ke.used = false;
+  } else {
+    hipEventRecord(r.a, m->ctx->stream);
+  }
   hipError_t e = launch();
-  hipEventRecord(r.b, m->ctx->stream);
+  if (ke.start) {
+    if (!ke.used) {   // the launch failed before its dispatch: empty interval
+      hipEventRecord(r.a, m->ctx->stream);
+      hipEventRecord(r.b, m->ctx->stream);
+    }
+    ke = ssk::KernelEvents();
+  }
+  if (cls != PC_Q4 && cls != PC_Q8 && cls != PC_ATTN) hipEventRecord(r.b, m->ctx->stream);
   m->prof_recs.push_back(r);
   return e;
 }

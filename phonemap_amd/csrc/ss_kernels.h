@@ -63,6 +63,15 @@ struct AttnArgs {
                              // for a merging consumer (ns <= kMergeSplits)
 };
 
+// Profiling: when start is set, the next matvec or attention launch on this
+// thread passes start/stop to hipExtLaunchKernel, so the dispatch records them
+// when the kernel begins and ends (kernel execution time), and sets used.
+struct KernelEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+  bool used = false;
+};
+KernelEvents& kernel_events();   // this thread's
+
 struct GemvPlan {
   int grid, threads, unit;
   size_t lds_bytes;

@@ -7,6 +7,8 @@
 
 #include <math.h>
 
+#include <hip/hip_ext.h>
+
 #include "ss_device.h"
 #include "ss_kernels.h"
 
@@ -428,10 +430,18 @@ __global__ void k_advance(int* dpos) { *dpos += 1; }
 template <int HD, int G>
 hipError_t launch_attn_t(int kv_type, const AttnArgs& a, hipStream_t s) {
   const dim3 grid(a.ns, a.n_kv_heads);
-  if (kv_type == 0)
+  KernelEvents& ev = kernel_events();
+  if (ev.start) {
+    if (kv_type == 0)
+      hipExtLaunchKernelGGL((k_attn<HD, G, 0>), grid, dim3(kAttnWaves * 64), 0, s, ev.start, ev.stop, 0, a);
+    else
+      hipExtLaunchKernelGGL((k_attn<HD, G, 1>), grid, dim3(kAttnWaves * 64), 0, s, ev.start, ev.stop, 0, a);
+    ev.used = true;
+  } else if (kv_type == 0) {
     hipLaunchKernelGGL((k_attn<HD, G, 0>), grid, dim3(kAttnWaves * 64), 0, s, a);
-  else
+  } else {
     hipLaunchKernelGGL((k_attn<HD, G, 1>), grid, dim3(kAttnWaves * 64), 0, s, a);
+  }
   return hipGetLastError();
 }
 
