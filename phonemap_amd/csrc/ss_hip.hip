@@ -152,10 +152,17 @@ void rope_row(float* cs, int rope_dim, int pos, float theta) {
 }
 
 // Splits per KV head: enough that a split of the longest context is one round
-// of k_attn loads (one HBM latency per split), at most kMaxSplits.
-int attn_splits(int head_dim, int group, int max_seq) {
+// of attention loads (one HBM latency per split), but no more than the
+// workgroups of all KV heads that are resident at once (a second generation
+// of workgroups would cost a whole split's latency again), at most kMaxSplits.
+int attn_splits(int head_dim, int group, int max_seq, int kv_type, int n_kv_heads, int n_cu) {
   const int round = ssk::attn_round_positions(head_dim, group);
   int ns = (max_seq + round - 1) / round;
+  const int per_cu = ssk::attn_resident_groups(head_dim, group, kv_type);
+  if (per_cu > 0 && n_cu > 0 && n_kv_heads > 0) {
+    const int cap = per_cu * n_cu / n_kv_heads;
+    if (ns > cap) ns = cap;
+  }
   if (ns > ssk::kMaxSplits) ns = ssk::kMaxSplits;
   if (ns < 1) ns = 1;
   return ns;
@@ -391,7 +398,7 @@ int32_t ss_hip_attention(ss_hip_ctx_t* c, float* out, const float* q, const void
   const int group = n_heads / n_kv_heads;
   if (!ssk::attention_supported(head_dim, group))
     return fail(kErrParams, "attention: head_dim %d / group %d not supported", head_dim, group);
-  const int ns = attn_splits(head_dim, group, max_seq);
+  const int ns = attn_splits(head_dim, group, max_seq, kv_type, n_kv_heads, c->n_cu);
   int32_t rc = ensure(c, (void**)&c->att_o, &c->att_o_floats,
                       sizeof(float) * (size_t)n_kv_heads * ns * group * head_dim, false);
   if (!rc) rc = ensure(c, (void**)&c->att_ml, &c->att_ml_floats,
@@ -1191,7 +1198,7 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
   m->qdim = m->H * m->hd;
   m->kvdim = m->KVH * m->hd;
   m->group = group;
-  m->ns = attn_splits(m->hd, m->group, m->max_seq);
+  m->ns = attn_splits(m->hd, m->group, m->max_seq, m->kv_type, m->KVH, c->n_cu);
 
   auto bail = [&](void) -> ss_hip_model_t* {
     model_release(m);

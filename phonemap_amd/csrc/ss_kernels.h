@@ -85,8 +85,10 @@ hipError_t launch_argmax_merge(const float2* part, int n, const float* y, int* o
                                int* dpos, hipStream_t s);
 hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, hipStream_t s);
 bool attention_supported(int head_dim, int group);
-// positions one k_attn workgroup covers in one round of loads
+// positions one attention workgroup covers in one round of loads
 int attn_round_positions(int head_dim, int group);
+// attention workgroups of this shape resident on one compute unit (0: unknown)
+int attn_resident_groups(int head_dim, int group, int kv_type);
 
 hipError_t launch_pack(int type, const uint8_t* src, uint8_t* qs, uint16_t* ds, int64_t nblocks,
                        int nb, int64_t row_off, hipStream_t s);

@@ -74,6 +74,149 @@ __host__ __device__ constexpr int attn_rows_per_lane(int group) {
   return group >= 8 ? 1 : group >= 4 ? 2 : 4;
 }
 
+// The workgroup's W waves hold per-wave (m, l, o) for the G heads in LDS:
+// combine them, then either write the output (one active split), leave the
+// split's partials for a merging consumer (a.cnt null), or write them and let
+// the last split of this KV head to finish merge all of them.
+template <int HD, int G, int W>
+__device__ __forceinline__ void attn_finish(const AttnArgs& a, int kvh, int active, const float (&wm)[W][G],
+                                            const float (&wl)[W][G], const float (&wo)[W][G][HD], int tid) {
+  const int lane = tid & 63, wave = tid >> 6;
+  constexpr int kThreads = W * 64;
+  if (a.cnt && active == 1) {
+    // the only split: the output directly (the merge below with one split)
+    for (int i = tid; i < G * HD; i += kThreads) {
+      const int g = i / HD, d = i % HD;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < W; ++w) M = fmaxf(M, wm[w][g]);
+      float so = 0.f, sl = 0.f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) {
+        const float f = expf(wm[w][g] - M);
+        so = fmaf(f, wo[w][g][d], so);
+        sl = fmaf(f, wl[w][g], sl);
+      }
+      a.out[((size_t)kvh * G + g) * HD + d] = so * (1.0f / sl);
+    }
+    return;
+  }
+  float* po = a.part_o + (((size_t)kvh * a.ns + blockIdx.x) * G) * HD;
+  float* pml = a.part_ml + (((size_t)kvh * a.ns + blockIdx.x) * G) * 2;
+  for (int i = tid; i < G * HD; i += kThreads) {
+    const int g = i / HD, d = i % HD;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) M = fmaxf(M, wm[w][g]);   // finite: wave 0 has position t0
+    float so = 0.f, sl = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      const float f = expf(wm[w][g] - M);
+      so = fmaf(f, wo[w][g][d], so);
+      sl = fmaf(f, wl[w][g], sl);
+    }
+    if (a.cnt) {   // merged below by another workgroup: coherent stores
+      cstf(po + g * HD + d, so);
+      if (d == 0) {
+        cstf(pml + g * 2, M);
+        cstf(pml + g * 2 + 1, sl);
+      }
+    } else {       // merged by the next kernel
+      po[g * HD + d] = so;
+      if (d == 0) {
+        pml[g * 2] = M;
+        pml[g * 2 + 1] = sl;
+      }
+    }
+  }
+  if (!a.cnt) return;   // the consumer (the Wo matvec) merges the splits
+
+  // The last split of this KV head to finish merges all of them:
+  // out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).
+  __shared__ uint32_t last;
+  __shared__ float wts[kMaxSplits * G];
+  vm_drain();        // this wave's partials have reached the coherent level
+  __syncthreads();
+  if (tid == 0)
+    last = __hip_atomic_fetch_add(a.cnt + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+           (uint32_t)(active - 1);
+  __syncthreads();
+  if (!last) return;
+  const float* ml = a.part_ml + (size_t)kvh * a.ns * G * 2;
+  const float* pob = a.part_o + (size_t)kvh * a.ns * G * HD;
+  // Thread (sub, quad) sums four consecutive outputs over the splits
+  // sub, sub + kSub, ..., kBatch 16-byte coherent loads in flight at a time
+  // (out-of-range loads of the buffer view read zero); the kSub partial sums
+  // are then added in subset order. The batch is smaller for small groups,
+  // whose registers the main loop does not fill (occupancy). The first batch
+  // is requested before the split weights are formed.
+  constexpr int kBatch = G >= 4 ? 16 : 8;
+  constexpr int kQuads = G * HD / 4;
+  constexpr int kSub = kThreads / kQuads;
+  static_assert(kThreads % kQuads == 0, "outputs in quads must divide the workgroup");
+  __shared__ float4 red[kThreads];
+  const int qd = tid % kQuads, sub = tid / kQuads;
+  const int gq = qd * 4 / HD;
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(pob), (short)0, active * G * HD * 4, kBufferFlags);
+  float4 v[kBatch];
+  auto fetch = [&](int sp0) {
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k)   // the builtin returns the 16 bytes as four 32-bit integers
+      v[k] = __builtin_bit_cast(
+          float4, __builtin_amdgcn_raw_buffer_load_b128(ro, ((sp0 + k * kSub) * kQuads + qd) * 16, 0, kSc1));
+  };
+  fetch(sub);
+  for (int g = wave; g < G; g += W) {
+    float mx = -INFINITY;
+    float mv[kMaxSplits / kWave], lv[kMaxSplits / kWave];
+#pragma unroll
+    for (int k = 0; k < kMaxSplits / kWave; ++k) {
+      const int sp = lane + k * kWave;
+      mv[k] = sp < active ? cldf(ml + (sp * G + g) * 2) : -INFINITY;
+      lv[k] = sp < active ? cldf(ml + (sp * G + g) * 2 + 1) : 0.f;
+    }
+    for (int k = 0; k < kMaxSplits / kWave; ++k) mx = fmaxf(mx, mv[k]);
+    mx = wave_max(mx);
+    float ls = 0.f;
+#pragma unroll
+    for (int k = 0; k < kMaxSplits / kWave; ++k) ls += lv[k] * expf(mv[k] - mx);
+    const float inv = 1.0f / wave_sum(ls);
+#pragma unroll
+    for (int k = 0; k < kMaxSplits / kWave; ++k) {
+      const int sp = lane + k * kWave;
+      if (sp < active) wts[sp * G + g] = expf(mv[k] - mx) * inv;
+    }
+  }
+  __syncthreads();
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int sp0 = sub; sp0 < active; sp0 += kBatch * kSub) {
+    if (sp0 != sub) fetch(sp0);
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int sp = sp0 + k * kSub;
+      const float w = sp < active ? wts[sp * G + gq] : 0.f;
+      acc.x = fmaf(v[k].x, w, acc.x);
+      acc.y = fmaf(v[k].y, w, acc.y);
+      acc.z = fmaf(v[k].z, w, acc.z);
+      acc.w = fmaf(v[k].w, w, acc.w);
+    }
+  }
+  red[tid] = acc;
+  __syncthreads();
+  if (sub == 0) {
+    for (int k = 1; k < kSub; ++k) {
+      const float4 r = red[k * kQuads + qd];
+      acc.x += r.x;
+      acc.y += r.y;
+      acc.z += r.z;
+      acc.w += r.w;
+    }
+    reinterpret_cast<float4*>(a.out + (size_t)kvh * G * HD)[qd] = acc;
+  }
+  if (tid == 0) cst(a.cnt + kvh, 0u);   // every split of this launch has arrived: ready for the next
+}
+
 template <int HD, int G, int KVT>
 __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
   using KE = KvElem<KVT>;
@@ -193,136 +336,171 @@ __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
     }
   }
   __syncthreads();
-  constexpr int kThreads = kAttnWaves * 64;
-  if (a.cnt && active == 1) {
-    // the only split: the output directly (the merge below with one split)
-    for (int i = tid; i < G * HD; i += kThreads) {
-      const int g = i / HD, d = i % HD;
-      float M = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, wm[w][g]);
-      float so = 0.f, sl = 0.f;
-#pragma unroll
-      for (int w = 0; w < kAttnWaves; ++w) {
-        const float f = expf(wm[w][g] - M);
-        so = fmaf(f, wo[w][g][d], so);
-        sl = fmaf(f, wl[w][g], sl);
-      }
-      a.out[((size_t)kvh * G + g) * HD + d] = so * (1.0f / sl);
-    }
-    return;
-  }
-  float* po = a.part_o + (((size_t)kvh * a.ns + blockIdx.x) * G) * HD;
-  float* pml = a.part_ml + (((size_t)kvh * a.ns + blockIdx.x) * G) * 2;
-  for (int i = tid; i < G * HD; i += kThreads) {
-    const int g = i / HD, d = i % HD;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) M = fmaxf(M, wm[w][g]);   // finite: wave 0 has position t0
-    float so = 0.f, sl = 0.f;
-#pragma unroll
-    for (int w = 0; w < kAttnWaves; ++w) {
-      const float f = expf(wm[w][g] - M);
-      so = fmaf(f, wo[w][g][d], so);
-      sl = fmaf(f, wl[w][g], sl);
-    }
-    if (a.cnt) {   // merged below by another workgroup: coherent stores
-      cstf(po + g * HD + d, so);
-      if (d == 0) {
-        cstf(pml + g * 2, M);
-        cstf(pml + g * 2 + 1, sl);
-      }
-    } else {       // merged by the next kernel
-      po[g * HD + d] = so;
-      if (d == 0) {
-        pml[g * 2] = M;
-        pml[g * 2 + 1] = sl;
-      }
-    }
-  }
-  if (!a.cnt) return;   // the consumer (the Wo matvec) merges the splits
+  attn_finish<HD, G, kAttnWaves>(a, kvh, active, wm, wl, wo, tid);
+}
 
-  // The last split of this KV head to finish merges all of them:
-  // out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).
-  __shared__ uint32_t last;
-  __shared__ float wts[kMaxSplits * G];
-  vm_drain();        // this wave's partials have reached the coherent level
-  __syncthreads();
-  if (tid == 0)
-    last = __hip_atomic_fetch_add(a.cnt + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-           (uint32_t)(active - 1);
-  __syncthreads();
-  if (!last) return;
-  const float* ml = a.part_ml + (size_t)kvh * a.ns * G * 2;
-  const float* pob = a.part_o + (size_t)kvh * a.ns * G * HD;
-  for (int g = wave; g < G; g += kAttnWaves) {
-    float mx = -INFINITY;
-    float mv[kMaxSplits / kWave], lv[kMaxSplits / kWave];
+// ------------------------------------------------------------ attention, heads on lanes
+// For groups of 4 or 8 query heads per KV head: lane l of a wave serves query
+// head l / (64/G) of the group and dims [c*DPL, c*DPL + DPL), c = l % (64/G),
+// DPL = HD*G/64, so a wave covers all G heads of one K/V row at once (64
+// lanes x DPL = G x HD multiply-adds per position). Scores are summed over
+// the 64/G lanes of a head with DPP. Each wave takes a contiguous share of the
+// workgroup's positions in batches of B rows (all of a batch's K and V
+// loaded before any is used, the next batch's loads issued before the
+// current one is used), keeps an online softmax per head (every lane of a
+// head holds the same m, l), and the waves are combined at the end by
+// attn_finish. Per lane: DPL query values, DPL outputs and two batches.
+constexpr int kHgWaves = 8;
+
+// B: rows of K and V per lane per batch; two batches (the one in use and
+// the next, in flight) hold at most 64 VGPRs: 2 * B * DPL words of fp16
+__host__ __device__ constexpr int hg_batch(int hd, int group) {
+  return 32 / (hd * group / kWave);
+}
+
+// N elements of one K or V row (fp16, or int8 times the row's scale)
+template <int KVT, int N>
+struct KvRow {
+  static constexpr int kWords = N * (KVT == 0 ? 2 : 1) / 4;
+  uint32_t w[kWords];
+  __device__ __forceinline__ void load(const uint8_t* p) {
+    if constexpr (kWords == 1) {
+      w[0] = *reinterpret_cast<const uint32_t*>(p);
+    } else if constexpr (kWords == 2) {
+      const uint2 v = *reinterpret_cast<const uint2*>(p);
+      w[0] = v.x;
+      w[1] = v.y;
+    } else {
 #pragma unroll
-    for (int k = 0; k < kMaxSplits / kWave; ++k) {
-      const int sp = lane + k * kWave;
-      mv[k] = sp < active ? cldf(ml + (sp * G + g) * 2) : -INFINITY;
-      lv[k] = sp < active ? cldf(ml + (sp * G + g) * 2 + 1) : 0.f;
-    }
-    for (int k = 0; k < kMaxSplits / kWave; ++k) mx = fmaxf(mx, mv[k]);
-    mx = wave_max(mx);
-    float ls = 0.f;
-#pragma unroll
-    for (int k = 0; k < kMaxSplits / kWave; ++k) ls += lv[k] * expf(mv[k] - mx);
-    const float inv = 1.0f / wave_sum(ls);
-#pragma unroll
-    for (int k = 0; k < kMaxSplits / kWave; ++k) {
-      const int sp = lane + k * kWave;
-      if (sp < active) wts[sp * G + g] = expf(mv[k] - mx) * inv;
-    }
-  }
-  __syncthreads();
-  // Thread (sub, quad) sums four consecutive outputs over the splits
-  // sub, sub + kSub, ..., kBatch 16-byte coherent loads in flight at a time
-  // (out-of-range loads of the buffer view read zero); the kSub partial sums
-  // are then added in subset order. The batch is smaller for small groups,
-  // whose registers the main loop does not fill (occupancy).
-  constexpr int kBatch = G >= 4 ? 16 : 8;
-  constexpr int kQuads = G * HD / 4;
-  constexpr int kSub = kThreads / kQuads;
-  static_assert(kThreads % kQuads == 0, "outputs in quads must divide the workgroup");
-  __shared__ float4 red[kThreads];
-  const int qd = tid % kQuads, sub = tid / kQuads;
-  const int g = qd * 4 / HD;
-  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(pob), (short)0, active * G * HD * 4, kBufferFlags);
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int sp0 = sub; sp0 < active; sp0 += kBatch * kSub) {
-    float4 v[kBatch];
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int sp = sp0 + k * kSub;   // past the last split: offset out of range, reads zero
-      // the builtin returns the 16 bytes as four 32-bit integers
-      v[k] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(ro, (sp * kQuads + qd) * 16, 0, kSc1));
-    }
-#pragma unroll
-    for (int k = 0; k < kBatch; ++k) {
-      const int sp = sp0 + k * kSub;
-      const float w = sp < active ? wts[sp * G + g] : 0.f;
-      acc.x = fmaf(v[k].x, w, acc.x);
-      acc.y = fmaf(v[k].y, w, acc.y);
-      acc.z = fmaf(v[k].z, w, acc.z);
-      acc.w = fmaf(v[k].w, w, acc.w);
+      for (int i = 0; i < kWords / 4; ++i) {
+        const uint4 v = reinterpret_cast<const uint4*>(p)[i];
+        w[4 * i] = v.x;
+        w[4 * i + 1] = v.y;
+        w[4 * i + 2] = v.z;
+        w[4 * i + 3] = v.w;
+      }
     }
   }
-  red[tid] = acc;
-  __syncthreads();
-  if (sub == 0) {
-    for (int k = 1; k < kSub; ++k) {
-      const float4 r = red[k * kQuads + qd];
-      acc.x += r.x;
-      acc.y += r.y;
-      acc.z += r.z;
-      acc.w += r.w;
-    }
-    reinterpret_cast<float4*>(a.out + (size_t)kvh * G * HD)[qd] = acc;
+  __device__ __forceinline__ float get(int i, float s) const {
+    if constexpr (KVT == 0)
+      return h2f((uint16_t)(w[i / 2] >> (16 * (i % 2))));
+    else
+      return (float)(int8_t)((w[i / 4] >> (8 * (i % 4))) & 0xffu) * s;
   }
-  if (tid == 0) cst(a.cnt + kvh, 0u);   // every split of this launch has arrived: ready for the next
+};
+
+template <int HD, int G, int KVT>
+__global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
+  constexpr int kLph = kWave / G;          // lanes per head
+  constexpr int kDpl = HD / kLph;          // dims per lane
+  constexpr int kB = hg_batch(HD, G);
+  constexpr int kEb = KVT == 0 ? 2 : 1;
+  using Row = KvRow<KVT, kDpl>;
+  static_assert(kLph == 8 || kLph == 16, "heads of 8 or 16 lanes");
+
+  __shared__ float wm[kHgWaves][G], wl[kHgWaves][G];
+  __shared__ float wo[kHgWaves][G][HD];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kvh = blockIdx.y;
+  int ctx, chunk, active;
+  attn_split(a, ctx, chunk, active);
+  if ((int)blockIdx.x >= active) return;   // whole workgroup
+  const int t0 = blockIdx.x * chunk;
+  const int t1 = min(ctx, t0 + chunk);
+  const int h = lane / kLph, c = lane % kLph;
+  // this wave's positions: a contiguous share of [t0, t1) (wave 0's holds t0)
+  const int per = (t1 - t0 + kHgWaves - 1) / kHgWaves;
+  const int p0 = t0 + wave * per;
+  const int p1 = min(t1, p0 + per);
+
+  const size_t head_base = (size_t)kvh * a.max_seq;
+  const uint8_t* kb = static_cast<const uint8_t*>(a.kc) + (head_base * HD + c * kDpl) * kEb;
+  const uint8_t* vb = static_cast<const uint8_t*>(a.vc) + (head_base * HD + c * kDpl) * kEb;
+
+  float q[kDpl], o[kDpl];
+  {
+    const float4* qp = reinterpret_cast<const float4*>(a.q + ((size_t)kvh * G + h) * HD + c * kDpl);
+#pragma unroll
+    for (int i = 0; i < kDpl / 4; ++i) {
+      const float4 x = qp[i];
+      q[4 * i] = x.x;
+      q[4 * i + 1] = x.y;
+      q[4 * i + 2] = x.z;
+      q[4 * i + 3] = x.w;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kDpl; ++i) o[i] = 0.f;
+  float m = -INFINITY, l = 0.f;
+
+  struct Batch {
+    Row k[kB], v[kB];
+    float ks[kB], vs[kB];
+  };
+  // rows past p1 reload p1 - 1 (branch-free; masked in use)
+  auto load = [&](Batch& bt, int pb) {
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      const int p = min(pb + j, p1 - 1);
+      bt.k[j].load(kb + (size_t)p * HD * kEb);
+      bt.v[j].load(vb + (size_t)p * HD * kEb);
+      if constexpr (KVT == 1) {
+        bt.ks[j] = a.ks[p];
+        bt.vs[j] = a.vs[p];
+      } else {
+        bt.ks[j] = bt.vs[j] = 1.f;
+      }
+    }
+  };
+  auto use = [&](const Batch& bt, int pb) {
+    float sc[kB];
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < kDpl; ++i) d = fmaf(q[i], bt.k[j].get(i, bt.ks[j]), d);
+      d = sum_lanes<kLph>(d) * a.scale;   // (q . k) * (1/sqrt(hd)), layer_scheduler.c:442-446
+      sc[j] = pb + j < p1 ? d : -INFINITY;
+    }
+    float bm = sc[0];                      // live: pb < p1
+#pragma unroll
+    for (int j = 1; j < kB; ++j) bm = fmaxf(bm, sc[j]);
+    const float mn = fmaxf(m, bm);
+    const float corr = expf(m - mn);      // 0 on the first batch (m = -inf)
+    l *= corr;
+#pragma unroll
+    for (int i = 0; i < kDpl; ++i) o[i] *= corr;
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+      const float pj = expf(sc[j] - mn);
+      l += pj;
+#pragma unroll
+      for (int i = 0; i < kDpl; ++i) o[i] = fmaf(pj, bt.v[j].get(i, bt.vs[j]), o[i]);
+    }
+    m = mn;
+  };
+  if (p0 < p1) {
+    Batch A, B;
+    load(A, p0);
+    for (int pb = p0;; pb += 2 * kB) {
+      load(B, pb + kB);
+      use(A, pb);
+      if (pb + kB >= p1) break;
+      load(A, pb + 2 * kB);
+      use(B, pb + kB);
+      if (pb + 2 * kB >= p1) break;
+    }
+  }
+
+  if (c == 0) {
+    wm[wave][h] = m;   // a wave without positions: -inf and 0, weight 0 below
+    wl[wave][h] = l;
+  }
+#pragma unroll
+  for (int i = 0; i < kDpl; ++i) wo[wave][h][c * kDpl + i] = o[i];
+  __syncthreads();
+  attn_finish<HD, G, kHgWaves>(a, kvh, active, wm, wl, wo, tid);
 }
 
 // ------------------------------------------------------------ small kernels
@@ -431,18 +609,34 @@ template <int HD, int G>
 hipError_t launch_attn_t(int kv_type, const AttnArgs& a, hipStream_t s) {
   const dim3 grid(a.ns, a.n_kv_heads);
   KernelEvents& ev = kernel_events();
-  if (ev.start) {
-    if (kv_type == 0)
-      hipExtLaunchKernelGGL((k_attn<HD, G, 0>), grid, dim3(kAttnWaves * 64), 0, s, ev.start, ev.stop, 0, a);
-    else
-      hipExtLaunchKernelGGL((k_attn<HD, G, 1>), grid, dim3(kAttnWaves * 64), 0, s, ev.start, ev.stop, 0, a);
-    ev.used = true;
-  } else if (kv_type == 0) {
-    hipLaunchKernelGGL((k_attn<HD, G, 0>), grid, dim3(kAttnWaves * 64), 0, s, a);
+  if constexpr (G >= 4) {   // heads on lanes
+    const dim3 block(kHgWaves * 64);
+    if (ev.start) {
+      if (kv_type == 0)
+        hipExtLaunchKernelGGL((k_attn_hg<HD, G, 0>), grid, block, 0, s, ev.start, ev.stop, 0, a);
+      else
+        hipExtLaunchKernelGGL((k_attn_hg<HD, G, 1>), grid, block, 0, s, ev.start, ev.stop, 0, a);
+      ev.used = true;
+    } else if (kv_type == 0) {
+      hipLaunchKernelGGL((k_attn_hg<HD, G, 0>), grid, block, 0, s, a);
+    } else {
+      hipLaunchKernelGGL((k_attn_hg<HD, G, 1>), grid, block, 0, s, a);
+    }
+    return hipGetLastError();
   } else {
-    hipLaunchKernelGGL((k_attn<HD, G, 1>), grid, dim3(kAttnWaves * 64), 0, s, a);
+    if (ev.start) {
+      if (kv_type == 0)
+        hipExtLaunchKernelGGL((k_attn<HD, G, 0>), grid, dim3(kAttnWaves * 64), 0, s, ev.start, ev.stop, 0, a);
+      else
+        hipExtLaunchKernelGGL((k_attn<HD, G, 1>), grid, dim3(kAttnWaves * 64), 0, s, ev.start, ev.stop, 0, a);
+      ev.used = true;
+    } else if (kv_type == 0) {
+      hipLaunchKernelGGL((k_attn<HD, G, 0>), grid, dim3(kAttnWaves * 64), 0, s, a);
+    } else {
+      hipLaunchKernelGGL((k_attn<HD, G, 1>), grid, dim3(kAttnWaves * 64), 0, s, a);
+    }
+    return hipGetLastError();
   }
-  return hipGetLastError();
 }
 
 template <int HD>
@@ -458,7 +652,40 @@ hipError_t launch_attn_hd(int group, int kv_type, const AttnArgs& a, hipStream_t
 
 }  // namespace
 
+namespace {
+template <int HD, int G>
+const void* attn_kernel_t(int kv_type) {
+  if constexpr (G >= 4)
+    return kv_type == 0 ? reinterpret_cast<const void*>(&k_attn_hg<HD, G, 0>)
+                        : reinterpret_cast<const void*>(&k_attn_hg<HD, G, 1>);
+  else
+    return kv_type == 0 ? reinterpret_cast<const void*>(&k_attn<HD, G, 0>)
+                        : reinterpret_cast<const void*>(&k_attn<HD, G, 1>);
+}
+template <int HD>
+const void* attn_kernel_hd(int group, int kv_type) {
+  switch (group) {
+    case 1: return attn_kernel_t<HD, 1>(kv_type);
+    case 2: return attn_kernel_t<HD, 2>(kv_type);
+    case 4: return attn_kernel_t<HD, 4>(kv_type);
+    case 8: return attn_kernel_t<HD, 8>(kv_type);
+    default: return nullptr;
+  }
+}
+}  // namespace
+
+int attn_resident_groups(int head_dim, int group, int kv_type) {
+  const void* f = head_dim == 64 ? attn_kernel_hd<64>(group, kv_type)
+                : head_dim == 128 ? attn_kernel_hd<128>(group, kv_type) : nullptr;
+  if (!f) return 0;
+  const int threads = (group >= 4 ? kHgWaves : kAttnWaves) * kWave;
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, threads, 0) != hipSuccess) return 0;
+  return n;
+}
+
 int attn_round_positions(int head_dim, int group) {
+  if (group >= 4) return kHgWaves * hg_batch(head_dim, group);   // k_attn_hg: one batch per wave
   const int rows_per_load = kWave / (head_dim / 8);
   return attn_rows_per_lane(group) * kAttnWaves * rows_per_load;
 }
