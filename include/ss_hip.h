@@ -83,6 +83,13 @@ int32_t ss_hip_pack_matrix(ss_hip_ctx_t *ctx, void *dst_dev, const void *src_hos
  * ss_metal_matvec_q4_0 (metal_backend.h:37-42). */
 int32_t ss_hip_matvec(ss_hip_ctx_t *ctx, float *y_dev, const void *w_dev, const float *x_dev,
                       int32_t rows, int32_t cols, int32_t ggml_type, void *stream);
+/* The same for one block type: ss_metal_matvec_q4_0 (metal_backend.h:37-42)
+ * on device buffers, and its Q8_0 counterpart (the reference has Q8_0 on the
+ * CPU only, quantize.c:139-149, 446-494). */
+int32_t ss_hip_matvec_q4_0(ss_hip_ctx_t *ctx, float *y_dev, const void *w_dev, const float *x_dev,
+                           int32_t rows, int32_t cols, void *stream);
+int32_t ss_hip_matvec_q8_0(ss_hip_ctx_t *ctx, float *y_dev, const void *w_dev, const float *x_dev,
+                           int32_t rows, int32_t cols, void *stream);
 
 /* y = W rmsnorm(x, nw, eps) (+ y when accumulate != 0): the matvec with the
  * RMSNorm of tensor.c:114-131 folded in front and the residual add of

@@ -323,6 +323,16 @@ int32_t ss_hip_matvec(ss_hip_ctx_t* c, float* y, const void* w, const float* x, 
   return ss_hip_matvec_fused(c, y, w, x, nullptr, 0.f, 0, rows, cols, type, stream);
 }
 
+int32_t ss_hip_matvec_q4_0(ss_hip_ctx_t* c, float* y, const void* w, const float* x, int32_t rows,
+                           int32_t cols, void* stream) {
+  return ss_hip_matvec(c, y, w, x, rows, cols, SS_HIP_Q4_0, stream);
+}
+
+int32_t ss_hip_matvec_q8_0(ss_hip_ctx_t* c, float* y, const void* w, const float* x, int32_t rows,
+                           int32_t cols, void* stream) {
+  return ss_hip_matvec(c, y, w, x, rows, cols, SS_HIP_Q8_0, stream);
+}
+
 int32_t ss_hip_matvec_fused(ss_hip_ctx_t* c, float* y, const void* w, const float* x,
                             const float* nw, float eps, int32_t accumulate, int32_t rows,
                             int32_t cols, int32_t type, void* stream) {

@@ -45,6 +45,24 @@ def test_matvec(hip, qtype, rows, cols):
 
 
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+def test_matvec_typed_entry_points(hip, qtype):
+    """ss_hip_matvec_q4_0 / _q8_0 give ss_hip_matvec's result bit for bit."""
+    rows, cols = 300, 4096
+    rng = np.random.default_rng(5)
+    w = make_blocks(qtype, rows, cols, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    W, X, Y1, Y2 = hip.packed(w, qtype, rows, cols), hip.upload(x), hip.buf(4 * rows), hip.buf(4 * rows)
+    assert hip.L.ss_hip_matvec(hip.ctx, Y1.ptr, W.ptr, X.ptr, rows, cols, qtype, None) == 0
+    typed = hip.L.ss_hip_matvec_q4_0 if qtype == Q4_0 else hip.L.ss_hip_matvec_q8_0
+    assert typed(hip.ctx, Y2.ptr, W.ptr, X.ptr, rows, cols, None) == 0, hip.err()
+    a, b = Y1.read(np.float32, rows), Y2.read(np.float32, rows)
+    assert np.array_equal(a, b)
+    assert rel_err(b, oracle.matvec(w, x, rows, cols, qtype)) <= TOL
+    for buf in (W, X, Y1, Y2):
+        buf.free()
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
 def test_matvec_fused_norm_residual(hip, qtype):
     rows, cols, eps = 300, 4096, 1e-5
     rng = np.random.default_rng(11)
