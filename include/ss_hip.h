@@ -86,6 +86,16 @@ int32_t ss_hip_matvec(ss_hip_ctx_t *ctx, float *y_dev, const void *w_dev, const 
 /* The same for one block type: ss_metal_matvec_q4_0 (metal_backend.h:37-42)
  * on device buffers, and its Q8_0 counterpart (the reference has Q8_0 on the
  * CPU only, quantize.c:139-149, 446-494). */
+/* Prompt products on MFMA: y[t] = W x[t] for n_tokens tokens (x [n][cols],
+ * y [n][rows], token-major), the matrix read once per 64 tokens. With nw,
+ * each token's x is RMSNorm'ed first (tensor.c:114-131, weight nw, eps);
+ * accumulate != 0 adds to y (the residual of layer_scheduler.c:484,566).
+ * Serves the layer-major prompt of ss_scheduler_prefill
+ * (layer_scheduler.c:681-803), which multiplies every token of a layer by
+ * the same matrices. */
+int32_t ss_hip_gemm(ss_hip_ctx_t *ctx, float *y_dev, const void *w_dev, const float *x_dev,
+                    const float *nw_dev, float eps, int32_t accumulate, int32_t rows, int32_t cols,
+                    int32_t n_tokens, int32_t ggml_type, void *stream);
 int32_t ss_hip_matvec_q4_0(ss_hip_ctx_t *ctx, float *y_dev, const void *w_dev, const float *x_dev,
                            int32_t rows, int32_t cols, void *stream);
 int32_t ss_hip_matvec_q8_0(ss_hip_ctx_t *ctx, float *y_dev, const void *w_dev, const float *x_dev,

@@ -41,6 +41,7 @@ _PROTOS = {
     "ss_hip_packed_bytes": (_sz, [_i32, _i32, _i32]),
     "ss_hip_pack_matrix": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32]),
     "ss_hip_matvec": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp]),
+    "ss_hip_gemm": (_i32, [_vp, _vp, _vp, _vp, _vp, _f32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "ss_hip_matvec_q4_0": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _vp]),
     "ss_hip_matvec_q8_0": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _vp]),
     "ss_hip_matvec_fused": (_i32, [_vp, _vp, _vp, _vp, _vp, _f32, _i32, _i32, _i32, _i32, _vp]),

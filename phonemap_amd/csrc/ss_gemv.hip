@@ -37,7 +37,6 @@ namespace {
 // dot products become exact integer sums (v_dot4) plus one fp32 rounding per
 // block. Words: [0,8) q1, [8,16) q2, [16,24) q3 (4 codes per word, column
 // order), [24] 8 * sum_j X_j (the Q4_0 offset term), [25] s3 (fp32 bits).
-constexpr int kXW = 28;   // words per block (7 x 16 B)
 
 // Q4_0 block (quantize.c:60-72): byte j holds weight j (low nibble) and
 // weight j+16 (high nibble), value = d * (nibble - 8). Returns
@@ -92,43 +91,6 @@ __device__ __forceinline__ float q8_block(const uint4 a, const uint4 b, const in
     if (l < 2) acc = s; else acc3 = s;
   }
   return fmaf((float)acc, 128.0f, (float)acc3);
-}
-
-__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
-  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
-         ((uint32_t)d << 24);
-}
-
-// Encode one group of 4 staged values (8 lanes per block, all active).
-__device__ __forceinline__ void encode4(int* xb, int sub, float4 v) {
-  float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
-  m = fmaxf(m, dpp<0xb1>(m));
-  m = fmaxf(m, dpp<0x4e>(m));
-  m = fmaxf(m, dpp<0x141>(m));
-  const float s3 = m * (1.0f / (127.0f * 16384.0f));
-  const float s1 = s3 * 16384.0f, s2 = s3 * 128.0f;
-  const float i1 = m > 0.f ? 127.0f / m : 0.f;   // 1 / s1
-  const float f[4] = {v.x, v.y, v.z, v.w};
-  int q1[4], q2[4], q3[4], X = 0;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    q1[k] = q8c(f[k] * i1);
-    const float r1 = fmaf((float)-q1[k], s1, f[k]);
-    q2[k] = q8c(r1 * (i1 * 128.0f));
-    const float r2 = fmaf((float)-q2[k], s2, r1);
-    q3[k] = q8c(r2 * (i1 * 16384.0f));
-    X += q1[k] * 16384 + q2[k] * 128 + q3[k];
-  }
-  X += dpp_i<0xb1>(X);
-  X += dpp_i<0x4e>(X);
-  X += dpp_i<0x141>(X);
-  xb[sub] = (int)pack4(q1[0], q1[1], q1[2], q1[3]);
-  xb[8 + sub] = (int)pack4(q2[0], q2[1], q2[2], q2[3]);
-  xb[16 + sub] = (int)pack4(q3[0], q3[1], q3[2], q3[3]);
-  if (sub == 0) {
-    xb[24] = 8 * X;
-    xb[25] = __float_as_int(m == m && m < INFINITY ? s3 : m);   // non-finite x stays non-finite
-  }
 }
 
 // A wave stages only the x slice of its own unit (UT*4 blocks of 32 values),

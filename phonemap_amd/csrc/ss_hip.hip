@@ -83,8 +83,9 @@ struct ss_hip_ctx {
   float* att_o = nullptr;
   float* att_ml = nullptr;
   uint32_t* att_cnt = nullptr;
+  float* g_ssq = nullptr;   // prompt products: sums of squares of x
 
-  size_t att_o_floats = 0, att_ml_floats = 0, att_cnt_bytes = 0;
+  size_t att_o_floats = 0, att_ml_floats = 0, att_cnt_bytes = 0, g_ssq_bytes = 0;
 
   // host-pointer plug (metal_backend.m:190-235 registry)
   std::unordered_map<const void*, void*> registry;
@@ -235,7 +236,7 @@ void ss_hip_free(ss_hip_ctx_t* c) {
   if (c->stream) hipStreamSynchronize(c->stream);
   for (auto& kv : c->registry) hipFree(kv.second);
   void* bufs[] = {c->staging, c->am_part, c->rope_row, c->att_o,
-                  c->att_ml, c->att_cnt, c->plug_x, c->plug_y};
+                  c->att_ml, c->att_cnt, c->g_ssq, c->plug_x, c->plug_y};
   for (void* b : bufs)
     if (b) hipFree(b);
   if (c->stream) hipStreamDestroy(c->stream);
@@ -321,6 +322,33 @@ static ssk::GemvArgs gemv_args(const void* w, const float* x, float* y, int rows
 int32_t ss_hip_matvec(ss_hip_ctx_t* c, float* y, const void* w, const float* x, int32_t rows,
                       int32_t cols, int32_t type, void* stream) {
   return ss_hip_matvec_fused(c, y, w, x, nullptr, 0.f, 0, rows, cols, type, stream);
+}
+
+int32_t ss_hip_gemm(ss_hip_ctx_t* c, float* y, const void* w, const float* x, const float* nw, float eps,
+                    int32_t accumulate, int32_t rows, int32_t cols, int32_t n_tokens, int32_t type, void* stream) {
+  if (!c || !y || !w || !x || rows <= 0 || cols <= 0 || cols % 32 || n_tokens <= 0 || !quant_type_ok(type))
+    return fail(kErrParams, "gemm: bad argument (rows %d cols %d tokens %d type %d)", rows, cols, n_tokens, type);
+  if (set_device(c)) return kErrBackend;
+  int32_t rc = ensure(c, (void**)&c->g_ssq, &c->g_ssq_bytes, sizeof(float) * n_tokens, false);
+  if (rc) return rc;
+  hipStream_t s = pick(c, stream);
+  if (nw) HIP_TRY(ssk::launch_sumsq(x, cols, n_tokens, c->g_ssq, s));
+  ssk::GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.w = view(w, type, rows, cols);
+  a.x = x;
+  a.nw = nw;
+  a.ssq = nw ? c->g_ssq : nullptr;
+  a.eps = eps;
+  a.y = y;
+  a.ldx = cols;
+  a.ldy = rows;
+  a.rows = rows;
+  a.cols = cols;
+  a.T = n_tokens;
+  a.type = type;
+  HIP_TRY(ssk::launch_gemm(accumulate ? ssk::EPI_ADD : ssk::EPI_STORE, a, s));
+  return 0;
 }
 
 int32_t ss_hip_matvec_q4_0(ss_hip_ctx_t* c, float* y, const void* w, const float* x, int32_t rows,

@@ -46,6 +46,17 @@ struct GemvArgs {
   int att_ns, att_group;     // splits per KV head, query heads per KV head
 };
 
+// Prompt products: Y[t] = W X[t] (+ epilogue) for T tokens on MFMA.
+struct GemmArgs {
+  PackedMat w, w2;           // w2: up projection for EPI_SWIGLU
+  const float* x;            // [T][ldx] token-major
+  const float* nw;           // RMSNorm weight [cols] applied to x, or nullptr
+  const float* ssq;          // [T] sums of squares of x: the RMSNorm scale applied, or nullptr
+  float eps;
+  float* y;                  // [T][ldy] (EPI_ADD: accumulated into)
+  int ldx, ldy, rows, cols, T, type;
+};
+
 struct AttnArgs {
   const float* q;            // [n_heads][hd]
   const void* kc;            // this layer: [kvh][max_seq][hd] fp16 or int8
@@ -84,6 +95,10 @@ hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t s);
 hipError_t launch_argmax_merge(const float2* part, int n, const float* y, int* out_idx, int* tokens,
                                int* dpos, hipStream_t s);
 hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, hipStream_t s);
+// ssq[t] = sum of x[t][c]^2 (x [T][cols])
+hipError_t launch_sumsq(const float* x, int cols, int T, float* ssq, hipStream_t s);
+// EPI_STORE, EPI_ADD, EPI_SWIGLU
+hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t s);
 bool attention_supported(int head_dim, int group);
 // positions one attention workgroup covers in one round of loads
 int attn_round_positions(int head_dim, int group);

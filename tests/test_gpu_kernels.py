@@ -63,6 +63,34 @@ def test_matvec_typed_entry_points(hip, qtype):
 
 
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
+@pytest.mark.parametrize("rows,cols,T", [(4096, 4096, 70), (48, 11008, 17), (300, 2048, 1), (12288, 4096, 64),
+                                         (40, 14368, 5)])
+def test_gemm_matches_oracle_per_token(hip, qtype, rows, cols, T):
+    """MFMA prompt product: every token's y = W rmsnorm(x, nw) within 1e-3 of
+    the oracle's RMSNorm + matvec; accumulate adds to y."""
+    print("gemm", qtype, rows, cols, T, flush=True)
+    rng = np.random.default_rng(rows + cols + T)
+    w = make_blocks(qtype, rows, cols, rng)
+    x = rng.standard_normal((T, cols)).astype(np.float32)
+    nw = (1.0 + 0.1 * rng.standard_normal(cols)).astype(np.float32)
+    y0 = rng.standard_normal((T, rows)).astype(np.float32)
+    W, X, NW = hip.packed(w, qtype, rows, cols), hip.upload(x), hip.upload(nw)
+    Y = hip.upload(y0)
+    assert hip.L.ss_hip_gemm(hip.ctx, Y.ptr, W.ptr, X.ptr, NW.ptr, C.c_float(1e-5), 1, rows, cols, T, qtype,
+                             None) == 0, hip.err()
+    acc = Y.read(np.float32, T * rows).reshape(T, rows)
+    assert hip.L.ss_hip_gemm(hip.ctx, Y.ptr, W.ptr, X.ptr, None, C.c_float(1e-5), 0, rows, cols, T, qtype,
+                             None) == 0, hip.err()
+    plain = Y.read(np.float32, T * rows).reshape(T, rows)
+    for t in range(T):
+        xn = oracle.rmsnorm(x[t], nw, 1e-5)
+        assert rel_err(acc[t] - y0[t], oracle.matvec(w, xn, rows, cols, qtype)) <= TOL, t
+        assert rel_err(plain[t], oracle.matvec(w, x[t], rows, cols, qtype)) <= TOL, t
+    for b in (W, X, NW, Y):
+        b.free()
+
+
+@pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
 def test_matvec_fused_norm_residual(hip, qtype):
     rows, cols, eps = 300, 4096, 1e-5
     rng = np.random.default_rng(11)
