@@ -199,9 +199,16 @@ void ss_hip_model_free(ss_hip_model_t *m);
 /* ss_scheduler_forward (layer_scheduler.h:107) */
 int32_t ss_hip_eval_token(ss_hip_model_t *m, int32_t token, int32_t pos, float *logits_host,
                           int32_t *argmax_out);
-/* ss_scheduler_prefill (layer_scheduler.h:119) */
+/* ss_scheduler_prefill (layer_scheduler.h:119). With an fp16 cache a prompt
+ * of at least the batch threshold (default 8 tokens) runs as matrix products
+ * over chunks of up to 512 tokens; shorter prompts and int8 caches run token
+ * by token. */
 int32_t ss_hip_eval_prompt(ss_hip_model_t *m, const int32_t *tokens, int32_t n,
                            int32_t start_pos, float *logits_host, int32_t *argmax_out);
+/* Batch threshold of ss_hip_eval_prompt: 0 restores the default, a negative
+ * value makes every prompt run token by token (no counterpart in the
+ * reference; for measurement and comparison). */
+int32_t ss_hip_set_prompt_batch(ss_hip_model_t *m, int32_t min_tokens);
 /* device-side greedy continuation (see ss_decode_greedy) */
 int32_t ss_hip_decode_greedy(ss_hip_model_t *m, int32_t n_steps, int32_t *tokens_out);
 /* ss_scheduler_reset (layer_scheduler.h:132) */

@@ -196,6 +196,11 @@ class Model:
         _check(rc, "ss_eval_prompt")
         return (lg, am.value) if want_logits else am.value
 
+    def set_prompt_batch(self, min_tokens):
+        """Shortest prompt evaluated as matrix products (0: default, < 0: never)."""
+        L = _lib()
+        _check(L.ss_hip_set_prompt_batch(L.ss_model_hip(self.h), min_tokens), "ss_hip_set_prompt_batch")
+
     def decode_greedy(self, n_steps):
         out = np.zeros(max(n_steps, 1), np.int32)
         _check(_lib().ss_decode_greedy(self.h, n_steps, _ptr(out, _ip)), "ss_decode_greedy")

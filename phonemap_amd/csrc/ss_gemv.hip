@@ -451,12 +451,14 @@ __global__ void k_pack(const uint8_t* __restrict__ src, uint8_t* __restrict__ qs
 }
 
 // Row `token` of a packed table, dequantised exactly as quantize.c:60-72 /
-// 139-149 (one fp32 multiply per weight).
+// 139-149 (one fp32 multiply per weight). With tokens set, workgroup z
+// writes row tokens[*dpos + z] to out + z * cols (a prompt's rows at once).
 template <int QT>
 __global__ void k_embed(PackedMat t, int cols, const int* tokens, const int* dpos, int token,
                         float* out) {
   constexpr int kQB = QTraits<QT>::kQB;
-  const int tok = tokens ? tokens[*dpos] : token;
+  const int tok = tokens ? tokens[*dpos + blockIdx.x] : token;
+  out += (size_t)blockIdx.x * cols;
   const int nb = cols >> 5;
   const int ntk = (nb + kTB - 1) / kTB;
   for (int b = threadIdx.x; b < nb; b += blockDim.x) {
@@ -621,6 +623,18 @@ hipError_t launch_embed(int type, PackedMat t, int cols, const int* tokens, cons
     hipLaunchKernelGGL(k_embed<2>, dim3(1), dim3(256), 0, s, t, cols, tokens, dpos, token, out);
   else if (type == 8)
     hipLaunchKernelGGL(k_embed<8>, dim3(1), dim3(256), 0, s, t, cols, tokens, dpos, token, out);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_embed_rows(int type, PackedMat t, int cols, const int* tokens, const int* dpos, int n,
+                             float* out, hipStream_t s) {
+  if (n <= 0 || !tokens || !dpos) return hipErrorInvalidValue;
+  if (type == 2)
+    hipLaunchKernelGGL(k_embed<2>, dim3(n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out);
+  else if (type == 8)
+    hipLaunchKernelGGL(k_embed<8>, dim3(n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -612,6 +612,11 @@ struct ss_hip_model {
   uint64_t host_bytes = 0;           // pinned bytes held
   int* pos_iota = nullptr;           // device [max_seq]: value i at index i
   float* hid_all = nullptr;          // device [max_seq][d]: residual streams of a prompt
+  // prompts as matrix products (fp16 KV): up to pf_cap tokens per pass over the
+  // layers, in row-major [token][...] buffers
+  int pf_min = 0;                    // shortest prompt evaluated this way (0: the default)
+  int pf_cap = 0;                    // chunk capacity (0: not set up)
+  float *pf_h = nullptr, *pf_qkv = nullptr, *pf_att = nullptr, *pf_f = nullptr, *pf_ssq = nullptr;
 };
 
 namespace {
@@ -1079,6 +1084,143 @@ int32_t enqueue_prompt_layer_major(ss_hip_model* m, const int32_t* tokens, int n
   return enqueue_head(m, m->hidden);
 }
 
+// ---- prompts as matrix products (ss_scheduler_prefill, layer_scheduler.c:681-803)
+// The reference evaluates a prompt layer by layer, each layer's matvecs once
+// per token. Here a chunk of up to kPrefillChunk tokens goes through each
+// layer as MFMA products of the quantised matrices with the chunk's rows
+// (ss_gemm.hip), one RoPE + fp16 append kernel and one attention launch
+// whose grid z is the token (each token attends to positions 0..its own, the
+// chunk's K/V having been appended first). Later chunks read the earlier
+// chunks' cache. Prompts shorter than kPrefillMin tokens, and int8 caches,
+// run token by token.
+constexpr int kPrefillChunk = 512;
+constexpr int kPrefillMin = 8;
+
+int32_t prefill_setup(ss_hip_model* m) {
+  if (m->pf_cap) return 0;
+  const int cap = std::min(kPrefillChunk, m->max_seq);
+  if (!m->pos_iota) {
+    if (int32_t rc = m_alloc(m, (void**)&m->pos_iota, sizeof(int) * m->max_seq, false)) return rc;
+    std::vector<int> iota(m->max_seq);
+    for (int i = 0; i < m->max_seq; i++) iota[i] = i;
+    HIP_TRY(hipMemcpy(m->pos_iota, iota.data(), sizeof(int) * m->max_seq, hipMemcpyHostToDevice));
+  }
+  const size_t c = (size_t)cap;
+  if (int32_t rc = m_alloc(m, (void**)&m->pf_h, sizeof(float) * c * m->d, false)) return rc;
+  if (int32_t rc = m_alloc(m, (void**)&m->pf_qkv, sizeof(float) * c * (m->qdim + 2 * m->kvdim), false)) return rc;
+  if (int32_t rc = m_alloc(m, (void**)&m->pf_att, sizeof(float) * c * m->qdim, false)) return rc;
+  if (int32_t rc = m_alloc(m, (void**)&m->pf_f, sizeof(float) * c * m->ffn, false)) return rc;
+  if (int32_t rc = m_alloc(m, (void**)&m->pf_ssq, sizeof(float) * c, false)) return rc;
+  m->pf_cap = cap;
+  return 0;
+}
+
+ssk::GemmArgs gemm_args(const void* w, int type, int rows, int cols, const float* x, float* y, int T) {
+  ssk::GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.w = view(w, type, rows, cols);
+  a.x = x;
+  a.y = y;
+  a.ldx = cols;
+  a.ldy = rows;
+  a.rows = rows;
+  a.cols = cols;
+  a.T = T;
+  a.type = type;
+  return a;
+}
+
+// One decoder layer (process_layer, layer_scheduler.c:291-567) for the T
+// prompt tokens at positions p0 .. p0+T-1 whose residual streams are the rows
+// of pf_h.
+int32_t enqueue_layer_rows(ss_hip_model* m, int l, const DevLayer& ly, int T, int p0) {
+  hipStream_t s = m->ctx->stream;
+  const int* dpos = m->pos_iota + p0;
+  uint16_t* kc = static_cast<uint16_t*>(m->kc) + (size_t)l * m->kv_layer_elems;
+  uint16_t* vc = static_cast<uint16_t*>(m->vc) + (size_t)l * m->kv_layer_elems;
+  const int ldq = m->qdim + 2 * m->kvdim;
+
+  // 1. rmsnorm(attn_norm) -> [Wq;Wk;Wv] -> RoPE -> KV append   (layer_scheduler.c:320-413)
+  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_sumsq(m->pf_h, m->d, T, m->pf_ssq, s); }));
+  ssk::GemmArgs a = gemm_args(ly.wqkv, ly.t_qkv, ldq, m->d, m->pf_h, m->pf_qkv, T);
+  a.nw = ly.attn_norm;
+  a.ssq = m->pf_ssq;
+  a.eps = m->eps;
+  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_gemm(ssk::EPI_STORE, a, s); }));
+  HIP_TRY(timed(m, PC_OTHER, 0, [&] {
+    return ssk::launch_rope_kv_rows(m->pf_qkv, ldq, m->qdim, m->kvdim, m->hd, m->rope_dim, m->rope_cs, dpos, kc, vc,
+                                    m->max_seq, T, s);
+  }));
+
+  // 2. attention of every token over positions 0..its own        (:415-468)
+  ssk::AttnArgs at;
+  memset(&at, 0, sizeof(at));
+  at.q = m->pf_qkv;
+  at.tok_q = ldq;
+  at.kc = kc;
+  at.vc = vc;
+  at.dpos = dpos;
+  at.max_seq = m->max_seq;
+  at.ns = 1;
+  at.n_kv_heads = m->KVH;
+  at.scale = 1.0f / sqrtf((float)m->hd);
+  at.out = m->pf_att;
+  at.tok_o = m->qdim;
+  at.part_o = m->att_o;
+  at.part_ml = m->att_ml;
+  at.cnt = m->att_cnt;   // one split: written directly, the counters stay untouched
+  at.n_tok = T;
+  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_attention(m->hd, m->group, 0, at, s); }));
+
+  // 3. hidden += Wo attn                                         (:470-484)
+  ssk::GemmArgs o = gemm_args(ly.wo, ly.t_o, m->d, m->qdim, m->pf_att, m->pf_h, T);
+  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_gemm(ssk::EPI_ADD, o, s); }));
+
+  // 4. rmsnorm(ffn_norm) -> gate, up -> silu(gate) * up           (:486-550)
+  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_sumsq(m->pf_h, m->d, T, m->pf_ssq, s); }));
+  ssk::GemmArgs gu = gemm_args(ly.wg, ly.t_gu, m->ffn, m->d, m->pf_h, m->pf_f, T);
+  gu.w2 = view(ly.wu, ly.t_gu, m->ffn, m->d);
+  gu.nw = ly.ffn_norm;
+  gu.ssq = m->pf_ssq;
+  gu.eps = m->eps;
+  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_gemm(ssk::EPI_SWIGLU, gu, s); }));
+
+  // 5. hidden += Wdown act                                       (:552-566)
+  ssk::GemmArgs dn = gemm_args(ly.wd, ly.t_d, m->d, m->ffn, m->pf_f, m->pf_h, T);
+  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_gemm(ssk::EPI_ADD, dn, s); }));
+  return 0;
+}
+
+// The prompt tokens[0..n) (already at m->tokens[start..]) at positions
+// start.., then the LM head of the last one.
+int32_t enqueue_prompt_rows(ss_hip_model* m, const int32_t* tokens, int n, int start) {
+  hipStream_t s = m->ctx->stream;
+  int T = 0;
+  for (int c0 = 0; c0 < n; c0 += T) {
+    T = std::min(m->pf_cap, n - c0);
+    const int p0 = start + c0;
+    HIP_TRY(timed(m, PC_OTHER, 0, [&] {
+      return ssk::launch_embed_rows(m->t_embd, view(m->embd, m->t_embd, m->embd_rows, m->d), m->d, m->tokens,
+                                    m->pos_iota + p0, T, m->pf_h, s);
+    }));
+    for (int l = 0; l < m->L; l++) {
+      if (m->cancel && *m->cancel) return fail(kErrCancel, "cancelled");
+      if (m->streaming) {
+        DevLayer ly;
+        if (int32_t rc = stream_acquire(m, l, &ly)) return rc;
+        if (int32_t rc = enqueue_layer_rows(m, l, ly, T, p0)) return rc;
+        if (int32_t rc = stream_release(m)) return rc;
+      } else {
+        if (int32_t rc = enqueue_layer_rows(m, l, m->layers[l], T, p0)) return rc;
+      }
+    }
+  }
+  HIP_TRY(hipMemcpyAsync(m->hidden, m->pf_h + (size_t)(T - 1) * m->d, sizeof(float) * m->d,
+                         hipMemcpyDeviceToDevice, s));
+  HIP_TRY(ssk::launch_set_state(m->dpos, m->tokens, start + n - 1, tokens[n - 1], s));
+  return enqueue_head(m, m->hidden);
+}
+
 int32_t capture(ss_hip_model* m, bool with_head, hipGraphExec_t* out) {
   hipStream_t s = m->ctx->stream;
   HIP_TRY(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
@@ -1435,6 +1577,16 @@ int32_t ss_hip_eval_prompt(ss_hip_model_t* m, const int32_t* tokens, int32_t n, 
   HIP_TRY(hipStreamSynchronize(s));
   HIP_TRY(hipMemcpy(m->tokens + start, tokens, sizeof(int) * n, hipMemcpyHostToDevice));
   HIP_TRY(ssk::launch_set_state(m->dpos, m->tokens, start, tokens[0], s));
+  const int pf_min = m->pf_min > 0 ? m->pf_min : kPrefillMin;
+  if (m->kv_type == 0 && m->pf_min >= 0 && n >= pf_min) {
+    if (int32_t rc = prefill_setup(m)) return rc;
+    if (int32_t rc = enqueue_prompt_rows(m, tokens, n, start)) {
+      hipStreamSynchronize(s);
+      return rc;
+    }
+    m->host_pos = start + n - 1;
+    return finish_eval(m, logits_host, argmax_out);
+  }
   if (m->streaming) {
     if (int32_t rc = enqueue_prompt_layer_major(m, tokens, n, start)) {
       hipStreamSynchronize(s);
@@ -1452,6 +1604,12 @@ int32_t ss_hip_eval_prompt(ss_hip_model_t* m, const int32_t* tokens, int32_t n, 
   }
   m->host_pos = start + n - 1;
   return finish_eval(m, logits_host, argmax_out);
+}
+
+int32_t ss_hip_set_prompt_batch(ss_hip_model_t* m, int32_t min_tokens) {
+  if (!m) return fail(kErrParams, "null model");
+  m->pf_min = min_tokens;
+  return 0;
 }
 
 int32_t ss_hip_decode_greedy(ss_hip_model_t* m, int32_t n_steps, int32_t* tokens_out) {

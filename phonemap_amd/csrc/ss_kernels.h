@@ -72,6 +72,9 @@ struct AttnArgs {
   uint32_t* cnt;             // [n_kv_heads] split arrivals, zero between launches: the last
                              // split merges into out; nullptr: the splits stay in part_o/part_ml
                              // for a merging consumer (ns <= kMergeSplits)
+  int n_tok;                 // > 1: a batch of tokens (grid z), token z at position dpos[z],
+                             // its query at q + z*tok_q, its output at out + z*tok_o (ns = 1)
+  int tok_q, tok_o;
 };
 
 // Profiling: when start is set, the next matvec or attention launch on this
@@ -109,6 +112,9 @@ hipError_t launch_pack(int type, const uint8_t* src, uint8_t* qs, uint16_t* ds, 
                        int nb, int64_t row_off, hipStream_t s);
 hipError_t launch_embed(int type, PackedMat t, int cols, const int* tokens, const int* dpos,
                         int token, float* out, hipStream_t s);
+// Rows tokens[*dpos + z], z < n, of the table into out[z][cols].
+hipError_t launch_embed_rows(int type, PackedMat t, int cols, const int* tokens, const int* dpos, int n,
+                             float* out, hipStream_t s);
 hipError_t launch_rmsnorm(float* out, const float* x, const float* w, int n, float eps,
                           hipStream_t s);
 hipError_t launch_rope(float* q, float* k, int n_heads, int n_kv_heads, int head_dim,
@@ -116,6 +122,11 @@ hipError_t launch_rope(float* q, float* k, int n_heads, int n_kv_heads, int head
 hipError_t launch_kv_append(void* kc, void* vc, float* ksc, float* vsc, const float* k,
                             const float* v, int n_kv_heads, int head_dim, int max_seq,
                             const int* dpos, int pos, int kv_type, hipStream_t s);
+// RoPE of the q and k parts of n prompt rows [q | k | v] (stride ld; token z
+// at position dpos[z]) and the fp16 cache append of k and v.
+hipError_t launch_rope_kv_rows(float* qkv, int ld, int qdim, int kvdim, int head_dim, int rope_dim,
+                               const float* cs, const int* dpos, uint16_t* kc, uint16_t* vc, int max_seq,
+                               int n, hipStream_t s);
 hipError_t launch_swiglu(float* out, const float* g, const float* u, int n, hipStream_t s);
 hipError_t launch_argmax(int* out, const float* x, int n, float2* part, hipStream_t s);
 hipError_t launch_set_state(int* dpos, int* tokens, int pos, int token, hipStream_t s);

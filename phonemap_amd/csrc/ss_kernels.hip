@@ -54,7 +54,7 @@ constexpr int kBufferFlags = 0x00020000;
 constexpr int kSc1 = 16;
 
 __device__ __forceinline__ void attn_split(const AttnArgs& a, int& ctx, int& chunk, int& active) {
-  ctx = a.dpos ? *a.dpos + 1 : a.seq_len;
+  ctx = a.dpos ? a.dpos[blockIdx.z] + 1 : a.seq_len;   // a batch of tokens: one position each
   attn_chunks(ctx, a.ns, chunk, active);
 }
 
@@ -97,7 +97,7 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, int kvh, int acti
         so = fmaf(f, wo[w][g][d], so);
         sl = fmaf(f, wl[w][g], sl);
       }
-      a.out[((size_t)kvh * G + g) * HD + d] = so * (1.0f / sl);
+      a.out[(size_t)blockIdx.z * a.tok_o + ((size_t)kvh * G + g) * HD + d] = so * (1.0f / sl);
     }
     return;
   }
@@ -212,7 +212,7 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, int kvh, int acti
       acc.z += r.z;
       acc.w += r.w;
     }
-    reinterpret_cast<float4*>(a.out + (size_t)kvh * G * HD)[qd] = acc;
+    reinterpret_cast<float4*>(a.out + (size_t)blockIdx.z * a.tok_o + (size_t)kvh * G * HD)[qd] = acc;
   }
   if (tid == 0) cst(a.cnt + kvh, 0u);   // every split of this launch has arrived: ready for the next
 }
@@ -246,7 +246,7 @@ __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
   float q[G][8];
 #pragma unroll
   for (int g = 0; g < G; ++g) {
-    const float4* qp = reinterpret_cast<const float4*>(a.q + ((size_t)kvh * G + g) * HD + c * 8);
+    const float4* qp = reinterpret_cast<const float4*>(a.q + (size_t)blockIdx.z * a.tok_q + ((size_t)kvh * G + g) * HD + c * 8);
     const float4 x0 = qp[0], x1 = qp[1];
     q[g][0] = x0.x; q[g][1] = x0.y; q[g][2] = x0.z; q[g][3] = x0.w;
     q[g][4] = x1.x; q[g][5] = x1.y; q[g][6] = x1.z; q[g][7] = x1.w;
@@ -420,7 +420,8 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
 
   float q[kDpl], o[kDpl];
   {
-    const float4* qp = reinterpret_cast<const float4*>(a.q + ((size_t)kvh * G + h) * HD + c * kDpl);
+    const float4* qp =
+        reinterpret_cast<const float4*>(a.q + (size_t)blockIdx.z * a.tok_q + ((size_t)kvh * G + h) * HD + c * kDpl);
 #pragma unroll
     for (int i = 0; i < kDpl / 4; ++i) {
       const float4 x = qp[i];
@@ -532,6 +533,43 @@ __global__ void k_rope(float* q, float* k, int n_heads, int n_kv_heads, int head
   }
 }
 
+// A prompt's rows after the [Wq;Wk;Wv] products: row z of qkv (stride ld)
+// is [q | k | v] of the token at position dpos[z]. Pairs (2j, 2j+1) of each
+// q and k head below rope_dim rotate by the position's (cos, sin)
+// (tensor.c:250-273; q in place for the attention that follows), then k and
+// v go to the fp16 cache [kvh][max_seq][hd] (layer_scheduler.c:392-413).
+// One thread per pair; grid y = tokens.
+__global__ void k_rope_kv_rows(float* qkv, int ld, int qdim, int kvdim, int head_dim, int rope_dim,
+                               const float* cs, const int* dpos, uint16_t* kc, uint16_t* vc, int max_seq) {
+  const int pos = dpos[blockIdx.y];
+  float* row = qkv + (size_t)blockIdx.y * ld;
+  const int npairs = (qdim + 2 * kvdim) >> 1;
+  for (int p = blockIdx.x * blockDim.x + threadIdx.x; p < npairs; p += gridDim.x * blockDim.x) {
+    const int r = 2 * p;
+    const float2 v = reinterpret_cast<const float2*>(row)[p];
+    float a = v.x, b = v.y;
+    if (r < qdim + kvdim) {
+      const int i0 = (r < qdim ? r : r - qdim) % head_dim;
+      if (i0 < rope_dim) {
+        const float c = cs[(size_t)pos * rope_dim + i0], s = cs[(size_t)pos * rope_dim + i0 + 1];
+        const float ra = a * c - b * s;
+        const float rb = a * s + b * c;
+        a = ra;
+        b = rb;
+      }
+    }
+    if (r < qdim) {
+      reinterpret_cast<float2*>(row)[p] = make_float2(a, b);
+    } else {
+      const bool is_v = r >= qdim + kvdim;
+      const int kr = r - qdim - (is_v ? kvdim : 0);
+      uint16_t* c = (is_v ? vc : kc) + ((size_t)(kr / head_dim) * max_seq + pos) * head_dim + kr % head_dim;
+      c[0] = f2h(a);
+      c[1] = f2h(b);
+    }
+  }
+}
+
 // KV append: fp16 (one thread per element) or the int8 absmax encoding of
 // layer_scheduler.c:101-118 (one workgroup each for K and V).
 __global__ void k_kv_append(void* kc, void* vc, float* ksc, float* vsc, const float* k,
@@ -607,7 +645,7 @@ __global__ void k_advance(int* dpos) { *dpos += 1; }
 // ------------------------------------------------------------ launchers
 template <int HD, int G>
 hipError_t launch_attn_t(int kv_type, const AttnArgs& a, hipStream_t s) {
-  const dim3 grid(a.ns, a.n_kv_heads);
+  const dim3 grid(a.ns, a.n_kv_heads, a.n_tok > 1 ? a.n_tok : 1);
   KernelEvents& ev = kernel_events();
   if constexpr (G >= 4) {   // heads on lanes
     const dim3 block(kHgWaves * 64);
@@ -697,6 +735,9 @@ bool attention_supported(int head_dim, int group) {
 
 hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, hipStream_t s) {
   if (a.ns < 1 || a.ns > kMaxSplits) return hipErrorInvalidValue;   // merge weights: kMaxSplits per head
+  // a batch of tokens writes each output directly: one split, and a counter
+  // array present (unused then) to select the direct path
+  if (a.n_tok > 1 && (a.ns != 1 || !a.cnt || !a.dpos)) return hipErrorInvalidValue;
   if (head_dim == 64) return launch_attn_hd<64>(group, kv_type, a, s);
   if (head_dim == 128) return launch_attn_hd<128>(group, kv_type, a, s);
   return hipErrorInvalidValue;
@@ -723,6 +764,17 @@ hipError_t launch_kv_append(void* kc, void* vc, float* ksc, float* vsc, const fl
   const int grid = kv_type == 0 ? (2 * n_kv_heads * head_dim + 255) / 256 : 2;
   hipLaunchKernelGGL(k_kv_append, dim3(grid), dim3(256), 0, s, kc, vc, ksc, vsc, k, v, n_kv_heads,
                      head_dim, max_seq, dpos, pos, kv_type);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_kv_rows(float* qkv, int ld, int qdim, int kvdim, int head_dim, int rope_dim,
+                               const float* cs, const int* dpos, uint16_t* kc, uint16_t* vc, int max_seq,
+                               int n, hipStream_t s) {
+  if (n <= 0 || ld % 2 || qdim % 2 || kvdim % 2 || head_dim % 2 || ld < qdim + 2 * kvdim) return hipErrorInvalidValue;
+  const int npairs = (qdim + 2 * kvdim) / 2;
+  const int gx = (npairs + 255) / 256;
+  hipLaunchKernelGGL(k_rope_kv_rows, dim3(gx, n), dim3(256), 0, s, qkv, ld, qdim, kvdim, head_dim, rope_dim, cs,
+                     dpos, kc, vc, max_seq);
   return hipGetLastError();
 }
 

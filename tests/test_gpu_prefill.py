@@ -1,0 +1,88 @@
+"""Prompts as matrix products: with an fp16 cache, ss_eval_prompt runs a
+prompt of 8 or more tokens through each layer as MFMA products over chunks of
+up to 512 tokens (ss_scheduler_prefill, layer_scheduler.c:681-803, evaluates
+a prompt layer by layer with one matvec per token and matrix).
+
+Bar, as for decode: last-token logits within max |gpu - oracle| / max |oracle|
+<= 1e-3 of the CPU oracle, identical argmax, and identical greedy tokens for
+the decode steps that read the cache the prompt wrote.
+"""
+import numpy as np
+import pytest
+
+import oracle
+from phonemap_amd import api
+from tests.test_gpu_model import GQA8, TINY, TINY_Q8, TOL, _model_file
+from tests.util import rel_err
+
+pytestmark = pytest.mark.gpu
+SPECS = {"tiny": TINY, "tiny_q8": TINY_Q8, "gqa8": GQA8}
+
+
+def _decode_against(m, om, tok, pos, steps):
+    for _ in range(steps):
+        lg, am = m.eval_token(tok, pos)
+        olg = om.forward(tok, pos)
+        assert rel_err(lg, olg) <= TOL, pos
+        assert am == oracle.argmax(olg), pos
+        tok, pos = am, pos + 1
+
+
+@pytest.mark.parametrize("launch", ["graph", "sweep"])
+@pytest.mark.parametrize("spec", ["tiny", "tiny_q8", "gqa8"])
+def test_batched_prompt_matches_oracle(spec, launch):
+    """A 600-token prompt (two chunks: 512 + 88), then a 30-token prompt that
+    continues it at position 600, then decode steps."""
+    kw = SPECS[spec]
+    path = _model_file(spec, **kw)
+    print("prefill", spec, launch, flush=True)
+    rng = np.random.default_rng(21)
+    p1 = rng.integers(3, kw["vocab"], 600).tolist()
+    p2 = rng.integers(3, kw["vocab"], 30).tolist()
+    om = oracle.Model(path, 1024, "f16")
+    with api.Model(path, max_context=1024, launch=launch) as m:
+        lg, am = m.eval_prompt(p1, 0)
+        olg = om.prefill(p1, 0)
+        assert rel_err(lg, olg) <= TOL
+        assert am == oracle.argmax(olg) == int(np.argmax(lg))
+        lg, am = m.eval_prompt(p2, len(p1))
+        olg = om.prefill(p2, len(p1))
+        assert rel_err(lg, olg) <= TOL
+        assert am == oracle.argmax(olg)
+        _decode_against(m, om, am, len(p1) + len(p2), 12)
+    om.close()
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 63, 64, 65])
+def test_batched_prompt_sizes(n):
+    """Chunk edges of the 64-token product tile, and the threshold: every
+    size forced through the products (threshold 1) against the oracle."""
+    path = _model_file("gqa8", **GQA8)
+    rng = np.random.default_rng(100 + n)
+    prompt = rng.integers(3, GQA8["vocab"], n).tolist()
+    om = oracle.Model(path, 256, "f16")
+    with api.Model(path, max_context=256) as m:
+        m.set_prompt_batch(1)
+        lg, am = m.eval_prompt(prompt, 0)
+        olg = om.prefill(prompt, 0)
+        assert rel_err(lg, olg) <= TOL
+        assert am == oracle.argmax(olg)
+        _decode_against(m, om, am, n, 6)
+    om.close()
+
+
+def test_batched_equals_token_by_token():
+    """The same prompt through the products and token by token: the same
+    greedy continuation, logits within the decode tolerance of each other."""
+    path = _model_file("gqa8", **GQA8)
+    rng = np.random.default_rng(5)
+    prompt = rng.integers(3, GQA8["vocab"], 100).tolist()
+    out = {}
+    for batch in (0, -1):
+        with api.Model(path, max_context=256) as m:
+            m.set_prompt_batch(batch)
+            lg, am = m.eval_prompt(prompt, 0)
+            out[batch] = (lg, am, m.decode_greedy(20))
+    (lb, ab, tb), (lt, at, tt) = out[0], out[-1]
+    assert rel_err(lb, lt) <= TOL
+    assert ab == at and tb == tt
