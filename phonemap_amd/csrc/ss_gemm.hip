@@ -13,6 +13,11 @@
 //
 // MFMA operand layout (checked on the device): lane l supplies A[l%16][l/16]
 // and B[l/16][l%16] and receives D[4*(l/16) + i][l%16], i = 0..3.
+//
+// The fast path (k_gemm_h, with a split-x scratch) runs the same products on
+// v_mfma_f32_16x16x32_f16: the codes are exact fp16 integers, x is split into
+// two fp16 parts, and d scales each block's fp32 result (see below): eight
+// times the fp32 MFMA rate per product, with x kept to 2^-22.
 
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -31,9 +36,10 @@ constexpr int kGemmTok = kGemmTiles * 16;
 constexpr int kXsPad = kGemmTok + 4;   // LDS row (one column of x for 64 tokens), padded
 
 // Sum of squares of each token's x (one workgroup per token), for the RMSNorm scale.
-__global__ void __launch_bounds__(256) k_sumsq(const float* __restrict__ x, int cols, float* __restrict__ ssq) {
+__global__ void __launch_bounds__(256) k_sumsq(const float* __restrict__ x, int ldx, int cols,
+                                               float* __restrict__ ssq) {
   __shared__ float red[4];
-  const float* xt = x + (size_t)blockIdx.x * cols;
+  const float* xt = x + (size_t)blockIdx.x * ldx;
   float ss = 0.f;
   for (int c = threadIdx.x * 4; c < cols; c += 1024) {
     const float4 v = *reinterpret_cast<const float4*>(xt + c);
@@ -74,6 +80,41 @@ __device__ __forceinline__ float weight(const WBlock<QT>& f, int s, int kq) {
     return f.d * (float)(nib - 8);
   } else {                   // byte kq of word s
     return f.d * (float)(int8_t)((f.w[s] >> (8 * kq)) & 0xFFu);
+  }
+}
+
+// Rows r0 .. r0+3 of token t from the products g (and u, the up projection,
+// for EPI_SWIGLU): the RMSNorm scale of the token, the epilogue, the store.
+template <int EPI>
+__device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int t, int r0, const float (&g)[4],
+                                              const float (&u)[4]) {
+  const float scale = a.nw ? 1.0f / sqrtf(a.ssq[t] / (float)a.cols + a.eps) : 1.0f;
+  float* yp = a.y + (size_t)t * a.ldy + r0;
+  float v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float x0 = g[i] * scale;
+    if constexpr (EPI == EPI_SWIGLU) {
+      const float up = u[i] * scale;
+      v[i] = up * (x0 / (1.0f + expf(-x0)));   // layer_scheduler.c:540-547
+    } else {
+      v[i] = x0;
+    }
+  }
+  if (r0 + 3 < a.rows) {
+    float4 o = make_float4(v[0], v[1], v[2], v[3]);
+    if constexpr (EPI == EPI_ADD) {
+      const float4 p = *reinterpret_cast<const float4*>(yp);
+      o.x += p.x;
+      o.y += p.y;
+      o.z += p.z;
+      o.w += p.w;
+    }
+    *reinterpret_cast<float4*>(yp) = o;
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (r0 + i < a.rows) yp[i] = EPI == EPI_ADD ? yp[i] + v[i] : v[i];
   }
 }
 
@@ -159,34 +200,289 @@ __global__ void __launch_bounds__(kGemmWaves * 64) k_gemm(const GemmArgs a) {
   for (int tt = 0; tt < kGemmTiles; ++tt) {
     const int t = t0 + tt * 16 + n;
     if (t >= a.T) continue;
-    const float scale = a.ssq ? 1.0f / sqrtf(a.ssq[t] / (float)a.cols + a.eps) : 1.0f;
-    float* yp = a.y + (size_t)t * a.ldy + r0;
-    float v[4];
+    float gv[4], uv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float x0 = acc[0][tt][i] * scale;
-      if constexpr (EPI == EPI_SWIGLU) {
-        const float u = acc[NMAT - 1][tt][i] * scale;
-        v[i] = u * (x0 / (1.0f + expf(-x0)));   // layer_scheduler.c:540-547
-      } else {
-        v[i] = x0;
-      }
+      gv[i] = acc[0][tt][i];
+      uv[i] = acc[NMAT - 1][tt][i];
     }
-    if (r0 + 3 < a.rows) {
-      float4 o = make_float4(v[0], v[1], v[2], v[3]);
-      if constexpr (EPI == EPI_ADD) {
-        const float4 p = *reinterpret_cast<const float4*>(yp);
-        o.x += p.x;
-        o.y += p.y;
-        o.z += p.z;
-        o.w += p.w;
-      }
-      *reinterpret_cast<float4*>(yp) = o;
-    } else {
+    gemm_epilogue<EPI>(a, t, r0, gv, uv);
+  }
+}
+
+// ---- fp16 products -----------------------------------------------------------
+// Each 16x16x32 step is one 32-column block: B holds the block's codes as
+// exact fp16 integers (nibble - 8, or the Q8_0 code), A the 16 tokens' x as
+// two fp16 parts, and the step's fp32 result is scaled by the block's d (one
+// per output row) into the accumulator. Codes come from a magic number: the
+// fp16 with bits 0x6400 | u is 1024 + u for u < 1024, and subtracting 1032
+// (Q4_0) or 1152 (Q8_0, u = code + 128) is exact.
+//
+// x of each token is scaled by a power of two s_t (its largest |x| then lies
+// in [2^13, 2^14)) and split into xh = fp16(x s_t) and xl = fp16(x s_t - xh):
+// xh + xl is within 2^-22 |x| of x (or 2^-25 / s_t absolute for the small
+// elements), against 2^-24 for fp32 itself; 1/s_t is applied in the epilogue.
+//
+// Slot order: lane group kq (= lane/16) supplies slots 8kq .. 8kq+7 of the
+// step. Q4_0: the 8 nibbles of 32-bit word kq of the block, two per fp16 pair
+// (bits 4k and 4k+16: slot 2k and 2k+1), i.e. slot s is column
+// 4kq + 2(s&1) + (s>>2) + 16((s>>1)&1). Q8_0: bytes 8kq .. 8kq+7, slot s is
+// column 8kq + 4(s>>2) + 2(s&1) + ((s>>1)&1). The split x holds each block in
+// slot order, so lane group kq reads 16 contiguous bytes.
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+constexpr int kHWaves = 4;
+constexpr int kHTiles = 4;                // 16-token tiles per workgroup
+constexpr int kHTok = kHTiles * 16;
+constexpr int kHChunks = 16;              // 16-byte chunks of one token's 128 columns
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __attribute__((address_space(1))) void* gbl_ptr_t;
+
+template <int QT>
+__host__ __device__ constexpr int slot_col(int s) {   // column within the block of slot s (s < 32)
+  return QT == 2 ? 4 * (s >> 3) + 2 * (s & 1) + ((s >> 2) & 1) + 16 * ((s >> 1) & 1)
+                 : 8 * (s >> 3) + 4 * ((s >> 2) & 1) + 2 * (s & 1) + ((s >> 1) & 1);
+}
+
+// Token blockIdx.x of x (times nw): the scale 1/s_t into xinv[t], then the
+// fp16 parts in slot order (ldxs: row length, a multiple of 128; columns past
+// cols are zero); with ssq set, first its sum of squares (of x alone).
+template <int QT>
+__global__ void __launch_bounds__(256) k_split_x(const float* __restrict__ x, int ldx, const float* __restrict__ nw,
+                                                 int cols, float* __restrict__ ssq, uint16_t* __restrict__ xh,
+                                                 uint16_t* __restrict__ xl, float* __restrict__ xinv, int ldxs) {
+  __shared__ float red[2][4];
+  const int t = blockIdx.x;
+  const float* xt = x + (size_t)t * ldx;
+  float ss = 0.f, mx = 0.f;
+  for (int c = threadIdx.x * 4; c < cols; c += 1024) {
+    const float4 v = *reinterpret_cast<const float4*>(xt + c);
+    ss = fmaf(v.x, v.x, ss);
+    ss = fmaf(v.y, v.y, ss);
+    ss = fmaf(v.z, v.z, ss);
+    ss = fmaf(v.w, v.w, ss);
+    float4 u = v;
+    if (nw) {
+      const float4 w = *reinterpret_cast<const float4*>(nw + c);
+      u = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
+    }
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
+  }
+  ss = wave_sum(ss);
+  mx = wave_max(mx);
+  if ((threadIdx.x & 63) == 0) {
+    red[0][threadIdx.x >> 6] = ss;
+    red[1][threadIdx.x >> 6] = mx;
+  }
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+  int e = 0;
+  if (mx > 0.f && mx <= 3.0e38f) frexpf(mx, &e);        // mx < 2^e
+  const float sc = ldexpf(1.0f, 14 - e);                // largest |x s| in [2^13, 2^14)
+  if (threadIdx.x == 0) {
+    if (ssq) ssq[t] = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+    xinv[t] = ldexpf(1.0f, e - 14);
+  }
+  uint4* oh = reinterpret_cast<uint4*>(xh + (size_t)t * ldxs);
+  uint4* ol = reinterpret_cast<uint4*>(xl + (size_t)t * ldxs);
+  for (int c = threadIdx.x; c < ldxs / 8; c += 256) {
+    const int blk = c >> 2, kq = c & 3;
+    const int base = blk * 32;
+    uint32_t h[4], l[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (r0 + i < a.rows) yp[i] = EPI == EPI_ADD ? yp[i] + v[i] : v[i];
+    for (int k = 0; k < 4; ++k) {
+      float v[2] = {0.f, 0.f};
+      if (base < cols) {   // cols is a multiple of 32: the whole block is there
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int col = base + slot_col<QT>(8 * kq + 2 * k + q);
+          v[q] = (nw ? xt[col] * nw[col] : xt[col]) * sc;
+        }
+      }
+      const _Float16 a = (_Float16)v[0], b = (_Float16)v[1];
+      const _Float16 la = (_Float16)(v[0] - (float)a), lb = (_Float16)(v[1] - (float)b);
+      h[k] = __builtin_bit_cast(uint32_t, h2{a, b});
+      l[k] = __builtin_bit_cast(uint32_t, h2{la, lb});
     }
+    oh[c] = make_uint4(h[0], h[1], h[2], h[3]);
+    ol[c] = make_uint4(l[0], l[1], l[2], l[3]);
+  }
+}
+
+// A lane's 8 codes of one block as exact fp16 values in slot order (Q4_0:
+// w0 = 32-bit word kq of the block; Q8_0: w0, w1 = words 2kq, 2kq+1).
+template <int QT>
+__device__ __forceinline__ v8h codes_f16(uint32_t w0, uint32_t w1) {
+  v4u r;
+  if constexpr (QT == 2) {
+    const h2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      r[k] = __builtin_bit_cast(uint32_t,
+                                __builtin_bit_cast(h2, ((w0 >> (4 * k)) & 0x000F000Fu) | 0x64006400u) + off);
+  } else {
+    const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+    const uint32_t u0 = w0 ^ 0x80808080u, u1 = w1 ^ 0x80808080u;
+    r[0] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, (u0 & 0x00FF00FFu) | 0x64006400u) + off);
+    r[1] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, ((u0 >> 8) & 0x00FF00FFu) | 0x64006400u) + off);
+    r[2] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, (u1 & 0x00FF00FFu) | 0x64006400u) + off);
+    r[3] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, ((u1 >> 8) & 0x00FF00FFu) | 0x64006400u) + off);
+  }
+  return __builtin_bit_cast(v8h, r);
+}
+
+// Workgroup: 4 waves x kHRG row groups of 16 rows x 64 tokens. Per packed tile
+// (4 blocks, 128 columns) the split x of the 64 tokens is copied into LDS by
+// direct global-to-LDS loads (double buffered; the next tile's x, codes and
+// scales in flight during this tile's products). Chunk q of token r sits at
+// slot q ^ (r % 16) of its LDS row, so the 16 tokens of a tile read one
+// chunk each from distinct banks. Lane (n, kq): weight row n of each row
+// group, token rows 4kq .. 4kq+3 of each 16-token tile in the results.
+template <int QT, int NMAT, int EPI, int kHRG>
+__global__ void __launch_bounds__(kHWaves * 64, 2) k_gemm_h(const GemmArgs a, int ldxs) {
+  __shared__ v4u xs[2][2][kHTok][kHChunks];   // [buffer][high, low][token][slot]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ngroups = (a.rows + kRG - 1) / kRG;
+  const int g0 = (blockIdx.x * kHWaves + wave) * kHRG;
+  const int nb = a.cols >> 5;
+  const int ntk = (nb + kTB - 1) / kTB;
+  const int t0 = blockIdx.y * kHTok;
+  const int n = lane & 15, kq = lane >> 4;
+  constexpr int kQW = QT == 2 ? 1 : 2;   // code words per lane per block
+  const uint16_t* xlo = a.xs + (size_t)a.T * ldxs;
+  const float* xinv = reinterpret_cast<const float*>(a.xs + 2 * (size_t)a.T * ldxs);
+
+  // staging: 2 parts x 64 tokens x 16 chunks per tile = 32 rows of 1 KB; wave
+  // w copies rows 8w .. 8w+7 (part R / 16, tokens 4(R % 16) .. +3), lane i
+  // token 4(R % 16) + i/16, slot i % 16
+  auto stage_x = [&](int tk, int buf) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int R = 8 * wave + k, part = R >> 4, r = 4 * (R & 15) + (lane >> 4), slot = lane & 15;
+      const int t = min(t0 + r, a.T - 1);
+      const uint16_t* src = (part ? xlo : a.xs) + (size_t)t * ldxs + tk * 128 + 8 * (slot ^ (r & 15));
+      __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)&xs[buf][part][4 * (R & 15)][0], 16, 0, 0);
+    }
+  };
+  uint32_t wq[NMAT][kHRG][kTB][kQW];
+  float wd[NMAT][kHRG][kTB];
+  auto load_w = [&](int tk, uint32_t (&q)[NMAT][kHRG][kTB][kQW], float (&d)[NMAT][kHRG][kTB]) {
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+      for (int r = 0; r < kHRG; ++r) {
+        const uint8_t* qs = mt == 0 ? a.w.qs : a.w2.qs;
+        const uint16_t* ds = mt == 0 ? a.w.ds : a.w2.ds;
+        const int g = min(g0 + r, ngroups - 1);
+#pragma unroll
+        for (int b = 0; b < kTB; ++b) {
+          const int tl = tile_lane(n, b);
+          const uint32_t* p =
+              reinterpret_cast<const uint32_t*>(qs + tile_idx(g, ntk, tk, tl) * QTraits<QT>::kQB) + kQW * kq;
+#pragma unroll
+          for (int k = 0; k < kQW; ++k) q[mt][r][b][k] = p[k];
+          // blocks past the row (the last tile's padding) are read and weighted 0
+          const float dv = h2f(ds[scale_idx(g, ntk, tk, tl)]);
+          d[mt][r][b] = tk * kTB + b < nb ? dv : 0.f;
+        }
+      }
+  };
+
+  v4f acc[NMAT][kHRG][kHTiles];
+#pragma unroll
+  for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+    for (int r = 0; r < kHRG; ++r)
+#pragma unroll
+      for (int tt = 0; tt < kHTiles; ++tt) acc[mt][r][tt] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  stage_x(0, 0);
+  load_w(0, wq, wd);
+  vm_drain();
+  __syncthreads();
+#pragma unroll 1
+  for (int tk = 0; tk < ntk; ++tk) {
+    const int buf = tk & 1;
+    // the next tile in flight (the last iteration reloads its own tile into
+    // the idle buffer: branch-free, read by no one)
+    const int tn = min(tk + 1, ntk - 1);
+    uint32_t nq[NMAT][kHRG][kTB][kQW];
+    float nd[NMAT][kHRG][kTB];
+    stage_x(tn, buf ^ 1);
+    load_w(tn, nq, nd);
+#pragma unroll
+    for (int b = 0; b < kTB; ++b) {
+      v8h wc[NMAT][kHRG];
+#pragma unroll
+      for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+        for (int r = 0; r < kHRG; ++r) wc[mt][r] = codes_f16<QT>(wq[mt][r][b][0], wq[mt][r][b][kQW - 1]);
+#pragma unroll
+      for (int tt = 0; tt < kHTiles; ++tt) {
+        const v8h xh = __builtin_bit_cast(v8h, xs[buf][0][tt * 16 + n][(4 * b + kq) ^ n]);
+        const v8h xl = __builtin_bit_cast(v8h, xs[buf][1][tt * 16 + n][(4 * b + kq) ^ n]);
+#pragma unroll
+        for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+          for (int r = 0; r < kHRG; ++r) {
+            v4f c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, wc[mt][r], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, wc[mt][r], c, 0, 0, 0);
+            const float d = wd[mt][r][b];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[mt][r][tt][i] = fmaf(d, c[i], acc[mt][r][tt][i]);
+          }
+      }
+      __builtin_amdgcn_sched_barrier(0);   // one block's operands live at a time
+    }
+#pragma unroll
+    for (int mt = 0; mt < NMAT; ++mt)
+#pragma unroll
+      for (int r = 0; r < kHRG; ++r)
+#pragma unroll
+        for (int b = 0; b < kTB; ++b) {
+#pragma unroll
+          for (int k = 0; k < kQW; ++k) wq[mt][r][b][k] = nq[mt][r][b][k];
+          wd[mt][r][b] = nd[mt][r][b];
+        }
+    vm_drain();   // this wave's direct LDS loads of the next tile have landed
+    __syncthreads();
+  }
+
+  // epilogue: lane holds row g*16 + n of tokens t0 + 16tt + 4kq + i
+  float tsc[kHTiles][4];   // per token: 1/s_t, times the RMSNorm scale
+#pragma unroll
+  for (int tt = 0; tt < kHTiles; ++tt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int t = min(t0 + tt * 16 + 4 * kq + i, a.T - 1);
+      tsc[tt][i] = xinv[t] * (a.nw ? 1.0f / sqrtf(a.ssq[t] / (float)a.cols + a.eps) : 1.0f);
+    }
+#pragma unroll
+  for (int r = 0; r < kHRG; ++r) {
+    const int g = g0 + r;
+    const int row = g * kRG + n;
+    if (g >= ngroups || row >= a.rows) continue;
+#pragma unroll
+    for (int tt = 0; tt < kHTiles; ++tt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int t = t0 + tt * 16 + 4 * kq + i;
+        if (t >= a.T) continue;
+        const float scale = tsc[tt][i];
+        const float x0 = acc[0][r][tt][i] * scale;
+        float v;
+        if constexpr (EPI == EPI_SWIGLU) {
+          const float up = acc[NMAT - 1][r][tt][i] * scale;
+          v = up * (x0 / (1.0f + expf(-x0)));   // layer_scheduler.c:540-547
+        } else {
+          v = x0;
+        }
+        float* yp = a.y + (size_t)t * a.ldy + row;
+        *yp = EPI == EPI_ADD ? *yp + v : v;
+      }
   }
 }
 
@@ -195,6 +491,14 @@ hipError_t launch_gemm_t(const GemmArgs& a, hipStream_t s) {
   const int ngroups = (a.rows + kRG - 1) / kRG;
   const dim3 grid((ngroups + kGemmWaves - 1) / kGemmWaves, (a.T + kGemmTok - 1) / kGemmTok);
   hipLaunchKernelGGL((k_gemm<QT, NMAT, EPI>), grid, dim3(kGemmWaves * 64), 0, s, a);
+  return hipGetLastError();
+}
+
+template <int QT, int NMAT, int EPI, int RG>
+hipError_t launch_gemm_h_t(const GemmArgs& a, int ldxs, hipStream_t s) {
+  const int ngroups = (a.rows + kRG - 1) / kRG;
+  const dim3 grid((ngroups + kHWaves * RG - 1) / (kHWaves * RG), (a.T + kHTok - 1) / kHTok);
+  hipLaunchKernelGGL((k_gemm_h<QT, NMAT, EPI, RG>), grid, dim3(kHWaves * 64), 0, s, a, ldxs);
   return hipGetLastError();
 }
 
@@ -208,17 +512,65 @@ hipError_t launch_gemm_q(int epi, const GemmArgs& a, hipStream_t s) {
   }
 }
 
+// Two matrices (gate/up) take one row group of each per wave; one matrix two
+// row groups per wave, or one when that leaves fewer than two workgroups per
+// compute unit.
+template <int QT>
+hipError_t launch_gemm_h(int epi, const GemmArgs& a, int ldxs, int n_cu, hipStream_t s) {
+  const int ngroups = (a.rows + kRG - 1) / kRG;
+  const long wg2 = (long)((ngroups + 2 * kHWaves - 1) / (2 * kHWaves)) * ((a.T + kHTok - 1) / kHTok);
+  const bool one = wg2 < 2L * n_cu;
+  switch (epi) {
+    case EPI_STORE:
+      return one ? launch_gemm_h_t<QT, 1, EPI_STORE, 1>(a, ldxs, s) : launch_gemm_h_t<QT, 1, EPI_STORE, 2>(a, ldxs, s);
+    case EPI_ADD:
+      return one ? launch_gemm_h_t<QT, 1, EPI_ADD, 1>(a, ldxs, s) : launch_gemm_h_t<QT, 1, EPI_ADD, 2>(a, ldxs, s);
+    case EPI_SWIGLU: return launch_gemm_h_t<QT, 2, EPI_SWIGLU, 1>(a, ldxs, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+int device_cus() {
+  static int n = 0;
+  if (!n) {
+    int dev = 0;
+    hipDeviceProp_t p;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&p, dev) == hipSuccess) n = p.multiProcessorCount;
+    if (n <= 0) n = 256;
+  }
+  return n;
+}
+
 }  // namespace
 
 hipError_t launch_sumsq(const float* x, int cols, int T, float* ssq, hipStream_t s) {
   if (T <= 0 || cols <= 0 || cols % 4) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(k_sumsq, dim3(T), dim3(256), 0, s, x, cols, ssq);
+  hipLaunchKernelGGL(k_sumsq, dim3(T), dim3(256), 0, s, x, cols, cols, ssq);
   return hipGetLastError();
 }
 
 hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t s) {
-  if (a.T <= 0 || a.rows <= 0 || a.cols <= 0 || a.cols % 32 || a.ldy < a.rows || a.ldx < a.cols)
+  if (a.T <= 0 || a.rows <= 0 || a.cols <= 0 || a.cols % 32 || a.ldy < a.rows || a.ldx < a.cols || a.ldx % 4 ||
+      (a.nw && !a.ssq))
     return hipErrorInvalidValue;
+  if (epi != EPI_STORE && epi != EPI_ADD && epi != EPI_SWIGLU) return hipErrorInvalidValue;
+  if (a.xs && (a.type == 2 || a.type == 8)) {
+    const int ldxs = (a.cols + 127) / 128 * 128;
+    uint16_t* xl = a.xs + (size_t)a.T * ldxs;
+    float* xinv = reinterpret_cast<float*>(a.xs + 2 * (size_t)a.T * ldxs);
+    float* ssq = a.nw ? a.ssq : nullptr;
+    if (a.type == 2)
+      hipLaunchKernelGGL(k_split_x<2>, dim3(a.T), dim3(256), 0, s, a.x, a.ldx, a.nw, a.cols, ssq, a.xs, xl, xinv, ldxs);
+    else
+      hipLaunchKernelGGL(k_split_x<8>, dim3(a.T), dim3(256), 0, s, a.x, a.ldx, a.nw, a.cols, ssq, a.xs, xl, xinv, ldxs);
+    if (hipError_t e = hipGetLastError()) return e;
+    const int n_cu = device_cus();
+    return a.type == 2 ? launch_gemm_h<2>(epi, a, ldxs, n_cu, s) : launch_gemm_h<8>(epi, a, ldxs, n_cu, s);
+  }
+  if (a.nw) {
+    hipLaunchKernelGGL(k_sumsq, dim3(a.T), dim3(256), 0, s, a.x, a.ldx, a.cols, a.ssq);
+    if (hipError_t e = hipGetLastError()) return e;
+  }
   if (a.type == 2) return launch_gemm_q<2>(epi, a, s);
   if (a.type == 8) return launch_gemm_q<8>(epi, a, s);
   return hipErrorInvalidValue;

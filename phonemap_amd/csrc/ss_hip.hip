@@ -83,9 +83,10 @@ struct ss_hip_ctx {
   float* att_o = nullptr;
   float* att_ml = nullptr;
   uint32_t* att_cnt = nullptr;
-  float* g_ssq = nullptr;   // prompt products: sums of squares of x
+  float* g_ssq = nullptr;      // prompt products: sums of squares of x
+  uint16_t* g_xs = nullptr;    // prompt products: x split into fp16 parts
 
-  size_t att_o_floats = 0, att_ml_floats = 0, att_cnt_bytes = 0, g_ssq_bytes = 0;
+  size_t att_o_floats = 0, att_ml_floats = 0, att_cnt_bytes = 0, g_ssq_bytes = 0, g_xs_bytes = 0;
 
   // host-pointer plug (metal_backend.m:190-235 registry)
   std::unordered_map<const void*, void*> registry;
@@ -236,7 +237,7 @@ void ss_hip_free(ss_hip_ctx_t* c) {
   if (c->stream) hipStreamSynchronize(c->stream);
   for (auto& kv : c->registry) hipFree(kv.second);
   void* bufs[] = {c->staging, c->am_part, c->rope_row, c->att_o,
-                  c->att_ml, c->att_cnt, c->g_ssq, c->plug_x, c->plug_y};
+                  c->att_ml, c->att_cnt, c->g_ssq, c->g_xs, c->plug_x, c->plug_y};
   for (void* b : bufs)
     if (b) hipFree(b);
   if (c->stream) hipStreamDestroy(c->stream);
@@ -330,15 +331,16 @@ int32_t ss_hip_gemm(ss_hip_ctx_t* c, float* y, const void* w, const float* x, co
     return fail(kErrParams, "gemm: bad argument (rows %d cols %d tokens %d type %d)", rows, cols, n_tokens, type);
   if (set_device(c)) return kErrBackend;
   int32_t rc = ensure(c, (void**)&c->g_ssq, &c->g_ssq_bytes, sizeof(float) * n_tokens, false);
+  if (!rc) rc = ensure(c, (void**)&c->g_xs, &c->g_xs_bytes, 2 * ssk::gemm_split_elems(n_tokens, cols), false);
   if (rc) return rc;
   hipStream_t s = pick(c, stream);
-  if (nw) HIP_TRY(ssk::launch_sumsq(x, cols, n_tokens, c->g_ssq, s));
   ssk::GemmArgs a;
   memset(&a, 0, sizeof(a));
   a.w = view(w, type, rows, cols);
   a.x = x;
   a.nw = nw;
-  a.ssq = nw ? c->g_ssq : nullptr;
+  a.ssq = c->g_ssq;
+  a.xs = c->g_xs;
   a.eps = eps;
   a.y = y;
   a.ldx = cols;
@@ -617,6 +619,7 @@ struct ss_hip_model {
   int pf_min = 0;                    // shortest prompt evaluated this way (0: the default)
   int pf_cap = 0;                    // chunk capacity (0: not set up)
   float *pf_h = nullptr, *pf_qkv = nullptr, *pf_att = nullptr, *pf_f = nullptr, *pf_ssq = nullptr;
+  uint16_t* pf_xs = nullptr;         // x of a product split into fp16 parts
 };
 
 namespace {
@@ -1111,16 +1114,21 @@ int32_t prefill_setup(ss_hip_model* m) {
   if (int32_t rc = m_alloc(m, (void**)&m->pf_att, sizeof(float) * c * m->qdim, false)) return rc;
   if (int32_t rc = m_alloc(m, (void**)&m->pf_f, sizeof(float) * c * m->ffn, false)) return rc;
   if (int32_t rc = m_alloc(m, (void**)&m->pf_ssq, sizeof(float) * c, false)) return rc;
+  const int widest = std::max(std::max(m->d, m->qdim), m->ffn);
+  if (int32_t rc = m_alloc(m, (void**)&m->pf_xs, 2 * ssk::gemm_split_elems(cap, widest), false)) return rc;
   m->pf_cap = cap;
   return 0;
 }
 
-ssk::GemmArgs gemm_args(const void* w, int type, int rows, int cols, const float* x, float* y, int T) {
+ssk::GemmArgs gemm_args(ss_hip_model* m, const void* w, int type, int rows, int cols, const float* x, float* y,
+                        int T) {
   ssk::GemmArgs a;
   memset(&a, 0, sizeof(a));
   a.w = view(w, type, rows, cols);
   a.x = x;
   a.y = y;
+  a.ssq = m->pf_ssq;
+  a.xs = m->pf_xs;
   a.ldx = cols;
   a.ldy = rows;
   a.rows = rows;
@@ -1141,10 +1149,8 @@ int32_t enqueue_layer_rows(ss_hip_model* m, int l, const DevLayer& ly, int T, in
   const int ldq = m->qdim + 2 * m->kvdim;
 
   // 1. rmsnorm(attn_norm) -> [Wq;Wk;Wv] -> RoPE -> KV append   (layer_scheduler.c:320-413)
-  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_sumsq(m->pf_h, m->d, T, m->pf_ssq, s); }));
-  ssk::GemmArgs a = gemm_args(ly.wqkv, ly.t_qkv, ldq, m->d, m->pf_h, m->pf_qkv, T);
+  ssk::GemmArgs a = gemm_args(m, ly.wqkv, ly.t_qkv, ldq, m->d, m->pf_h, m->pf_qkv, T);
   a.nw = ly.attn_norm;
-  a.ssq = m->pf_ssq;
   a.eps = m->eps;
   HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_gemm(ssk::EPI_STORE, a, s); }));
   HIP_TRY(timed(m, PC_OTHER, 0, [&] {
@@ -1173,20 +1179,18 @@ int32_t enqueue_layer_rows(ss_hip_model* m, int l, const DevLayer& ly, int T, in
   HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_attention(m->hd, m->group, 0, at, s); }));
 
   // 3. hidden += Wo attn                                         (:470-484)
-  ssk::GemmArgs o = gemm_args(ly.wo, ly.t_o, m->d, m->qdim, m->pf_att, m->pf_h, T);
+  ssk::GemmArgs o = gemm_args(m, ly.wo, ly.t_o, m->d, m->qdim, m->pf_att, m->pf_h, T);
   HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_gemm(ssk::EPI_ADD, o, s); }));
 
   // 4. rmsnorm(ffn_norm) -> gate, up -> silu(gate) * up           (:486-550)
-  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_sumsq(m->pf_h, m->d, T, m->pf_ssq, s); }));
-  ssk::GemmArgs gu = gemm_args(ly.wg, ly.t_gu, m->ffn, m->d, m->pf_h, m->pf_f, T);
+  ssk::GemmArgs gu = gemm_args(m, ly.wg, ly.t_gu, m->ffn, m->d, m->pf_h, m->pf_f, T);
   gu.w2 = view(ly.wu, ly.t_gu, m->ffn, m->d);
   gu.nw = ly.ffn_norm;
-  gu.ssq = m->pf_ssq;
   gu.eps = m->eps;
   HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_gemm(ssk::EPI_SWIGLU, gu, s); }));
 
   // 5. hidden += Wdown act                                       (:552-566)
-  ssk::GemmArgs dn = gemm_args(ly.wd, ly.t_d, m->d, m->ffn, m->pf_f, m->pf_h, T);
+  ssk::GemmArgs dn = gemm_args(m, ly.wd, ly.t_d, m->d, m->ffn, m->pf_f, m->pf_h, T);
   HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_gemm(ssk::EPI_ADD, dn, s); }));
   return 0;
 }

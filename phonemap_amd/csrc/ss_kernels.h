@@ -50,12 +50,19 @@ struct GemvArgs {
 struct GemmArgs {
   PackedMat w, w2;           // w2: up projection for EPI_SWIGLU
   const float* x;            // [T][ldx] token-major
-  const float* nw;           // RMSNorm weight [cols] applied to x, or nullptr
-  const float* ssq;          // [T] sums of squares of x: the RMSNorm scale applied, or nullptr
+  const float* nw;           // RMSNorm weight [cols]: x is normalised (tensor.c:114-131), or nullptr
+  float* ssq;                // [T] scratch for the sums of squares of x (required with nw)
   float eps;
   float* y;                  // [T][ldy] (EPI_ADD: accumulated into)
+  uint16_t* xs;              // scratch of gemm_split_elems(T, cols) 16-bit words: x split into
+                             // two fp16 parts and a scale per token (fp16 products), or
+                             // nullptr (fp32 products)
   int ldx, ldy, rows, cols, T, type;
 };
+// 16-bit words of GemmArgs::xs for T tokens of cols columns
+inline size_t gemm_split_elems(int T, int cols) {
+  return 2 * (size_t)T * (size_t)((cols + 127) / 128 * 128) + 2 * (size_t)T;
+}
 
 struct AttnArgs {
   const float* q;            // [n_heads][hd]
@@ -100,7 +107,10 @@ hipError_t launch_argmax_merge(const float2* part, int n, const float* y, int* o
 hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, hipStream_t s);
 // ssq[t] = sum of x[t][c]^2 (x [T][cols])
 hipError_t launch_sumsq(const float* x, int cols, int T, float* ssq, hipStream_t s);
-// EPI_STORE, EPI_ADD, EPI_SWIGLU
+// Y = W X over T tokens with EPI_STORE, EPI_ADD or EPI_SWIGLU; with nw set,
+// first the sums of squares of X into a.ssq. With a.xs: X is split into fp16
+// parts first and the products run in fp16 (exact codes, fp32 accumulation
+// and scales); otherwise in fp32.
 hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t s);
 bool attention_supported(int head_dim, int group);
 // positions one attention workgroup covers in one round of loads
