@@ -1174,9 +1174,8 @@ int32_t enqueue_layer_rows(ss_hip_model* m, int l, const DevLayer& ly, int T, in
   at.tok_o = m->qdim;
   at.part_o = m->att_o;
   at.part_ml = m->att_ml;
-  at.cnt = m->att_cnt;   // one split: written directly, the counters stay untouched
   at.n_tok = T;
-  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_attention(m->hd, m->group, 0, at, s); }));
+  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_attention_rows(m->hd, m->group, at, s); }));
 
   // 3. hidden += Wo attn                                         (:470-484)
   ssk::GemmArgs o = gemm_args(m, ly.wo, ly.t_o, m->d, m->qdim, m->pf_att, m->pf_h, T);

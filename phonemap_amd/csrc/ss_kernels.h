@@ -79,9 +79,8 @@ struct AttnArgs {
   uint32_t* cnt;             // [n_kv_heads] split arrivals, zero between launches: the last
                              // split merges into out; nullptr: the splits stay in part_o/part_ml
                              // for a merging consumer (ns <= kMergeSplits)
-  int n_tok;                 // > 1: a batch of tokens (grid z), token z at position dpos[z],
-                             // its query at q + z*tok_q, its output at out + z*tok_o (ns = 1)
-  int tok_q, tok_o;
+  int n_tok;                 // prompt rows (launch_attention_rows): token z at position dpos[z],
+  int tok_q, tok_o;          // its query at q + z*tok_q, its output at out + z*tok_o
 };
 
 // Profiling: when start is set, the next matvec or attention launch on this
@@ -105,6 +104,9 @@ hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t s);
 hipError_t launch_argmax_merge(const float2* part, int n, const float* y, int* out_idx, int* tokens,
                                int* dpos, hipStream_t s);
 hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, hipStream_t s);
+// Causal attention of a.n_tok prompt rows (token z: query a.q + z*a.tok_q,
+// positions 0..a.dpos[z], output a.out + z*a.tok_o), fp16 cache.
+hipError_t launch_attention_rows(int head_dim, int group, const AttnArgs& a, hipStream_t s);
 // ssq[t] = sum of x[t][c]^2 (x [T][cols])
 hipError_t launch_sumsq(const float* x, int cols, int T, float* ssq, hipStream_t s);
 // Y = W X over T tokens with EPI_STORE, EPI_ADD or EPI_SWIGLU; with nw set,
