@@ -209,6 +209,11 @@ int32_t ss_hip_eval_prompt(ss_hip_model_t *m, const int32_t *tokens, int32_t n,
  * value makes every prompt run token by token (no counterpart in the
  * reference; for measurement and comparison). */
 int32_t ss_hip_set_prompt_batch(ss_hip_model_t *m, int32_t min_tokens);
+/* ss_scheduler_embed (layer_scheduler.c:805-911): tokens at positions
+ * 0..n-1 (the cache is overwritten there), every token's final hidden state
+ * through the output norm, mean-pooled and L2-normalised into out_host[hidden].
+ * With the fp16 cache the prompt runs as matrix products. */
+int32_t ss_hip_embed(ss_hip_model_t *m, const int32_t *tokens, int32_t n, float *out_host);
 /* device-side greedy continuation (see ss_decode_greedy) */
 int32_t ss_hip_decode_greedy(ss_hip_model_t *m, int32_t n_steps, int32_t *tokens_out);
 /* ss_scheduler_reset (layer_scheduler.h:132) */

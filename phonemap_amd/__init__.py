@@ -61,6 +61,7 @@ _PROTOS = {
     "ss_hip_eval_prompt": (_i32, [_vp, _ip, _i32, _i32, _fp, _ip]),
     "ss_hip_decode_greedy": (_i32, [_vp, _i32, _ip]),
     "ss_hip_set_prompt_batch": (_i32, [_vp, _i32]),
+    "ss_hip_embed": (_i32, [_vp, _ip, _i32, _fp]),
     "ss_hip_kv_reset": (_i32, [_vp]),
     "ss_hip_kv_write": (_i32, [_vp, _i32, _i32, _i32, _u16p, _u16p]),
     "ss_hip_hidden": (_i32, [_vp, _fp]),

@@ -486,20 +486,13 @@ ss_error_t ss_embed(ss_model_t *m, const char *prompt, float **out, uint32_t *ou
     if (n > m->n_ctx) return set_err(SS_ERROR_INVALID_PARAMS);
     if (m->progress_cb) m->progress_cb(0, (uint32_t)n, "embedding", m->progress_user_data);
     const int32_t d = m->n_embd;
-    float *e = (float *)calloc((size_t)d, sizeof(float));
-    float *h = (float *)malloc(sizeof(float) * (size_t)d);
-    if (!e || !h) { free(e); free(h); return set_err(SS_ERROR_OUT_OF_MEMORY); }
-    for (int32_t i = 0; i < n; i++) {
-        int32_t rc = ss_hip_eval_token(m->hm, toks[i], i, NULL, NULL);
-        if (rc == 0) rc = ss_hip_hidden(m->hm, h);
-        if (rc != 0) { free(e); free(h); return map_rc(rc) == SS_ERROR_CANCELLED ? SS_ERROR_CANCELLED : set_err(SS_ERROR_BACKEND); }
-        for (int32_t j = 0; j < d; j++) e[j] += h[j];
+    float *e = (float *)malloc(sizeof(float) * (size_t)d);
+    if (!e) return set_err(SS_ERROR_OUT_OF_MEMORY);
+    int32_t rc = ss_hip_embed(m->hm, toks, n, e);   /* layer_scheduler.c:805-911 */
+    if (rc != 0) {
+        free(e);
+        return map_rc(rc) == SS_ERROR_CANCELLED ? SS_ERROR_CANCELLED : set_err(SS_ERROR_BACKEND);
     }
-    float inv = 1.0f / (float)n, l2 = 0.0f;
-    for (int32_t j = 0; j < d; j++) { e[j] *= inv; l2 += e[j] * e[j]; }
-    float s = 1.0f / (sqrtf(l2) + 1e-12f);
-    for (int32_t j = 0; j < d; j++) e[j] *= s;
-    free(h);
     *out = e;
     *out_dim = (uint32_t)d;
     return set_err(SS_OK);

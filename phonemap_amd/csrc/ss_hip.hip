@@ -620,6 +620,7 @@ struct ss_hip_model {
   int pf_cap = 0;                    // chunk capacity (0: not set up)
   float *pf_h = nullptr, *pf_qkv = nullptr, *pf_att = nullptr, *pf_f = nullptr, *pf_ssq = nullptr;
   uint16_t* pf_xs = nullptr;         // x of a product split into fp16 parts
+  float* emb = nullptr;              // [2d + 64]: pooled sum, embedding, a sum of squares
 };
 
 namespace {
@@ -1194,9 +1195,11 @@ int32_t enqueue_layer_rows(ss_hip_model* m, int l, const DevLayer& ly, int T, in
   return 0;
 }
 
-// The prompt tokens[0..n) (already at m->tokens[start..]) at positions
-// start.., then the LM head of the last one.
-int32_t enqueue_prompt_rows(ss_hip_model* m, const int32_t* tokens, int n, int start) {
+// The prompt m->tokens[start .. start+n) at positions start.., chunk by
+// chunk through every layer; with pool, each chunk's final hidden states
+// through the output norm are added to m->emb (ss_scheduler_embed). Returns
+// in *last the rows of the last chunk (its last row is the last token).
+int32_t enqueue_rows(ss_hip_model* m, int n, int start, bool pool, int* last) {
   hipStream_t s = m->ctx->stream;
   int T = 0;
   for (int c0 = 0; c0 < n; c0 += T) {
@@ -1217,7 +1220,21 @@ int32_t enqueue_prompt_rows(ss_hip_model* m, const int32_t* tokens, int n, int s
         if (int32_t rc = enqueue_layer_rows(m, l, m->layers[l], T, p0)) return rc;
       }
     }
+    if (pool) {
+      if (m->out_norm) HIP_TRY(ssk::launch_sumsq(m->pf_h, m->d, T, m->pf_ssq, s));
+      HIP_TRY(ssk::launch_pool_rows(m->pf_h, T, m->d, m->out_norm, m->pf_ssq, m->eps, m->emb, s));
+    }
   }
+  *last = T;
+  return 0;
+}
+
+// The prompt tokens[0..n) (already at m->tokens[start..]) at positions
+// start.., then the LM head of the last one.
+int32_t enqueue_prompt_rows(ss_hip_model* m, const int32_t* tokens, int n, int start) {
+  hipStream_t s = m->ctx->stream;
+  int T = 0;
+  if (int32_t rc = enqueue_rows(m, n, start, false, &T)) return rc;
   HIP_TRY(hipMemcpyAsync(m->hidden, m->pf_h + (size_t)(T - 1) * m->d, sizeof(float) * m->d,
                          hipMemcpyDeviceToDevice, s));
   HIP_TRY(ssk::launch_set_state(m->dpos, m->tokens, start + n - 1, tokens[n - 1], s));
@@ -1479,7 +1496,8 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
       m_alloc(m, (void**)&m->lm_part, sizeof(float2) * lm_grid) ||
       m_alloc(m, (void**)&m->att_o, sizeof(float) * (size_t)m->KVH * m->ns * m->group * m->hd) ||
       m_alloc(m, (void**)&m->att_ml, sizeof(float) * (size_t)m->KVH * m->ns * m->group * 2) ||
-      m_alloc(m, (void**)&m->att_cnt, sizeof(uint32_t) * m->KVH))
+      m_alloc(m, (void**)&m->att_cnt, sizeof(uint32_t) * m->KVH) ||
+      m_alloc(m, (void**)&m->emb, sizeof(float) * (2 * (size_t)m->d + 64)))
     return bail();
   // RoPE (cos, sin) table for every position, computed with the host libm
   // exactly as tensor.c:250-254 computes each pair.
@@ -1613,6 +1631,46 @@ int32_t ss_hip_set_prompt_batch(ss_hip_model_t* m, int32_t min_tokens) {
   if (!m) return fail(kErrParams, "null model");
   m->pf_min = min_tokens;
   return 0;
+}
+
+int32_t ss_hip_embed(ss_hip_model_t* m, const int32_t* tokens, int32_t n, float* out_host) {
+  if (!m || !tokens || n <= 0 || !out_host) return fail(kErrParams, "embed: bad argument");
+  if (n > m->max_seq) return fail(kErrParams, "embed: %d tokens exceed the context of %d", n, m->max_seq);
+  for (int i = 0; i < n; i++)
+    if (tokens[i] < 0 || tokens[i] >= m->embd_rows)
+      return fail(kErrParams, "embed token %d = %d outside [0, %d)", i, tokens[i], m->embd_rows);
+  if (set_device(m->ctx)) return kErrBackend;
+  hipStream_t s = m->ctx->stream;
+  HIP_TRY(hipStreamSynchronize(s));
+  HIP_TRY(hipMemcpy(m->tokens, tokens, sizeof(int) * n, hipMemcpyHostToDevice));
+  HIP_TRY(hipMemsetAsync(m->emb, 0, sizeof(float) * m->d, s));
+  m->host_pos = -1;   // the cache holds positions 0..n-1, but no token to continue from
+  int32_t rc = 0;
+  if (m->kv_type == 0 && m->pf_min >= 0) {
+    int T = 0;
+    rc = prefill_setup(m);
+    if (!rc) rc = enqueue_rows(m, n, 0, true, &T);
+  } else {
+    float* ssq = m->emb + 2 * (size_t)m->d;
+    HIP_TRY(ssk::launch_set_state(m->dpos, m->tokens, 0, tokens[0], s));
+    for (int i = 0; i < n && !rc; i++) {
+      if (m->cancel && *m->cancel) {
+        rc = fail(kErrCancel, "cancelled");
+        break;
+      }
+      rc = run_token(m, false, i);
+      if (!rc && m->out_norm) rc = ssk::launch_sumsq(m->hidden, m->d, 1, ssq, s) ? kErrBackend : 0;
+      if (!rc) rc = ssk::launch_pool_rows(m->hidden, 1, m->d, m->out_norm, ssq, m->eps, m->emb, s) ? kErrBackend : 0;
+    }
+  }
+  if (rc) {
+    hipStreamSynchronize(s);
+    return rc < 0 ? rc : kErrBackend;
+  }
+  HIP_TRY(ssk::launch_embed_finish(m->emb, m->d, n, m->emb + m->d, s));
+  HIP_TRY(hipMemcpyAsync(out_host, m->emb + m->d, sizeof(float) * m->d, hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  return sweep_check(m);
 }
 
 int32_t ss_hip_decode_greedy(ss_hip_model_t* m, int32_t n_steps, int32_t* tokens_out) {

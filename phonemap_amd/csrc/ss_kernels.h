@@ -139,6 +139,12 @@ hipError_t launch_kv_append(void* kc, void* vc, float* ksc, float* vsc, const fl
 hipError_t launch_rope_kv_rows(float* qkv, int ld, int qdim, int kvdim, int head_dim, int rope_dim,
                                const float* cs, const int* dpos, uint16_t* kc, uint16_t* vc, int max_seq,
                                int n, hipStream_t s);
+// acc[j] += sum over the T rows x[t] (stride d) of x[t][j] * k_t * w[j] (the
+// output RMSNorm, k_t from ssq[t]), or of x[t][j] when w is null
+hipError_t launch_pool_rows(const float* x, int T, int d, const float* w, const float* ssq, float eps, float* acc,
+                            hipStream_t s);
+// out = (acc / n) / (|acc / n| + 1e-12)
+hipError_t launch_embed_finish(const float* acc, int d, int n, float* out, hipStream_t s);
 hipError_t launch_swiglu(float* out, const float* g, const float* u, int n, hipStream_t s);
 hipError_t launch_argmax(int* out, const float* x, int n, float2* part, hipStream_t s);
 hipError_t launch_set_state(int* dpos, int* tokens, int pos, int token, hipStream_t s);

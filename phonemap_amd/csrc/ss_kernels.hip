@@ -659,6 +659,39 @@ hipError_t launch_attn_rows_hd(int group, const AttnArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// ------------------------------------------------------------ embedding of a prompt
+// ss_scheduler_embed (layer_scheduler.c:864-911): every token's final hidden
+// state through the output norm (x * k_t * w, k_t = 1/sqrt(ssq_t/d + eps)),
+// summed over the tokens in order into acc (one thread per column), then the
+// mean and the L2 normalisation.
+__global__ void k_pool_rows(const float* __restrict__ x, int T, int d, const float* __restrict__ w,
+                            const float* __restrict__ ssq, float eps, float* __restrict__ acc) {
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  if (j >= d) return;
+  float s = acc[j];
+  for (int t = 0; t < T; ++t) {
+    const float v = x[(size_t)t * d + j];
+    s += w ? v * (1.0f / sqrtf(ssq[t] / (float)d + eps)) * w[j] : v;
+  }
+  acc[j] = s;
+}
+
+__global__ void __launch_bounds__(256) k_embed_finish(const float* __restrict__ acc, int d, int n,
+                                                      float* __restrict__ out) {
+  __shared__ float red[4];
+  const float inv = 1.0f / (float)n;
+  float l2 = 0.f;
+  for (int j = threadIdx.x; j < d; j += 256) {
+    const float e = acc[j] * inv;
+    l2 = fmaf(e, e, l2);
+  }
+  l2 = wave_sum(l2);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = l2;
+  __syncthreads();
+  const float sc = 1.0f / (sqrtf((red[0] + red[1]) + (red[2] + red[3])) + 1e-12f);
+  for (int j = threadIdx.x; j < d; j += 256) out[j] = acc[j] * inv * sc;
+}
+
 // ------------------------------------------------------------ small kernels
 __global__ void k_rmsnorm(float* out, const float* x, const float* w, int n, float eps) {
   __shared__ float red[4];
@@ -900,6 +933,19 @@ hipError_t launch_attention_rows(int head_dim, int group, const AttnArgs& a, hip
   if (head_dim == 64) return launch_attn_rows_hd<64>(group, a, s);
   if (head_dim == 128) return launch_attn_rows_hd<128>(group, a, s);
   return hipErrorInvalidValue;
+}
+
+hipError_t launch_pool_rows(const float* x, int T, int d, const float* w, const float* ssq, float eps, float* acc,
+                            hipStream_t s) {
+  if (T < 1 || d < 1 || (w && !ssq)) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_pool_rows, dim3((d + 255) / 256), dim3(256), 0, s, x, T, d, w, ssq, eps, acc);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed_finish(const float* acc, int d, int n, float* out, hipStream_t s) {
+  if (d < 1 || n < 1) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_embed_finish, dim3(1), dim3(256), 0, s, acc, d, n, out);
+  return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm(float* out, const float* x, const float* w, int n, float eps,

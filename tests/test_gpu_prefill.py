@@ -86,3 +86,33 @@ def test_batched_equals_token_by_token():
     (lb, ab, tb), (lt, at, tt) = out[0], out[-1]
     assert rel_err(lb, lt) <= TOL
     assert ab == at and tb == tt
+
+
+@pytest.mark.parametrize("mode", ["products", "token_by_token", "int8"])
+def test_embed_prompt_matches_oracle(mode):
+    """ss_embed (ss_scheduler_embed, layer_scheduler.c:805-911): every
+    token's final hidden state through the output norm, mean-pooled, L2
+    normalised; a text of a few hundred tokens through the products, token
+    by token, and with the int8 cache."""
+    import ctypes as C
+    path = _model_file("gqa8", **GQA8)
+    text = " ".join("word%d, and the PhoneMap index %d;" % (i, i * 7) for i in range(30))
+    kv = "int8" if mode == "int8" else "f16"
+    L = api._lib()
+    libc = C.CDLL(None)
+    libc.free.argtypes = [C.c_void_p]
+    with api.Model(path, max_context=1024, kv=kv) as m:
+        if mode == "token_by_token":
+            m.set_prompt_batch(-1)
+        toks = m.tokenize(text)
+        assert 100 <= len(toks) <= 1024
+        out = C.POINTER(C.c_float)()
+        dim = C.c_uint32(0)
+        assert L.ss_embed(m.h, text.encode(), C.byref(out), C.byref(dim)) == 0
+        got = np.ctypeslib.as_array(out, (dim.value,)).copy()
+        libc.free(C.cast(out, C.c_void_p))
+    om = oracle.Model(path, 1024, kv)
+    want = om.embed(toks)
+    om.close()
+    assert abs(np.linalg.norm(got) - 1.0) < 1e-5
+    assert rel_err(got, want) <= (TOL if kv == "f16" else 5e-2)
