@@ -136,24 +136,200 @@ __device__ __forceinline__ void cstf(float* p, float v) {
 // every vector memory operation of this wave has completed
 __device__ __forceinline__ void vm_drain() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
-// An x record: 32 values v_j of one block as three int8 levels,
-// v_j ~= s3 * X_j with X_j = 16384*q1_j + 128*q2_j + q3_j (q1 = v/s1 rounded,
-// q2 and q3 the rounded remainders at 1/128 and 1/16384 of s1 = max|v|/127).
-// Words: [0,8) q1, [8,16) q2, [16,24) q3 (4 codes per word, column order),
-// [24] 8 * sum_j X_j (the Q4_0 offset term), [25] s3 (fp32 bits).
-constexpr int kXW = 28;   // words per block (7 x 16 B)
-
 __device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
   return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
          ((uint32_t)d << 24);
 }
 
-// Encode one group of 4 staged values (8 lanes per block, all active).
+template <int QT>
+struct QTraits;
+template <>
+struct QTraits<2> {            // Q4_0
+  static constexpr int kQB = 16;         // code bytes per block
+  static constexpr int kGgufBytes = 18;  // GGUF block bytes
+};
+template <>
+struct QTraits<8> {            // Q8_0
+  static constexpr int kQB = 32;
+  static constexpr int kGgufBytes = 34;
+};
+
+
+// ------------------------------------------------------------ x records
+// Matvec inputs as x records: 16 consecutive values v (times the consumer's
+// RMSNorm weight when it has one) as three int8 levels,
+// v ~= s3 * (16384*q1 + 128*q2 + q3) with s1 = max|v|/127, s3 = s1/16384,
+// exact to max|v| * 2.4e-7 (fp32 rounding size). Record words: [0,4) q1,
+// [4,8) q2, [8,12) q3 (4 codes per word, value order), [12] 8*sum X (the
+// Q4_0 offset term), [13] s3, [14] sum of squares of the unnormalised values
+// (the consumer's RMSNorm statistic), [15] 0. A block dot product of 32
+// weights is two exact integer sums of v_dot4 over the levels (one per
+// 16-value half) and one fp32 rounding per half.
+constexpr int kRW = 16;    // words per x record
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+typedef __attribute__((address_space(1))) void* gbl_ptr_t;
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xf, 0xf, false));
+}
+// reductions over the 16 lanes of a DPP row (all 16 active)
+__device__ __forceinline__ float row16_max(float m) {
+  m = fmaxf(m, dppf<0xb1>(m));
+  m = fmaxf(m, dppf<0x4e>(m));
+  m = fmaxf(m, dppf<0x141>(m));
+  m = fmaxf(m, dppf<0x140>(m));
+  return m;
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dppf<0xb1>(v);
+  v += dppf<0x4e>(v);
+  v += dppf<0x141>(v);
+  v += dppf<0x140>(v);
+  return v;
+}
+__device__ __forceinline__ int row16_sum_i(int v) {
+  v += dpp_i<0xb1>(v);
+  v += dpp_i<0x4e>(v);
+  v += dpp_i<0x141>(v);
+  v += dpp_i<0x140>(v);
+  return v;
+}
+// the low bytes of the 4 lanes of a quad as one word, in every lane of it
+__device__ __forceinline__ uint32_t quad_pack(int q) {
+  return ((uint32_t)dpp_i<0x00>(q) & 0xffu) | (((uint32_t)dpp_i<0x55>(q) & 0xffu) << 8) |
+         (((uint32_t)dpp_i<0xaa>(q) & 0xffu) << 16) | ((uint32_t)dpp_i<0xff>(q) << 24);
+}
+
+struct Enc {
+  uint32_t w[3];
+  uint32_t x8, s3, ssq;
+};
+
+// Encode the values v of the 16 lanes of a row (lane r holds value r);
+// raw is the unnormalised value for the sum of squares. Lane r with r%4 == 0
+// gets words 4l + r/4 (l = 0, 1, 2); every lane gets words 12..14.
+__device__ __forceinline__ Enc enc16(float v, float raw) {
+  const float m = row16_max(fabsf(v));
+  const float s3 = m * (1.0f / (127.0f * 16384.0f));
+  const float s1 = s3 * 16384.0f, s2 = s3 * 128.0f;
+  const float i1 = m > 0.f ? 127.0f / m : 0.f;   // 1 / s1
+  const int q1 = q8c(v * i1);
+  const float r1 = fmaf((float)-q1, s1, v);
+  const int q2 = q8c(r1 * (i1 * 128.0f));
+  const float r2 = fmaf((float)-q2, s2, r1);
+  const int q3 = q8c(r2 * (i1 * 16384.0f));
+  const int X = row16_sum_i(q1 * 16384 + q2 * 128 + q3);
+  Enc e;
+  e.w[0] = quad_pack(q1);
+  e.w[1] = quad_pack(q2);
+  e.w[2] = quad_pack(q3);
+  e.x8 = (uint32_t)(8 * X);
+  e.s3 = __float_as_uint(m == m && m < INFINITY ? s3 : m);   // non-finite input stays non-finite
+  e.ssq = __float_as_uint(row16_sum(raw * raw));
+  return e;
+}
+
+// Write a record (16 lanes, lane r) to LDS or, coherently, to global memory.
+__device__ __forceinline__ void put_rec_lds(uint32_t* dst, const Enc& e, int r) {
+  if ((r & 3) == 0) {
+#pragma unroll
+    for (int l = 0; l < 3; ++l) dst[4 * l + r / 4] = e.w[l];
+  }
+  if (r == 0) {
+    dst[12] = e.x8;
+    dst[13] = e.s3;
+    dst[14] = e.ssq;
+    dst[15] = 0;
+  }
+}
+__device__ __forceinline__ void put_rec_global(uint32_t* dst, const Enc& e, int r) {
+  if ((r & 3) == 0) {
+#pragma unroll
+    for (int l = 0; l < 3; ++l) cst(dst + 4 * l + r / 4, e.w[l]);
+  }
+  if (r == 0) {
+    cst(dst + 12, e.x8);
+    cst(dst + 13, e.s3);
+    cst(dst + 14, e.ssq);
+    cst(dst + 15, 0u);
+  }
+}
+
+// ------------------------------------------------------------ block dot products
+// Q4_0 block (quantize.c:60-72: byte j holds weight j in its low nibble and
+// weight j+16 in its high nibble, value d * (nibble - 8)) against the x
+// records of its two 16-column halves; the caller multiplies by d. The -8
+// offset comes from the records' 8 * sum X. |sum nibble * X| <= 16 * 15 *
+// 2097151 < 2^31.
+__device__ __forceinline__ float q4_dot(const uint4 q, const uint32_t* ra, const uint32_t* rb) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  int a = 0, b = 0;
+#pragma unroll
+  for (int l = 0; l < 3; ++l) {
+    const uint4 xa = *reinterpret_cast<const uint4*>(ra + 4 * l);
+    const uint4 xb = *reinterpret_cast<const uint4*>(rb + 4 * l);
+    if (l) {
+      a <<= 7;
+      b <<= 7;
+    }
+    a = sdot4(w[0] & 0x0F0F0F0Fu, (int)xa.x, a);
+    a = sdot4(w[1] & 0x0F0F0F0Fu, (int)xa.y, a);
+    a = sdot4(w[2] & 0x0F0F0F0Fu, (int)xa.z, a);
+    a = sdot4(w[3] & 0x0F0F0F0Fu, (int)xa.w, a);
+    b = sdot4((w[0] >> 4) & 0x0F0F0F0Fu, (int)xb.x, b);
+    b = sdot4((w[1] >> 4) & 0x0F0F0F0Fu, (int)xb.y, b);
+    b = sdot4((w[2] >> 4) & 0x0F0F0F0Fu, (int)xb.z, b);
+    b = sdot4((w[3] >> 4) & 0x0F0F0F0Fu, (int)xb.w, b);
+  }
+  const uint2 ta = *reinterpret_cast<const uint2*>(ra + 12);
+  const uint2 tb = *reinterpret_cast<const uint2*>(rb + 12);
+  return fmaf((float)(a - (int)ta.x), __uint_as_float(ta.y), (float)(b - (int)tb.x) * __uint_as_float(tb.y));
+}
+
+// Q8_0 block (quantize.c:139-149: 32 int8 codes, value d * code); levels 1-2
+// and level 3 are summed apart to stay in int32 and joined in fp32.
+__device__ __forceinline__ float q8_dot(const uint4 qa, const uint4 qb, const uint32_t* ra, const uint32_t* rb) {
+  const uint32_t wa[4] = {qa.x, qa.y, qa.z, qa.w}, wb[4] = {qb.x, qb.y, qb.z, qb.w};
+  int a12 = 0, b12 = 0, a3 = 0, b3 = 0;
+#pragma unroll
+  for (int l = 0; l < 3; ++l) {
+    const uint4 xa = *reinterpret_cast<const uint4*>(ra + 4 * l);
+    const uint4 xb = *reinterpret_cast<const uint4*>(rb + 4 * l);
+    int sa = l == 1 ? a12 << 7 : 0, sb = l == 1 ? b12 << 7 : 0;
+    sa = sdot4(wa[0], (int)xa.x, sa);
+    sa = sdot4(wa[1], (int)xa.y, sa);
+    sa = sdot4(wa[2], (int)xa.z, sa);
+    sa = sdot4(wa[3], (int)xa.w, sa);
+    sb = sdot4(wb[0], (int)xb.x, sb);
+    sb = sdot4(wb[1], (int)xb.y, sb);
+    sb = sdot4(wb[2], (int)xb.z, sb);
+    sb = sdot4(wb[3], (int)xb.w, sb);
+    if (l < 2) {
+      a12 = sa;
+      b12 = sb;
+    } else {
+      a3 = sa;
+      b3 = sb;
+    }
+  }
+  const float sa3 = __uint_as_float(ra[13]), sb3 = __uint_as_float(rb[13]);
+  return fmaf(fmaf((float)a12, 128.0f, (float)a3), sa3, fmaf((float)b12, 128.0f, (float)b3) * sb3);
+}
+
+
+// A 32-column block staged in LDS by a matvec: the records of its two
+// 16-value halves, back to back.
+constexpr int kXW = 2 * kRW;   // words per block
+
+// Encode one group of 4 values into the block's records in LDS: 8 lanes per
+// block (all active), lane sub holding values 4*sub .. 4*sub+3, so each
+// record is one DPP quad. Word [14] (the sum of squares) is not written: a
+// matvec that encodes its own x sums the squares itself.
 __device__ __forceinline__ void encode4(int* xb, int sub, float4 v) {
   float m = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
   m = fmaxf(m, dpp<0xb1>(m));
   m = fmaxf(m, dpp<0x4e>(m));
-  m = fmaxf(m, dpp<0x141>(m));
   const float s3 = m * (1.0f / (127.0f * 16384.0f));
   const float s1 = s3 * 16384.0f, s2 = s3 * 128.0f;
   const float i1 = m > 0.f ? 127.0f / m : 0.f;   // 1 / s1
@@ -170,27 +346,15 @@ __device__ __forceinline__ void encode4(int* xb, int sub, float4 v) {
   }
   X += dpp_i<0xb1>(X);
   X += dpp_i<0x4e>(X);
-  X += dpp_i<0x141>(X);
-  xb[sub] = (int)pack4(q1[0], q1[1], q1[2], q1[3]);
-  xb[8 + sub] = (int)pack4(q2[0], q2[1], q2[2], q2[3]);
-  xb[16 + sub] = (int)pack4(q3[0], q3[1], q3[2], q3[3]);
-  if (sub == 0) {
-    xb[24] = 8 * X;
-    xb[25] = __float_as_int(m == m && m < INFINITY ? s3 : m);   // non-finite x stays non-finite
+  int* r = xb + (sub >> 2) * kRW;
+  const int w = sub & 3;
+  r[w] = (int)pack4(q1[0], q1[1], q1[2], q1[3]);
+  r[4 + w] = (int)pack4(q2[0], q2[1], q2[2], q2[3]);
+  r[8 + w] = (int)pack4(q3[0], q3[1], q3[2], q3[3]);
+  if (w == 0) {
+    r[12] = 8 * X;
+    r[13] = __float_as_int(m == m && m < INFINITY ? s3 : m);   // non-finite x stays non-finite
   }
 }
-
-template <int QT>
-struct QTraits;
-template <>
-struct QTraits<2> {            // Q4_0
-  static constexpr int kQB = 16;         // code bytes per block
-  static constexpr int kGgufBytes = 18;  // GGUF block bytes
-};
-template <>
-struct QTraits<8> {            // Q8_0
-  static constexpr int kQB = 32;
-  static constexpr int kGgufBytes = 34;
-};
 
 }  // namespace ssk

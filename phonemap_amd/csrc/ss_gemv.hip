@@ -38,61 +38,6 @@ namespace {
 // block. Words: [0,8) q1, [8,16) q2, [16,24) q3 (4 codes per word, column
 // order), [24] 8 * sum_j X_j (the Q4_0 offset term), [25] s3 (fp32 bits).
 
-// Q4_0 block (quantize.c:60-72): byte j holds weight j (low nibble) and
-// weight j+16 (high nibble), value = d * (nibble - 8). Returns
-// sum_j (nibble_j - 8) * X_j exactly; the caller multiplies by d * s3. The -8
-// offset is applied through the staged 8 * sum_j X_j. |sum_j nibble_j X_j|
-// <= 32 * 15 * 127 * 16513 < 2^31.
-__device__ __forceinline__ float q4_block(const uint4 q, const int* __restrict__ xb) {
-  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-  uint32_t lo[4], hi[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    lo[k] = w[k] & 0x0F0F0F0Fu;
-    hi[k] = (w[k] >> 4) & 0x0F0F0F0Fu;
-  }
-  int acc = 0;
-#pragma unroll
-  for (int l = 0; l < 3; ++l) {
-    if (l) acc <<= 7;
-    const int4 xa = *reinterpret_cast<const int4*>(xb + 8 * l);
-    const int4 xc = *reinterpret_cast<const int4*>(xb + 8 * l + 4);
-    acc = sdot4(lo[0], xa.x, acc);
-    acc = sdot4(lo[1], xa.y, acc);
-    acc = sdot4(lo[2], xa.z, acc);
-    acc = sdot4(lo[3], xa.w, acc);
-    acc = sdot4(hi[0], xc.x, acc);
-    acc = sdot4(hi[1], xc.y, acc);
-    acc = sdot4(hi[2], xc.z, acc);
-    acc = sdot4(hi[3], xc.w, acc);
-  }
-  return (float)(acc - xb[24]);
-}
-
-// Q8_0 block (quantize.c:139-149): 32 int8 codes, value = d * code. Returns
-// sum_j code_j * X_j; levels 1-2 and level 3 are summed apart to stay in
-// int32, and joined in fp32.
-__device__ __forceinline__ float q8_block(const uint4 a, const uint4 b, const int* __restrict__ xb) {
-  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-  int acc = 0, acc3 = 0;
-#pragma unroll
-  for (int l = 0; l < 3; ++l) {
-    const int4 xa = *reinterpret_cast<const int4*>(xb + 8 * l);
-    const int4 xc = *reinterpret_cast<const int4*>(xb + 8 * l + 4);
-    int s = l == 1 ? acc << 7 : 0;
-    s = sdot4(w[0], xa.x, s);
-    s = sdot4(w[1], xa.y, s);
-    s = sdot4(w[2], xa.z, s);
-    s = sdot4(w[3], xa.w, s);
-    s = sdot4(w[4], xc.x, s);
-    s = sdot4(w[5], xc.y, s);
-    s = sdot4(w[6], xc.z, s);
-    s = sdot4(w[7], xc.w, s);
-    if (l < 2) acc = s; else acc3 = s;
-  }
-  return fmaf((float)acc, 128.0f, (float)acc3);
-}
-
 // A wave stages only the x slice of its own unit (UT*4 blocks of 32 values),
 // times the RMSNorm weight nw when set (the x*w of cpu_neon.c:114; the 1/rms
 // factor is applied to the row sums), into its own LDS region: the waves of a
@@ -266,42 +211,86 @@ __device__ __forceinline__ void load_round(Round<QT, NMAT, UT>& f, const GemvArg
   }
 }
 
-// xs holds the unit's staged x; kb is this lane's block within a tile. Tiles
-// past the row (last unit) meet an all-zero x slice (s3 = 0) and add exactly
-// 0, so every tile is processed and the loads have no conditional use.
+// xs holds the unit's staged x records; kb is this lane's block within a
+// tile. Tiles past the row (last unit) meet all-zero records (s3 = 0) and
+// add exactly 0, so every tile is processed and the loads have no
+// conditional use.
 template <int QT, int NMAT, int UT>
 __device__ __forceinline__ void fma_round(float (&acc)[NMAT], const Round<QT, NMAT, UT>& f, const int* xs,
                                           int kb) {
 #pragma unroll
   for (int k = 0; k < UT; ++k) {
-    {
-      const int* xb = xs + (k * kTB + kb) * kXW;
-      const float s3 = __int_as_float(xb[25]);
+    const uint32_t* ra = reinterpret_cast<const uint32_t*>(xs + (k * kTB + kb) * kXW);
 #pragma unroll
-      for (int m = 0; m < NMAT; ++m) {
-        float s;
-        if constexpr (QT == 2)
-          s = q4_block(f.q[m][k][0], xb);
-        else
-          s = q8_block(f.q[m][k][0], f.q[m][k][1], xb);
-        const uint32_t sw = f.sc[m][k / 2];
-        const float d = h2f((uint16_t)(k & 1 ? sw >> 16 : sw & 0xffffu));
-        acc[m] = fmaf(d * s3, s, acc[m]);
-      }
+    for (int m = 0; m < NMAT; ++m) {
+      float s;
+      if constexpr (QT == 2)
+        s = q4_dot(f.q[m][k][0], ra, ra + kRW);
+      else
+        s = q8_dot(f.q[m][k][0], f.q[m][k][1], ra, ra + kRW);
+      const uint32_t sw = f.sc[m][k / 2];
+      const float d = h2f((uint16_t)(k & 1 ? sw >> 16 : sw & 0xffffu));
+      acc[m] = fmaf(d, s, acc[m]);
     }
   }
 }
 
+// Pre-encoded x: the unit's records (UT tiles x 4 blocks x 2 records of
+// 64 B, written by the producer of x) copied straight into this wave's LDS
+// region, 16 bytes per lane per instruction. The record buffer is padded
+// with zero records to a multiple of 8 tiles, so the last unit of a row
+// reads zeros past the vector.
+template <int UT>
+__device__ __forceinline__ void rfetch(int* xw, const uint32_t* __restrict__ xr, int u, int lane) {
+  constexpr int kPieces = UT * kTB * kXW / 4;   // 16-byte pieces of the unit
+  const uint32_t* src = xr + (size_t)u * UT * kTB * kXW;
+#pragma unroll
+  for (int i = 0; i < kPieces; i += kWave)
+    __builtin_amdgcn_global_load_lds((gbl_ptr_t)(src + (size_t)(i + lane) * 4), (lds_ptr_t)(xw + i * 4), 16, 0,
+                                     0);
+}
+
 // Epilogue in wave 0: every lane holds row `row`'s final value(s) v[]; lanes
 // with `own` set (one per row) write.
+// Values every lane of wave 0 loads before the weights, for its epilogue:
+// the residual y[row] (EPI_ADD) and the next consumer's RMSNorm weight
+// nw_out[row], so no load waits at the end of the kernel.
+struct EpiPre {
+  float y = 0.f, nw = 1.f;
+};
+
+template <int EPI>
+__device__ __forceinline__ EpiPre epi_prefetch(const GemvArgs& a, int row) {
+  EpiPre p;
+  const int rr = min(row, a.rows - 1);
+  if constexpr (EPI == EPI_ADD) p.y = a.y[rr];
+  if constexpr (EPI == EPI_STORE || EPI == EPI_ADD || EPI == EPI_SWIGLU)
+    if (a.xr_out && a.nw_out) p.nw = a.nw_out[rr];
+  return p;
+}
+
+// Epilogue in wave 0: every lane holds row `row`'s final value(s) v[]; lanes
+// with `own` set (one per row) write. With xr_out set, the 16 rows of the
+// group are also written as one x record of (value * nw_out) for the next
+// matvec (each DPP row of the wave holds the group's 16 rows in order).
 template <int EPI, int NMAT>
-__device__ __forceinline__ void epilogue(const GemvArgs& a, int row, bool own, const float (&v)[NMAT]) {
+__device__ __forceinline__ void epilogue(const GemvArgs& a, int row, bool own, const float (&v)[NMAT],
+                                         const EpiPre& pre) {
   const bool valid = own && row < a.rows;
-  if constexpr (EPI == EPI_STORE || EPI == EPI_ADD) {
-    if (valid) a.y[row] = EPI == EPI_ADD ? v[0] + a.y[row] : v[0];   // layer_scheduler.c:484,566
-  } else if constexpr (EPI == EPI_SWIGLU) {
-    const float g = v[0], u = v[NMAT - 1];
-    if (valid) a.y[row] = u * (g / (1.0f + expf(-g)));                // layer_scheduler.c:540-547
+  if constexpr (EPI == EPI_STORE || EPI == EPI_ADD || EPI == EPI_SWIGLU) {
+    float out;
+    if constexpr (EPI == EPI_SWIGLU) {
+      const float g = v[0], u = v[NMAT - 1];
+      out = u * (g / (1.0f + expf(-g)));                               // layer_scheduler.c:540-547
+    } else {
+      out = EPI == EPI_ADD ? v[0] + pre.y : v[0];                       // layer_scheduler.c:484,566
+    }
+    if (row >= a.rows) out = 0.f;
+    if (valid) a.y[row] = out;
+    if (a.xr_out) {
+      const Enc e = enc16(out * pre.nw, out);
+      if (own) put_rec_lds(a.xr_out + (size_t)(row / kRG) * kRW, e, row % kRG);
+    }
   } else if constexpr (EPI == EPI_QKV) {
     // rows of [Wq; Wk; Wv]; q and k rows (i, i+1) are lanes (2j, 2j+1): rotate
     // the pair with the position's (cos, sin), tensor.c:250-273
@@ -349,7 +338,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int row, bool own, c
 template <int QT, int NMAT>
 constexpr int gemv_max_waves() { return QT == 8 || NMAT == 2 ? 8 : 16; }
 
-template <int QT, int NMAT, int EPI, int UT, bool MERGE>
+template <int QT, int NMAT, int EPI, int UT, bool MERGE, bool PX>
 __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(const GemvArgs a) {
   extern __shared__ float4 smem4[];
   int* xs = reinterpret_cast<int*>(smem4);
@@ -370,11 +359,19 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
   for (int m = 0; m < NMAT; ++m) acc[m] = 0.f;
   float ssq = 0.f;
   Round<QT, NMAT, UT> rd;
+  EpiPre pre;
+  if (wave == 0) pre = epi_prefetch<EPI>(a, g * kRG + lane % kRG);
 
   // units go to waves round robin (one round for rows of up to S units)
   const int active = MERGE ? merge_active(a) : 0;
   for (int u = wave; u < nu; u += S) {
-    if constexpr (MERGE) {
+    if constexpr (PX) {
+      // records first: vector memory operations complete in order
+      rfetch<UT>(xw, a.xr, u, lane);
+      load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
+      vm_drain();
+      if (a.nw && lane < UT * kTB * 2) ssq += __int_as_float(xw[lane * kRW + 14]);
+    } else if constexpr (MERGE) {
       MSlice<UT> mp;
       mfetch<UT>(mp, a, u, active, lane);
       load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
@@ -420,7 +417,7 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
 #pragma unroll
     for (int m = 0; m < NMAT; ++m) v[m] *= scale;
   }
-  epilogue<EPI, NMAT>(a, g * kRG + r, lane < kRG, v);
+  epilogue<EPI, NMAT>(a, g * kRG + r, lane < kRG, v, pre);
 }
 
 // GGUF blocks -> tiled planes. Source block i of a [rows x nb] tensor whose
@@ -453,29 +450,42 @@ __global__ void k_pack(const uint8_t* __restrict__ src, uint8_t* __restrict__ qs
 // Row `token` of a packed table, dequantised exactly as quantize.c:60-72 /
 // 139-149 (one fp32 multiply per weight). With tokens set, workgroup z
 // writes row tokens[*dpos + z] to out + z * cols (a prompt's rows at once).
+// With xr set (one row), the row is also written as x records of
+// row * nw (the first layer's attn_norm) for the first matvec.
+template <int QT>
+__device__ __forceinline__ float embed_value(const PackedMat& t, int tok, int ntk, int j) {
+  constexpr int kQB = QTraits<QT>::kQB;
+  const int b = j >> 5, p = j & 31;
+  const int l = tile_lane(tok % kRG, b);
+  const uint8_t* q = t.qs + tile_idx(tok / kRG, ntk, b / kTB, l) * kQB;
+  const float d = h2f(t.ds[scale_idx(tok / kRG, ntk, b / kTB, l)]);
+  if constexpr (QT == 2) {
+    const uint8_t v = q[p & 15];
+    return d * (float)((int)(p < 16 ? v & 0xF : v >> 4) - 8);
+  } else {
+    return d * (float)(int8_t)q[p];
+  }
+}
+
 template <int QT>
 __global__ void k_embed(PackedMat t, int cols, const int* tokens, const int* dpos, int token,
-                        float* out) {
-  constexpr int kQB = QTraits<QT>::kQB;
+                        float* out, const float* nw, uint32_t* xr) {
   const int tok = tokens ? tokens[*dpos + blockIdx.x] : token;
   out += (size_t)blockIdx.x * cols;
   const int nb = cols >> 5;
   const int ntk = (nb + kTB - 1) / kTB;
-  for (int b = threadIdx.x; b < nb; b += blockDim.x) {
-    const int l = tile_lane(tok % kRG, b);
-    const size_t i = tile_idx(tok / kRG, ntk, b / kTB, l);
-    const float d = h2f(t.ds[scale_idx(tok / kRG, ntk, b / kTB, l)]);
-    const uint8_t* q = t.qs + i * kQB;
-    float* o = out + b * 32;
-    if constexpr (QT == 2) {
-      for (int j = 0; j < 16; ++j) {
-        const uint8_t v = q[j];
-        o[j] = d * (float)((int)(v & 0xF) - 8);
-        o[j + 16] = d * (float)((int)(v >> 4) - 8);
-      }
-    } else {
-      for (int j = 0; j < 32; ++j) o[j] = d * (float)(int8_t)q[j];
-    }
+  for (int j = threadIdx.x; j < cols; j += blockDim.x) out[j] = embed_value<QT>(t, tok, ntk, j);
+  if (!xr) return;
+  // lane r of each 16-lane row holds value 16 * record + r; the loop bound
+  // is uniform per wave (blockDim is a multiple of 64), so enc16 sees all
+  // 16 lanes of its row
+  const int lane = threadIdx.x & 63;
+  for (int base = (threadIdx.x >> 6) * kWave; base < cols; base += blockDim.x) {
+    const int j = base + lane;
+    const bool in = j < cols;
+    const float v = in ? embed_value<QT>(t, tok, ntk, j) : 0.f;
+    const Enc e = enc16(in ? v * nw[j] : 0.f, v);
+    if (in) put_rec_lds(xr + (size_t)(j >> 4) * kRW, e, j & 15);
   }
 }
 
@@ -512,29 +522,35 @@ __global__ void k_argmax_merge(const float2* part, int n, const float* y, int* o
   }
 }
 
-template <int QT, int NMAT, int EPI, bool MERGE = false>
+template <int QT, int NMAT, int EPI, bool MERGE = false, bool PX = false>
 hipError_t launch_t(const GemvArgs& a, hipStream_t s) {
   GemvPlan p = gemv_plan(a.rows, a.cols, QT, NMAT);
   KernelEvents& ev = kernel_events();
   if (ev.start) {
-    hipExtLaunchKernelGGL((k_gemv<QT, NMAT, EPI, kGemvUnit, MERGE>), dim3(p.grid), dim3(p.threads),
+    hipExtLaunchKernelGGL((k_gemv<QT, NMAT, EPI, kGemvUnit, MERGE, PX>), dim3(p.grid), dim3(p.threads),
                           p.lds_bytes, s, ev.start, ev.stop, 0, a);
     ev.used = true;
   } else {
-    hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, kGemvUnit, MERGE>), dim3(p.grid), dim3(p.threads), p.lds_bytes,
-                       s, a);
+    hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, kGemvUnit, MERGE, PX>), dim3(p.grid), dim3(p.threads),
+                       p.lds_bytes, s, a);
   }
   return hipGetLastError();
+}
+
+// x read from the producer's records (a.xr) or staged from a.x by the matvec
+template <int QT, int NMAT, int EPI>
+hipError_t launch_x(const GemvArgs& a, hipStream_t s) {
+  return a.xr ? launch_t<QT, NMAT, EPI, false, true>(a, s) : launch_t<QT, NMAT, EPI>(a, s);
 }
 
 template <int QT>
 hipError_t launch_q(int epi, const GemvArgs& a, hipStream_t s) {
   switch (epi) {
-    case EPI_STORE: return launch_t<QT, 1, EPI_STORE>(a, s);
-    case EPI_ADD: return a.att_o ? launch_t<QT, 1, EPI_ADD, true>(a, s) : launch_t<QT, 1, EPI_ADD>(a, s);
-    case EPI_SWIGLU: return launch_t<QT, 2, EPI_SWIGLU>(a, s);
-    case EPI_QKV: return launch_t<QT, 1, EPI_QKV>(a, s);
-    case EPI_LOGITS: return launch_t<QT, 1, EPI_LOGITS>(a, s);
+    case EPI_STORE: return launch_x<QT, 1, EPI_STORE>(a, s);
+    case EPI_ADD: return a.att_o ? launch_t<QT, 1, EPI_ADD, true>(a, s) : launch_x<QT, 1, EPI_ADD>(a, s);
+    case EPI_SWIGLU: return launch_x<QT, 2, EPI_SWIGLU>(a, s);
+    case EPI_QKV: return launch_x<QT, 1, EPI_QKV>(a, s);
+    case EPI_LOGITS: return launch_x<QT, 1, EPI_LOGITS>(a, s);
     default: return hipErrorInvalidValue;
   }
 }
@@ -591,6 +607,8 @@ PackedMat packed_view(const void* base, int type, int64_t rows, int cols) {
 }
 
 hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t s) {
+  if (a.att_o && a.xr) return hipErrorInvalidValue;
+  if (a.xr_out && epi != EPI_STORE && epi != EPI_ADD && epi != EPI_SWIGLU) return hipErrorInvalidValue;
   if (a.att_o && (epi != EPI_ADD || !a.att_ml || !a.dpos || a.att_ns < 1 || a.att_ns > kMergeSplits ||
                   a.att_group < 1 || a.head_dim < 32 || a.head_dim % 32 || a.cols % a.head_dim))
     return hipErrorInvalidValue;
@@ -618,11 +636,12 @@ hipError_t launch_pack(int type, const uint8_t* src, uint8_t* qs, uint16_t* ds, 
 }
 
 hipError_t launch_embed(int type, PackedMat t, int cols, const int* tokens, const int* dpos,
-                        int token, float* out, hipStream_t s) {
+                        int token, float* out, const float* nw, uint32_t* xr, hipStream_t s) {
+  if (xr && !nw) return hipErrorInvalidValue;
   if (type == 2)
-    hipLaunchKernelGGL(k_embed<2>, dim3(1), dim3(256), 0, s, t, cols, tokens, dpos, token, out);
+    hipLaunchKernelGGL(k_embed<2>, dim3(1), dim3(256), 0, s, t, cols, tokens, dpos, token, out, nw, xr);
   else if (type == 8)
-    hipLaunchKernelGGL(k_embed<8>, dim3(1), dim3(256), 0, s, t, cols, tokens, dpos, token, out);
+    hipLaunchKernelGGL(k_embed<8>, dim3(1), dim3(256), 0, s, t, cols, tokens, dpos, token, out, nw, xr);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -632,9 +651,9 @@ hipError_t launch_embed_rows(int type, PackedMat t, int cols, const int* tokens,
                              float* out, hipStream_t s) {
   if (n <= 0 || !tokens || !dpos) return hipErrorInvalidValue;
   if (type == 2)
-    hipLaunchKernelGGL(k_embed<2>, dim3(n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out);
+    hipLaunchKernelGGL(k_embed<2>, dim3(n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out, nullptr, nullptr);
   else if (type == 8)
-    hipLaunchKernelGGL(k_embed<8>, dim3(n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out);
+    hipLaunchKernelGGL(k_embed<8>, dim3(n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out, nullptr, nullptr);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -482,8 +482,8 @@ int32_t ss_hip_embed_row(ss_hip_ctx_t* c, float* out, const void* table, int32_t
                          int32_t rows, int32_t cols, int32_t token, void* stream) {
   if (!c || !out || !table || token < 0 || token >= rows) return fail(kErrParams, "embed: bad argument");
   if (int32_t rc = check_mv(rows, cols, type)) return rc;
-  HIP_TRY(ssk::launch_embed(type, view(table, type, rows, cols), cols, nullptr, nullptr, token, out,
-                            pick(c, stream)));
+  HIP_TRY(ssk::launch_embed(type, view(table, type, rows, cols), cols, nullptr, nullptr, token, out, nullptr,
+                            nullptr, pick(c, stream)));
   return 0;
 }
 
@@ -581,6 +581,10 @@ struct ss_hip_model {
   int lm_grid = 0;
   float *att_o = nullptr, *att_ml = nullptr;
   uint32_t* att_cnt = nullptr;   // [KVH] split arrivals of the attention merge (zero between launches)
+  // x records (ss_device.h) passed from each matvec to the next: xr_hid holds
+  // the residual stream times the next RMSNorm weight (written by the
+  // embedding, Wo and down), xr_ffn the SwiGLU output (written by gate/up)
+  uint32_t *xr_hid = nullptr, *xr_ffn = nullptr;
 
   int* h_io = nullptr;   // pinned host scratch
   hipGraphExec_t g_full = nullptr, g_nohead = nullptr;
@@ -614,6 +618,7 @@ struct ss_hip_model {
   uint64_t host_bytes = 0;           // pinned bytes held
   int* pos_iota = nullptr;           // device [max_seq]: value i at index i
   float* hid_all = nullptr;          // device [max_seq][d]: residual streams of a prompt
+  uint32_t* xr_all = nullptr;        // device [max_seq][xrec_words(d)]: their x records
   // prompts as matrix products (fp16 KV): up to pf_cap tokens per pass over the
   // layers, in row-major [token][...] buffers
   int pf_min = 0;                    // shortest prompt evaluated this way (0: the default)
@@ -862,20 +867,28 @@ int32_t sweep_check(ss_hip_model* m) {
               w[1] & 0xffffu, w[1] >> 16);
 }
 
-// Token embedding of tokens[*dpos] into hidden (layer_scheduler.c:578-595).
-int32_t enqueue_embed(ss_hip_model* m, const int* dpos, float* hidden) {
+// Token embedding of tokens[*dpos] into hidden (layer_scheduler.c:578-595),
+// and the x records of hidden * attn_norm[0] into xr for the first layer's
+// QKV matvec.
+int32_t enqueue_embed(ss_hip_model* m, const int* dpos, float* hidden, uint32_t* xr) {
   hipStream_t s = m->ctx->stream;
   HIP_TRY(timed(m, PC_OTHER, 0, [&] {
     return ssk::launch_embed(m->t_embd, view(m->embd, m->t_embd, m->embd_rows, m->d), m->d, m->tokens,
-                             dpos, 0, hidden, s);
+                             dpos, 0, hidden, m->layers[0].attn_norm, xr, s);
   }));
   return 0;
 }
 
 // One decoder layer (process_layer, layer_scheduler.c:291-567) for the token
 // at position *dpos whose residual stream is hidden; ly holds the layer's
-// weights (resident, or the streaming slot it was uploaded to).
-int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden, const int* dpos) {
+// weights (resident, or the streaming slot it was uploaded to). xr holds the
+// token's hidden * attn_norm as x records (written by the embedding or the
+// previous layer's down matvec), which the QKV matvec reads; down writes the
+// records of the next layer's attn_norm (or output_norm after the last) back
+// into xr. Inside the layer, Wo writes the records (xr_hid) gate/up reads
+// and gate/up those (xr_ffn) down reads.
+int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden, const int* dpos,
+                      uint32_t* xr) {
   hipStream_t s = m->ctx->stream;
   int* dp = const_cast<int*>(dpos);
   char* kc = static_cast<char*>(m->kc) + (size_t)l * m->kv_layer_elems * (m->kv_type ? 1 : 2);
@@ -898,6 +911,7 @@ int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden,
   a.kcache = kc;
   a.vcache = vc;
   a.kv_f32 = m->kv_f32;
+  a.xr = xr;
   HIP_TRY(timed(m, q_class(ly.t_qkv), matvec_bytes(ly.t_qkv, a.rows, m->d, 1),
                 [&] { return ssk::launch_gemv(ssk::EPI_QKV, a, s); }));
   if (m->kv_type == 1)
@@ -938,6 +952,8 @@ int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden,
     o.head_dim = m->hd;
     o.dpos = dp;
   }
+  o.xr_out = m->xr_hid;
+  o.nw_out = ly.ffn_norm;
   HIP_TRY(timed(m, q_class(ly.t_o), matvec_bytes(ly.t_o, m->d, m->qdim, 1),
                 [&] { return ssk::launch_gemv(ssk::EPI_ADD, o, s); }));
 
@@ -946,11 +962,16 @@ int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden,
   gu.w2 = view(ly.wu, ly.t_gu, m->ffn, m->d);
   gu.nw = ly.ffn_norm;
   gu.eps = m->eps;
+  gu.xr = m->xr_hid;
+  gu.xr_out = m->xr_ffn;
   HIP_TRY(timed(m, q_class(ly.t_gu), matvec_bytes(ly.t_gu, m->ffn, m->d, 2),
                 [&] { return ssk::launch_gemv(ssk::EPI_SWIGLU, gu, s); }));
 
   // 5. hidden += Wdown act                                       (:552-566)
   ssk::GemvArgs dn = gemv_args(ly.wd, m->ffn_act, hidden, m->d, m->ffn, ly.t_d);
+  dn.xr = m->xr_ffn;
+  dn.xr_out = xr;
+  dn.nw_out = l + 1 < m->L ? m->layers[l + 1].attn_norm : m->out_norm;
   HIP_TRY(timed(m, q_class(ly.t_d), matvec_bytes(ly.t_d, m->d, m->ffn, 1),
                 [&] { return ssk::launch_gemv(ssk::EPI_ADD, dn, s); }));
   return 0;
@@ -958,11 +979,14 @@ int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden,
 
 // output_norm + LM head + first-max argmax (:634-662, tensor.c:318-328) of the
 // token at *m->dpos: the winner goes to tokens[pos + 1] and pos advances.
-int32_t enqueue_head(ss_hip_model* m, const float* hidden) {
+// With xr set, it holds hidden * output_norm as x records (the last layer's
+// down matvec wrote them); otherwise the matvec stages hidden itself.
+int32_t enqueue_head(ss_hip_model* m, const float* hidden, const uint32_t* xr) {
   hipStream_t s = m->ctx->stream;
   ssk::GemvArgs h = gemv_args(m->out, hidden, m->logits, m->vocab, m->d, m->t_out);
   h.nw = m->out_norm;
   h.eps = m->eps;
+  h.xr = xr;
   h.part = m->lm_part;
   HIP_TRY(timed(m, q_class(m->t_out), matvec_bytes(m->t_out, m->vocab, m->d, 1),
                 [&] { return ssk::launch_gemv(ssk::EPI_LOGITS, h, s); }));
@@ -1049,19 +1073,19 @@ int32_t enqueue_token(ss_hip_model* m, bool with_head) {
     m->sw_epoch += (uint32_t)ssk::sweep_phases(m->L, with_head);
     return 0;
   }
-  if (int32_t rc = enqueue_embed(m, m->dpos, m->hidden)) return rc;
+  if (int32_t rc = enqueue_embed(m, m->dpos, m->hidden, m->xr_hid)) return rc;
   for (int l = 0; l < m->L; l++) {
     if (m->cancel && *m->cancel && !m->prof) return fail(kErrCancel, "cancelled");
     if (m->streaming) {
       DevLayer ly;
       if (int32_t rc = stream_acquire(m, l, &ly)) return rc;
-      if (int32_t rc = enqueue_layer(m, l, ly, m->hidden, m->dpos)) return rc;
+      if (int32_t rc = enqueue_layer(m, l, ly, m->hidden, m->dpos, m->xr_hid)) return rc;
       if (int32_t rc = stream_release(m)) return rc;
     } else {
-      if (int32_t rc = enqueue_layer(m, l, m->layers[l], m->hidden, m->dpos)) return rc;
+      if (int32_t rc = enqueue_layer(m, l, m->layers[l], m->hidden, m->dpos, m->xr_hid)) return rc;
     }
   }
-  if (with_head) return enqueue_head(m, m->hidden);
+  if (with_head) return enqueue_head(m, m->hidden, m->xr_hid);
   HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_advance(m->dpos, s); }));
   return 0;
 }
@@ -1070,22 +1094,26 @@ int32_t enqueue_token(ss_hip_model* m, bool with_head) {
 // (layer_scheduler.c:681-803): every layer is uploaded once for the whole
 // prompt and applied to each token in order (a token's attention reads the
 // K/V the earlier tokens of the prompt appended to this layer's cache).
+// x records of prompt token i in the layer-major order
+uint32_t* xr_of(ss_hip_model* m, int i) { return m->xr_all + (size_t)i * ssk::xrec_words(m->d); }
+
 int32_t enqueue_prompt_layer_major(ss_hip_model* m, const int32_t* tokens, int n, int start) {
   hipStream_t s = m->ctx->stream;
   for (int i = 0; i < n; i++)
-    if (int32_t rc = enqueue_embed(m, m->pos_iota + start + i, m->hid_all + (size_t)i * m->d)) return rc;
+    if (int32_t rc = enqueue_embed(m, m->pos_iota + start + i, m->hid_all + (size_t)i * m->d, xr_of(m, i))) return rc;
   for (int l = 0; l < m->L; l++) {
     if (m->cancel && *m->cancel) return fail(kErrCancel, "cancelled");
     DevLayer ly;
     if (int32_t rc = stream_acquire(m, l, &ly)) return rc;
     for (int i = 0; i < n; i++)
-      if (int32_t rc = enqueue_layer(m, l, ly, m->hid_all + (size_t)i * m->d, m->pos_iota + start + i)) return rc;
+      if (int32_t rc = enqueue_layer(m, l, ly, m->hid_all + (size_t)i * m->d, m->pos_iota + start + i, xr_of(m, i)))
+        return rc;
     if (int32_t rc = stream_release(m)) return rc;
   }
   HIP_TRY(hipMemcpyAsync(m->hidden, m->hid_all + (size_t)(n - 1) * m->d, sizeof(float) * m->d,
                          hipMemcpyDeviceToDevice, s));
   HIP_TRY(ssk::launch_set_state(m->dpos, m->tokens, start + n - 1, tokens[n - 1], s));
-  return enqueue_head(m, m->hidden);
+  return enqueue_head(m, m->hidden, xr_of(m, n - 1));
 }
 
 // ---- prompts as matrix products (ss_scheduler_prefill, layer_scheduler.c:681-803)
@@ -1238,7 +1266,7 @@ int32_t enqueue_prompt_rows(ss_hip_model* m, const int32_t* tokens, int n, int s
   HIP_TRY(hipMemcpyAsync(m->hidden, m->pf_h + (size_t)(T - 1) * m->d, sizeof(float) * m->d,
                          hipMemcpyDeviceToDevice, s));
   HIP_TRY(ssk::launch_set_state(m->dpos, m->tokens, start + n - 1, tokens[n - 1], s));
-  return enqueue_head(m, m->hidden);
+  return enqueue_head(m, m->hidden, nullptr);
 }
 
 int32_t capture(ss_hip_model* m, bool with_head, hipGraphExec_t* out) {
@@ -1312,7 +1340,8 @@ int32_t stream_setup(ss_hip_model* m, const ss_hip_model_desc_t* d) {
   std::vector<int> iota(m->max_seq);
   for (int i = 0; i < m->max_seq; i++) iota[i] = i;
   HIP_TRY(hipMemcpy(m->pos_iota, iota.data(), sizeof(int) * m->max_seq, hipMemcpyHostToDevice));
-  return m_alloc(m, (void**)&m->hid_all, sizeof(float) * (size_t)m->max_seq * m->d, false);
+  if (int32_t rc = m_alloc(m, (void**)&m->hid_all, sizeof(float) * (size_t)m->max_seq * m->d, false)) return rc;
+  return m_alloc(m, (void**)&m->xr_all, sizeof(uint32_t) * (size_t)m->max_seq * ssk::xrec_words(m->d));
 }
 
 // Streaming mode: layer l's matrices were packed into slot 0; keep them in
@@ -1497,6 +1526,8 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
       m_alloc(m, (void**)&m->att_o, sizeof(float) * (size_t)m->KVH * m->ns * m->group * m->hd) ||
       m_alloc(m, (void**)&m->att_ml, sizeof(float) * (size_t)m->KVH * m->ns * m->group * 2) ||
       m_alloc(m, (void**)&m->att_cnt, sizeof(uint32_t) * m->KVH) ||
+      m_alloc(m, (void**)&m->xr_hid, sizeof(uint32_t) * ssk::xrec_words(m->d)) ||
+      m_alloc(m, (void**)&m->xr_ffn, sizeof(uint32_t) * ssk::xrec_words(m->ffn)) ||
       m_alloc(m, (void**)&m->emb, sizeof(float) * (2 * (size_t)m->d + 64)))
     return bail();
   // RoPE (cos, sin) table for every position, computed with the host libm

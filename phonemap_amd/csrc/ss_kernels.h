@@ -44,7 +44,19 @@ struct GemvArgs {
   const float* att_o;        // [kvh][ns][G][head_dim] partial outputs, or nullptr
   const float* att_ml;       // [kvh][ns][G][2] partial (max, sum)
   int att_ns, att_group;     // splits per KV head, query heads per KV head
+  // x records (ss_device.h): when xr is set, x is read from these records
+  // (written by the producer of x, with the RMSNorm weight nw already
+  // applied and the sums of squares in word 14) instead of from x; the
+  // buffer holds xrec_words(cols) words, zero past the vector
+  const uint32_t* xr;
+  // producer side (EPI_STORE, EPI_ADD, EPI_SWIGLU): also write the output as
+  // records of y * nw_out (nw_out may be nullptr) for the next matvec
+  uint32_t* xr_out;
+  const float* nw_out;
 };
+// 32-bit words of an x record buffer for a vector of n values: 16-value
+// records, padded with zero records to a multiple of 1024 values
+inline size_t xrec_words(int n) { return (size_t)((n + 1023) / 1024) * 64 * 16; }
 
 // Prompt products: Y[t] = W X[t] (+ epilogue) for T tokens on MFMA.
 struct GemmArgs {
@@ -122,8 +134,9 @@ int attn_resident_groups(int head_dim, int group, int kv_type);
 
 hipError_t launch_pack(int type, const uint8_t* src, uint8_t* qs, uint16_t* ds, int64_t nblocks,
                        int nb, int64_t row_off, hipStream_t s);
+// With xr set, also the x records of row * nw (xrec_words(cols) words).
 hipError_t launch_embed(int type, PackedMat t, int cols, const int* tokens, const int* dpos,
-                        int token, float* out, hipStream_t s);
+                        int token, float* out, const float* nw, uint32_t* xr, hipStream_t s);
 // Rows tokens[*dpos + z], z < n, of the table into out[z][cols].
 hipError_t launch_embed_rows(int type, PackedMat t, int cols, const int* tokens, const int* dpos, int n,
                              float* out, hipStream_t s);
