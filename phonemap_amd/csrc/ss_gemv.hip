@@ -448,7 +448,7 @@ __global__ void k_pack(const uint8_t* __restrict__ src, uint8_t* __restrict__ qs
 }
 
 // Row `token` of a packed table, dequantised exactly as quantize.c:60-72 /
-// 139-149 (one fp32 multiply per weight). With tokens set, workgroup z
+// 139-149 (one fp32 multiply per weight). With tokens set, workgroup row z
 // writes row tokens[*dpos + z] to out + z * cols (a prompt's rows at once).
 // With xr set (one row), the row is also written as x records of
 // row * nw (the first layer's attn_norm) for the first matvec.
@@ -467,26 +467,22 @@ __device__ __forceinline__ float embed_value(const PackedMat& t, int tok, int nt
   }
 }
 
+// Grid (ceil(cols / 256), rows): thread j of a row writes value j; with xr,
+// lane r of each 16-lane row holds value 16 * record + r, so the records are
+// encoded in the same pass (every lane of a wave takes part in enc16).
 template <int QT>
-__global__ void k_embed(PackedMat t, int cols, const int* tokens, const int* dpos, int token,
-                        float* out, const float* nw, uint32_t* xr) {
-  const int tok = tokens ? tokens[*dpos + blockIdx.x] : token;
-  out += (size_t)blockIdx.x * cols;
-  const int nb = cols >> 5;
-  const int ntk = (nb + kTB - 1) / kTB;
-  for (int j = threadIdx.x; j < cols; j += blockDim.x) out[j] = embed_value<QT>(t, tok, ntk, j);
+__global__ void __launch_bounds__(256) k_embed(PackedMat t, int cols, const int* tokens, const int* dpos,
+                                               int token, float* out, const float* nw, uint32_t* xr) {
+  const int tok = tokens ? tokens[*dpos + blockIdx.y] : token;
+  out += (size_t)blockIdx.y * cols;
+  const int ntk = (cols / 32 + kTB - 1) / kTB;
+  const int j = blockIdx.x * blockDim.x + threadIdx.x;
+  const bool in = j < cols;
+  const float v = in ? embed_value<QT>(t, tok, ntk, j) : 0.f;
+  if (in) out[j] = v;
   if (!xr) return;
-  // lane r of each 16-lane row holds value 16 * record + r; the loop bound
-  // is uniform per wave (blockDim is a multiple of 64), so enc16 sees all
-  // 16 lanes of its row
-  const int lane = threadIdx.x & 63;
-  for (int base = (threadIdx.x >> 6) * kWave; base < cols; base += blockDim.x) {
-    const int j = base + lane;
-    const bool in = j < cols;
-    const float v = in ? embed_value<QT>(t, tok, ntk, j) : 0.f;
-    const Enc e = enc16(in ? v * nw[j] : 0.f, v);
-    if (in) put_rec_lds(xr + (size_t)(j >> 4) * kRW, e, j & 15);
-  }
+  const Enc e = enc16(in ? v * nw[j] : 0.f, v);
+  if (in) put_rec_lds(xr + (size_t)(j >> 4) * kRW, e, j & 15);
 }
 
 // Picks the first maximum among per-workgroup candidates, writes it, and for
@@ -522,16 +518,16 @@ __global__ void k_argmax_merge(const float2* part, int n, const float* y, int* o
   }
 }
 
-template <int QT, int NMAT, int EPI, bool MERGE = false, bool PX = false>
+template <int QT, int NMAT, int EPI, bool MERGE = false, bool PX = false, int UT = kGemvUnit>
 hipError_t launch_t(const GemvArgs& a, hipStream_t s) {
-  GemvPlan p = gemv_plan(a.rows, a.cols, QT, NMAT);
+  GemvPlan p = gemv_plan(a.rows, a.cols, QT, NMAT, UT);
   KernelEvents& ev = kernel_events();
   if (ev.start) {
-    hipExtLaunchKernelGGL((k_gemv<QT, NMAT, EPI, kGemvUnit, MERGE, PX>), dim3(p.grid), dim3(p.threads),
+    hipExtLaunchKernelGGL((k_gemv<QT, NMAT, EPI, UT, MERGE, PX>), dim3(p.grid), dim3(p.threads),
                           p.lds_bytes, s, ev.start, ev.stop, 0, a);
     ev.used = true;
   } else {
-    hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, kGemvUnit, MERGE, PX>), dim3(p.grid), dim3(p.threads),
+    hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, UT, MERGE, PX>), dim3(p.grid), dim3(p.threads),
                        p.lds_bytes, s, a);
   }
   return hipGetLastError();
@@ -543,13 +539,24 @@ hipError_t launch_x(const GemvArgs& a, hipStream_t s) {
   return a.xr ? launch_t<QT, NMAT, EPI, false, true>(a, s) : launch_t<QT, NMAT, EPI>(a, s);
 }
 
+// [Wq;Wk;Wv] from records: four-tile units (8-wave workgroups) when there are
+// at least kQkvWideGroups row groups (7B shape: 7.8 against 8.6 us per launch
+// with two-tile units; the other matrices measured fastest with two)
+constexpr int kQkvWideGroups = 512;
+template <int QT>
+hipError_t launch_qkv(const GemvArgs& a, hipStream_t s) {
+  if (QT == 2 && a.xr && (a.rows + kRG - 1) / kRG >= kQkvWideGroups)
+    return launch_t<QT, 1, EPI_QKV, false, true, 4>(a, s);
+  return launch_x<QT, 1, EPI_QKV>(a, s);
+}
+
 template <int QT>
 hipError_t launch_q(int epi, const GemvArgs& a, hipStream_t s) {
   switch (epi) {
     case EPI_STORE: return launch_x<QT, 1, EPI_STORE>(a, s);
     case EPI_ADD: return a.att_o ? launch_t<QT, 1, EPI_ADD, true>(a, s) : launch_x<QT, 1, EPI_ADD>(a, s);
     case EPI_SWIGLU: return launch_x<QT, 2, EPI_SWIGLU>(a, s);
-    case EPI_QKV: return launch_x<QT, 1, EPI_QKV>(a, s);
+    case EPI_QKV: return launch_qkv<QT>(a, s);
     case EPI_LOGITS: return launch_x<QT, 1, EPI_LOGITS>(a, s);
     default: return hipErrorInvalidValue;
   }
@@ -566,12 +573,12 @@ KernelEvents& kernel_events() {
 // row, up to 16 (Q4_0, one matrix) or 8 waves; rows wider than that take
 // several rounds per wave. Two-tile units measured fastest for every 7B shape
 // (fewest registers, most waves resident, shortest work after the last load).
-GemvPlan gemv_plan(int rows, int cols, int type, int nmat) {
+GemvPlan gemv_plan(int rows, int cols, int type, int nmat, int unit) {
   GemvPlan p;
   const int groups = (rows + kRG - 1) / kRG;
   const int ntk = (cols / 32 + kTB - 1) / kTB;
   const int smax = type == 8 || nmat == 2 ? gemv_max_waves<8, 1>() : gemv_max_waves<2, 1>();
-  const int ut = kGemvUnit;
+  const int ut = unit;
   const int nu = (ntk + ut - 1) / ut;
   const int S = nu < smax ? nu : smax;
   p.unit = ut;
@@ -639,9 +646,11 @@ hipError_t launch_embed(int type, PackedMat t, int cols, const int* tokens, cons
                         int token, float* out, const float* nw, uint32_t* xr, hipStream_t s) {
   if (xr && !nw) return hipErrorInvalidValue;
   if (type == 2)
-    hipLaunchKernelGGL(k_embed<2>, dim3(1), dim3(256), 0, s, t, cols, tokens, dpos, token, out, nw, xr);
+    hipLaunchKernelGGL(k_embed<2>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out, nw,
+                       xr);
   else if (type == 8)
-    hipLaunchKernelGGL(k_embed<8>, dim3(1), dim3(256), 0, s, t, cols, tokens, dpos, token, out, nw, xr);
+    hipLaunchKernelGGL(k_embed<8>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out, nw,
+                       xr);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -651,9 +660,11 @@ hipError_t launch_embed_rows(int type, PackedMat t, int cols, const int* tokens,
                              float* out, hipStream_t s) {
   if (n <= 0 || !tokens || !dpos) return hipErrorInvalidValue;
   if (type == 2)
-    hipLaunchKernelGGL(k_embed<2>, dim3(n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out, nullptr, nullptr);
+    hipLaunchKernelGGL(k_embed<2>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
+                       nullptr, nullptr);
   else if (type == 8)
-    hipLaunchKernelGGL(k_embed<8>, dim3(n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out, nullptr, nullptr);
+    hipLaunchKernelGGL(k_embed<8>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
+                       nullptr, nullptr);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -585,6 +585,7 @@ struct ss_hip_model {
   // the residual stream times the next RMSNorm weight (written by the
   // embedding, Wo and down), xr_ffn the SwiGLU output (written by gate/up)
   uint32_t *xr_hid = nullptr, *xr_ffn = nullptr;
+  uint32_t* xr_att = nullptr;   // the attention output (written by its split merge) for Wo
 
   int* h_io = nullptr;   // pinned host scratch
   hipGraphExec_t g_full = nullptr, g_nohead = nullptr;
@@ -936,10 +937,12 @@ int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden,
   at.out = m->attn;
   at.part_o = m->att_o;
   at.part_ml = m->att_ml;
-  // with few splits the Wo matvec merges them while staging; with more, the
-  // last split of each KV head to finish merges them
+  // with few splits the Wo matvec merges them while staging (measured
+  // faster than the last-arriver merge for up to kMergeSplits splits)
   const bool fused = m->ns <= ssk::kMergeSplits;
   at.cnt = fused ? nullptr : m->att_cnt;
+  at.xr_out = fused ? nullptr : m->xr_att;   // otherwise the last split of each KV head merges
+                                             // and writes the output as x records for Wo
   HIP_TRY(timed(m, PC_ATTN, 0, [&] { return ssk::launch_attention(m->hd, m->group, m->kv_type, at, s); }));
 
   // 3. hidden += Wo attn                                         (:470-484)
@@ -951,6 +954,8 @@ int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden,
     o.att_group = m->group;
     o.head_dim = m->hd;
     o.dpos = dp;
+  } else {
+    o.xr = m->xr_att;
   }
   o.xr_out = m->xr_hid;
   o.nw_out = ly.ffn_norm;
@@ -1528,6 +1533,7 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
       m_alloc(m, (void**)&m->att_cnt, sizeof(uint32_t) * m->KVH) ||
       m_alloc(m, (void**)&m->xr_hid, sizeof(uint32_t) * ssk::xrec_words(m->d)) ||
       m_alloc(m, (void**)&m->xr_ffn, sizeof(uint32_t) * ssk::xrec_words(m->ffn)) ||
+      m_alloc(m, (void**)&m->xr_att, sizeof(uint32_t) * ssk::xrec_words(m->qdim)) ||
       m_alloc(m, (void**)&m->emb, sizeof(float) * (2 * (size_t)m->d + 64)))
     return bail();
   // RoPE (cos, sin) table for every position, computed with the host libm

@@ -91,6 +91,7 @@ struct AttnArgs {
   uint32_t* cnt;             // [n_kv_heads] split arrivals, zero between launches: the last
                              // split merges into out; nullptr: the splits stay in part_o/part_ml
                              // for a merging consumer (ns <= kMergeSplits)
+  uint32_t* xr_out;          // with cnt set: also the output as x records (xrec_words(n_heads * hd))
   int n_tok;                 // prompt rows (launch_attention_rows): token z at position dpos[z],
   int tok_q, tok_o;          // its query at q + z*tok_q, its output at out + z*tok_o
 };
@@ -108,7 +109,8 @@ struct GemvPlan {
   int grid, threads, unit;
   size_t lds_bytes;
 };
-GemvPlan gemv_plan(int rows, int cols, int type, int nmat);
+// unit: tiles per wave per round (2, 4 or 8); two unless the launcher chooses
+GemvPlan gemv_plan(int rows, int cols, int type, int nmat, int unit = 2);
 // bytes and plane views of a packed matrix (16-row x 4-block tiles, see ss_gemv.hip)
 size_t packed_bytes(int type, int64_t rows, int cols);
 PackedMat packed_view(const void* base, int type, int64_t rows, int cols);
@@ -167,7 +169,7 @@ constexpr int kArgmaxMaxBlocks = 1024;
 constexpr int kRG = 16;                    // rows per packed row group
 constexpr int kTB = 4;                     // 32-column blocks per tile (kRG * kTB = 64 lanes)
 constexpr int kUT = 8;                     // tiles per scale group (16 B of scales per lane)
-constexpr int kGemvUnit = 2;               // tiles per wave per round (2, 4 or 8)
+constexpr int kGemvUnit = 2;               // default tiles per wave per round (2, 4 or 8)
 constexpr int kGemvMaxSplit = 16;          // waves per matvec workgroup
 constexpr int kMaxSplits = 256;            // attention splits per KV head
 constexpr int kMergeSplits = 8;            // splits the Wo matvec merges itself

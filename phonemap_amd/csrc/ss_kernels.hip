@@ -74,6 +74,14 @@ __host__ __device__ constexpr int attn_rows_per_lane(int group) {
   return group >= 8 ? 1 : group >= 4 ? 2 : 4;
 }
 
+// Four consecutive outputs (quad q of the output vector) into out and, with
+// xr_out set, into the x records of the Wo matvec's input: the 4 lanes of an
+// aligned quad (all active) hold one record's 16 values.
+__device__ __forceinline__ void attn_store4(const AttnArgs& a, int q, float4 v) {
+  reinterpret_cast<float4*>(a.out)[q] = v;
+  if (a.xr_out) encode4(reinterpret_cast<int*>(a.xr_out) + (q / 8) * kXW, q % 8, v);
+}
+
 // The workgroup's W waves hold per-wave (m, l, o) for the G heads in LDS:
 // combine them, then either write the output (one active split), leave the
 // split's partials for a merging consumer (a.cnt null), or write them and let
@@ -84,20 +92,27 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, int kvh, int acti
   const int lane = tid & 63, wave = tid >> 6;
   constexpr int kThreads = W * 64;
   if (a.cnt && active == 1) {
-    // the only split: the output directly (the merge below with one split)
-    for (int i = tid; i < G * HD; i += kThreads) {
-      const int g = i / HD, d = i % HD;
-      float M = -INFINITY;
+    // the only split: the output directly (the merge below with one split),
+    // four consecutive outputs per thread; quads of lanes hold the 16 values
+    // of one x record (G * HD / 4 is a multiple of 8)
+    for (int i4 = tid; i4 < G * HD / 4; i4 += kThreads) {
+      float r[4];
 #pragma unroll
-      for (int w = 0; w < W; ++w) M = fmaxf(M, wm[w][g]);
-      float so = 0.f, sl = 0.f;
+      for (int c = 0; c < 4; ++c) {
+        const int i = i4 * 4 + c, g = i / HD, d = i % HD;
+        float M = -INFINITY;
 #pragma unroll
-      for (int w = 0; w < W; ++w) {
-        const float f = expf(wm[w][g] - M);
-        so = fmaf(f, wo[w][g][d], so);
-        sl = fmaf(f, wl[w][g], sl);
+        for (int w = 0; w < W; ++w) M = fmaxf(M, wm[w][g]);
+        float so = 0.f, sl = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) {
+          const float f = expf(wm[w][g] - M);
+          so = fmaf(f, wo[w][g][d], so);
+          sl = fmaf(f, wl[w][g], sl);
+        }
+        r[c] = so * (1.0f / sl);
       }
-      a.out[((size_t)kvh * G + g) * HD + d] = so * (1.0f / sl);
+      attn_store4(a, kvh * G * HD / 4 + i4, make_float4(r[0], r[1], r[2], r[3]));
     }
     return;
   }
@@ -212,7 +227,7 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, int kvh, int acti
       acc.z += r.z;
       acc.w += r.w;
     }
-    reinterpret_cast<float4*>(a.out + (size_t)kvh * G * HD)[qd] = acc;
+    attn_store4(a, kvh * G * HD / 4 + qd, acc);
   }
   if (tid == 0) cst(a.cnt + kvh, 0u);   // every split of this launch has arrived: ready for the next
 }
