@@ -148,6 +148,16 @@ int32_t ss_hip_swiglu(ss_hip_ctx_t *ctx, float *out_dev, const float *gate_dev,
 int32_t ss_hip_argmax(ss_hip_ctx_t *ctx, int32_t *out_dev, const float *x_dev, int32_t n,
                       void *stream);
 
+/* ss_sample (tensor.c:363-451) over n device logits: with temperature > 0,
+ * softmax of logits / temperature, top-k and top-p filtering, renormalising
+ * and one xorshift64 draw from *rng_state (advanced in place); the sampled
+ * index goes to *out_host. temperature <= 0 is the first-max argmax and
+ * leaves the state alone. Sums are exact fixed point rather than the
+ * reference's sequential fp32, so the index can differ from the reference's
+ * only where the draw lies within fp32 rounding of a cumulative boundary. */
+int32_t ss_hip_sample_logits(ss_hip_ctx_t *ctx, const float *logits_dev, int32_t n, float temperature,
+                             float top_p, int32_t top_k, uint64_t *rng_state, int32_t *out_host);
+
 /* dequantise row `token` of a packed [rows x cols] table (layer_scheduler.c:584-595) */
 int32_t ss_hip_embed_row(ss_hip_ctx_t *ctx, float *out_dev, const void *table_dev,
                          int32_t ggml_type, int32_t rows, int32_t cols, int32_t token,
@@ -214,6 +224,11 @@ int32_t ss_hip_set_prompt_batch(ss_hip_model_t *m, int32_t min_tokens);
  * through the output norm, mean-pooled and L2-normalised into out_host[hidden].
  * With the fp16 cache the prompt runs as matrix products. */
 int32_t ss_hip_embed(ss_hip_model_t *m, const int32_t *tokens, int32_t n, float *out_host);
+/* ss_hip_sample_logits over the logits of the model's last evaluated token
+ * (left in HBM by ss_hip_eval_token / ss_hip_eval_prompt, which need not
+ * copy them to the host) */
+int32_t ss_hip_sample(ss_hip_model_t *m, float temperature, float top_p, int32_t top_k,
+                      uint64_t *rng_state, int32_t *token_out);
 /* device-side greedy continuation (see ss_decode_greedy) */
 int32_t ss_hip_decode_greedy(ss_hip_model_t *m, int32_t n_steps, int32_t *tokens_out);
 /* ss_scheduler_reset (layer_scheduler.h:132) */

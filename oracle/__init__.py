@@ -46,6 +46,7 @@ def lib():
         "orc_rope": (None, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, C.c_float, _i32]),
         "orc_rope_table": (None, [_vp, _i32, _i32, C.c_float]),
         "orc_argmax": (_i32, [_vp, _i32]),
+        "orc_sample": (_i32, [_vp, _i32, C.c_float, C.c_float, _i32, C.POINTER(C.c_uint64), _vp, _vp]),
         "orc_kv_int8_encode": (None, [_vp, _vp, _vp, _i32]),
         "orc_attention_head": (None, [_vp, _vp, _vp, _vp, _i32, _i32, _i32]),
         "orc_set_threads": (None, [_i32]),
@@ -150,6 +151,17 @@ def attention_head(q, keys, values):
 def argmax(x):
     x = np.ascontiguousarray(x, np.float32)
     return int(lib().orc_argmax(_ptr(x), x.size))
+
+
+def sample(logits, temperature, top_p, top_k, rng):
+    """ss_sample (tensor.c:363-451): returns (index, new rng state, final
+    probabilities, uniform draw)."""
+    x = np.ascontiguousarray(logits, np.float32)
+    st = C.c_uint64(rng)
+    probs = np.zeros(x.size, np.float32)
+    r = np.zeros(1, np.float32)
+    i = lib().orc_sample(_ptr(x), x.size, temperature, top_p, top_k, C.byref(st), _ptr(probs), _ptr(r))
+    return int(i), int(st.value), probs, float(r[0])
 
 
 def softmax(x):

@@ -258,6 +258,73 @@ int32_t orc_argmax(const float *x, int32_t n) {
     return idx;
 }
 
+/* tensor.c:330-343: xorshift64 and the 53-bit uniform draw. */
+static uint64_t orc_xorshift64(uint64_t *s) {
+    uint64_t x = *s;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *s = x;
+    return x;
+}
+
+typedef struct { int32_t id; float prob; } orc_tp_t;
+
+/* tensor.c:352-361: descending, NaN ranked as 0. */
+static int orc_tp_cmp(const void *a, const void *b) {
+    float pa = ((const orc_tp_t *)a)->prob, pb = ((const orc_tp_t *)b)->prob;
+    if (isnan(pa)) pa = 0.0f;
+    if (isnan(pb)) pb = 0.0f;
+    if (pa > pb) return -1;
+    if (pa < pb) return 1;
+    return 0;
+}
+
+/* tensor.c:363-451 (ss_sample). probs_out (optional, n floats) receives the
+ * final distribution the draw walks, r_out (optional) the uniform draw. */
+int32_t orc_sample(const float *logits, int32_t n, float temperature, float top_p, int32_t top_k,
+                   uint64_t *rng, float *probs_out, float *r_out) {
+    if (temperature <= 0.0f) return orc_argmax(logits, n);
+    float *p = (float *)malloc(sizeof(float) * (size_t)n);
+    orc_tp_t *srt = (orc_tp_t *)malloc(sizeof(orc_tp_t) * (size_t)n);
+    if (!p || !srt) { free(p); free(srt); return orc_argmax(logits, n); }
+    for (int32_t i = 0; i < n; i++) p[i] = isnan(logits[i]) ? -FLT_MAX : logits[i] / temperature;
+    orc_softmax(p, n);
+    for (int32_t i = 0; i < n; i++) { srt[i].id = i; srt[i].prob = isnan(p[i]) ? 0.0f : p[i]; }
+    qsort(srt, (size_t)n, sizeof(orc_tp_t), orc_tp_cmp);
+    if (top_k > 0 && top_k < n) {                         /* :391-396 */
+        const float th = srt[top_k - 1].prob;
+        for (int32_t i = 0; i < n; i++) if (p[i] < th) p[i] = 0.0f;
+    }
+    if (top_p > 0.0f && top_p < 1.0f) {                   /* :399-417 */
+        float cum = 0.0f, cutoff = 0.0f;
+        for (int32_t i = 0; i < n; i++) {
+            const float v = p[srt[i].id];
+            if (v > 0.0f) cum += v;
+            if (cum >= top_p) { cutoff = v; break; }
+        }
+        for (int32_t i = 0; i < n; i++) if (p[i] < cutoff) p[i] = 0.0f;
+    }
+    free(srt);
+    float sum = 0.0f;                                     /* :423-429 */
+    for (int32_t i = 0; i < n; i++) sum += p[i];
+    if (sum > 0.0f) {
+        const float inv = 1.0f / sum;
+        for (int32_t i = 0; i < n; i++) p[i] *= inv;
+    }
+    const float r = (float)(orc_xorshift64(rng) >> 11) / (float)(1ULL << 53);   /* :431-442 */
+    float cdf = 0.0f;
+    int32_t out = n - 1;
+    for (int32_t i = 0; i < n; i++) {
+        cdf += p[i];
+        if (r < cdf) { out = i; break; }
+    }
+    if (probs_out) memcpy(probs_out, p, sizeof(float) * (size_t)n);
+    if (r_out) *r_out = r;
+    free(p);
+    return out;
+}
+
 /* layer_scheduler.c:101-118 */
 void orc_kv_int8_encode(const float *src, int8_t *q, float *scale, int32_t n) {
     float max_val = 0.0f;

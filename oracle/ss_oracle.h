@@ -39,6 +39,8 @@ void     orc_rope(float *q, float *k, int32_t n_heads, int32_t n_kv_heads, int32
                   int32_t rope_dim, int32_t pos, float theta, int32_t is_neox); /* tensor.c:220-275 */
 void     orc_rope_table(float *cs, int32_t rope_dim, int32_t n_pos, float theta); /* cos/sin of tensor.c:250-254 */
 int32_t  orc_argmax(const float *x, int32_t n);      /* tensor.c:318-328 */
+int32_t  orc_sample(const float *logits, int32_t n, float temperature, float top_p, int32_t top_k,
+                    uint64_t *rng, float *probs_out, float *r_out);      /* tensor.c:363-451 */
 void     orc_kv_int8_encode(const float *src, int8_t *q, float *scale, int32_t n); /* layer_scheduler.c:101-118 */
 void     orc_attention_head(float *out, const float *q, const float *keys, const float *values,
                             int32_t head_dim, int32_t seq_len, int32_t kv_stride); /* layer_scheduler.c:421-467 */

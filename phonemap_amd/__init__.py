@@ -52,6 +52,8 @@ _PROTOS = {
     "ss_hip_attention": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "ss_hip_swiglu": (_i32, [_vp, _vp, _vp, _vp, _i32, _vp]),
     "ss_hip_argmax": (_i32, [_vp, _vp, _vp, _i32, _vp]),
+    "ss_hip_sample_logits": (_i32, [_vp, _vp, _i32, _f32, _f32, _i32, C.POINTER(_u64), _ip]),
+    "ss_hip_sample": (_i32, [_vp, _f32, _f32, _i32, C.POINTER(_u64), _ip]),
     "ss_hip_embed_row": (_i32, [_vp, _vp, _vp, _i32, _i32, _i32, _i32, _vp]),
     "ss_hip_matvec_host": (_i32, [_vp, _fp, _vp, _fp, _i32, _i32, _i32]),
     "ss_hip_should_use_gpu": (_i32, [_i32, _i32]),

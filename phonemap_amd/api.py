@@ -201,6 +201,16 @@ class Model:
         L = _lib()
         _check(L.ss_hip_set_prompt_batch(L.ss_model_hip(self.h), min_tokens), "ss_hip_set_prompt_batch")
 
+    def sample(self, temperature, top_p, top_k, rng):
+        """ss_sample over the last evaluated token's logits, on the device:
+        returns (token, advanced rng state)."""
+        L = _lib()
+        st = C.c_uint64(rng)
+        tok = C.c_int32(-1)
+        _check(L.ss_hip_sample(L.ss_model_hip(self.h), temperature, top_p, top_k, C.byref(st), C.byref(tok)),
+               "ss_hip_sample")
+        return tok.value, st.value
+
     def decode_greedy(self, n_steps):
         out = np.zeros(max(n_steps, 1), np.int32)
         _check(_lib().ss_decode_greedy(self.h, n_steps, _ptr(out, _ip)), "ss_decode_greedy")

@@ -428,7 +428,9 @@ ss_error_t ss_generate(ss_model_t *m, const char *prompt, const ss_generate_para
     if (m->progress_cb) m->progress_cb(0, (uint32_t)n, "prefill", m->progress_user_data);
     double t0 = now_sec();
     int32_t next = 0;
-    int32_t rc = ss_hip_eval_prompt(m->hm, toks, n, 0, greedy ? NULL : m->logits, &next);
+    /* the logits stay in HBM: greedy tokens come from the device argmax,
+     * sampled ones from ss_hip_sample over the same logits */
+    int32_t rc = ss_hip_eval_prompt(m->hm, toks, n, 0, NULL, &next);
     double t1 = now_sec();
     if (m->progress_cb) m->progress_cb((uint32_t)n, (uint32_t)n, "prefill", m->progress_user_data);
     if (rc != 0) return map_rc(rc) == SS_ERROR_CANCELLED ? SS_ERROR_CANCELLED : set_err(SS_ERROR_BACKEND);
@@ -442,7 +444,8 @@ ss_error_t ss_generate(ss_model_t *m, const char *prompt, const ss_generate_para
     for (uint32_t t = 0; t < p.max_tokens; t++) {
         if (__atomic_load_n(&m->cancelled, __ATOMIC_SEQ_CST)) return set_err(SS_ERROR_CANCELLED);
         /* sample over the logits the model produces (the clamped vocab) */
-        int32_t id = greedy ? next : ss_sample(m->logits, m->vocab, p.temperature, p.top_p, (int32_t)p.top_k, &rng);
+        int32_t id = next;
+        if (!greedy && (rc = ss_hip_sample(m->hm, p.temperature, p.top_p, (int32_t)p.top_k, &rng, &id)) != 0) break;
         if (id == eos) break;
         const char *text = ss_tok_decode(m->tok, id);
         if (text && (!strcmp(text, "<|im_end|>") || !strcmp(text, "<|eot_id|>") || !strcmp(text, "<|end|>") ||
@@ -460,7 +463,7 @@ ss_error_t ss_generate(ss_model_t *m, const char *prompt, const ss_generate_para
         }
         if (cb && !cb(text, (uint32_t)id, ud)) break;
         if (pos >= m->n_ctx) break;
-        rc = ss_hip_eval_token(m->hm, id, pos, greedy ? NULL : m->logits, &next);
+        rc = ss_hip_eval_token(m->hm, id, pos, NULL, &next);
         if (rc != 0) break;
         pos++;
         generated++;

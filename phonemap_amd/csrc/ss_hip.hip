@@ -87,6 +87,9 @@ struct ss_hip_ctx {
   uint16_t* g_xs = nullptr;    // prompt products: x split into fp16 parts
 
   size_t att_o_floats = 0, att_ml_floats = 0, att_cnt_bytes = 0, g_ssq_bytes = 0, g_xs_bytes = 0;
+  float* smp = nullptr;        // sampling: probabilities [n]
+  size_t smp_bytes = 0;
+  uint64_t* smp_io = nullptr;  // sampling: [0] index, [1] advanced state
 
   // host-pointer plug (metal_backend.m:190-235 registry)
   std::unordered_map<const void*, void*> registry;
@@ -236,8 +239,8 @@ void ss_hip_free(ss_hip_ctx_t* c) {
   hipSetDevice(c->device);
   if (c->stream) hipStreamSynchronize(c->stream);
   for (auto& kv : c->registry) hipFree(kv.second);
-  void* bufs[] = {c->staging, c->am_part, c->rope_row, c->att_o,
-                  c->att_ml, c->att_cnt, c->g_ssq, c->g_xs, c->plug_x, c->plug_y};
+  void* bufs[] = {c->staging, c->am_part, c->rope_row, c->att_o, c->att_ml, c->att_cnt,
+                  c->g_ssq, c->g_xs, c->plug_x, c->plug_y, c->smp, c->smp_io};
   for (void* b : bufs)
     if (b) hipFree(b);
   if (c->stream) hipStreamDestroy(c->stream);
@@ -475,6 +478,37 @@ int32_t ss_hip_swiglu(ss_hip_ctx_t* c, float* out, const float* g, const float* 
 int32_t ss_hip_argmax(ss_hip_ctx_t* c, int32_t* out, const float* x, int32_t n, void* stream) {
   if (!c || !out || !x || n <= 0) return fail(kErrParams, "argmax: bad argument");
   HIP_TRY(ssk::launch_argmax(out, x, n, c->am_part, pick(c, stream)));
+  return 0;
+}
+
+int32_t ss_hip_sample_logits(ss_hip_ctx_t* c, const float* logits, int32_t n, float temperature, float top_p,
+                             int32_t top_k, uint64_t* rng_state, int32_t* out_host) {
+  if (!c || !logits || n <= 0 || !rng_state || !out_host) return fail(kErrParams, "sample: bad argument");
+  if (int32_t rc = set_device(c)) return rc;
+  if (!c->smp_io) HIP_TRY(hipMalloc((void**)&c->smp_io, 2 * sizeof(uint64_t)));
+  hipStream_t s = c->stream;
+  if (!(temperature > 0.0f)) {   // tensor.c:366-368
+    HIP_TRY(ssk::launch_argmax(reinterpret_cast<int*>(c->smp_io), logits, n, c->am_part, s));
+  } else {
+    if (int32_t rc = ensure(c, (void**)&c->smp, &c->smp_bytes, sizeof(float) * (size_t)n, false)) return rc;
+    ssk::SampleArgs a;
+    memset(&a, 0, sizeof(a));
+    a.logits = logits;
+    a.V = n;
+    a.temperature = temperature;
+    a.top_p = top_p;
+    a.top_k = top_k;
+    a.rng = *rng_state;
+    a.probs = c->smp;
+    a.out = reinterpret_cast<int*>(c->smp_io);
+    a.rng_out = c->smp_io + 1;
+    HIP_TRY(ssk::launch_sample(a, s));
+  }
+  uint64_t io[2];
+  HIP_TRY(hipMemcpyAsync(io, c->smp_io, sizeof(io), hipMemcpyDeviceToHost, s));
+  HIP_TRY(hipStreamSynchronize(s));
+  *out_host = (int32_t)(uint32_t)(io[0] & 0xffffffffu);
+  if (temperature > 0.0f) *rng_state = io[1];
   return 0;
 }
 
@@ -1708,6 +1742,14 @@ int32_t ss_hip_embed(ss_hip_model_t* m, const int32_t* tokens, int32_t n, float*
   HIP_TRY(hipMemcpyAsync(out_host, m->emb + m->d, sizeof(float) * m->d, hipMemcpyDeviceToHost, s));
   HIP_TRY(hipStreamSynchronize(s));
   return sweep_check(m);
+}
+
+int32_t ss_hip_sample(ss_hip_model_t* m, float temperature, float top_p, int32_t top_k, uint64_t* rng_state,
+                      int32_t* token_out) {
+  if (!m) return fail(kErrParams, "sample: no model");
+  if (m->host_pos < 0) return fail(kErrParams, "sample: evaluate a token or prompt first");
+  if (int32_t rc = sweep_check(m)) return rc;
+  return ss_hip_sample_logits(m->ctx, m->logits, m->vocab, temperature, top_p, top_k, rng_state, token_out);
 }
 
 int32_t ss_hip_decode_greedy(ss_hip_model_t* m, int32_t n_steps, int32_t* tokens_out) {

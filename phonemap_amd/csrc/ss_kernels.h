@@ -162,6 +162,21 @@ hipError_t launch_pool_rows(const float* x, int T, int d, const float* w, const 
 hipError_t launch_embed_finish(const float* acc, int d, int n, float* out, hipStream_t s);
 hipError_t launch_swiglu(float* out, const float* g, const float* u, int n, hipStream_t s);
 hipError_t launch_argmax(int* out, const float* x, int n, float2* part, hipStream_t s);
+// Non-greedy sampling of ss_sample (tensor.c:363-451) over logits[V] on the
+// device (ss_sample.hip); one workgroup.
+struct SampleArgs {
+  const float* logits;
+  int V;
+  float temperature, top_p;  // temperature > 0
+  int top_k;
+  uint64_t rng;              // xorshift64 state before the draw
+  float* probs;              // scratch [V]
+  int* out;                  // sampled index
+  uint64_t* rng_out;         // state after the draw
+  int* tokens;               // optional: tokens[*dpos + 1] = index, then *dpos += 1
+  int* dpos;
+};
+hipError_t launch_sample(const SampleArgs& a, hipStream_t s);
 hipError_t launch_set_state(int* dpos, int* tokens, int pos, int token, hipStream_t s);
 hipError_t launch_advance(int* dpos, hipStream_t s);
 

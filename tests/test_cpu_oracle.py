@@ -277,3 +277,75 @@ def test_thread_count_does_not_change_results():
         outs.append(oracle.matvec(w, x, 333, 2048, Q4_0))
     L.orc_set_threads(n0)
     assert all(np.array_equal(outs[0], o) for o in outs[1:])
+
+
+# ---------------------------------------------------------------- sampling
+# ss_sample (tensor.c:363-451), pinned by closed forms: the xorshift64 stream
+# (tensor.c:331-343), greedy and top-k = 1 reducing to the argmax, a
+# hand-worked top-p renormalisation, and the uniform-distribution draw.
+
+M64 = (1 << 64) - 1
+
+
+def xorshift64(s):
+    s ^= (s << 13) & M64
+    s ^= s >> 7
+    s ^= (s << 17) & M64
+    return s
+
+
+def uniform_draw(s):
+    return float(np.float32(np.float32(s >> 11) / np.float32(2.0 ** 53)))
+
+
+def test_sample_rng_stream_closed_form():
+    x = np.zeros(16, np.float32)
+    st = 0x9E3779B97F4A7C15
+    for _ in range(20):
+        _, nst, _, r = oracle.sample(x, 1.0, 1.0, 0, st)
+        assert nst == xorshift64(st)
+        assert r == uniform_draw(nst)
+        st = nst
+
+
+def test_sample_greedy_and_top1_are_argmax():
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal(500).astype(np.float32)
+    x[123] = x[77] = x.max() + 1.0            # a tie: the first index wins
+    i, st, _, _ = oracle.sample(x, 0.0, 0.9, 40, 99)
+    assert (i, st) == (77, 99)                # T <= 0: argmax, state untouched
+    for seed in range(1, 20):
+        i, st, _, _ = oracle.sample(x, 0.7, 1.0, 1, seed)
+        assert i in (77, 123) and st == xorshift64(seed)
+
+
+def test_sample_top_p_hand_worked():
+    # probabilities 0.5, 0.3, 0.2 (and tiny others): top_p 0.6 keeps 0.5 and
+    # 0.3 (the running sum reaches 0.8 at 0.3), renormalised to 0.625, 0.375
+    x = np.log(np.array([0.5, 0.3, 0.2], np.float64)).astype(np.float32)
+    for seed in range(1, 200):
+        i, st, p, r = oracle.sample(x, 1.0, 0.6, 0, seed)
+        assert p[2] == 0.0
+        assert abs(p[0] - 0.625) < 1e-6 and abs(p[1] - 0.375) < 1e-6
+        if abs(r - 0.625) > 1e-5:
+            assert i == (0 if r < 0.625 else 1)
+
+
+def test_sample_top_k_keeps_k_largest():
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal(300).astype(np.float32)
+    _, _, p, _ = oracle.sample(x, 1.0, 1.0, 10, 11)
+    kept = set(np.nonzero(p)[0].tolist())
+    assert kept == set(np.argsort(-x)[:10].tolist())
+    assert abs(float(p.sum(dtype=np.float64)) - 1.0) < 1e-5
+
+
+def test_sample_uniform_draw_index():
+    V = 1000
+    x = np.zeros(V, np.float32)
+    for seed in range(1, 300):
+        i, _, p, r = oracle.sample(x, 1.0, 1.0, 0, seed)
+        assert np.all(p == p[0])
+        j = int(np.floor(r * V))
+        if abs(r * V - round(r * V)) > 1e-3:   # away from a cell boundary
+            assert i == j
