@@ -199,6 +199,10 @@ typedef struct {
                           * Launches are then per kernel (EAGER). */
     ss_hip_tensor_t token_embd, output_norm, output;
     const ss_hip_tensor_t *layers;   /* n_layers * SS_HIP_LAYER_TENSORS */
+    /* NULL, or n_layers * 3 bias vectors (q, k, v; F32 or F16; data NULL where
+     * a layer has none), added to the projections before RoPE
+     * (layer_scheduler.c:367-402). */
+    const ss_hip_tensor_t *qkv_bias;
 } ss_hip_model_desc_t;
 
 /* ss_scheduler_init (layer_scheduler.h:95-96): upload + pack all weights,

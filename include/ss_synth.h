@@ -11,7 +11,7 @@
  * random nibbles; Q8_0 blocks have d = fp16(|N(0, scale_sigma / 16)|) and int8
  * codes uniform in [-127, 127] (the codes' spread is 16 times the nibbles', so
  * both types give weights of the same spread); norm weights are fp32
- * 1 + N(0, norm_sigma).
+ * 1 + N(0, norm_sigma); q/k/v biases (when asked for) are N(0, 0.1).
  * The bytes depend only on the spec (seed included), not on n_threads.
  */
 #ifndef SS_SYNTH_H
@@ -34,6 +34,12 @@ typedef struct {
     float norm_sigma;     /* 0 = 0.01 */
     int32_t with_vocab;   /* write tokenizer.ggml.tokens/scores (SentencePiece-style) */
     int32_t n_threads;    /* 0 = hardware concurrency */
+    /* Architecture variants. A variant changes no weight: a fused or biased
+     * file holds the same matrices as the plain one with the same seed. */
+    int32_t arch;         /* 0: "llama"; 1: "qwen2" (NeoX RoPE, layer_scheduler.c:145-149) */
+    int32_t fused_qkv;    /* blk.N.attn_qkv.weight = [Wq; Wk; Wv] in place of three tensors */
+    int32_t fused_up;     /* blk.N.ffn_up.weight = [Wgate; Wup] (2 * ffn rows), no ffn_gate */
+    int32_t qkv_bias;     /* blk.N.attn_q/k/v.bias: 0 none, 1 F32, 2 F16; values N(0, 0.1) */
 } ss_synth_spec_t;
 
 /* Returns 0, or a negative ss_error_t value (-5 bad spec, -1 cannot write). */

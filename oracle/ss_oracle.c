@@ -19,8 +19,11 @@
  *  - Besides the reference's int8 KV cache there is an fp16 KV mode: K and V
  *    are rounded to binary16 when appended and widened when read, inside the
  *    fp32 KV structure of layer_scheduler.c.orig:289-342.
- *  - Only the llama block is restated (no fused qkv, biases, Gemma or NeoX
- *    branches); orc_model_open rejects files that need them.
+ *  - The llama block and the branches the reference takes by tensor name or
+ *    by architecture outside Gemma are restated: fused attn_qkv and fused
+ *    ffn_up (layer_scheduler.c:337-347,518-524), q/k/v biases (:367-402) and
+ *    NeoX RoPE pairs for qwen/falcon/phi/deepseek (:144-149). Gemma files
+ *    are rejected.
  *
  * Parity unpinned: the summation order of Apple vDSP_dotpr / cblas_saxpy
  * (system frameworks, no version pin; orc_dot's order is checked against the
@@ -520,6 +523,7 @@ typedef struct {
 
 typedef struct {
     const orc_tensor_t *attn_norm, *wq, *wk, *wv, *wo, *ffn_norm, *wg, *wu, *wd;
+    const orc_tensor_t *wqkv, *bq, *bk, *bv;   /* fused [Wq;Wk;Wv]; Qwen biases (optional) */
 } orc_layer_t;
 
 struct orc_model {
@@ -754,6 +758,17 @@ static int matrix_ok(const orc_tensor_t *t, uint64_t rows, uint64_t cols) {
 static int vector_ok(const orc_tensor_t *t, uint64_t n) {
     return t && t->type == ORC_F32 && t->dims[0] == n;
 }
+static int bias_ok(const orc_tensor_t *t, uint64_t n) {
+    return (t->type == ORC_F32 || t->type == ORC_F16) && t->dims[0] == n;
+}
+
+/* layer_scheduler.c:367-402 with safe_load_f32 (:284-289): x[i] += b[i] */
+static void add_bias(const orc_model_t *m, float *x, const orc_tensor_t *b, int32_t n) {
+    if (!b) return;
+    const void *p = m->base + b->offset;
+    for (int32_t i = 0; i < n; i++)
+        x[i] = x[i] + (b->type == ORC_F16 ? orc_f16_to_f32(((const uint16_t *)p)[i]) : ((const float *)p)[i]);
+}
 
 orc_model_t *orc_model_open(const char *path, int32_t max_seq, int32_t kv_mode) {
     if (!path) return NULL;
@@ -768,11 +783,13 @@ orc_model_t *orc_model_open(const char *path, int32_t max_seq, int32_t kv_mode) 
     if (m->base == MAP_FAILED) { m->base = NULL; orc_model_close(m); return NULL; }
     if (parse_gguf(m) != 0) { orc_model_close(m); return NULL; }
 
-    if (strstr(m->arch, "qwen") || strstr(m->arch, "falcon") || strstr(m->arch, "phi") ||
-        strstr(m->arch, "deepseek") || strstr(m->arch, "gemma")) {
-        orc_model_close(m);   /* non-llama branches are not restated */
+    if (strstr(m->arch, "gemma")) {
+        orc_model_close(m);   /* the Gemma branches are not restated */
         return NULL;
     }
+    /* layer_scheduler.c:144-149 */
+    m->neox = strstr(m->arch, "qwen") || strstr(m->arch, "falcon") || strstr(m->arch, "phi") ||
+              strstr(m->arch, "deepseek");
     if (m->n_kv_heads == 0) m->n_kv_heads = m->n_heads;
     if (m->n_layers == 0 || m->d == 0 || m->n_heads == 0) { orc_model_close(m); return NULL; }
 
@@ -825,11 +842,19 @@ orc_model_t *orc_model_open(const char *path, int32_t max_seq, int32_t kv_mode) 
         ly->wg = find_suffix(m, l, "ffn_gate.weight");
         ly->wu = find_suffix(m, l, "ffn_up.weight");
         ly->wd = find_suffix(m, l, "ffn_down.weight");
-        if (!vector_ok(ly->attn_norm, d) || !matrix_ok(ly->wq, qdim, d) ||
-            !matrix_ok(ly->wk, m->kv_dim, d) || !matrix_ok(ly->wv, m->kv_dim, d) ||
-            !matrix_ok(ly->wo, d, qdim) || !vector_ok(ly->ffn_norm, d) ||
-            !matrix_ok(ly->wg, ffn, d) || !matrix_ok(ly->wu, ffn, d) || !matrix_ok(ly->wd, d, ffn) ||
-            find_suffix(m, l, "attn_q.bias") || find_suffix(m, l, "attn_qkv.weight")) {
+        ly->wqkv = find_suffix(m, l, "attn_qkv.weight");
+        ly->bq = find_suffix(m, l, "attn_q.bias");
+        ly->bk = find_suffix(m, l, "attn_k.bias");
+        ly->bv = find_suffix(m, l, "attn_v.bias");
+        int qkv_ok = ly->wqkv ? matrix_ok(ly->wqkv, qdim + 2 * (uint64_t)m->kv_dim, d)
+                              : matrix_ok(ly->wq, qdim, d) && matrix_ok(ly->wk, m->kv_dim, d) &&
+                                    matrix_ok(ly->wv, m->kv_dim, d);
+        int ffn_ok = ly->wg ? matrix_ok(ly->wg, ffn, d) && matrix_ok(ly->wu, ffn, d)
+                            : matrix_ok(ly->wu, 2 * (uint64_t)ffn, d);   /* fused, :518-524 */
+        if (!vector_ok(ly->attn_norm, d) || !qkv_ok || !matrix_ok(ly->wo, d, qdim) ||
+            !vector_ok(ly->ffn_norm, d) || !ffn_ok || !matrix_ok(ly->wd, d, ffn) ||
+            (ly->bq && !bias_ok(ly->bq, qdim)) || (ly->bk && !bias_ok(ly->bk, m->kv_dim)) ||
+            (ly->bv && !bias_ok(ly->bv, m->kv_dim))) {
             orc_model_close(m);
             return NULL;
         }
@@ -943,11 +968,25 @@ static void process_layer(orc_model_t *m, int32_t l, int32_t pos) {
     int32_t d = (int32_t)m->d, ffn = (int32_t)m->ffn;
     memcpy(m->residual, m->hidden, (size_t)d * 4);
     orc_rmsnorm(m->hidden, m->residual, (const float *)tdata(m, ly->attn_norm), d, m->eps);
-    matvec_t(m, m->q, ly->wq, m->hidden);
-    matvec_t(m, m->k, ly->wk, m->hidden);
-    matvec_t(m, m->v, ly->wv, m->hidden);
+    int32_t qdim = (int32_t)m->n_heads * m->hd, kvd = m->kv_dim;
+    if (ly->wqkv) {   /* :337-347: one product, then split (attn_qkv.bias is never applied) */
+        float *qkv = (float *)malloc((size_t)(qdim + 2 * kvd) * 4);
+        if (!qkv) abort();
+        matvec_t(m, qkv, ly->wqkv, m->hidden);
+        memcpy(m->q, qkv, (size_t)qdim * 4);
+        memcpy(m->k, qkv + qdim, (size_t)kvd * 4);
+        memcpy(m->v, qkv + qdim + kvd, (size_t)kvd * 4);
+        free(qkv);
+    } else {
+        matvec_t(m, m->q, ly->wq, m->hidden);
+        matvec_t(m, m->k, ly->wk, m->hidden);
+        matvec_t(m, m->v, ly->wv, m->hidden);
+    }
+    add_bias(m, m->q, ly->bq, qdim);
+    add_bias(m, m->k, ly->bk, kvd);
+    add_bias(m, m->v, ly->bv, kvd);
     orc_rope(m->q, m->k, (int32_t)m->n_heads, (int32_t)m->n_kv_heads, m->hd, m->rope_dim, pos,
-             m->theta, 0);
+             m->theta, m->neox);
     kv_store(m, l, pos, m->k, m->v);
 
     attn_job_t j = {m, l, pos + 1, (int32_t)(m->n_heads / m->n_kv_heads),
@@ -960,8 +999,17 @@ static void process_layer(orc_model_t *m, int32_t l, int32_t pos) {
 
     memcpy(m->residual, m->hidden, (size_t)d * 4);
     orc_rmsnorm(m->hidden, m->residual, (const float *)tdata(m, ly->ffn_norm), d, m->eps);
-    matvec_t(m, m->ffn_gate, ly->wg, m->hidden);
-    matvec_t(m, m->ffn_buf, ly->wu, m->hidden);
+    if (ly->wg) {
+        matvec_t(m, m->ffn_gate, ly->wg, m->hidden);
+        matvec_t(m, m->ffn_buf, ly->wu, m->hidden);
+    } else {          /* :518-524: fused [gate; up] */
+        float *gu = (float *)malloc((size_t)2 * ffn * 4);
+        if (!gu) abort();
+        matvec_t(m, gu, ly->wu, m->hidden);
+        memcpy(m->ffn_gate, gu, (size_t)ffn * 4);
+        memcpy(m->ffn_buf, gu + ffn, (size_t)ffn * 4);
+        free(gu);
+    }
     for (int32_t i = 0; i < ffn; i++) m->ffn_buf[i] = orc_silu_mul(m->ffn_gate[i], m->ffn_buf[i]);
     matvec_t(m, m->hidden, ly->wd, m->ffn_buf);
     for (int32_t i = 0; i < d; i++) m->hidden[i] = m->hidden[i] + m->residual[i];   /* :566 */

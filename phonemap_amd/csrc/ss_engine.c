@@ -37,6 +37,7 @@ struct ss_model {
     void *progress_user_data;
     int32_t vocab, n_ctx, n_embd;
     float *logits;
+    int32_t neox_hd, neox_rope, kvdim;   /* NeoX models: the K order of neox_order (else 0) */
 };
 
 static __thread ss_error_t g_last_error = SS_OK;   /* engine.c:27 */
@@ -90,6 +91,46 @@ static void fill_tensor(ss_hip_tensor_t *d, const ss_gguf_file_t *f, const ss_gg
     d->rows = t->n_dims >= 2 ? (int32_t)t->dims[1] : 1;
 }
 
+/* bytes of one row of a GGUF tensor (gguf_loader.c:22-62) */
+static size_t row_bytes(int32_t type, int32_t cols) {
+    switch (type) {
+    case SS_HIP_F32: return (size_t)cols * 4;
+    case SS_HIP_F16: return (size_t)cols * 2;
+    case SS_HIP_Q4_0: return (size_t)cols / 32 * 18;
+    case SS_HIP_Q8_0: return (size_t)cols / 32 * 34;
+    default: return 0;
+    }
+}
+
+/* rows [r0, r0 + n) of a fused matrix as a tensor of their own */
+static ss_hip_tensor_t row_view(const ss_hip_tensor_t *t, int32_t r0, int32_t n) {
+    ss_hip_tensor_t v = *t;
+    v.data = (const uint8_t *)t->data + (size_t)r0 * row_bytes(t->type, t->cols);
+    v.rows = n;
+    return v;
+}
+
+/* NeoX RoPE (tensor.c:223-248) rotates the pairs (i, i + rope_dim/2) of each
+ * head. In the order where unit 2i of a head holds source unit i and unit
+ * 2i+1 holds i + rope_dim/2 (units at or past rope_dim stay), those pairs are
+ * adjacent, and the GPT-J branch (:249-274) rotates them with the same angle,
+ * cos and sin, term for term. Attention uses q and K of a head only through
+ * q.k, which is the same when both are in that order. So a NeoX model runs
+ * as a GPT-J one whose Wq and Wk rows (and q/k biases, and injected K rows)
+ * are put in this order once. Returns a malloc'd copy of n_units units of
+ * `unit` bytes. */
+static void *neox_order(const void *src, size_t unit, int32_t n_units, int32_t hd, int32_t rope_dim) {
+    uint8_t *dst = (uint8_t *)malloc((size_t)n_units * unit);
+    if (!dst) return NULL;
+    const int32_t half = rope_dim / 2;
+    for (int32_t u = 0; u < n_units; u++) {
+        const int32_t h = u / hd, p = u % hd;
+        const int32_t from = p < 2 * half ? (p & 1 ? p / 2 + half : p / 2) : p;
+        memcpy(dst + (size_t)u * unit, (const uint8_t *)src + ((size_t)h * hd + from) * unit, unit);
+    }
+    return dst;
+}
+
 ss_model_t *ss_model_load(const char *path, const ss_model_config_t *config) {
     return ss_model_load_ex(path, config, NULL);
 }
@@ -120,14 +161,15 @@ ss_model_t *ss_model_load_ex(const char *path, const ss_model_config_t *config,
     m->tok = ss_tok_create(g->vocab, g->vocab_scores, g->vocab ? g->vocab_size : 0, g->merges,
                            g->n_merges, g->arch);
 
-    const char *bad_arch[] = {"qwen", "falcon", "phi", "deepseek", "gemma"};
-    for (size_t i = 0; i < sizeof(bad_arch) / sizeof(bad_arch[0]); i++)
-        if (strstr(g->arch, bad_arch[i])) {
-            fprintf(stderr, "SlipStream: architecture '%s' is not supported by the HIP path\n", g->arch);
-            ss_model_free(m);
-            set_err(SS_ERROR_BACKEND);
-            return NULL;
-        }
+    if (strstr(g->arch, "gemma")) {
+        fprintf(stderr, "SlipStream: architecture '%s' is not supported by the HIP path\n", g->arch);
+        ss_model_free(m);
+        set_err(SS_ERROR_BACKEND);
+        return NULL;
+    }
+    /* layer_scheduler.c:144-149 */
+    const int neox = strstr(g->arch, "qwen") || strstr(g->arch, "falcon") || strstr(g->arch, "phi") ||
+                     strstr(g->arch, "deepseek");
 
     /* shape, layer_scheduler.c:157-197 */
     int32_t d = (int32_t)g->hidden_size, H = (int32_t)g->num_heads;
@@ -160,31 +202,99 @@ ss_model_t *ss_model_load_ex(const char *path, const ss_model_config_t *config,
     if (m->ext.max_context > 0) ctx_size = m->ext.max_context;
 
     const uint32_t L = g->num_layers;
+    const int32_t qdim = H * hd, kvdim = KVH * hd, ffn = (int32_t)g->intermediate_size;
+    if (neox && (rope_dim % 2 || rope_dim > hd)) {
+        fprintf(stderr, "SlipStream: NeoX RoPE needs an even rope dimension <= head_dim\n");
+        ss_model_free(m);
+        set_err(SS_ERROR_INVALID_MODEL);
+        return NULL;
+    }
     ss_hip_tensor_t *lt = (ss_hip_tensor_t *)calloc((size_t)L * SS_HIP_LAYER_TENSORS, sizeof(ss_hip_tensor_t));
-    if (!lt) { ss_model_free(m); set_err(SS_ERROR_OUT_OF_MEMORY); return NULL; }
+    ss_hip_tensor_t *bias = (ss_hip_tensor_t *)calloc((size_t)L * 3, sizeof(ss_hip_tensor_t));
+    void **owned = (void **)calloc((size_t)L * 4 + 1, sizeof(void *));   /* NeoX-ordered copies */
+    int n_owned = 0, any_bias = 0;
+    ss_error_t err = SS_OK;
+    if (!lt || !bias || !owned) err = SS_ERROR_OUT_OF_MEMORY;
     static const char *sfx[SS_HIP_LAYER_TENSORS] = {
         "attn_norm.weight", "attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_output.weight",
         "ffn_norm.weight", "ffn_gate.weight", "ffn_up.weight", "ffn_down.weight"};
-    for (uint32_t l = 0; l < L; l++) {
-        if (ss_gguf_find_in_layer(g, l, "attn_qkv.weight") || ss_gguf_find_in_layer(g, l, "attn_q.bias") ||
-            ss_gguf_find_in_layer(g, l, "post_attention_norm.weight")) {
-            fprintf(stderr, "SlipStream: blk.%u uses fused qkv, biases or post norms (not supported)\n", l);
-            free(lt);
-            ss_model_free(m);
-            set_err(SS_ERROR_BACKEND);
-            return NULL;
+    static const char *bsfx[3] = {"attn_q.bias", "attn_k.bias", "attn_v.bias"};
+    for (uint32_t l = 0; l < L && err == SS_OK; l++) {
+        ss_hip_tensor_t *t = lt + (size_t)l * SS_HIP_LAYER_TENSORS;
+        if (ss_gguf_find_in_layer(g, l, "post_attention_norm.weight")) {
+            fprintf(stderr, "SlipStream: blk.%u uses post norms (not supported)\n", l);
+            err = SS_ERROR_BACKEND;
+            break;
         }
-        for (int k = 0; k < SS_HIP_LAYER_TENSORS; k++) {
-            const ss_gguf_tensor_t *t = ss_gguf_find_in_layer(g, l, sfx[k]);
-            if (!t) {
+        const ss_gguf_tensor_t *wqkv = ss_gguf_find_in_layer(g, l, "attn_qkv.weight");
+        const ss_gguf_tensor_t *wgate = ss_gguf_find_in_layer(g, l, "ffn_gate.weight");
+        for (int k = 0; k < SS_HIP_LAYER_TENSORS && err == SS_OK; k++) {
+            if ((wqkv && (k == SS_HIP_WQ || k == SS_HIP_WK || k == SS_HIP_WV)) || (!wgate && k == SS_HIP_W_GATE))
+                continue;
+            const ss_gguf_tensor_t *tt = ss_gguf_find_in_layer(g, l, sfx[k]);
+            if (!tt) {
                 fprintf(stderr, "SlipStream: blk.%u.%s missing\n", l, sfx[k]);
-                free(lt);
-                ss_model_free(m);
-                set_err(SS_ERROR_INVALID_MODEL);
-                return NULL;
+                err = SS_ERROR_INVALID_MODEL;
+                break;
             }
-            fill_tensor(&lt[l * SS_HIP_LAYER_TENSORS + k], g, t);
+            fill_tensor(&t[k], g, tt);
         }
+        if (err != SS_OK) break;
+        if (wqkv) {   /* layer_scheduler.c:337-347: [Wq; Wk; Wv] in one tensor */
+            ss_hip_tensor_t f;
+            fill_tensor(&f, g, wqkv);
+            if (f.rows != qdim + 2 * kvdim || !row_bytes(f.type, f.cols)) {
+                fprintf(stderr, "SlipStream: blk.%u.attn_qkv.weight has %d rows, %d expected\n", l, f.rows,
+                        qdim + 2 * kvdim);
+                err = SS_ERROR_INVALID_MODEL;
+                break;
+            }
+            t[SS_HIP_WQ] = row_view(&f, 0, qdim);
+            t[SS_HIP_WK] = row_view(&f, qdim, kvdim);
+            t[SS_HIP_WV] = row_view(&f, qdim + kvdim, kvdim);
+        }
+        if (!wgate) {  /* :518-524: ffn_up = [gate; up], 2 * ffn rows */
+            const ss_hip_tensor_t f = t[SS_HIP_W_UP];
+            if (f.rows != 2 * ffn || !row_bytes(f.type, f.cols)) {
+                fprintf(stderr, "SlipStream: blk.%u has no ffn_gate and ffn_up is not [gate; up]\n", l);
+                err = SS_ERROR_INVALID_MODEL;
+                break;
+            }
+            t[SS_HIP_W_GATE] = row_view(&f, 0, ffn);
+            t[SS_HIP_W_UP] = row_view(&f, ffn, ffn);
+        }
+        /* :367-402 (attn_qkv.bias is looked up there but never applied) */
+        for (int k = 0; k < 3; k++) {
+            fill_tensor(&bias[l * 3 + k], g, ss_gguf_find_in_layer(g, l, bsfx[k]));
+            if (bias[l * 3 + k].data) any_bias = 1;
+        }
+        if (neox) {
+            for (int k = 0; k < 2 && err == SS_OK; k++) {   /* Wq, Wk and their biases */
+                ss_hip_tensor_t *w = &t[SS_HIP_WQ + k], *b = &bias[l * 3 + k];
+                const size_t rb = row_bytes(w->type, w->cols);
+                void *c = rb && w->rows % hd == 0 ? neox_order(w->data, rb, w->rows, hd, rope_dim) : NULL;
+                if (!c) { err = rb && w->rows % hd == 0 ? SS_ERROR_OUT_OF_MEMORY : SS_ERROR_INVALID_MODEL; break; }
+                owned[n_owned++] = c;
+                w->data = c;
+                if (b->data) {
+                    const int32_t n = b->rows * b->cols;
+                    const size_t eb = row_bytes(b->type, 1);
+                    void *cb = eb && n % hd == 0 ? neox_order(b->data, eb, n, hd, rope_dim) : NULL;
+                    if (!cb) { err = eb && n % hd == 0 ? SS_ERROR_OUT_OF_MEMORY : SS_ERROR_INVALID_MODEL; break; }
+                    owned[n_owned++] = cb;
+                    b->data = cb;
+                }
+            }
+        }
+    }
+    if (err != SS_OK) {
+        for (int i = 0; i < n_owned; i++) free(owned[i]);
+        free(owned);
+        free(bias);
+        free(lt);
+        ss_model_free(m);
+        set_err(err);
+        return NULL;
     }
     ss_hip_model_desc_t desc;
     memset(&desc, 0, sizeof(desc));
@@ -206,16 +316,23 @@ ss_model_t *ss_model_load_ex(const char *path, const ss_model_config_t *config,
     fill_tensor(&desc.output_norm, g, ss_gguf_find(g, "output_norm.weight"));
     fill_tensor(&desc.output, g, ss_gguf_find(g, "output.weight"));
     desc.layers = lt;
+    desc.qkv_bias = any_bias ? bias : NULL;
 
     m->ctx = ss_hip_init(m->ext.device);
     if (!m->ctx) {
         fprintf(stderr, "SlipStream: HIP backend unavailable: %s\n", ss_hip_last_error());
+        for (int i = 0; i < n_owned; i++) free(owned[i]);
+        free(owned);
+        free(bias);
         free(lt);
         ss_model_free(m);
         set_err(SS_ERROR_BACKEND);
         return NULL;
     }
     m->hm = ss_hip_model_create(m->ctx, &desc);
+    for (int i = 0; i < n_owned; i++) free(owned[i]);
+    free(owned);
+    free(bias);
     free(lt);
     if (!m->hm) {
         fprintf(stderr, "SlipStream: model upload failed: %s\n", ss_hip_last_error());
@@ -224,6 +341,11 @@ ss_model_t *ss_model_load_ex(const char *path, const ss_model_config_t *config,
         return NULL;
     }
     ss_hip_set_cancel_flag(m->hm, &m->cancelled);
+    if (neox) {
+        m->neox_hd = hd;
+        m->neox_rope = rope_dim;
+    }
+    m->kvdim = kvdim;
     m->vocab = vocab;
     m->n_ctx = (int32_t)ctx_size;
     m->n_embd = d;
@@ -409,7 +531,13 @@ ss_error_t ss_decode_greedy(ss_model_t *m, int32_t n_steps, int32_t *out) {
 ss_error_t ss_kv_write(ss_model_t *m, int32_t layer, int32_t pos0, int32_t n_pos, const uint16_t *k,
                        const uint16_t *v) {
     if (!m) return set_err(SS_ERROR_INVALID_PARAMS);
-    return map_rc(ss_hip_kv_write(m->hm, layer, pos0, n_pos, k, v));
+    if (!m->neox_hd || !k || n_pos <= 0) return map_rc(ss_hip_kv_write(m->hm, layer, pos0, n_pos, k, v));
+    /* K rows in the NeoX model's head order (see neox_order) */
+    uint16_t *kk = (uint16_t *)neox_order(k, 2, n_pos * m->kvdim, m->neox_hd, m->neox_rope);
+    if (!kk) return set_err(SS_ERROR_OUT_OF_MEMORY);
+    ss_error_t rc = map_rc(ss_hip_kv_write(m->hm, layer, pos0, n_pos, kk, v));
+    free(kk);
+    return rc;
 }
 
 /* ---- generate, engine.c:174-306 ---- */

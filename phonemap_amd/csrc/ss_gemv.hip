@@ -294,18 +294,20 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int row, bool own, c
   } else if constexpr (EPI == EPI_QKV) {
     // rows of [Wq; Wk; Wv]; q and k rows (i, i+1) are lanes (2j, 2j+1): rotate
     // the pair with the position's (cos, sin), tensor.c:250-273
-    const float partner = __shfl_xor(v[0], 1, kWave);
+    // the bias (layer_scheduler.c:367-402) is added before RoPE
+    const float x = a.bias && row < a.rows ? v[0] + a.bias[row] : v[0];
+    const float partner = __shfl_xor(x, 1, kWave);
     if (!valid) return;
     const int pos = *a.dpos;
     const int hd = a.head_dim;
-    float out = v[0];
+    float out = x;
     if (row < a.qdim + a.kvdim) {
       const int i = (row < a.qdim ? row : row - a.qdim) % hd;
       const int i0 = i & ~1;
       if (i0 < a.rope_dim) {
         const float* cs = a.rope_cs + (size_t)pos * a.rope_dim;
         const float c = cs[i0], s = cs[i0 + 1];
-        out = (i & 1) ? partner * s + v[0] * c : v[0] * c - partner * s;
+        out = (i & 1) ? partner * s + x * c : x * c - partner * s;
       }
     }
     if (row < a.qdim) {

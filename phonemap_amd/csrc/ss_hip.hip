@@ -569,6 +569,7 @@ struct DevLayer {
   float* attn_norm = nullptr;
   float* ffn_norm = nullptr;
   void* wqkv = nullptr;   // packed [Wq;Wk;Wv]
+  float* bqkv = nullptr;  // q/k/v biases [qdim + 2*kvdim] in fp32, or nullptr
   void* wo = nullptr;
   void* wg = nullptr;
   void* wu = nullptr;
@@ -676,14 +677,24 @@ int32_t m_alloc(ss_hip_model* m, void** p, size_t bytes, bool zero = true) {
   return 0;
 }
 
+// An F32 or F16 vector of n elements widened to fp32 into h.
+int32_t host_f32(const ss_hip_tensor_t& t, int n, const char* what, float* h);
+
 int32_t upload_vec(ss_hip_model* m, float** dst, const ss_hip_tensor_t& t, int n, const char* what) {
+  std::vector<float> h((size_t)n);
+  if (int32_t rc = host_f32(t, n, what, h.data())) return rc;
+  if (int32_t rc = m_alloc(m, (void**)dst, sizeof(float) * n, false)) return rc;
+  HIP_TRY(hipMemcpy(*dst, h.data(), sizeof(float) * n, hipMemcpyHostToDevice));
+  return 0;
+}
+
+int32_t host_f32(const ss_hip_tensor_t& t, int n, const char* what, float* h) {
   if (!t.data) return fail(kErrParams, "model: missing %s", what);
   if (t.type != SS_HIP_F32 && t.type != SS_HIP_F16)
     return fail(kErrParams, "model: %s has type %d (F32/F16 expected)", what, t.type);
   if ((int64_t)t.rows * t.cols != n) return fail(kErrParams, "model: %s has %d x %d elements, %d expected", what, t.rows, t.cols, n);
-  std::vector<float> h((size_t)n);
   if (t.type == SS_HIP_F32) {
-    memcpy(h.data(), t.data, sizeof(float) * n);
+    memcpy(h, t.data, sizeof(float) * n);
   } else {
     // exact binary16 widening (quantize.c:20-56)
     const uint16_t* s = static_cast<const uint16_t*>(t.data);
@@ -707,8 +718,6 @@ int32_t upload_vec(ss_hip_model* m, float** dst, const ss_hip_tensor_t& t, int n
       memcpy(&h[i], &bits, 4);
     }
   }
-  if (int32_t rc = m_alloc(m, (void**)dst, sizeof(float) * n, false)) return rc;
-  HIP_TRY(hipMemcpy(*dst, h.data(), sizeof(float) * n, hipMemcpyHostToDevice));
   return 0;
 }
 
@@ -947,6 +956,7 @@ int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden,
   a.vcache = vc;
   a.kv_f32 = m->kv_f32;
   a.xr = xr;
+  a.bias = ly.bqkv;
   HIP_TRY(timed(m, q_class(ly.t_qkv), matvec_bytes(ly.t_qkv, a.rows, m->d, 1),
                 [&] { return ssk::launch_gemv(ssk::EPI_QKV, a, s); }));
   if (m->kv_type == 1)
@@ -1222,8 +1232,8 @@ int32_t enqueue_layer_rows(ss_hip_model* m, int l, const DevLayer& ly, int T, in
   a.eps = m->eps;
   HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_gemm(ssk::EPI_STORE, a, s); }));
   HIP_TRY(timed(m, PC_OTHER, 0, [&] {
-    return ssk::launch_rope_kv_rows(m->pf_qkv, ldq, m->qdim, m->kvdim, m->hd, m->rope_dim, m->rope_cs, dpos, kc, vc,
-                                    m->max_seq, T, s);
+    return ssk::launch_rope_kv_rows(m->pf_qkv, ly.bqkv, ldq, m->qdim, m->kvdim, m->hd, m->rope_dim, m->rope_cs, dpos,
+                                    kc, vc, m->max_seq, T, s);
   }));
 
   // 2. attention of every token over positions 0..its own        (:415-468)
@@ -1519,6 +1529,26 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
     if (t[SS_HIP_WQ].rows != m->qdim || t[SS_HIP_WK].rows != m->kvdim) {
       fail(kErrParams, "model: blk.%d q/k/v row counts do not match the head shape", l);
       return bail();
+    }
+    if (d->qkv_bias) {   // layer_scheduler.c:367-402: q, k, v biases as one fp32 vector
+      const ss_hip_tensor_t* b = d->qkv_bias + (size_t)l * 3;
+      if (b[0].data || b[1].data || b[2].data) {
+        if (d->launch == SS_HIP_LAUNCH_SWEEP) {
+          fail(kErrParams, "model: the persistent launch does not apply q/k/v biases");
+          return bail();
+        }
+        const int n3[3] = {m->qdim, m->kvdim, m->kvdim};
+        std::vector<float> h((size_t)m->qdim + 2 * m->kvdim, 0.f);
+        for (int k = 0, o = 0; k < 3; o += n3[k], k++) {
+          snprintf(what, sizeof(what), "blk.%d attn_%c.bias", l, "qkv"[k]);
+          if (b[k].data && host_f32(b[k], n3[k], what, h.data() + o)) return bail();
+        }
+        if (m_alloc(m, (void**)&ly.bqkv, sizeof(float) * h.size(), false) ||
+            hipMemcpy(ly.bqkv, h.data(), sizeof(float) * h.size(), hipMemcpyHostToDevice) != hipSuccess) {
+          fail(kErrBackend, "bias upload failed");
+          return bail();
+        }
+      }
     }
     snprintf(what, sizeof(what), "blk.%d attn_output", l);
     if (upload_mat(m, &ly.wo, t + SS_HIP_WO, 1, m->d, m->qdim, &ly.t_o, what, blk ? blk + off[1] : nullptr))

@@ -33,6 +33,7 @@ struct GemvArgs {
   // EPI_QKV
   int qdim, kvdim, head_dim, rope_dim, max_seq, kv_type;
   const float* rope_cs;      // [max_seq][rope_dim/2][2]
+  const float* bias;         // EPI_QKV: q/k/v bias [qdim + 2*kvdim] added before RoPE, or nullptr
   const int* dpos;           // device position
   void* kcache;              // this layer: [kvh][max_seq][head_dim] fp16 (kv_type 0)
   void* vcache;
@@ -151,7 +152,7 @@ hipError_t launch_kv_append(void* kc, void* vc, float* ksc, float* vsc, const fl
                             const int* dpos, int pos, int kv_type, hipStream_t s);
 // RoPE of the q and k parts of n prompt rows [q | k | v] (stride ld; token z
 // at position dpos[z]) and the fp16 cache append of k and v.
-hipError_t launch_rope_kv_rows(float* qkv, int ld, int qdim, int kvdim, int head_dim, int rope_dim,
+hipError_t launch_rope_kv_rows(float* qkv, const float* bias, int ld, int qdim, int kvdim, int head_dim, int rope_dim,
                                const float* cs, const int* dpos, uint16_t* kc, uint16_t* vc, int max_seq,
                                int n, hipStream_t s);
 // acc[j] += sum over the T rows x[t] (stride d) of x[t][j] * k_t * w[j] (the

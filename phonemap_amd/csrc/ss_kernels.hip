@@ -742,8 +742,9 @@ __global__ void k_rope(float* q, float* k, int n_heads, int n_kv_heads, int head
 // (tensor.c:250-273; q in place for the attention that follows), then k and
 // v go to the fp16 cache [kvh][max_seq][hd] (layer_scheduler.c:392-413).
 // One thread per pair; grid y = tokens.
-__global__ void k_rope_kv_rows(float* qkv, int ld, int qdim, int kvdim, int head_dim, int rope_dim,
-                               const float* cs, const int* dpos, uint16_t* kc, uint16_t* vc, int max_seq) {
+__global__ void k_rope_kv_rows(float* qkv, const float* bias, int ld, int qdim, int kvdim, int head_dim,
+                               int rope_dim, const float* cs, const int* dpos, uint16_t* kc, uint16_t* vc,
+                               int max_seq) {
   const int pos = dpos[blockIdx.y];
   float* row = qkv + (size_t)blockIdx.y * ld;
   const int npairs = (qdim + 2 * kvdim) >> 1;
@@ -751,6 +752,11 @@ __global__ void k_rope_kv_rows(float* qkv, int ld, int qdim, int kvdim, int head
     const int r = 2 * p;
     const float2 v = reinterpret_cast<const float2*>(row)[p];
     float a = v.x, b = v.y;
+    if (bias) {   // layer_scheduler.c:367-402, before RoPE
+      const float2 bb = reinterpret_cast<const float2*>(bias)[p];
+      a = a + bb.x;
+      b = b + bb.y;
+    }
     if (r < qdim + kvdim) {
       const int i0 = (r < qdim ? r : r - qdim) % head_dim;
       if (i0 < rope_dim) {
@@ -987,14 +993,14 @@ hipError_t launch_kv_append(void* kc, void* vc, float* ksc, float* vsc, const fl
   return hipGetLastError();
 }
 
-hipError_t launch_rope_kv_rows(float* qkv, int ld, int qdim, int kvdim, int head_dim, int rope_dim,
+hipError_t launch_rope_kv_rows(float* qkv, const float* bias, int ld, int qdim, int kvdim, int head_dim, int rope_dim,
                                const float* cs, const int* dpos, uint16_t* kc, uint16_t* vc, int max_seq,
                                int n, hipStream_t s) {
   if (n <= 0 || ld % 2 || qdim % 2 || kvdim % 2 || head_dim % 2 || ld < qdim + 2 * kvdim) return hipErrorInvalidValue;
   const int npairs = (qdim + 2 * kvdim) / 2;
   const int gx = (npairs + 255) / 256;
-  hipLaunchKernelGGL(k_rope_kv_rows, dim3(gx, n), dim3(256), 0, s, qkv, ld, qdim, kvdim, head_dim, rope_dim, cs,
-                     dpos, kc, vc, max_seq);
+  hipLaunchKernelGGL(k_rope_kv_rows, dim3(gx, n), dim3(256), 0, s, qkv, bias, ld, qdim, kvdim, head_dim, rope_dim,
+                     cs, dpos, kc, vc, max_seq);
   return hipGetLastError();
 }
 

@@ -29,8 +29,14 @@ typedef struct {
     int32_t type;
     uint64_t offset;   /* relative to the data section */
     uint64_t bytes;
-    int norm;
+    int norm;          /* 1: norm weight 1 + N(0, norm_sigma); 2: bias N(0, kBiasSigma) */
+    uint64_t sid;      /* seed id of the random stream: the tensor's index in the unfused,
+                        * bias-free layout, so fused and biased files keep every weight */
+    int join_next;     /* the next tensor continues this one's rows (one fused GGUF tensor) */
 } syn_tensor_t;
+
+#define T_F16 1
+static const double kBiasSigma = 0.1;
 
 /* ---- random numbers ---- */
 static uint64_t splitmix64(uint64_t *s) {
@@ -142,10 +148,22 @@ static void gen_item(job_t *j, uint64_t it, uint8_t *buf) {
     const syn_tensor_t *t = &j->t[j->item_tensor[it]];
     uint64_t chunk = j->item_chunk[it];
     xo_t x;
-    xo_seed(&x, j->seed, j->item_tensor[it] + 1, chunk);
+    xo_seed(&x, j->seed, t->sid + 1, chunk);
     size_t n = 0;
     uint64_t off = 0;
-    if (t->type == T_F32) {
+    if (t->norm == 2) {
+        uint64_t ne = t->dims[0];
+        for (uint64_t i = 0; i < ne; i++) {
+            float v = (float)(kBiasSigma * xo_normal(&x));
+            if (t->type == T_F16) {
+                uint16_t h = to_f16(v);
+                memcpy(buf + 2 * i, &h, 2);
+            } else {
+                memcpy(buf + 4 * i, &v, 4);
+            }
+        }
+        n = ne * (t->type == T_F16 ? 2 : 4);
+    } else if (t->type == T_F32) {
         uint64_t ne = t->dims[0] * (t->n_dims > 1 ? t->dims[1] : 1);
         float *f = (float *)buf;
         for (uint64_t i = 0; i < ne; i++) f[i] = (float)(1.0 + j->norm_sigma * xo_normal(&x));
@@ -183,13 +201,13 @@ static void *worker(void *arg) {
     uint8_t *buf = (uint8_t *)malloc((size_t)CHUNK_BLOCKS * 34 + (1u << 20));
     uint64_t max_vec = 0;
     for (int i = 0; i < j->nt; i++)
-        if (j->t[i].type == T_F32 && j->t[i].bytes > max_vec) max_vec = j->t[i].bytes;
+        if (j->t[i].norm && j->t[i].bytes > max_vec) max_vec = j->t[i].bytes;
     uint8_t *vbuf = max_vec > (size_t)CHUNK_BLOCKS * 34 ? (uint8_t *)malloc(max_vec) : NULL;
     if (!buf) { __atomic_store_n(&j->failed, 1, __ATOMIC_RELAXED); return NULL; }
     for (;;) {
         uint64_t it = __atomic_fetch_add(&j->next, 1, __ATOMIC_RELAXED);
         if (it >= j->n_items || __atomic_load_n(&j->failed, __ATOMIC_RELAXED)) break;
-        gen_item(j, it, (vbuf && j->t[j->item_tensor[it]].type == T_F32) ? vbuf : buf);
+        gen_item(j, it, (vbuf && j->t[j->item_tensor[it]].norm) ? vbuf : buf);
     }
     free(vbuf);
     free(buf);
@@ -203,15 +221,18 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
         (s->n_heads * s->head_dim) % 32 || (s->n_kv_heads * s->head_dim) % 32 ||
         (s->layer_type != T_Q4_0 && s->layer_type != T_Q8_0) ||
         (s->embd_type != T_Q4_0 && s->embd_type != T_Q8_0) ||
-        (s->out_type != -1 && s->out_type != T_Q4_0 && s->out_type != T_Q8_0))
+        (s->out_type != -1 && s->out_type != T_Q4_0 && s->out_type != T_Q8_0) ||
+        s->arch < 0 || s->arch > 1 || s->qkv_bias < 0 || s->qkv_bias > 2)
         return -5;
+    const char *arch = s->arch == 1 ? "qwen2" : "llama";
     const int L = s->n_layers;
     const uint64_t d = (uint64_t)s->hidden, q = (uint64_t)s->n_heads * s->head_dim,
                    kv = (uint64_t)s->n_kv_heads * s->head_dim, f = (uint64_t)s->ffn;
-    int nt = 1 + 9 * L + 1 + (s->out_type >= 0 ? 1 : 0);
+    int nt = 1 + 9 * L + 1 + (s->out_type >= 0 ? 1 : 0) + (s->qkv_bias ? 3 * L : 0);
     syn_tensor_t *t = (syn_tensor_t *)calloc((size_t)nt, sizeof(syn_tensor_t));
     if (!t) return -3;
     int k = 0;
+    uint64_t sid = 0;
 #define ADD(nm, type_, cols, rows, isnorm)                                           \
     do {                                                                             \
         snprintf(t[k].name, sizeof(t[k].name), "%s", nm);                           \
@@ -220,30 +241,51 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
         t[k].dims[1] = (rows);                                                       \
         t[k].n_dims = (isnorm) ? 1 : 2;                                              \
         t[k].norm = (isnorm);                                                        \
-        t[k].bytes = (isnorm) ? (uint64_t)(cols) * 4                                 \
-                              : (uint64_t)(cols) * (rows) / 32 * ((type_) == T_Q4_0 ? 18 : 34); \
+        t[k].sid = (isnorm) == 2 ? 0x100000u + (uint64_t)k : sid++;                 \
+        t[k].bytes = (isnorm) == 2 ? (uint64_t)(cols) * ((type_) == T_F16 ? 2 : 4)   \
+                     : (isnorm) ? (uint64_t)(cols) * 4                               \
+                                : (uint64_t)(cols) * (rows) / 32 * ((type_) == T_Q4_0 ? 18 : 34); \
         k++;                                                                         \
     } while (0)
     ADD("token_embd.weight", s->embd_type, d, (uint64_t)s->vocab, 0);
     char nm[64];
     for (int l = 0; l < L; l++) {
         snprintf(nm, sizeof(nm), "blk.%d.attn_norm.weight", l); ADD(nm, T_F32, d, 1, 1);
-        snprintf(nm, sizeof(nm), "blk.%d.attn_q.weight", l); ADD(nm, s->layer_type, d, q, 0);
+        /* fused: one tensor [Wq; Wk; Wv] (layer_scheduler.c:337-347) of the same parts */
+        snprintf(nm, sizeof(nm), "blk.%d.%s.weight", l, s->fused_qkv ? "attn_qkv" : "attn_q");
+        ADD(nm, s->layer_type, d, q, 0);
+        t[k - 1].join_next = s->fused_qkv;
         snprintf(nm, sizeof(nm), "blk.%d.attn_k.weight", l); ADD(nm, s->layer_type, d, kv, 0);
+        t[k - 1].join_next = s->fused_qkv;
         snprintf(nm, sizeof(nm), "blk.%d.attn_v.weight", l); ADD(nm, s->layer_type, d, kv, 0);
+        if (s->qkv_bias) {   /* Qwen2 biases (layer_scheduler.c:367-402) */
+            const int bt = s->qkv_bias == 2 ? T_F16 : T_F32;
+            snprintf(nm, sizeof(nm), "blk.%d.attn_q.bias", l); ADD(nm, bt, q, 1, 2);
+            snprintf(nm, sizeof(nm), "blk.%d.attn_k.bias", l); ADD(nm, bt, kv, 1, 2);
+            snprintf(nm, sizeof(nm), "blk.%d.attn_v.bias", l); ADD(nm, bt, kv, 1, 2);
+        }
         snprintf(nm, sizeof(nm), "blk.%d.attn_output.weight", l); ADD(nm, s->layer_type, q, d, 0);
         snprintf(nm, sizeof(nm), "blk.%d.ffn_norm.weight", l); ADD(nm, T_F32, d, 1, 1);
-        snprintf(nm, sizeof(nm), "blk.%d.ffn_gate.weight", l); ADD(nm, s->layer_type, d, f, 0);
+        /* fused: ffn_up = [Wgate; Wup], 2 * ffn rows (layer_scheduler.c:518-524) */
+        snprintf(nm, sizeof(nm), "blk.%d.%s.weight", l, s->fused_up ? "ffn_up" : "ffn_gate");
+        ADD(nm, s->layer_type, d, f, 0);
+        t[k - 1].join_next = s->fused_up;
         snprintf(nm, sizeof(nm), "blk.%d.ffn_up.weight", l); ADD(nm, s->layer_type, d, f, 0);
         snprintf(nm, sizeof(nm), "blk.%d.ffn_down.weight", l); ADD(nm, s->layer_type, f, d, 0);
     }
     ADD("output_norm.weight", T_F32, d, 1, 1);
     if (s->out_type >= 0) ADD("output.weight", s->out_type, d, (uint64_t)s->vocab, 0);
 #undef ADD
+    /* the parts of a fused tensor are contiguous; tensors start 32-byte aligned */
     uint64_t off = 0;
+    int n_phys = 0;
     for (int i = 0; i < nt; i++) {
         t[i].offset = off;
-        off = (off + t[i].bytes + 31) & ~(uint64_t)31;
+        off += t[i].bytes;
+        if (!t[i].join_next) {
+            off = (off + 31) & ~(uint64_t)31;
+            n_phys++;
+        }
     }
     const uint64_t data_bytes = off;
 
@@ -251,20 +293,23 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
     const uint32_t n_kv = 12 + (s->with_vocab ? 3 : 0);
     wb_u32(&b, 0x46554747u);
     wb_u32(&b, 3);
-    wb_u64(&b, (uint64_t)nt);
+    wb_u64(&b, (uint64_t)n_phys);
     wb_u64(&b, n_kv);
-    kv_str(&b, "general.architecture", "llama");
-    kv_str(&b, "general.name", "synthetic-llama");
+    char key[96], gname[48];
+#define AK(sfx) (snprintf(key, sizeof(key), "%s.%s", arch, sfx), key)
+    snprintf(gname, sizeof(gname), "synthetic-%s", arch);
+    kv_str(&b, "general.architecture", arch);
+    kv_str(&b, "general.name", gname);
     kv_u32(&b, "general.alignment", 32);
-    kv_u32(&b, "llama.block_count", (uint32_t)L);
-    kv_u32(&b, "llama.context_length", (uint32_t)(s->context_length > 0 ? s->context_length : 2048));
-    kv_u32(&b, "llama.embedding_length", (uint32_t)d);
-    kv_u32(&b, "llama.feed_forward_length", (uint32_t)f);
-    kv_u32(&b, "llama.attention.head_count", (uint32_t)s->n_heads);
-    kv_u32(&b, "llama.attention.head_count_kv", (uint32_t)s->n_kv_heads);
-    kv_u32(&b, "llama.rope.dimension_count", (uint32_t)s->head_dim);
-    kv_f32(&b, "llama.rope.freq_base", s->rope_theta > 0 ? s->rope_theta : 10000.0f);
-    kv_f32(&b, "llama.attention.layer_norm_rms_epsilon", s->rms_eps > 0 ? s->rms_eps : 1e-5f);
+    kv_u32(&b, AK("block_count"), (uint32_t)L);
+    kv_u32(&b, AK("context_length"), (uint32_t)(s->context_length > 0 ? s->context_length : 2048));
+    kv_u32(&b, AK("embedding_length"), (uint32_t)d);
+    kv_u32(&b, AK("feed_forward_length"), (uint32_t)f);
+    kv_u32(&b, AK("attention.head_count"), (uint32_t)s->n_heads);
+    kv_u32(&b, AK("attention.head_count_kv"), (uint32_t)s->n_kv_heads);
+    kv_u32(&b, AK("rope.dimension_count"), (uint32_t)s->head_dim);
+    kv_f32(&b, AK("rope.freq_base"), s->rope_theta > 0 ? s->rope_theta : 10000.0f);
+    kv_f32(&b, AK("attention.layer_norm_rms_epsilon"), s->rms_eps > 0 ? s->rms_eps : 1e-5f);
     if (s->with_vocab) {
         char vb[64];
         kv_str(&b, "tokenizer.ggml.model", "llama");
@@ -279,12 +324,18 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
         wb_u64(&b, (uint64_t)s->vocab);
         for (int i = 0; i < s->vocab; i++) wb_f32(&b, i < 259 ? 0.0f : -(float)(i - 259) * 0.01f);
     }
-    for (int i = 0; i < nt; i++) {
+#undef AK
+    for (int i = 0; i < nt;) {
+        int e = i;   /* parts i..e form one GGUF tensor */
+        uint64_t rows = t[i].dims[1];
+        while (t[e].join_next) rows += t[++e].dims[1];
         wb_str(&b, t[i].name);
         wb_u32(&b, t[i].n_dims);
-        for (uint32_t dd = 0; dd < t[i].n_dims; dd++) wb_u64(&b, t[i].dims[dd]);
+        wb_u64(&b, t[i].dims[0]);
+        if (t[i].n_dims > 1) wb_u64(&b, rows);
         wb_u32(&b, (uint32_t)t[i].type);
         wb_u64(&b, t[i].offset);
+        i = e + 1;
     }
     if (b.bad) { free(b.p); free(t); return -3; }
     const uint64_t data_off = (b.n + 31) & ~(uint64_t)31;
@@ -308,13 +359,13 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
     j.nt = nt;
     uint64_t items = 0;
     for (int i = 0; i < nt; i++)
-        items += t[i].type == T_F32 ? 1 : (tensor_blocks(&t[i]) + CHUNK_BLOCKS - 1) / CHUNK_BLOCKS;
+        items += t[i].norm ? 1 : (tensor_blocks(&t[i]) + CHUNK_BLOCKS - 1) / CHUNK_BLOCKS;
     j.item_tensor = (uint64_t *)malloc(items * 8);
     j.item_chunk = (uint64_t *)malloc(items * 8);
     if (!j.item_tensor || !j.item_chunk) rc = -3;
     uint64_t it = 0;
     for (int i = 0; rc == 0 && i < nt; i++) {
-        uint64_t nc = t[i].type == T_F32 ? 1 : (tensor_blocks(&t[i]) + CHUNK_BLOCKS - 1) / CHUNK_BLOCKS;
+        uint64_t nc = t[i].norm ? 1 : (tensor_blocks(&t[i]) + CHUNK_BLOCKS - 1) / CHUNK_BLOCKS;
         for (uint64_t c = 0; c < nc; c++) { j.item_tensor[it] = (uint64_t)i; j.item_chunk[it] = c; it++; }
     }
     j.n_items = items;
