@@ -40,6 +40,8 @@ typedef struct {
     int32_t fused_qkv;    /* blk.N.attn_qkv.weight = [Wq; Wk; Wv] in place of three tensors */
     int32_t fused_up;     /* blk.N.ffn_up.weight = [Wgate; Wup] (2 * ffn rows), no ffn_gate */
     int32_t qkv_bias;     /* blk.N.attn_q/k/v.bias: 0 none, 1 F32, 2 F16; values N(0, 0.1) */
+    int32_t alignment;    /* general.alignment and the data/tensor alignment in bytes (a power
+                           * of two); 0 = 32, the only alignment the reference reads */
 } ss_synth_spec_t;
 
 /* Returns 0, or a negative ss_error_t value (-5 bad spec, -1 cannot write). */

@@ -214,6 +214,10 @@ ss_gguf_file_t *ss_gguf_open(const char *path) {
     f->n_tensors = u64(&r);
     f->n_kv = u64(&r);
     uint32_t n_tok_strings = 0;
+    /* Data alignment: general.alignment when present (the GGUF format's rule;
+     * a power of two), else 32. The reference always uses 32
+     * (gguf_loader.c:426), which misplaces the data of any other alignment. */
+    uint64_t align = 32;
     for (uint64_t i = 0; i < f->n_kv && !r.bad; i++) {   /* gguf_loader.c:270-364 */
         uint64_t kl;
         const char *k = str(&r, &kl);
@@ -226,6 +230,13 @@ ss_gguf_file_t *ss_gguf_open(const char *path) {
                 size_t c = sl < sizeof(f->arch) - 1 ? sl : sizeof(f->arch) - 1;
                 memcpy(f->arch, s, c);
                 f->arch[c] = 0;
+            }
+        } else if (equals(k, kl, "general.alignment") && vt == 4) {
+            align = u32(&r);
+            if (align == 0 || (align & (align - 1))) {
+                gerr("general.alignment %llu is not a power of two", (unsigned long long)align);
+                ss_gguf_close(f);
+                return NULL;
             }
         } else if (ends_with(k, kl, ".embedding_length") && vt == 4) {
             f->hidden_size = u32(&r);
@@ -307,7 +318,7 @@ ss_gguf_file_t *ss_gguf_open(const char *path) {
         t->layer_index = layer_of(t->name);
     }
     if (r.bad) { gerr("tensor table truncated or malformed"); ss_gguf_close(f); return NULL; }
-    f->data_offset = (r.pos + 31) & ~(uint64_t)31;                   /* :426 */
+    f->data_offset = (r.pos + align - 1) & ~(align - 1);             /* :426 */
     for (uint64_t i = 0; i < f->n_tensors; i++) f->tensors[i].offset += f->data_offset;
 
     if (f->num_layers > 0) {                                           /* :434-475 */

@@ -225,6 +225,8 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
         s->arch < 0 || s->arch > 1 || s->qkv_bias < 0 || s->qkv_bias > 2)
         return -5;
     const char *arch = s->arch == 1 ? "qwen2" : "llama";
+    const uint64_t align = s->alignment > 0 ? (uint64_t)s->alignment : 32;
+    if (align & (align - 1)) return -5;
     const int L = s->n_layers;
     const uint64_t d = (uint64_t)s->hidden, q = (uint64_t)s->n_heads * s->head_dim,
                    kv = (uint64_t)s->n_kv_heads * s->head_dim, f = (uint64_t)s->ffn;
@@ -276,14 +278,14 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
     ADD("output_norm.weight", T_F32, d, 1, 1);
     if (s->out_type >= 0) ADD("output.weight", s->out_type, d, (uint64_t)s->vocab, 0);
 #undef ADD
-    /* the parts of a fused tensor are contiguous; tensors start 32-byte aligned */
+    /* the parts of a fused tensor are contiguous; tensors start aligned */
     uint64_t off = 0;
     int n_phys = 0;
     for (int i = 0; i < nt; i++) {
         t[i].offset = off;
         off += t[i].bytes;
         if (!t[i].join_next) {
-            off = (off + 31) & ~(uint64_t)31;
+            off = (off + align - 1) & ~(align - 1);
             n_phys++;
         }
     }
@@ -300,7 +302,7 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
     snprintf(gname, sizeof(gname), "synthetic-%s", arch);
     kv_str(&b, "general.architecture", arch);
     kv_str(&b, "general.name", gname);
-    kv_u32(&b, "general.alignment", 32);
+    kv_u32(&b, "general.alignment", (uint32_t)align);
     kv_u32(&b, AK("block_count"), (uint32_t)L);
     kv_u32(&b, AK("context_length"), (uint32_t)(s->context_length > 0 ? s->context_length : 2048));
     kv_u32(&b, AK("embedding_length"), (uint32_t)d);
@@ -338,7 +340,7 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
         i = e + 1;
     }
     if (b.bad) { free(b.p); free(t); return -3; }
-    const uint64_t data_off = (b.n + 31) & ~(uint64_t)31;
+    const uint64_t data_off = (b.n + align - 1) & ~(align - 1);
     while (b.n < data_off) { uint8_t z = 0; wb_put(&b, &z, 1); }
 
     int fd = open(path, O_WRONLY | O_CREAT | O_TRUNC, 0644);

@@ -132,7 +132,8 @@ def parse_gguf(path):
         t = rd("<I")
         off = rd("<Q")
         tensors.append((name, dims, t, off))
-    data = (o + 31) & ~31
+    a = meta.get("general.alignment", 32)          # the GGUF format's data alignment
+    data = (o + a - 1) & ~(a - 1)
     return version, meta, tensors, data, b
 
 
@@ -172,13 +173,19 @@ def gguf_open(path):
     return lib, f
 
 
+@pytest.mark.parametrize("alignment", [0, 64, 4096])
 @pytest.mark.parametrize("out_type", [-1, 8])
-def test_synthetic_gguf_round_trip(tmp_path, out_type):
+def test_synthetic_gguf_round_trip(tmp_path, out_type, alignment):
+    """Writer and reader agree, for the reference's 32-byte alignment and for
+    general.alignment values the reference would misread (gguf_loader.c:426)."""
     path = str(tmp_path / "m.gguf")
-    spec = tiny_spec(out_type=out_type)
+    spec = tiny_spec(out_type=out_type, alignment=alignment)
     api.write_synthetic_gguf(path, spec)
     version, meta, tensors, data_off, raw = parse_gguf(path)
     assert version in (2, 3)
+    a = alignment or 32
+    assert meta["general.alignment"] == a and data_off % a == 0
+    assert all(off % a == 0 for _, _, _, off in tensors)
     assert meta["general.architecture"] == "llama"
     assert meta["llama.embedding_length"] == 64
     assert meta["llama.block_count"] == 2

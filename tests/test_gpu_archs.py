@@ -134,3 +134,22 @@ def test_variants_streaming_matches_resident(spec):
                 pos += 1
             out.append(np.stack(seq))
     assert np.array_equal(out[0], out[1])
+
+
+def test_general_alignment_is_honoured():
+    """A file whose data is 4096-byte aligned (general.alignment) holds the
+    same weights as the 32-byte aligned one and gives identical logits."""
+    paths = [_model_file("align%d" % a, **dict(TINY, seed=35, alignment=a)) for a in (32, 4096)]
+    prompt = [3, 14, 15, 92, 65, 35, 89, 79, 32, 38]
+    out = []
+    for path in paths:
+        with api.Model(path, max_context=64) as m:
+            lg, am = m.eval_prompt(prompt, 0)
+            seq = [lg]
+            tok, pos = am, len(prompt)
+            for _ in range(6):
+                lg, tok = m.eval_token(tok, pos)
+                seq.append(lg)
+                pos += 1
+            out.append(np.stack(seq))
+    assert np.array_equal(out[0], out[1])
