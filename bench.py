@@ -46,19 +46,19 @@ HBM_PEAK_GBS = 8000.0
 CONFIGS = {
     "llama2-7b": dict(spec=dict(n_layers=32, hidden=4096, n_heads=32, n_kv_heads=32, head_dim=128,
                                 ffn=11008, vocab=32000, context_length=4096, layer_type=2, embd_type=8,
-                                out_type=8, seed=7), prompt=512, steps=256,
+                                out_type=8, seed=7, scale_mode=1), prompt=512, steps=256,
                       name="llama2-7b-shape, Q4_0 layers + Q8_0 token_embd/output"),
     "tinyllama": dict(spec=dict(n_layers=22, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=64,
                                 ffn=5632, vocab=32000, context_length=2048, layer_type=2, embd_type=2,
-                                out_type=2, seed=1001), prompt=32, steps=128,
+                                out_type=2, seed=1001, scale_mode=1), prompt=32, steps=128,
                       name="tinyllama-1.1b-shape, all Q4_0"),
     "llama3-8b": dict(spec=dict(n_layers=32, hidden=4096, n_heads=32, n_kv_heads=8, head_dim=128,
                                 ffn=14336, vocab=128256, context_length=8192, rope_theta=500000.0,
-                                layer_type=8, embd_type=8, out_type=8, seed=8), prompt=0, kv_fill=4096,
+                                layer_type=8, embd_type=8, out_type=8, seed=8, scale_mode=1), prompt=0, kv_fill=4096,
                       steps=128, name="llama3-8b-shape, all Q8_0"),
     "llama2-70b": dict(spec=dict(n_layers=80, hidden=8192, n_heads=64, n_kv_heads=8, head_dim=128,
                                  ffn=28672, vocab=32000, context_length=4096, layer_type=2, embd_type=2,
-                                 out_type=2, seed=70), prompt=1024, steps=64,
+                                 out_type=2, seed=70, scale_mode=1), prompt=1024, steps=64,
                        name="llama2-70b-shape, all Q4_0, resident in HBM"),
     "llama2-70b-stream": dict(model="llama2-70b", streaming=True, prompt=1024, steps=64, profile_steps=2,
                               name="llama2-70b-shape, all Q4_0, streaming mode (layers uploaded per use "
@@ -71,6 +71,20 @@ for _c in CONFIGS.values():       # a streaming config shares its model's file a
 
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
+
+
+def model_file(name, model_dir="/tmp"):
+    """The synthetic GGUF of config `name` (written once; the name carries the
+    seed and the scale mode, so a file of another spec is never reused)."""
+    from phonemap_amd import api
+    spec = CONFIGS[name]["spec"]
+    path = os.path.join(model_dir, "ss_bench_%s_s%d_m%d.gguf" % (name, spec["seed"], spec.get("scale_mode", 0)))
+    if not os.path.exists(path):
+        t = time.perf_counter()
+        api.write_synthetic_gguf(path + ".part", api.SynthSpec(**spec))
+        os.replace(path + ".part", path)
+        log("wrote %s (%.2f GB) in %.1f s" % (path, os.path.getsize(path) / 1e9, time.perf_counter() - t))
+    return path
 
 
 def token_bytes(spec, ctx):
@@ -170,12 +184,7 @@ def main():
     kv_fill = cfg.get("kv_fill", 0)
     streaming = cfg.get("streaming", False)
     prof_steps = args.profile_steps if args.profile_steps is not None else cfg.get("profile_steps", 16)
-    path = os.path.join(args.model_dir, "ss_bench_%s_s%d.gguf" % (cfg.get("model", args.config), spec["seed"]))
-    if not os.path.exists(path):
-        t = time.perf_counter()
-        api.write_synthetic_gguf(path + ".part", api.SynthSpec(**spec))
-        os.replace(path + ".part", path)
-        log("wrote %s (%.2f GB) in %.1f s" % (path, os.path.getsize(path) / 1e9, time.perf_counter() - t))
+    path = model_file(cfg.get("model", args.config), args.model_dir)
     max_ctx = prompt_len + kv_fill + 1 + warm + steps + prof_steps + 2
     t = time.perf_counter()
     m = api.Model(path, max_context=max_ctx, kv=args.kv, launch=args.launch, streaming=streaming)

@@ -7,11 +7,19 @@
  * dims[1] = rows). No counterpart in the reference; it stands in for the
  * checkpoints that cannot be downloaded.
  *
- * Distributions: Q4_0 blocks have d = fp16(|N(0, scale_sigma)|) and uniform
- * random nibbles; Q8_0 blocks have d = fp16(|N(0, scale_sigma / 16)|) and int8
- * codes uniform in [-127, 127] (the codes' spread is 16 times the nibbles', so
- * both types give weights of the same spread); norm weights are fp32
- * 1 + N(0, norm_sigma); q/k/v biases (when asked for) are N(0, 0.1).
+ * Distributions: Q4_0 blocks have uniform random nibbles, Q8_0 blocks int8
+ * codes uniform in [-127, 127]. The block scale d is, with scale_mode 0,
+ * fp16(|N(0, scale_sigma)|) for Q4_0 and fp16(|N(0, scale_sigma / 16)|) for
+ * Q8_0 (the codes' spread is 16 times the nibbles', so both types give
+ * weights of the same spread); with scale_mode 1 it is signed,
+ * fp16(N(0, 1 / (c * sqrt(cols)))) with c the RMS of the codes (sqrt(21.5)
+ * for Q4_0 nibbles - 8, sqrt(127 * 128 / 3) for Q8_0), so every weight has
+ * standard deviation 1/sqrt(cols) and zero mean. Mode 0 with positive d
+ * gives every Q4_0 block the mean -d/2 (nibbles average 7.5 - 8): a shared
+ * direction that, compounded over the layers, makes deep models emit nearly
+ * the same logits for any input; mode 1 models respond to their input.
+ * Norm weights are fp32 1 + N(0, norm_sigma); q/k/v biases (when asked for)
+ * are N(0, 0.1).
  * The bytes depend only on the spec (seed included), not on n_threads.
  */
 #ifndef SS_SYNTH_H
@@ -42,6 +50,8 @@ typedef struct {
     int32_t qkv_bias;     /* blk.N.attn_q/k/v.bias: 0 none, 1 F32, 2 F16; values N(0, 0.1) */
     int32_t alignment;    /* general.alignment and the data/tensor alignment in bytes (a power
                            * of two); 0 = 32, the only alignment the reference reads */
+    int32_t scale_mode;   /* block scale distribution, see above: 0 |N(0, scale_sigma)|,
+                           * 1 signed fan-in scaled */
 } ss_synth_spec_t;
 
 /* Returns 0, or a negative ss_error_t value (-5 bad spec, -1 cannot write). */

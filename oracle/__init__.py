@@ -58,6 +58,7 @@ def lib():
         "orc_model_theta": (C.c_float, [_vp]),
         "orc_forward": (_fp, [_vp, _i32, _i32]),
         "orc_prefill": (_fp, [_vp, _vp, _i32, _i32]),
+        "orc_prefill_serial": (_fp, [_vp, _vp, _i32, _i32]),
         "orc_embed": (_i32, [_vp, _vp, _i32, _vp]),
         "orc_reset": (None, [_vp]),
         "orc_kv_write": (_i32, [_vp, _i32, _i32, _vp, _vp]),
@@ -208,6 +209,13 @@ class Model:
             raise RuntimeError("oracle prefill failed")
         return np.ctypeslib.as_array(p, (self.vocab,)).copy()
 
+    def prefill_serial(self, tokens, start_pos=0):
+        t = np.ascontiguousarray(tokens, np.int32)
+        p = lib().orc_prefill_serial(self.h, _ptr(t), t.size, start_pos)
+        if not p:
+            raise RuntimeError("oracle prefill failed")
+        return np.ctypeslib.as_array(p, (self.vocab,)).copy()
+
     def embed(self, tokens):
         t = np.ascontiguousarray(tokens, np.int32)
         out = np.zeros(self.d, np.float32)
@@ -223,6 +231,15 @@ class Model:
         v = np.ascontiguousarray(v_f16, np.uint16)
         if lib().orc_kv_write(self.h, layer, pos, _ptr(k), _ptr(v)) != 0:
             raise RuntimeError("oracle kv_write failed")
+
+    def kv_write_rows(self, layer, pos0, k_f16, v_f16):
+        """Rows pos0 .. pos0 + n - 1 of one layer from [n][kv_dim] binary16 arrays."""
+        k = np.ascontiguousarray(k_f16, np.uint16)
+        v = np.ascontiguousarray(v_f16, np.uint16)
+        kvd = k.shape[1]
+        for i in range(k.shape[0]):
+            if lib().orc_kv_write(self.h, layer, pos0 + i, _ptr(k[i]), _ptr(v[i])) != 0:
+                raise RuntimeError("oracle kv_write failed")
 
     def greedy(self, prompt, n_steps):
         """Prefill then n_steps greedy tokens; returns (first, [tokens])."""

@@ -507,6 +507,101 @@ void orc_dequant_matvec(float *out, const void *w, const float *x, int32_t rows,
     free(j.tmp);
 }
 
+/* Four dot products sharing a: each in exactly orc_dot's order (eight
+ * strided partial sums folded pairwise, then the tail), so every result is
+ * bit-identical to orc_dot(a, bk, n). */
+/* eight fp32 lanes: lane j is orc_dot's partial sum j */
+typedef float orc_v8 __attribute__((vector_size(32)));
+
+static inline orc_v8 ld8(const float *p) {
+    orc_v8 v;
+    memcpy(&v, p, sizeof v);
+    return v;
+}
+
+static inline float fold8(orc_v8 c) {
+    return ((c[0] + c[4]) + (c[1] + c[5])) + ((c[2] + c[6]) + (c[3] + c[7]));
+}
+
+static void dot4(const float *a, const float *b0, const float *b1, const float *b2, const float *b3,
+                 int32_t n, float *out) {
+    orc_v8 c0 = {0}, c1 = {0}, c2 = {0}, c3 = {0};
+    int32_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+        const orc_v8 av = ld8(a + i);
+        c0 += av * ld8(b0 + i);
+        c1 += av * ld8(b1 + i);
+        c2 += av * ld8(b2 + i);
+        c3 += av * ld8(b3 + i);
+    }
+    float s0 = fold8(c0), s1 = fold8(c1), s2 = fold8(c2), s3 = fold8(c3);
+    for (; i < n; i++) {
+        s0 += a[i] * b0[i];
+        s1 += a[i] * b1[i];
+        s2 += a[i] * b2[i];
+        s3 += a[i] * b3[i];
+    }
+    out[0] = s0;
+    out[1] = s1;
+    out[2] = s2;
+    out[3] = s3;
+}
+
+/* out[t*ldo + r] = W x_t for n vectors x_t = x + t*ldx: the per-token matvec
+ * of orc_dequant_matvec (same row chunks, same dequantisation, same dot
+ * order), with each row dequantised once for all n vectors. Serves the
+ * layer-major prompt (layer_scheduler.c:721-755), where every token of a
+ * layer meets the same matrices. */
+typedef struct {
+    float *out;
+    const uint8_t *w;
+    const float *x;
+    float *tmp;
+    int32_t rows, cols, type, n, ldx, ldo, rows_per_chunk;
+    size_t row_bytes;
+} mm_job_t;
+
+static void mm_chunk(void *arg, int32_t chunk) {
+    mm_job_t *j = (mm_job_t *)arg;
+    int32_t r0 = chunk * j->rows_per_chunk;
+    int32_t r1 = r0 + j->rows_per_chunk;
+    if (r1 > j->rows) r1 = j->rows;
+    const size_t cols = (size_t)j->cols;
+    float *tmp = j->tmp + (size_t)chunk * j->rows_per_chunk * cols;
+    /* rows in blocks of 4: the block's dequantised rows stay in cache while
+     * every token's x meets them (a*b and b*a round alike, so dot4 over
+     * (x, four rows) gives each row's orc_dot(row, x) exactly) */
+    for (int32_t r = r0; r < r1; r++) orc_dequantize(j->w + (size_t)r * j->row_bytes, tmp + (r - r0) * cols, j->cols, j->type);
+    int32_t r = r0;
+    for (; r + 4 <= r1; r += 4) {
+        const float *w0 = tmp + (r - r0) * cols;
+        for (int32_t t = 0; t < j->n; t++) {
+            float o[4];
+            dot4(j->x + (size_t)t * j->ldx, w0, w0 + cols, w0 + 2 * cols, w0 + 3 * cols, j->cols, o);
+            for (int k = 0; k < 4; k++) j->out[(size_t)t * j->ldo + r + k] = o[k];
+        }
+    }
+    for (; r < r1; r++)
+        for (int32_t t = 0; t < j->n; t++)
+            j->out[(size_t)t * j->ldo + r] = orc_dot(tmp + (r - r0) * cols, j->x + (size_t)t * j->ldx, j->cols);
+}
+
+static void dequant_matmul(float *out, int32_t ldo, const void *w, const float *x, int32_t ldx, int32_t n,
+                           int32_t rows, int32_t cols, int32_t type) {
+    size_t rb = orc_row_bytes(cols, type);
+    if (rb == 0 || rows <= 0 || n <= 0) return;
+    /* chunks of a few rows (a multiple of 4, about 256 KB of dequantised
+     * weights) handed to the threads dynamically */
+    int32_t per = (int32_t)((256u << 10) / ((size_t)cols * 4)) & ~3;
+    if (per < 4) per = 4;
+    mm_job_t j = {out, (const uint8_t *)w, x, NULL, rows, cols, type, n, ldx, ldo, per, rb};
+    int32_t nchunk = (rows + per - 1) / per;
+    j.tmp = (float *)malloc((size_t)nchunk * per * cols * sizeof(float));
+    if (!j.tmp) abort();
+    pool_run(mm_chunk, &j, nchunk);
+    free(j.tmp);
+}
+
 /* ------------------------------------------------------------------------ */
 /* GGUF parse: gguf_loader.c:22-62, 174-206, 210-485                         */
 /* ------------------------------------------------------------------------ */
@@ -937,29 +1032,35 @@ typedef struct {
     float scale;
 } attn_job_t;
 
-/* layer_scheduler.c:424-468, one query head per task */
-static void attn_head(void *arg, int32_t h) {
-    attn_job_t *j = (attn_job_t *)arg;
-    orc_model_t *m = j->m;
+/* layer_scheduler.c:424-468 for one query head: scores over positions
+ * 0..seq_len-1 of KV head kvh, softmax, weighted sum of values into dst. */
+static void attend(const orc_model_t *m, int32_t layer, int32_t seq_len, int32_t kvh, float scale,
+                   const float *q, float *dst) {
     int32_t hd = m->hd;
-    const float *q = m->q + (size_t)h * hd;
-    int32_t kvh = h / j->heads_per_kv;
-    float *scores = (float *)malloc((size_t)j->seq_len * sizeof(float));
+    float *scores = (float *)malloc((size_t)seq_len * sizeof(float));
     float *tmp = (float *)malloc((size_t)hd * sizeof(float));
-    for (int32_t t = 0; t < j->seq_len; t++) {
-        kv_read(m, 0, j->layer, t, kvh, tmp);
-        scores[t] = orc_dot(q, tmp, hd) * j->scale;
+    if (!scores || !tmp) abort();
+    for (int32_t t = 0; t < seq_len; t++) {
+        kv_read(m, 0, layer, t, kvh, tmp);
+        scores[t] = orc_dot(q, tmp, hd) * scale;
     }
-    orc_softmax(scores, j->seq_len);
-    float *dst = m->attn_out + (size_t)h * hd;
+    orc_softmax(scores, seq_len);
     memset(dst, 0, (size_t)hd * sizeof(float));
-    for (int32_t t = 0; t < j->seq_len; t++) {
-        kv_read(m, 1, j->layer, t, kvh, tmp);
+    for (int32_t t = 0; t < seq_len; t++) {
+        kv_read(m, 1, layer, t, kvh, tmp);
         float w = scores[t];
         for (int32_t i = 0; i < hd; i++) dst[i] = w * tmp[i] + dst[i];
     }
     free(tmp);
     free(scores);
+}
+
+/* one query head per task */
+static void attn_head(void *arg, int32_t h) {
+    attn_job_t *j = (attn_job_t *)arg;
+    orc_model_t *m = j->m;
+    attend(m, j->layer, j->seq_len, h / j->heads_per_kv, j->scale, m->q + (size_t)h * m->hd,
+           m->attn_out + (size_t)h * m->hd);
 }
 
 /* layer_scheduler.c:291-567 (llama branch) */
@@ -1015,6 +1116,121 @@ static void process_layer(orc_model_t *m, int32_t l, int32_t pos) {
     for (int32_t i = 0; i < d; i++) m->hidden[i] = m->hidden[i] + m->residual[i];   /* :566 */
 }
 
+/* process_layer for tokens start..start+n-1 of one layer at once (the
+ * layer-major order of layer_scheduler.c:721-755). Every token goes through
+ * exactly process_layer's arithmetic; the matrices are applied to all n
+ * tokens by dequant_matmul (each row dequantised once, the same dot order),
+ * and all n tokens' K/V are stored before any attends, which reads only
+ * positions up to its own: every output is bit-identical to n calls of
+ * process_layer. X is [n][d], in place. */
+/* attend() over fp32 rows: K row t at K + t * ld (the cache widened once
+ * per layer; kv_read's widening is exact or one fp32 product, so the rows
+ * hold the values attend() reads) */
+static void attend_rows(const float *K, const float *V, size_t ld, int32_t seq_len, int32_t hd, float scale,
+                        const float *q, float *dst) {
+    float *scores = (float *)malloc((size_t)seq_len * sizeof(float));
+    if (!scores) abort();
+    for (int32_t t = 0; t < seq_len; t++) scores[t] = orc_dot(q, K + t * ld, hd) * scale;
+    orc_softmax(scores, seq_len);
+    memset(dst, 0, (size_t)hd * sizeof(float));
+    for (int32_t t = 0; t < seq_len; t++) {
+        const float w = scores[t], *v = V + t * ld;
+        for (int32_t i = 0; i < hd; i++) dst[i] = w * v[i] + dst[i];
+    }
+    free(scores);
+}
+
+typedef struct {
+    const orc_model_t *m;
+    int32_t start, heads_per_kv;
+    float scale;
+    const float *K, *V;   /* the layer's cache rows 0..start+n-1, widened, [pos][kv_dim] */
+    const float *q;       /* [n][qdim] */
+    float *out;           /* [n][qdim] */
+} attn_batch_job_t;
+
+static void attn_batch_task(void *arg, int32_t task) {
+    attn_batch_job_t *j = (attn_batch_job_t *)arg;
+    const orc_model_t *m = j->m;
+    int32_t H = (int32_t)m->n_heads, i = task / H, h = task % H, hd = m->hd;
+    size_t qdim = (size_t)H * hd, koff = (size_t)(h / j->heads_per_kv) * hd;
+    attend_rows(j->K + koff, j->V + koff, (size_t)m->kv_dim, j->start + i + 1, hd, j->scale,
+                j->q + i * qdim + (size_t)h * hd, j->out + i * qdim + (size_t)h * hd);
+}
+
+static void layer_batch(orc_model_t *m, int32_t l, int32_t start, int32_t n, float *X) {
+    const orc_layer_t *ly = &m->layers[l];
+    const int32_t d = (int32_t)m->d, ffn = (int32_t)m->ffn, qdim = (int32_t)m->n_heads * m->hd;
+    const int32_t kvd = m->kv_dim, nqkv = qdim + 2 * kvd;
+    float *res = (float *)malloc((size_t)n * d * 4), *xn = (float *)malloc((size_t)n * d * 4);
+    float *qkv = (float *)malloc((size_t)n * nqkv * 4), *att = (float *)malloc((size_t)n * qdim * 4);
+    float *gu = (float *)malloc((size_t)n * 2 * ffn * 4);
+    if (!res || !xn || !qkv || !att || !gu) abort();
+    for (int32_t i = 0; i < n; i++) {
+        memcpy(res + (size_t)i * d, X + (size_t)i * d, (size_t)d * 4);
+        orc_rmsnorm(xn + (size_t)i * d, res + (size_t)i * d, (const float *)tdata(m, ly->attn_norm), d, m->eps);
+    }
+    /* [q | k | v] per token, from one fused product or three */
+    if (ly->wqkv) {
+        dequant_matmul(qkv, nqkv, tdata(m, ly->wqkv), xn, d, n, nqkv, d, ly->wqkv->type);
+    } else {
+        dequant_matmul(qkv, nqkv, tdata(m, ly->wq), xn, d, n, qdim, d, ly->wq->type);
+        dequant_matmul(qkv + qdim, nqkv, tdata(m, ly->wk), xn, d, n, kvd, d, ly->wk->type);
+        dequant_matmul(qkv + qdim + kvd, nqkv, tdata(m, ly->wv), xn, d, n, kvd, d, ly->wv->type);
+    }
+    float *q = (float *)malloc((size_t)n * qdim * 4);
+    if (!q) abort();
+    for (int32_t i = 0; i < n; i++) {
+        float *qi = qkv + (size_t)i * nqkv, *ki = qi + qdim, *vi = ki + kvd;
+        add_bias(m, qi, ly->bq, qdim);
+        add_bias(m, ki, ly->bk, kvd);
+        add_bias(m, vi, ly->bv, kvd);
+        orc_rope(qi, ki, (int32_t)m->n_heads, (int32_t)m->n_kv_heads, m->hd, m->rope_dim, start + i, m->theta,
+                 m->neox);
+        kv_store(m, l, start + i, ki, vi);
+        memcpy(q + (size_t)i * qdim, qi, (size_t)qdim * 4);
+    }
+    const int32_t npos = start + n;
+    float *K = (float *)malloc((size_t)npos * kvd * 4), *V = (float *)malloc((size_t)npos * kvd * 4);
+    if (!K || !V) abort();
+    for (int32_t t = 0; t < npos; t++)
+        for (int32_t g = 0; g < (int32_t)m->n_kv_heads; g++) {
+            kv_read(m, 0, l, t, g, K + (size_t)t * kvd + (size_t)g * m->hd);
+            kv_read(m, 1, l, t, g, V + (size_t)t * kvd + (size_t)g * m->hd);
+        }
+    attn_batch_job_t aj = {m, start, (int32_t)(m->n_heads / m->n_kv_heads), 1.0f / sqrtf((float)m->hd), K, V, q, att};
+    pool_run(attn_batch_task, &aj, n * (int32_t)m->n_heads);
+    free(V);
+    free(K);
+    dequant_matmul(X, d, tdata(m, ly->wo), att, qdim, n, (int32_t)ly->wo->dims[1], (int32_t)ly->wo->dims[0],
+                   ly->wo->type);
+    for (size_t e = 0; e < (size_t)n * d; e++) X[e] = X[e] + res[e];                 /* :484 */
+    for (int32_t i = 0; i < n; i++) {
+        memcpy(res + (size_t)i * d, X + (size_t)i * d, (size_t)d * 4);
+        orc_rmsnorm(xn + (size_t)i * d, res + (size_t)i * d, (const float *)tdata(m, ly->ffn_norm), d, m->eps);
+    }
+    /* gate | up per token: two products, or the fused [gate; up] (:518-524) */
+    if (ly->wg) {
+        dequant_matmul(gu, 2 * ffn, tdata(m, ly->wg), xn, d, n, ffn, d, ly->wg->type);
+        dequant_matmul(gu + ffn, 2 * ffn, tdata(m, ly->wu), xn, d, n, ffn, d, ly->wu->type);
+    } else {
+        dequant_matmul(gu, 2 * ffn, tdata(m, ly->wu), xn, d, n, 2 * ffn, d, ly->wu->type);
+    }
+    for (int32_t i = 0; i < n; i++) {
+        float *g = gu + (size_t)i * 2 * ffn, *u = g + ffn;
+        for (int32_t k = 0; k < ffn; k++) u[k] = orc_silu_mul(g[k], u[k]);
+    }
+    dequant_matmul(X, d, tdata(m, ly->wd), gu + ffn, 2 * ffn, n, (int32_t)ly->wd->dims[1], (int32_t)ly->wd->dims[0],
+                   ly->wd->type);
+    for (size_t e = 0; e < (size_t)n * d; e++) X[e] = X[e] + res[e];                 /* :566 */
+    free(q);
+    free(gu);
+    free(att);
+    free(qkv);
+    free(xn);
+    free(res);
+}
+
 static void embed_row(orc_model_t *m, int32_t token, float *dst) {   /* :584-595 */
     size_t rb = orc_row_bytes((int32_t)m->d, m->embd->type);
     const uint8_t *row = (const uint8_t *)tdata(m, m->embd) + (size_t)token * rb;
@@ -1036,8 +1252,10 @@ const float *orc_forward(orc_model_t *m, int32_t token, int32_t pos) {
     return m->logits;
 }
 
-const float *orc_prefill(orc_model_t *m, const int32_t *tokens, int32_t n, int32_t start_pos) {
-    if (!m || n <= 0 || start_pos < 0 || start_pos + n > m->max_seq) return NULL;
+/* The prompt's embeddings, layer-major through the layers (:681-803). The
+ * tokens of a layer go through layer_batch; orc_prefill_serial is the
+ * literal token-by-token loop, kept to show the two agree bit for bit. */
+static float *prefill_embed(orc_model_t *m, const int32_t *tokens, int32_t n) {
     int32_t d = (int32_t)m->d;
     float *batch = (float *)malloc((size_t)n * d * 4);
     if (!batch) return NULL;
@@ -1045,6 +1263,36 @@ const float *orc_prefill(orc_model_t *m, const int32_t *tokens, int32_t n, int32
         if (tokens[i] < 0 || (uint64_t)tokens[i] >= m->embd->dims[1]) { free(batch); return NULL; }
         embed_row(m, tokens[i], batch + (size_t)i * d);
     }
+    return batch;
+}
+
+/* at most this many tokens per layer_batch call (bounds its buffers) */
+#define ORC_BATCH_TOKENS 256
+
+static void layers_batched(orc_model_t *m, int32_t start_pos, int32_t n, float *batch) {
+    for (int32_t l = 0; l < (int32_t)m->n_layers; l++)
+        for (int32_t i0 = 0; i0 < n; i0 += ORC_BATCH_TOKENS) {
+            int32_t nb = n - i0 < ORC_BATCH_TOKENS ? n - i0 : ORC_BATCH_TOKENS;
+            layer_batch(m, l, start_pos + i0, nb, batch + (size_t)i0 * m->d);
+        }
+}
+
+const float *orc_prefill(orc_model_t *m, const int32_t *tokens, int32_t n, int32_t start_pos) {
+    if (!m || n <= 0 || start_pos < 0 || start_pos + n > m->max_seq) return NULL;
+    float *batch = prefill_embed(m, tokens, n);
+    if (!batch) return NULL;
+    layers_batched(m, start_pos, n, batch);
+    memcpy(m->hidden, batch + (size_t)(n - 1) * m->d, (size_t)m->d * 4);
+    free(batch);
+    head(m);
+    return m->logits;
+}
+
+const float *orc_prefill_serial(orc_model_t *m, const int32_t *tokens, int32_t n, int32_t start_pos) {
+    if (!m || n <= 0 || start_pos < 0 || start_pos + n > m->max_seq) return NULL;
+    int32_t d = (int32_t)m->d;
+    float *batch = prefill_embed(m, tokens, n);
+    if (!batch) return NULL;
     for (int32_t l = 0; l < (int32_t)m->n_layers; l++)               /* layer-major, :721-755 */
         for (int32_t i = 0; i < n; i++) {
             memcpy(m->hidden, batch + (size_t)i * d, (size_t)d * 4);
@@ -1062,18 +1310,9 @@ const float *orc_prefill(orc_model_t *m, const int32_t *tokens, int32_t n, int32
 int32_t orc_embed(orc_model_t *m, const int32_t *tokens, int32_t n, float *out) {
     if (!m || n <= 0 || n > m->max_seq) return -1;
     int32_t d = (int32_t)m->d;
-    float *batch = (float *)malloc((size_t)n * d * 4);
+    float *batch = prefill_embed(m, tokens, n);
     if (!batch) return -1;
-    for (int32_t i = 0; i < n; i++) {
-        if (tokens[i] < 0 || (uint64_t)tokens[i] >= m->embd->dims[1]) { free(batch); return -1; }
-        embed_row(m, tokens[i], batch + (size_t)i * d);
-    }
-    for (int32_t l = 0; l < (int32_t)m->n_layers; l++)
-        for (int32_t i = 0; i < n; i++) {
-            memcpy(m->hidden, batch + (size_t)i * d, (size_t)d * 4);
-            process_layer(m, l, i);
-            memcpy(batch + (size_t)i * d, m->hidden, (size_t)d * 4);
-        }
+    layers_batched(m, 0, n, batch);
     if (m->out_norm)
         for (int32_t i = 0; i < n; i++)
             orc_rmsnorm(batch + (size_t)i * d, batch + (size_t)i * d,

@@ -58,6 +58,8 @@ float        orc_model_eps(const orc_model_t *m);
 float        orc_model_theta(const orc_model_t *m);
 const float *orc_forward(orc_model_t *m, int32_t token, int32_t pos);    /* layer_scheduler.c:571-679 */
 const float *orc_prefill(orc_model_t *m, const int32_t *tokens, int32_t n, int32_t start_pos); /* :681-803 */
+/* the same, token by token as the reference loops (bit-identical to orc_prefill) */
+const float *orc_prefill_serial(orc_model_t *m, const int32_t *tokens, int32_t n, int32_t start_pos);
 int32_t      orc_embed(orc_model_t *m, const int32_t *tokens, int32_t n, float *out); /* :805-915 */
 void         orc_reset(orc_model_t *m);                                  /* :917-936 */
 int32_t      orc_kv_write(orc_model_t *m, int32_t layer, int32_t pos,

@@ -1833,12 +1833,19 @@ int32_t ss_hip_kv_write(ss_hip_model_t* m, int32_t layer, int32_t pos0, int32_t 
   char* kc = static_cast<char*>(m->kc) + (size_t)layer * m->kv_layer_elems * esz;
   char* vc = static_cast<char*>(m->vc) + (size_t)layer * m->kv_layer_elems * esz;
   if (m->kv_type == 0) {
-    for (int g = 0; g < m->KVH; g++) {
-      const size_t dst = ((size_t)g * m->max_seq + pos0) * m->hd * 2;
-      HIP_TRY(hipMemcpy2D(kc + dst, (size_t)m->hd * 2, k + (size_t)g * m->hd, (size_t)m->kvdim * 2,
-                          (size_t)m->hd * 2, n_pos, hipMemcpyHostToDevice));
-      HIP_TRY(hipMemcpy2D(vc + dst, (size_t)m->hd * 2, v + (size_t)g * m->hd, (size_t)m->kvdim * 2,
-                          (size_t)m->hd * 2, n_pos, hipMemcpyHostToDevice));
+    // the rows of one KV head are contiguous in the cache: gather them on the
+    // host and copy each head's slab at once
+    std::vector<uint16_t> slab((size_t)n_pos * m->hd);
+    for (int which = 0; which < 2; which++) {
+      const uint16_t* src = which ? v : k;
+      char* cache = which ? vc : kc;
+      for (int g = 0; g < m->KVH; g++) {
+        for (int p = 0; p < n_pos; p++)
+          memcpy(slab.data() + (size_t)p * m->hd, src + (size_t)p * m->kvdim + (size_t)g * m->hd,
+                 (size_t)m->hd * 2);
+        HIP_TRY(hipMemcpy(cache + ((size_t)g * m->max_seq + pos0) * m->hd * 2, slab.data(),
+                          (size_t)n_pos * m->hd * 2, hipMemcpyHostToDevice));
+      }
     }
     return 0;
   }

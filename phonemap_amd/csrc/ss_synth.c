@@ -134,6 +134,7 @@ typedef struct {
     int fd;
     uint64_t data_off, seed;
     float scale_sigma, norm_sigma;
+    int scale_mode;
     syn_tensor_t *t;
     int nt;
     /* work items: (tensor, chunk) flattened */
@@ -172,11 +173,21 @@ static void gen_item(job_t *j, uint64_t it, uint8_t *buf) {
         uint64_t nb = tensor_blocks(t), b0 = chunk * CHUNK_BLOCKS;
         uint64_t b1 = b0 + CHUNK_BLOCKS < nb ? b0 + CHUNK_BLOCKS : nb;
         size_t bb = t->type == T_Q4_0 ? 18 : 34;
-        /* int8 codes spread 16 times as wide as nibbles: same weight spread */
-        const double sigma = t->type == T_Q4_0 ? j->scale_sigma : j->scale_sigma / 16.0;
+        /* mode 0: int8 codes spread 16 times as wide as nibbles, so both
+         * types give weights of the same spread. mode 1: signed d with the
+         * weights' standard deviation 1/sqrt(cols), the RMS of the codes
+         * being sqrt(21.5) for Q4_0 (nibble - 8) and sqrt(127*128/3) for
+         * uniform int8 in [-127, 127]. */
+        double sigma;
+        if (j->scale_mode == 1)
+            sigma = 1.0 / ((t->type == T_Q4_0 ? sqrt(21.5) : sqrt(127.0 * 128.0 / 3.0)) *
+                           sqrt((double)t->dims[0]));
+        else
+            sigma = t->type == T_Q4_0 ? j->scale_sigma : j->scale_sigma / 16.0;
         for (uint64_t b = b0; b < b1; b++) {
             uint8_t *p = buf + (b - b0) * bb;
-            uint16_t d = to_f16((float)fabs(sigma * xo_normal(&x)));
+            const double dv = sigma * xo_normal(&x);
+            uint16_t d = to_f16((float)(j->scale_mode == 1 ? dv : fabs(dv)));
             memcpy(p, &d, 2);
             if (t->type == T_Q4_0) {
                 uint64_t r0 = xo_next(&x), r1 = xo_next(&x);
@@ -222,7 +233,8 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
         (s->layer_type != T_Q4_0 && s->layer_type != T_Q8_0) ||
         (s->embd_type != T_Q4_0 && s->embd_type != T_Q8_0) ||
         (s->out_type != -1 && s->out_type != T_Q4_0 && s->out_type != T_Q8_0) ||
-        s->arch < 0 || s->arch > 1 || s->qkv_bias < 0 || s->qkv_bias > 2)
+        s->arch < 0 || s->arch > 1 || s->qkv_bias < 0 || s->qkv_bias > 2 || s->scale_mode < 0 ||
+        s->scale_mode > 1)
         return -5;
     const char *arch = s->arch == 1 ? "qwen2" : "llama";
     const uint64_t align = s->alignment > 0 ? (uint64_t)s->alignment : 32;
@@ -357,6 +369,7 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
     j.seed = s->seed;
     j.scale_sigma = s->scale_sigma > 0 ? s->scale_sigma : 0.02f;
     j.norm_sigma = s->norm_sigma > 0 ? s->norm_sigma : 0.01f;
+    j.scale_mode = s->scale_mode;
     j.t = t;
     j.nt = nt;
     uint64_t items = 0;

@@ -40,8 +40,6 @@ TINY = dict(n_layers=2, hidden=256, n_heads=4, n_kv_heads=2, head_dim=64, ffn=51
 TINY_Q8 = dict(TINY, layer_type=8, embd_type=8, out_type=-1, seed=2)        # tied embeddings
 GQA8 = dict(n_layers=3, hidden=1024, n_heads=16, n_kv_heads=2, head_dim=64, ffn=2816, vocab=3000,
             context_length=256, seed=3, embd_type=8, out_type=8)
-TINYLLAMA = dict(n_layers=22, hidden=2048, n_heads=32, n_kv_heads=4, head_dim=64, ffn=5632, vocab=32000,
-                 context_length=2048, seed=1001)
 
 
 TINY7 = dict(TINY, n_layers=7, seed=4)    # more layers than streaming slots, not a multiple of them
@@ -173,19 +171,6 @@ def test_streaming_matches_resident(spec, kv):
         tok = oracle.argmax(om.forward(tok, pos))
         pos += 1
     om.close()
-
-
-def test_tinyllama_shape_128_steps():
-    """TinyLlama-1.1B shape, 32-token random prompt, 128 greedy steps (ctx 160)."""
-    path = _model_file("tinyllama", **TINYLLAMA)
-    rng = np.random.default_rng(2024)
-    prompt = rng.integers(3, 32000, 32).tolist()
-    with api.Model(path, max_context=192) as m:
-        got = m.greedy(prompt, 128)
-    om = oracle.Model(path, 192, "f16")
-    want = om.greedy(prompt, 128)
-    om.close()
-    assert got == want
 
 
 def test_kv_injection_matches_oracle():
