@@ -125,8 +125,23 @@ def cpu_baseline(path, spec, prompt_len, budget_s=15.0, max_steps=160):
     threads = oracle.lib().orc_get_threads()
     om.close()
     return {"value": n / dt, "unit": "tok/s", "cores": int(threads), "kind": "port",
+            "cpu": host_cpu(),
             "sample": "%d decode steps at context %d (KV pre-filled), same GGUF, %d threads, %.1f s"
                       % (n, prompt_len + 1, threads, dt)}
+
+
+def host_cpu():
+    """The host CPU model and the CPUs this process may use."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return "%s, %d CPUs in the affinity mask of %d online" % (model, len(os.sched_getaffinity(0)),
+                                                             os.cpu_count() or 0)
 
 
 def copy_calibration(mib):
@@ -373,6 +388,7 @@ def bench_matvec(args):
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": "k_gemv Q4_0",
                      "avg_us": round(us, 3), "bytes_per_launch": alg},
         "cpu_baseline": {"value": round(alg / cpu_s / 1e9, 2), "unit": "GB/s", "cores": int(threads),
+                         "cpu": host_cpu(),
                          "kind": "port", "sample": "%d oracle GEMVs of the same matrix in %.1f s" % (n, n * cpu_s)},
     }), flush=True)
 

@@ -166,8 +166,12 @@ int32_t ss_hip_embed_row(ss_hip_ctx_t *ctx, float *out_dev, const void *table_de
 /* ---- Metal-shaped plug on host pointers (metal_backend.h:27-70) ----
  * W is a host pointer in GGUF block layout (e.g. into the GGUF mmap); it is
  * packed and uploaded the first time it is seen and kept, keyed by pointer
- * (the zero-copy registry of metal_backend.m:190-235). Returns false on any
- * failure, like the Metal calls. */
+ * (the zero-copy registry of metal_backend.m:190-235).
+ * ss_hip_matvec_host returns the Metal calls' bool, NOT the 0-on-success
+ * convention of the rest of this header: nonzero (true) when out holds
+ * W vec, 0 (false) on any failure, after which the caller computes on the
+ * CPU (gpu_success in layer_scheduler.c:251-263). ss_hip_should_use_gpu is
+ * metal_backend.m:336-340's size test (true when rows * cols > 1024). */
 int32_t ss_hip_matvec_host(ss_hip_ctx_t *ctx, float *out, const void *mat, const float *vec,
                            int32_t rows, int32_t cols, int32_t ggml_type);
 int32_t ss_hip_should_use_gpu(int32_t rows, int32_t cols);

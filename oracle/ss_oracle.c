@@ -38,6 +38,7 @@
 #include <float.h>
 #include <math.h>
 #include <pthread.h>
+#include <sched.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -424,7 +425,11 @@ void orc_set_threads(int32_t n) {
     if (n <= 0) {
         const char *env = getenv("OMP_NUM_THREADS");
         n = env ? atoi(env) : 0;
-        if (n <= 0) n = (int32_t)sysconf(_SC_NPROCESSORS_ONLN);
+        if (n <= 0) {   /* the CPUs this process may run on */
+            cpu_set_t set;
+            n = sched_getaffinity(0, sizeof set, &set) == 0 ? CPU_COUNT(&set)
+                                                           : (int32_t)sysconf(_SC_NPROCESSORS_ONLN);
+        }
     }
     if (n < 1) n = 1;
     if (n > ORC_MAX_THREADS) n = ORC_MAX_THREADS;

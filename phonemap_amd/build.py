@@ -54,9 +54,6 @@ def build(verbose=False):
     tmp = LIB + ".tmp"
     _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs + ["-lpthread", "-lm"])
     os.replace(tmp, LIB)
-    # the CPU oracle (test infrastructure) and, when the reference tree is
-    # present, oracle/_ref from the reference's own sources
-    _run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "all"])
     return LIB
 
 

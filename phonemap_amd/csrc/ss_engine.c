@@ -603,6 +603,11 @@ ss_error_t ss_generate(ss_model_t *m, const char *prompt, const ss_generate_para
         fprintf(stderr, "Decode : %d tokens in %.2f seconds (%.2f tok/s)\n", generated, t3 - t2, generated / (t3 - t2));
     fprintf(stderr, "===================================\n\n");
     if (rc == SS_ERROR_CANCELLED) return set_err(SS_ERROR_CANCELLED);
+    /* A failed step (e.g. a persistent launch abandoned at its wait bound)
+     * ends the loop with the text so far delivered; the reference's loop
+     * (engine.c:283-290) stops the same way but reports success, which here
+     * would hide a truncated output. */
+    if (rc != 0) return set_err(SS_ERROR_BACKEND);
     return set_err(SS_OK);
 }
 

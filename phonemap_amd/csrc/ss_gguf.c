@@ -214,6 +214,7 @@ ss_gguf_file_t *ss_gguf_open(const char *path) {
     f->n_tensors = u64(&r);
     f->n_kv = u64(&r);
     uint32_t n_tok_strings = 0;
+    uint64_t n_scores = 0;
     /* Data alignment: general.alignment when present (the GGUF format's rule;
      * a power of two), else 32. The reference always uses 32
      * (gguf_loader.c:426), which misplaces the data of any other alignment. */
@@ -275,6 +276,7 @@ ss_gguf_file_t *ss_gguf_open(const char *path) {
                 f->vocab_scores = (float *)malloc(n * sizeof(float));
                 if (!f->vocab_scores) { r.bad = 1; break; }
                 for (uint64_t v = 0; v < n; v++) f->vocab_scores[v] = f32(&r);
+                n_scores = n;
             } else {
                 for (uint64_t v = 0; v < n && !r.bad; v++) skip_value(&r, at, 1);
             }
@@ -285,8 +287,13 @@ ss_gguf_file_t *ss_gguf_open(const char *path) {
         }
     }
     if (r.bad) { gerr("metadata truncated or malformed"); ss_gguf_close(f); return NULL; }
-    /* a vocab without matching scores cannot be used as scores */
-    if (f->vocab_scores && !f->vocab) { free(f->vocab_scores); f->vocab_scores = NULL; }
+    /* scores are used only with a vocab of exactly as many tokens; otherwise
+     * the tokenizer ranks merges by string length (the reference reads
+     * scores[i] for every token regardless, past the end of a short array) */
+    if (f->vocab_scores && (!f->vocab || n_scores != n_tok_strings)) {
+        free(f->vocab_scores);
+        f->vocab_scores = NULL;
+    }
     if (f->vocab && f->vocab_size != n_tok_strings) f->vocab_size = n_tok_strings;
 
     if (f->rms_norm_eps == 0.0f) f->rms_norm_eps = 1e-5f;            /* gguf_loader.c:370-379 */

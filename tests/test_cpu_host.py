@@ -377,3 +377,40 @@ def test_host_sample_equals_oracle():
         got = L.ss_sample(x.ctypes.data_as(C.POINTER(C.c_float)), V, C.c_float(T), C.c_float(top_p), top_k,
                           C.byref(st))
         assert (got, st.value) == (want, want_st), trial
+
+
+def _gguf_bytes(kvs):
+    """A GGUF v3 file with the given metadata and no tensors."""
+    def s(x):
+        b = x.encode()
+        return struct.pack("<Q", len(b)) + b
+    out = b"GGUF" + struct.pack("<IQQ", 3, 0, len(kvs))
+    for k, (vt, v) in kvs.items():
+        out += s(k) + struct.pack("<I", vt)
+        if vt == 8:
+            out += s(v)
+        elif vt == 9:
+            et, items = v
+            out += struct.pack("<IQ", et, len(items))
+            for it in items:
+                out += s(it) if et == 8 else struct.pack(GGUF_SCALAR[et], it)
+        else:
+            out += struct.pack(GGUF_SCALAR[vt], v)
+    return out + b"\0" * ((-len(out)) % 32)
+
+
+@pytest.mark.parametrize("n_scores", [3, 5, 7])
+def test_gguf_scores_used_only_when_they_match_the_vocab(tmp_path, n_scores):
+    """tokenizer.ggml.scores shorter or longer than tokenizer.ggml.tokens is
+    dropped (merges then rank by string length) instead of being read past
+    its end."""
+    path = str(tmp_path / "v.gguf")
+    toks = ["<unk>", "<s>", "</s>", "a", "b"]
+    open(path, "wb").write(_gguf_bytes({"general.architecture": (8, "llama"),
+                                        "tokenizer.ggml.tokens": (9, (8, toks)),
+                                        "tokenizer.ggml.scores": (9, (6, [0.5] * n_scores))}))
+    lib, f = gguf_open(path)
+    assert f, lib.ss_gguf_error()
+    assert f.contents.vocab_size == 5
+    assert bool(f.contents.vocab_scores) == (n_scores == 5)
+    lib.ss_gguf_close(f)

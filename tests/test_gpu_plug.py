@@ -1,0 +1,44 @@
+"""The per-matvec backend plug from a C caller: tests/c/plug_snippet.c is
+the INTEGRATION.md snippet inside a copy of ss_matmul_dispatch
+(layer_scheduler.c:248-279), built with gcc against include/ss_hip.h and
+linked with the library. Its GPU results must match the oracle's matvec
+(quantize.c:446-494), and a shape the plug rejects must reach the CPU
+branch (ss_hip_matvec_host returns false, the Metal calls' convention)."""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+import oracle
+from tests.util import Q4_0, Q8_0, make_blocks, rel_err
+
+pytestmark = pytest.mark.gpu
+EXE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c", "plug_snippet")
+
+
+def _run(tmp_path, w, x, rows, cols, qtype):
+    wp, xp, yp = (str(tmp_path / n) for n in ("w.bin", "x.bin", "y.bin"))
+    np.ascontiguousarray(w).tofile(wp)
+    np.ascontiguousarray(x, np.float32).tofile(xp)
+    r = subprocess.run([EXE, wp, xp, yp, str(rows), str(cols), str(qtype)], capture_output=True, text=True,
+                       timeout=120)
+    assert r.returncode == 0, (r.returncode, r.stderr)
+    return int(r.stdout.split()[-1]), np.fromfile(yp, np.float32)
+
+
+@pytest.mark.parametrize("qtype,rows,cols", [(Q4_0, 512, 4096), (Q8_0, 1000, 2048), (Q4_0, 33, 96)])
+def test_plug_snippet_matches_oracle(tmp_path, qtype, rows, cols):
+    rng = np.random.default_rng(rows + cols)
+    w = make_blocks(qtype, rows, cols, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    fallbacks, y = _run(tmp_path, w, x, rows, cols, qtype)
+    assert fallbacks == 0
+    assert rel_err(y, oracle.matvec(w, x, rows, cols, qtype)) <= 1e-3
+
+
+def test_plug_snippet_rejected_shape_falls_back(tmp_path):
+    rows, cols = 64, 40          # not a whole number of 32-weight blocks: the plug says false
+    fallbacks, y = _run(tmp_path, np.zeros(rows * 2 * 18, np.uint8), np.ones(cols, np.float32), rows, cols, Q4_0)
+    assert fallbacks == 2
+    assert np.all(y == -1.0)
