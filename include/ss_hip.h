@@ -140,6 +140,21 @@ int32_t ss_hip_attention(ss_hip_ctx_t *ctx, float *out_dev, const float *q_dev,
                          int32_t head_dim, int32_t max_seq, int32_t seq_len, int32_t kv_type,
                          void *stream);
 
+/* ss_hip_attention with no device allocation. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). The split partials and arrival counters live in one fixed
+ * 12 MiB device array per GPU (held until the process ends); a shape that
+ * needs more fails with SS_ERROR_INVALID_PARAMS. Every call on a GPU shares
+ * that array, so calls that overlap on one GPU (other streams or threads)
+ * race; calls in one stream are safe. Same arguments and results as
+ * ss_hip_attention. */
+int32_t ss_hip_attention_noalloc(ss_hip_ctx_t *ctx, float *out_dev, const float *q_dev,
+                                 const void *k_cache, const void *v_cache, const float *k_scale,
+                                 const float *v_scale, int32_t n_heads, int32_t n_kv_heads,
+                                 int32_t head_dim, int32_t max_seq, int32_t seq_len, int32_t kv_type,
+                                 void *stream);
+
 /* out[i] = up[i] * (g / (1 + exp(-g))), g = gate[i] (layer_scheduler.c:533-549) */
 int32_t ss_hip_swiglu(ss_hip_ctx_t *ctx, float *out_dev, const float *gate_dev,
                       const float *up_dev, int32_t n, void *stream);

@@ -91,12 +91,30 @@ struct ss_hip_ctx {
   size_t smp_bytes = 0;
   uint64_t* smp_io = nullptr;  // sampling: [0] index, [1] advanced state
 
+  // device address of this device's copy of `scratch` (ss_hip_attention_noalloc)
+  void* scratch = nullptr;
+
   // host-pointer plug (metal_backend.m:190-235 registry)
   std::unordered_map<const void*, void*> registry;
   float* plug_x = nullptr;
   float* plug_y = nullptr;
   size_t plug_x_n = 0, plug_y_n = 0;
 };
+
+// Scratch of ss_hip_attention_noalloc: the split partials (o, then (m, l))
+// and the per-KV-head arrival counters of one attention call. Each device
+// holds its own copy for the life of the process; host code reaches it only
+// through the address hipGetSymbolAddress gives (ss_hip_ctx::scratch), never
+// through the name, which on the host is a stand-in, not a device address.
+constexpr size_t kNoAllocScratchBytes = (size_t)12 << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+// zero n words (a kernel rather than hipMemsetAsync, so that a caller may
+// capture the call in a HIP graph)
+__global__ void k_zero_words(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
 
 namespace {
 
@@ -228,6 +246,12 @@ ss_hip_ctx_t* ss_hip_init(int32_t device) {
   if (hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking) != hipSuccess ||
       hipMalloc(&c->am_part, sizeof(float2) * ssk::kArgmaxMaxBlocks) != hipSuccess) {
     fail(kErrBackend, "HIP context set-up failed on device %d", device);
+    ss_hip_free(c);
+    return nullptr;
+  }
+  // this device's copy of the no-allocation scratch (device is current here)
+  if (hipGetSymbolAddress(&c->scratch, HIP_SYMBOL(scratch)) != hipSuccess || !c->scratch) {
+    fail(kErrBackend, "no address for the scratch array on device %d", device);
     ss_hip_free(c);
     return nullptr;
   }
@@ -430,25 +454,24 @@ int32_t ss_hip_kv_append(ss_hip_ctx_t* c, void* kc, void* vc, float* ksc, float*
   return 0;
 }
 
-int32_t ss_hip_attention(ss_hip_ctx_t* c, float* out, const float* q, const void* kc,
-                         const void* vc, const float* ksc, const float* vsc, int32_t n_heads,
-                         int32_t n_kv_heads, int32_t head_dim, int32_t max_seq, int32_t seq_len,
-                         int32_t kv_type, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Arguments and split count shared by ss_hip_attention and its
+// allocation-free variant; returns 0 or the error already recorded.
+int32_t attention_setup(ss_hip_ctx_t* c, const char* what, ssk::AttnArgs& a, int& group, int& ns,
+                        float* out, const float* q, const void* kc, const void* vc, const float* ksc,
+                        const float* vsc, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                        int32_t max_seq, int32_t seq_len, int32_t kv_type) {
   if (!c || !out || !q || !kc || !vc || n_kv_heads <= 0 || n_heads % n_kv_heads ||
       seq_len <= 0 || seq_len > max_seq || (kv_type != 0 && kv_type != 1) ||
       (kv_type == 1 && (!ksc || !vsc)))
-    return fail(kErrParams, "attention: bad argument");
-  const int group = n_heads / n_kv_heads;
+    return fail(kErrParams, "%s: bad argument", what);
+  group = n_heads / n_kv_heads;
   if (!ssk::attention_supported(head_dim, group))
-    return fail(kErrParams, "attention: head_dim %d / group %d not supported", head_dim, group);
-  const int ns = attn_splits(head_dim, group, max_seq, kv_type, n_kv_heads, c->n_cu);
-  int32_t rc = ensure(c, (void**)&c->att_o, &c->att_o_floats,
-                      sizeof(float) * (size_t)n_kv_heads * ns * group * head_dim, false);
-  if (!rc) rc = ensure(c, (void**)&c->att_ml, &c->att_ml_floats,
-                       sizeof(float) * (size_t)n_kv_heads * ns * group * 2, false);
-  if (!rc) rc = ensure(c, (void**)&c->att_cnt, &c->att_cnt_bytes, sizeof(uint32_t) * (size_t)n_kv_heads, true);
-  if (rc) return rc;
-  ssk::AttnArgs a;
+    return fail(kErrParams, "%s: head_dim %d / group %d not supported", what, head_dim, group);
+  ns = attn_splits(head_dim, group, max_seq, kv_type, n_kv_heads, c->n_cu);
   memset(&a, 0, sizeof(a));
   a.q = q;
   a.kc = kc;
@@ -461,10 +484,63 @@ int32_t ss_hip_attention(ss_hip_ctx_t* c, float* out, const float* q, const void
   a.n_kv_heads = n_kv_heads;
   a.scale = 1.0f / sqrtf((float)head_dim);
   a.out = out;
+  return 0;
+}
+
+size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+}  // namespace
+
+extern "C" {
+
+int32_t ss_hip_attention(ss_hip_ctx_t* c, float* out, const float* q, const void* kc,
+                         const void* vc, const float* ksc, const float* vsc, int32_t n_heads,
+                         int32_t n_kv_heads, int32_t head_dim, int32_t max_seq, int32_t seq_len,
+                         int32_t kv_type, void* stream) {
+  ssk::AttnArgs a;
+  int group = 0, ns = 0;
+  if (int32_t rc = attention_setup(c, "attention", a, group, ns, out, q, kc, vc, ksc, vsc, n_heads, n_kv_heads,
+                                   head_dim, max_seq, seq_len, kv_type))
+    return rc;
+  int32_t rc = ensure(c, (void**)&c->att_o, &c->att_o_floats,
+                      sizeof(float) * (size_t)n_kv_heads * ns * group * head_dim, false);
+  if (!rc) rc = ensure(c, (void**)&c->att_ml, &c->att_ml_floats,
+                       sizeof(float) * (size_t)n_kv_heads * ns * group * 2, false);
+  if (!rc) rc = ensure(c, (void**)&c->att_cnt, &c->att_cnt_bytes, sizeof(uint32_t) * (size_t)n_kv_heads, true);
+  if (rc) return rc;
   a.part_o = c->att_o;
   a.part_ml = c->att_ml;
   a.cnt = c->att_cnt;
   HIP_TRY(ssk::launch_attention(head_dim, group, kv_type, a, pick(c, stream)));
+  return 0;
+}
+
+int32_t ss_hip_attention_noalloc(ss_hip_ctx_t* c, float* out, const float* q, const void* kc,
+                                 const void* vc, const float* ksc, const float* vsc, int32_t n_heads,
+                                 int32_t n_kv_heads, int32_t head_dim, int32_t max_seq, int32_t seq_len,
+                                 int32_t kv_type, void* stream) {
+  ssk::AttnArgs a;
+  int group = 0, ns = 0;
+  if (int32_t rc = attention_setup(c, "attention_noalloc", a, group, ns, out, q, kc, vc, ksc, vsc, n_heads,
+                                   n_kv_heads, head_dim, max_seq, seq_len, kv_type))
+    return rc;
+  if (!c->scratch) return fail(kErrBackend, "attention_noalloc: no scratch address for this context");
+  const size_t o_bytes = round256(sizeof(float) * (size_t)n_kv_heads * ns * group * head_dim);
+  const size_t ml_bytes = round256(sizeof(float) * (size_t)n_kv_heads * ns * group * 2);
+  const size_t cnt_bytes = sizeof(uint32_t) * (size_t)n_kv_heads;
+  if (o_bytes + ml_bytes + cnt_bytes > kNoAllocScratchBytes)
+    return fail(kErrParams, "attention_noalloc: needs %zu bytes of scratch, more than its %zu (%d KV heads, "
+                "%d splits, group %d, head_dim %d)", o_bytes + ml_bytes + cnt_bytes, kNoAllocScratchBytes,
+                n_kv_heads, ns, group, head_dim);
+  uint8_t* base = static_cast<uint8_t*>(c->scratch);
+  a.part_o = reinterpret_cast<float*>(base);
+  a.part_ml = reinterpret_cast<float*>(base + o_bytes);
+  a.cnt = reinterpret_cast<uint32_t*>(base + o_bytes + ml_bytes);
+  hipStream_t s = pick(c, stream);
+  // the arrival counters must start at zero; the array keeps the last call's contents
+  hipLaunchKernelGGL(k_zero_words, dim3((n_kv_heads + 255) / 256), dim3(256), 0, s, a.cnt, n_kv_heads);
+  HIP_TRY(hipGetLastError());
+  HIP_TRY(ssk::launch_attention(head_dim, group, kv_type, a, s));
   return 0;
 }
 
