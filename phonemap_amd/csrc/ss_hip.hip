@@ -181,10 +181,22 @@ void rope_row(float* cs, int rope_dim, int pos, float theta) {
 int attn_splits(int head_dim, int group, int max_seq, int kv_type, int n_kv_heads, int n_cu) {
   const int round = ssk::attn_round_positions(head_dim, group);
   int ns = (max_seq + round - 1) / round;
+  // every split resident at once (a second generation of workgroups costs
+  // a whole split again)
   const int per_cu = ssk::attn_resident_groups(head_dim, group, kv_type);
   if (per_cu > 0 && n_cu > 0 && n_kv_heads > 0) {
     const int cap = per_cu * n_cu / n_kv_heads;
     if (ns > cap) ns = cap;
+  }
+  if (group >= 4 && ns > ssk::kMergeSplits && n_kv_heads > 0 && n_cu > 0) {
+    // heads on lanes, merged by the last split: one workgroup per compute
+    // unit, splits of at least 16 positions (measured at the 8B and 70B
+    // shapes against 16 to 128 splits per KV head: 32 splits of 8 KV heads
+    // ran 13.9 and 11.9 us per call, every split resident at once (64
+    // splits) 15.8 and 14.9)
+    ns = (n_cu + n_kv_heads - 1) / n_kv_heads;
+    const int lim = (max_seq + 15) / 16;
+    if (ns > lim) ns = lim;
   }
   if (ns > ssk::kMaxSplits) ns = ssk::kMaxSplits;
   if (ns < 1) ns = 1;
