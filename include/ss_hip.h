@@ -22,7 +22,11 @@
  * (16 or 32 bytes per entry), then at the next 256-byte boundary the
  * binary16 scales with the same index. R is padded to a multiple of 16 and
  * C/32 to a multiple of 4 with zero entries. ss_hip_pack_matrix makes it;
- * ss_hip_packed_bytes gives its size.
+ * ss_hip_packed_bytes gives its size. A Q4_K matrix (quantize.c:265-310)
+ * uses the same tiles for its 32-weight sub-blocks (nibbles without offset,
+ * scale-plane entry = 6-bit scale | 6-bit min << 8), then at the next
+ * 256-byte boundary a third plane with each row's super-block (d, dmin)
+ * binary16 pairs, [row group][super-block][16 rows].
  */
 #ifndef SS_HIP_H
 #define SS_HIP_H
@@ -42,6 +46,7 @@ typedef struct ss_hip_model ss_hip_model_t;
 #define SS_HIP_F16 1
 #define SS_HIP_Q4_0 2
 #define SS_HIP_Q8_0 8
+#define SS_HIP_Q4_K 12   /* 256-weight super-blocks (cols a multiple of 256) */
 
 /* token launch modes (match SS_LAUNCH_* in slipstream.h): per-kernel eager,
  * per-kernel replayed from a HIP graph, or one persistent launch per token
@@ -99,6 +104,11 @@ int32_t ss_hip_gemm(ss_hip_ctx_t *ctx, float *y_dev, const void *w_dev, const fl
 int32_t ss_hip_matvec_q4_0(ss_hip_ctx_t *ctx, float *y_dev, const void *w_dev, const float *x_dev,
                            int32_t rows, int32_t cols, void *stream);
 int32_t ss_hip_matvec_q8_0(ss_hip_ctx_t *ctx, float *y_dev, const void *w_dev, const float *x_dev,
+                           int32_t rows, int32_t cols, void *stream);
+/* The Q4_K matvec: ss_metal_matvec_q4_K (metal_backend.h:44-52) on device
+ * buffers (the reference runs it on Metal, or dequant_q4_K + the CPU GEMV,
+ * quantize.c:265-310, 446-494). */
+int32_t ss_hip_matvec_q4_k(ss_hip_ctx_t *ctx, float *y_dev, const void *w_dev, const float *x_dev,
                            int32_t rows, int32_t cols, void *stream);
 
 /* y = W rmsnorm(x, nw, eps) (+ y when accumulate != 0): the matvec with the

@@ -144,6 +144,40 @@ void orc_dequantize(const void *src, float *dst, int32_t n, int32_t type) {
                 dst[b * 32 + i] = scale * (float)(int8_t)blk[2 + i];
         }
         break;
+    case ORC_Q4_K:
+        /* quantize.c:265-310: super-blocks of 256 weights, 144 bytes: d and
+         * dmin (binary16), 12 bytes of packed 6-bit sub-block scales and
+         * mins, 128 bytes of nibbles. Sub-blocks 2j and 2j + 1 take the low
+         * and the high nibbles of bytes 32j .. 32j + 31; weight = d*sc * q -
+         * dmin*m. The scale and min of sub-block k (get_scale_min_k4,
+         * :267-275): k < 4 from the low 6 bits of bytes k and k + 4;
+         * otherwise the low and high nibbles of byte k + 4 with the top two
+         * bits of bytes k - 4 and k on top. */
+        for (int32_t b = 0; b < n / 256; b++) {
+            const uint8_t *blk = p + (size_t)b * 144;
+            uint16_t dh, mh;
+            memcpy(&dh, blk, 2);
+            memcpy(&mh, blk + 2, 2);
+            const float d = orc_f16_to_f32(dh), dmin = orc_f16_to_f32(mh);
+            const uint8_t *sc = blk + 4, *q = blk + 16;
+            for (int32_t k = 0; k < 8; k++) {
+                uint8_t s6, m6;
+                if (k < 4) {
+                    s6 = sc[k] & 63;
+                    m6 = sc[k + 4] & 63;
+                } else {
+                    s6 = (uint8_t)((sc[k + 4] & 0xF) | ((sc[k - 4] >> 6) << 4));
+                    m6 = (uint8_t)((sc[k + 4] >> 4) | ((sc[k] >> 6) << 4));
+                }
+                const float d1 = d * (float)s6, m1 = dmin * (float)m6;
+                const uint8_t *qk = q + 32 * (k / 2);
+                for (int32_t l = 0; l < 32; l++) {
+                    const int32_t nib = k % 2 ? qk[l] >> 4 : qk[l] & 0xF;
+                    dst[b * 256 + k * 32 + l] = d1 * (float)nib - m1;
+                }
+            }
+        }
+        break;
     default:
         memset(dst, 0, (size_t)n * sizeof(float));
         break;
@@ -156,6 +190,7 @@ static size_t orc_row_bytes(int32_t cols, int32_t type) {
     case ORC_F16: return (size_t)cols * 2;
     case ORC_Q4_0: return (size_t)(cols / 32) * 18;
     case ORC_Q8_0: return (size_t)(cols / 32) * 34;
+    case ORC_Q4_K: return (size_t)(cols / 256) * 144;
     default: return 0;
     }
 }
@@ -707,13 +742,17 @@ static int key_ends(const char *k, uint64_t kl, const char *s) {
     return kl >= sl && memcmp(k + kl - sl, s, sl) == 0;
 }
 
-static uint32_t type_block(int32_t t) { return (t == ORC_Q4_0 || t == ORC_Q8_0) ? 32 : 1; }
+/* gguf_loader.c:22-62: weights per block and bytes per block */
+static uint32_t type_block(int32_t t) {
+    return (t == ORC_Q4_0 || t == ORC_Q8_0) ? 32 : t == ORC_Q4_K ? 256 : 1;
+}
 static uint32_t type_size(int32_t t) {
     switch (t) {
     case ORC_F32: return 4;
     case ORC_F16: return 2;
     case ORC_Q4_0: return 18;
     case ORC_Q8_0: return 34;
+    case ORC_Q4_K: return 144;
     default: return 0;
     }
 }
@@ -853,7 +892,8 @@ void orc_model_close(orc_model_t *m) {
 
 static int matrix_ok(const orc_tensor_t *t, uint64_t rows, uint64_t cols) {
     return t && t->n_dims == 2 && t->dims[0] == cols && t->dims[1] == rows &&
-           (t->type == ORC_Q4_0 || t->type == ORC_Q8_0 || t->type == ORC_F32 || t->type == ORC_F16);
+           (t->type == ORC_Q4_0 || t->type == ORC_Q8_0 || t->type == ORC_F32 || t->type == ORC_F16 ||
+            (t->type == ORC_Q4_K && cols % 256 == 0));
 }
 static int vector_ok(const orc_tensor_t *t, uint64_t n) {
     return t && t->type == ORC_F32 && t->dims[0] == n;

@@ -19,7 +19,7 @@ extern "C" {
 #endif
 
 /* ggml tensor types used on the path (src/core/gguf_loader.h:41-55) */
-enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q8_0 = 8 };
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_Q4_K = 12 };
 
 /* KV cache storage modes */
 enum { ORC_KV_INT8 = 0,   /* reference: per-(layer,pos) absmax int8, layer_scheduler.c:101-125 */

@@ -44,6 +44,7 @@ _PROTOS = {
     "ss_hip_gemm": (_i32, [_vp, _vp, _vp, _vp, _vp, _f32, _i32, _i32, _i32, _i32, _i32, _vp]),
     "ss_hip_matvec_q4_0": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _vp]),
     "ss_hip_matvec_q8_0": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _vp]),
+    "ss_hip_matvec_q4_k": (_i32, [_vp, _vp, _vp, _vp, _i32, _i32, _vp]),
     "ss_hip_matvec_fused": (_i32, [_vp, _vp, _vp, _vp, _vp, _f32, _i32, _i32, _i32, _i32, _vp]),
     "ss_hip_ffn_gate_up": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _f32, _i32, _i32, _i32, _vp]),
     "ss_hip_rmsnorm": (_i32, [_vp, _vp, _vp, _vp, _i32, _f32, _vp]),

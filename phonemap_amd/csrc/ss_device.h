@@ -153,6 +153,11 @@ struct QTraits<8> {            // Q8_0
   static constexpr int kQB = 32;
   static constexpr int kGgufBytes = 34;
 };
+template <>
+struct QTraits<12> {           // Q4_K: a 32-weight sub-block packs like a Q4_0 block
+  static constexpr int kQB = 16;
+  static constexpr int kGgufBytes = 144;   // per 256-weight super-block
+};
 
 
 // ------------------------------------------------------------ x records
@@ -285,6 +290,40 @@ __device__ __forceinline__ float q4_dot(const uint4 q, const uint32_t* ra, const
   const uint2 ta = *reinterpret_cast<const uint2*>(ra + 12);
   const uint2 tb = *reinterpret_cast<const uint2*>(rb + 12);
   return fmaf((float)(a - (int)ta.x), __uint_as_float(ta.y), (float)(b - (int)tb.x) * __uint_as_float(tb.y));
+}
+
+// Q4_K sub-block (quantize.c:265-310: weight = dsc * q - dmn with q the
+// nibble, dsc = d * scale and dmn = dmin * min of the sub-block, both exact
+// in fp32), packed like a Q4_0 block (nibble j of weight j, j + 16 in the
+// high nibble) but without the -8 offset: sum w x = dsc * sum q X s3 -
+// dmn * sum X s3 per 16-value record, sum X being the records' [12] / 8.
+__device__ __forceinline__ float q4k_dot(const uint4 q, const uint32_t* ra, const uint32_t* rb, float dsc,
+                                         float dmn) {
+  const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+  int a = 0, b = 0;
+#pragma unroll
+  for (int l = 0; l < 3; ++l) {
+    const uint4 xa = *reinterpret_cast<const uint4*>(ra + 4 * l);
+    const uint4 xb = *reinterpret_cast<const uint4*>(rb + 4 * l);
+    if (l) {
+      a <<= 7;
+      b <<= 7;
+    }
+    a = sdot4(w[0] & 0x0F0F0F0Fu, (int)xa.x, a);
+    a = sdot4(w[1] & 0x0F0F0F0Fu, (int)xa.y, a);
+    a = sdot4(w[2] & 0x0F0F0F0Fu, (int)xa.z, a);
+    a = sdot4(w[3] & 0x0F0F0F0Fu, (int)xa.w, a);
+    b = sdot4((w[0] >> 4) & 0x0F0F0F0Fu, (int)xb.x, b);
+    b = sdot4((w[1] >> 4) & 0x0F0F0F0Fu, (int)xb.y, b);
+    b = sdot4((w[2] >> 4) & 0x0F0F0F0Fu, (int)xb.z, b);
+    b = sdot4((w[3] >> 4) & 0x0F0F0F0Fu, (int)xb.w, b);
+  }
+  const uint2 ta = *reinterpret_cast<const uint2*>(ra + 12);
+  const uint2 tb = *reinterpret_cast<const uint2*>(rb + 12);
+  const float sa = __uint_as_float(ta.y), sb = __uint_as_float(tb.y);
+  const float qx = fmaf((float)a, sa, (float)b * sb);
+  const float sx = fmaf((float)((int)ta.x >> 3), sa, (float)((int)tb.x >> 3) * sb);
+  return fmaf(dsc, qx, -dmn * sx);
 }
 
 // Q8_0 block (quantize.c:139-149: 32 int8 codes, value d * code); levels 1-2

@@ -98,6 +98,7 @@ static size_t row_bytes(int32_t type, int32_t cols) {
     case SS_HIP_F16: return (size_t)cols * 2;
     case SS_HIP_Q4_0: return (size_t)cols / 32 * 18;
     case SS_HIP_Q8_0: return (size_t)cols / 32 * 34;
+    case SS_HIP_Q4_K: return (size_t)cols / 256 * 144;
     default: return 0;
     }
 }

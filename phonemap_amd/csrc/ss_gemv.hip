@@ -10,6 +10,14 @@
 // 16 and blocks to a multiple of 4 with zero codes and scales. A wave loads a
 // tile as one contiguous 1 KiB (Q4_0) read.
 //
+// Q4_K matrices (256-weight super-blocks of eight 32-weight sub-blocks, each
+// with a 6-bit scale and min, quantize.c:265-310) use the same tiles: a
+// sub-block's 32 nibbles are stored as a Q4_0 block's (without the -8
+// offset), its entry in the scale plane is scale | min << 8, and a third
+// plane holds each row's super-block (d, dmin) pair of binary16s:
+// su[(g * nsb + sb) * 16 + row % 16], nsb = cols / 256. 18.5 bytes per 32
+// weights against the GGUF format's 18.
+//
 // k_gemv: workgroup = one 16-row group; wave s takes units (UT consecutive
 // tiles) s, s+S, ... of it. A wave requests its x slice, then every chunk and
 // scale of its unit, before using any; it encodes its own slice of x into its
@@ -178,7 +186,8 @@ template <int QT, int NMAT, int UT>
 struct Round {
   static constexpr int kNV = QTraits<QT>::kQB / 16;
   uint4 q[NMAT][UT][kNV];
-  uint32_t sc[NMAT][UT / 2];   // the unit's binary16 scales, tile order
+  uint32_t sc[NMAT][UT / 2];   // the unit's binary16 scales (Q4_K: scale | min << 8), tile order
+  uint32_t su[NMAT][QT == kQ4K ? UT / 2 : 1];   // Q4_K: (d, dmin) of the unit's super-blocks
 };
 
 template <int QT, int NMAT, int UT>
@@ -199,6 +208,12 @@ __device__ __forceinline__ void load_round(Round<QT, NMAT, UT>& f, const GemvArg
       f.sc[m][0] = v.x; f.sc[m][1] = v.y;
     } else {
       f.sc[m][0] = *sp;
+    }
+    if constexpr (QT == kQ4K) {   // a unit (an even number of tiles) covers UT / 2 super-blocks
+      const int nsb = ntk / 2;
+#pragma unroll
+      for (int j = 0; j < UT / 2; ++j)
+        f.su[m][j] = w.su[((size_t)g * nsb + min(t0 / 2 + j, nsb - 1)) * kRG + lane % kRG];
     }
 #pragma unroll
     for (int k = 0; k < UT; ++k) {
@@ -223,14 +238,21 @@ __device__ __forceinline__ void fma_round(float (&acc)[NMAT], const Round<QT, NM
     const uint32_t* ra = reinterpret_cast<const uint32_t*>(xs + (k * kTB + kb) * kXW);
 #pragma unroll
     for (int m = 0; m < NMAT; ++m) {
-      float s;
-      if constexpr (QT == 2)
-        s = q4_dot(f.q[m][k][0], ra, ra + kRW);
-      else
-        s = q8_dot(f.q[m][k][0], f.q[m][k][1], ra, ra + kRW);
       const uint32_t sw = f.sc[m][k / 2];
-      const float d = h2f((uint16_t)(k & 1 ? sw >> 16 : sw & 0xffffu));
-      acc[m] = fmaf(d, s, acc[m]);
+      const uint32_t e = k & 1 ? sw >> 16 : sw & 0xffffu;
+      if constexpr (QT == kQ4K) {
+        const uint32_t sup = f.su[m][k / 2];
+        const float dsc = h2f((uint16_t)(sup & 0xffffu)) * (float)(e & 0xffu);   // exact
+        const float dmn = h2f((uint16_t)(sup >> 16)) * (float)(e >> 8);
+        acc[m] += q4k_dot(f.q[m][k][0], ra, ra + kRW, dsc, dmn);
+      } else {
+        float s;
+        if constexpr (QT == 2)
+          s = q4_dot(f.q[m][k][0], ra, ra + kRW);
+        else
+          s = q8_dot(f.q[m][k][0], f.q[m][k][1], ra, ra + kRW);
+        acc[m] = fmaf(h2f((uint16_t)e), s, acc[m]);
+      }
     }
   }
 }
@@ -338,7 +360,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int row, bool own, c
 // Q8_0 and two-matrix rounds hold 64 VGPRs of codes: at most 8 waves, so
 // 256 VGPRs are available to them.
 template <int QT, int NMAT>
-constexpr int gemv_max_waves() { return QT == 8 || NMAT == 2 ? 8 : 16; }
+constexpr int gemv_max_waves() { return QT == 8 || NMAT == 2 || (QT == kQ4K) ? 8 : 16; }
 
 template <int QT, int NMAT, int EPI, int UT, bool MERGE, bool PX>
 __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(const GemvArgs a) {
@@ -449,6 +471,45 @@ __global__ void k_pack(const uint8_t* __restrict__ src, uint8_t* __restrict__ qs
   }
 }
 
+// GGUF Q4_K super-blocks -> tiled planes: thread i takes sub-block i % nb of
+// row row_off + i / nb (nb = cols / 32 sub-blocks per row): its 6-bit scale
+// and min (get_scale_min_k4, quantize.c:267-275) into the scale plane, its
+// 32 nibbles (low or high nibbles of 32 bytes, quantize.c:296-305) in Q4_0
+// order into the code plane, and with sub-block 0 of a super-block the
+// super-block's (d, dmin) into the third plane.
+__global__ void k_pack_q4k(const uint8_t* __restrict__ src, uint8_t* __restrict__ qs, uint16_t* __restrict__ ds,
+                           uint32_t* __restrict__ su, int64_t nsub, int nb, int64_t row_off) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nsub) return;
+  const int64_t r = i / nb;
+  const int b = (int)(i % nb), k = b % 8, nsb = nb / 8;
+  const int64_t row = row_off + r;
+  const uint8_t* sb = src + (r * nsb + b / 8) * 144;
+  const uint8_t* sc = sb + 4;
+  uint32_t s6, m6;
+  if (k < 4) {
+    s6 = sc[k] & 63u;
+    m6 = sc[k + 4] & 63u;
+  } else {
+    s6 = (sc[k + 4] & 0xFu) | ((uint32_t)(sc[k - 4] >> 6) << 4);
+    m6 = (sc[k + 4] >> 4) | ((uint32_t)(sc[k] >> 6) << 4);
+  }
+  const uint8_t* q = sb + 16 + 32 * (k / 2);
+  const int sh = 4 * (k % 2);
+  uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const uint32_t lo = (q[j] >> sh) & 0xFu, hi = (q[j + 16] >> sh) & 0xFu;
+    w[j / 4] |= (lo | (hi << 4)) << (8 * (j % 4));
+  }
+  const int ntk = (nb + kTB - 1) / kTB, g = (int)(row / kRG), l = tile_lane((int)(row % kRG), b);
+  *reinterpret_cast<uint4*>(qs + tile_idx(g, ntk, b / kTB, l) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+  ds[scale_idx(g, ntk, b / kTB, l)] = (uint16_t)(s6 | (m6 << 8));
+  if (k == 0)
+    su[((size_t)g * nsb + b / 8) * kRG + row % kRG] =
+        (uint32_t)(sb[0] | (sb[1] << 8)) | ((uint32_t)(sb[2] | (sb[3] << 8)) << 16);
+}
+
 // Row `token` of a packed table, dequantised exactly as quantize.c:60-72 /
 // 139-149 (one fp32 multiply per weight). With tokens set, workgroup row z
 // writes row tokens[*dpos + z] to out + z * cols (a prompt's rows at once).
@@ -464,6 +525,15 @@ __device__ __forceinline__ float embed_value(const PackedMat& t, int tok, int nt
   if constexpr (QT == 2) {
     const uint8_t v = q[p & 15];
     return d * (float)((int)(p < 16 ? v & 0xF : v >> 4) - 8);
+  } else if constexpr (QT == kQ4K) {
+    // quantize.c:287-305: d1 = d * scale, m1 = dmin * min, weight d1 * q - m1
+    // with both fp32 roundings kept apart (no fused multiply-add)
+    const uint8_t v = q[p & 15];
+    const uint32_t e = t.ds[scale_idx(tok / kRG, ntk, b / kTB, l)];
+    const uint32_t sup = t.su[((size_t)(tok / kRG) * (ntk / 2) + b / 8) * kRG + tok % kRG];
+    const float d1 = h2f((uint16_t)(sup & 0xffffu)) * (float)(e & 0xffu);
+    const float m1 = h2f((uint16_t)(sup >> 16)) * (float)(e >> 8);
+    return __fsub_rn(__fmul_rn(d1, (float)(p < 16 ? v & 0xF : v >> 4)), m1);
   } else {
     return d * (float)(int8_t)q[p];
   }
@@ -579,7 +649,7 @@ GemvPlan gemv_plan(int rows, int cols, int type, int nmat, int unit) {
   GemvPlan p;
   const int groups = (rows + kRG - 1) / kRG;
   const int ntk = (cols / 32 + kTB - 1) / kTB;
-  const int smax = type == 8 || nmat == 2 ? gemv_max_waves<8, 1>() : gemv_max_waves<2, 1>();
+  const int smax = type == 8 || type == kQ4K || nmat == 2 ? gemv_max_waves<8, 1>() : gemv_max_waves<2, 1>();
   const int ut = unit;
   const int nu = (ntk + ut - 1) / ut;
   const int S = nu < smax ? nu : smax;
@@ -591,27 +661,36 @@ GemvPlan gemv_plan(int rows, int cols, int type, int nmat, int unit) {
 }
 
 // code and scale bytes of a packed [rows x cols] matrix
-static void packed_sizes(int type, int64_t rows, int cols, size_t* code, size_t* scales) {
+// code, scale and (Q4_K) super-block plane bytes of a packed [rows x cols]
+// matrix; the scale plane starts at a 256-byte boundary, and so does the
+// super-block plane
+static void packed_sizes(int type, int64_t rows, int cols, size_t* code, size_t* scales, size_t* sup) {
   const size_t groups = (size_t)((rows + kRG - 1) / kRG);
   const int ntk = (cols / 32 + kTB - 1) / kTB;
   const int nu = (ntk + kUT - 1) / kUT;
-  const int kqb = type == 2 ? 16 : type == 8 ? 32 : 0;
+  const int kqb = type == 2 || type == kQ4K ? 16 : type == 8 ? 32 : 0;
   *code = ((groups * ntk * kWave * kqb) + 255) & ~(size_t)255;
   *scales = groups * nu * kWave * kUT * 2;
+  *sup = 0;
+  if (type == kQ4K) {
+    *scales = (*scales + 255) & ~(size_t)255;
+    *sup = groups * (size_t)(cols / 256) * kRG * 4;
+  }
 }
 
 size_t packed_bytes(int type, int64_t rows, int cols) {
-  size_t c, sc;
-  packed_sizes(type, rows, cols, &c, &sc);
-  return c + sc;
+  size_t c, sc, su;
+  packed_sizes(type, rows, cols, &c, &sc, &su);
+  return c + sc + su;
 }
 
 PackedMat packed_view(const void* base, int type, int64_t rows, int cols) {
-  size_t c, sc;
-  packed_sizes(type, rows, cols, &c, &sc);
+  size_t c, sc, su;
+  packed_sizes(type, rows, cols, &c, &sc, &su);
   PackedMat m;
   m.qs = static_cast<const uint8_t*>(base);
   m.ds = reinterpret_cast<const uint16_t*>(m.qs + c);
+  m.su = su ? reinterpret_cast<const uint32_t*>(m.qs + c + sc) : nullptr;
   return m;
 }
 
@@ -623,6 +702,7 @@ hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t s) {
     return hipErrorInvalidValue;
   if (a.type == 2) return launch_q<2>(epi, a, s);
   if (a.type == 8) return launch_q<8>(epi, a, s);
+  if (a.type == kQ4K) return launch_q<kQ4K>(epi, a, s);
   return hipErrorInvalidValue;
 }
 
@@ -632,13 +712,18 @@ hipError_t launch_argmax_merge(const float2* part, int n, const float* y, int* o
   return hipGetLastError();
 }
 
-hipError_t launch_pack(int type, const uint8_t* src, uint8_t* qs, uint16_t* ds, int64_t nblocks,
-                       int nb, int64_t row_off, hipStream_t s) {
+hipError_t launch_pack(int type, const uint8_t* src, PackedMat dst, int64_t nblocks, int nb, int64_t row_off,
+                       hipStream_t s) {
   const int64_t grid = (nblocks + 255) / 256;
+  uint8_t* qs = const_cast<uint8_t*>(dst.qs);
+  uint16_t* ds = const_cast<uint16_t*>(dst.ds);
   if (type == 2)
     hipLaunchKernelGGL(k_pack<2>, dim3((unsigned)grid), dim3(256), 0, s, src, qs, ds, nblocks, nb, row_off);
   else if (type == 8)
     hipLaunchKernelGGL(k_pack<8>, dim3((unsigned)grid), dim3(256), 0, s, src, qs, ds, nblocks, nb, row_off);
+  else if (type == kQ4K && dst.su && nb % 8 == 0)
+    hipLaunchKernelGGL(k_pack_q4k, dim3((unsigned)grid), dim3(256), 0, s, src, qs, ds, const_cast<uint32_t*>(dst.su),
+                       nblocks, nb, row_off);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -653,6 +738,9 @@ hipError_t launch_embed(int type, PackedMat t, int cols, const int* tokens, cons
   else if (type == 8)
     hipLaunchKernelGGL(k_embed<8>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out, nw,
                        xr);
+  else if (type == kQ4K)
+    hipLaunchKernelGGL(k_embed<kQ4K>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out,
+                       nw, xr);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -666,6 +754,9 @@ hipError_t launch_embed_rows(int type, PackedMat t, int cols, const int* tokens,
                        nullptr, nullptr);
   else if (type == 8)
     hipLaunchKernelGGL(k_embed<8>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
+                       nullptr, nullptr);
+  else if (type == kQ4K)
+    hipLaunchKernelGGL(k_embed<kQ4K>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
                        nullptr, nullptr);
   else
     return hipErrorInvalidValue;

@@ -52,10 +52,13 @@ int32_t fail(int32_t code, const char* fmt, ...) {
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-int code_bytes(int type) { return type == SS_HIP_Q4_0 ? 16 : type == SS_HIP_Q8_0 ? 32 : 0; }
-int gguf_block_bytes(int type) { return type == SS_HIP_Q4_0 ? 18 : type == SS_HIP_Q8_0 ? 34 : 0; }
+int code_bytes(int type) { return type == SS_HIP_Q4_0 || type == SS_HIP_Q4_K ? 16 : type == SS_HIP_Q8_0 ? 32 : 0; }
+// GGUF bytes per 32 weights (a Q4_K super-block of 256 is 144 bytes: 18 per 32)
+int gguf_block_bytes(int type) { return type == SS_HIP_Q4_0 || type == SS_HIP_Q4_K ? 18 : type == SS_HIP_Q8_0 ? 34 : 0; }
 
-bool quant_type_ok(int type) { return type == SS_HIP_Q4_0 || type == SS_HIP_Q8_0; }
+bool quant_type_ok(int type) { return type == SS_HIP_Q4_0 || type == SS_HIP_Q8_0 || type == SS_HIP_Q4_K; }
+// columns a row of this type must be a multiple of (whole blocks, or super-blocks)
+int col_unit(int type) { return type == SS_HIP_Q4_K ? 256 : 32; }
 
 ssk::PackedMat view(const void* base, int type, int64_t rows, int cols) {
   return ssk::packed_view(base, type, rows, cols);
@@ -156,9 +159,8 @@ int32_t pack_rows(ss_hip_ctx* c, void* dst, int64_t total_rows, int64_t row_off,
     const int64_t n = rows - r < chunk_rows ? rows - r : chunk_rows;
     HIP_TRY(hipMemcpyAsync(c->staging, static_cast<const uint8_t*>(src) + (size_t)r * row_bytes,
                            (size_t)n * row_bytes, hipMemcpyHostToDevice, c->stream));
-    HIP_TRY(ssk::launch_pack(type, static_cast<const uint8_t*>(c->staging),
-                             const_cast<uint8_t*>(v.qs), const_cast<uint16_t*>(v.ds),
-                             n * nb, nb, row_off + r, c->stream));
+    HIP_TRY(ssk::launch_pack(type, static_cast<const uint8_t*>(c->staging), v, n * nb, nb, row_off + r,
+                             c->stream));
   }
   HIP_TRY(hipStreamSynchronize(c->stream));
   return 0;
@@ -322,14 +324,14 @@ int32_t ss_hip_memcpy_d2h(ss_hip_ctx_t* c, void* host, const void* dev, size_t b
 }
 
 size_t ss_hip_packed_bytes(int32_t type, int32_t rows, int32_t cols) {
-  if (!quant_type_ok(type) || rows <= 0 || cols <= 0 || cols % 32) return 0;
+  if (!quant_type_ok(type) || rows <= 0 || cols <= 0 || cols % col_unit(type)) return 0;
   return ssk::packed_bytes(type, rows, cols);
 }
 
 int32_t ss_hip_pack_matrix(ss_hip_ctx_t* c, void* dst, const void* src, int32_t type,
                            int32_t rows, int32_t cols) {
   if (!c || !dst || !src) return fail(kErrParams, "null argument");
-  if (!quant_type_ok(type) || rows <= 0 || cols <= 0 || cols % 32)
+  if (!quant_type_ok(type) || rows <= 0 || cols <= 0 || cols % col_unit(type))
     return fail(kErrParams, "pack: unsupported type %d or shape %dx%d", type, rows, cols);
   if (set_device(c)) return kErrBackend;
   // rows are padded to a multiple of 64 with zero codes and zero scales
@@ -339,9 +341,9 @@ int32_t ss_hip_pack_matrix(ss_hip_ctx_t* c, void* dst, const void* src, int32_t 
 
 // ============================================================== single ops
 static int32_t check_mv(int32_t rows, int32_t cols, int32_t type) {
-  if (!quant_type_ok(type)) return fail(kErrParams, "matvec: type %d is not Q4_0/Q8_0", type);
-  if (rows <= 0 || cols <= 0 || cols % 32)
-    return fail(kErrParams, "matvec: bad shape %dx%d (cols must be a multiple of 32)", rows, cols);
+  if (!quant_type_ok(type)) return fail(kErrParams, "matvec: type %d is not Q4_0/Q8_0/Q4_K", type);
+  if (rows <= 0 || cols <= 0 || cols % col_unit(type))
+    return fail(kErrParams, "matvec: bad shape %dx%d (cols must be a multiple of %d)", rows, cols, col_unit(type));
   return 0;
 }
 
@@ -366,7 +368,9 @@ int32_t ss_hip_matvec(ss_hip_ctx_t* c, float* y, const void* w, const float* x, 
 
 int32_t ss_hip_gemm(ss_hip_ctx_t* c, float* y, const void* w, const float* x, const float* nw, float eps,
                     int32_t accumulate, int32_t rows, int32_t cols, int32_t n_tokens, int32_t type, void* stream) {
-  if (!c || !y || !w || !x || rows <= 0 || cols <= 0 || cols % 32 || n_tokens <= 0 || !quant_type_ok(type))
+  // the MFMA products take Q4_0 and Q8_0 (Q4_K prompts run token by token)
+  if (!c || !y || !w || !x || rows <= 0 || cols <= 0 || cols % 32 || n_tokens <= 0 ||
+      (type != SS_HIP_Q4_0 && type != SS_HIP_Q8_0))
     return fail(kErrParams, "gemm: bad argument (rows %d cols %d tokens %d type %d)", rows, cols, n_tokens, type);
   if (set_device(c)) return kErrBackend;
   int32_t rc = ensure(c, (void**)&c->g_ssq, &c->g_ssq_bytes, sizeof(float) * n_tokens, false);
@@ -400,6 +404,11 @@ int32_t ss_hip_matvec_q4_0(ss_hip_ctx_t* c, float* y, const void* w, const float
 int32_t ss_hip_matvec_q8_0(ss_hip_ctx_t* c, float* y, const void* w, const float* x, int32_t rows,
                            int32_t cols, void* stream) {
   return ss_hip_matvec(c, y, w, x, rows, cols, SS_HIP_Q8_0, stream);
+}
+
+int32_t ss_hip_matvec_q4_k(ss_hip_ctx_t* c, float* y, const void* w, const float* x, int32_t rows,
+                           int32_t cols, void* stream) {
+  return ss_hip_matvec(c, y, w, x, rows, cols, SS_HIP_Q4_K, stream);
 }
 
 int32_t ss_hip_matvec_fused(ss_hip_ctx_t* c, float* y, const void* w, const float* x,
@@ -687,6 +696,7 @@ struct ss_hip_model {
   int t_embd = 0;
   void* out = nullptr;   // == embd when tied
   int t_out = 0;
+  bool any_q4k = false;   // some matrix is Q4_K: prompts run token by token
   float* out_norm = nullptr;
   // KV cache: [L][KVH][max_seq][hd] (+ [L][max_seq] scales for int8)
   void* kc = nullptr;
@@ -821,9 +831,11 @@ int32_t upload_mat(ss_hip_model* m, void** dst, const ss_hip_tensor_t* parts, in
     if (parts[i].cols != cols) return fail(kErrParams, "model: %s has %d columns, %d expected", what, parts[i].cols, cols);
     total += parts[i].rows;
   }
-  if (!quant_type_ok(type)) return fail(kErrParams, "model: %s has type %d; Q4_0 and Q8_0 are supported", what, type);
+  if (!quant_type_ok(type))
+    return fail(kErrParams, "model: %s has type %d; Q4_0, Q8_0 and Q4_K are supported", what, type);
   if (total != rows_expect_total) return fail(kErrParams, "model: %s has %lld rows, %d expected", what, (long long)total, rows_expect_total);
-  if (cols % 32) return fail(kErrParams, "model: %s columns %d not a multiple of 32", what, cols);
+  if (cols % col_unit(type))
+    return fail(kErrParams, "model: %s columns %d not a multiple of %d", what, cols, col_unit(type));
   // zero-filled: rows are padded to a multiple of 64 with zero codes and scales
   if (into)
     *dst = into;
@@ -876,7 +888,7 @@ hipError_t timed(ss_hip_model* m, int cls, double bytes, F&& launch) {
   return e;
 }
 
-int q_class(int type) { return type == SS_HIP_Q4_0 ? PC_Q4 : PC_Q8; }
+int q_class(int type) { return type == SS_HIP_Q8_0 ? PC_Q8 : PC_Q4; }   // 4-bit codes: Q4_0 and Q4_K
 
 // Algorithmic HBM bytes of one token at context ctx: every weight byte once
 // (GGUF block sizes), the fp16 K/V read and appended, the norm weights.
@@ -893,7 +905,8 @@ double token_bytes(const ss_hip_model* m, int ctx, bool with_head) {
 }
 
 // One persistent launch per token when the shape allows it: fp16 KV, one
-// quantisation type for all layer matrices, a supported head shape, and the
+// quantisation type (Q4_0 or Q8_0) for all layer matrices and the head, a
+// Q4_0/Q8_0 embedding, a supported head shape, and the
 // workgroups (one per compute unit) co-resident. Otherwise the model keeps
 // the per-kernel launches (graph mode).
 int32_t sweep_setup(ss_hip_model* m) {
@@ -902,6 +915,7 @@ int32_t sweep_setup(ss_hip_model* m) {
   for (const DevLayer& ly : m->layers)
     if (ly.t_qkv != lt || ly.t_o != lt || ly.t_gu != lt || ly.t_d != lt) return 1;
   if (!ssk::sweep_supported(m->hd, m->group, lt, m->t_out)) return 1;
+  if (m->t_embd != SS_HIP_Q4_0 && m->t_embd != SS_HIP_Q8_0) return 1;   // the sweep stages Q4_0/Q8_0 rows only
   int nwg = m->ctx->n_cu < ssk::kSweepMaxWg ? m->ctx->n_cu : ssk::kSweepMaxWg;
   if (m->KVH > nwg) return 1;
   ssk::SweepArgs& a = m->sw;
@@ -1452,7 +1466,8 @@ int32_t stream_setup(ss_hip_model* m, const ss_hip_model_desc_t* d) {
     size_t o = 0;
     for (int i = 0; i < 5; i++) {
       if (!quant_type_ok(types[i]))
-        return fail(kErrParams, "model: blk.%d matrix %d has type %d; Q4_0 and Q8_0 are supported", l, i, types[i]);
+        return fail(kErrParams, "model: blk.%d matrix %d has type %d; Q4_0, Q8_0 and Q4_K are supported", l, i,
+                    types[i]);
       m->layer_off[(size_t)l * 5 + i] = o;
       o += align256(ss_hip_packed_bytes(types[i], rows[i], cols[i]));
     }
@@ -1572,6 +1587,9 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
   };
 
   // weights
+  m->any_q4k = d->token_embd.type == SS_HIP_Q4_K || (d->output.data && d->output.type == SS_HIP_Q4_K);
+  for (int i = 0; i < m->L * SS_HIP_LAYER_TENSORS; i++)
+    if (d->layers[i].data && d->layers[i].type == SS_HIP_Q4_K) m->any_q4k = true;
   if (!d->token_embd.data || d->token_embd.cols != m->d || d->token_embd.rows < m->vocab) {
     fail(kErrParams, "model: token_embd must be [>= vocab x hidden]");
     return bail();
@@ -1788,7 +1806,7 @@ int32_t ss_hip_eval_prompt(ss_hip_model_t* m, const int32_t* tokens, int32_t n, 
   HIP_TRY(hipMemcpy(m->tokens + start, tokens, sizeof(int) * n, hipMemcpyHostToDevice));
   HIP_TRY(ssk::launch_set_state(m->dpos, m->tokens, start, tokens[0], s));
   const int pf_min = m->pf_min > 0 ? m->pf_min : kPrefillMin;
-  if (m->kv_type == 0 && m->pf_min >= 0 && n >= pf_min) {
+  if (m->kv_type == 0 && m->pf_min >= 0 && n >= pf_min && !m->any_q4k) {
     if (int32_t rc = prefill_setup(m)) return rc;
     if (int32_t rc = enqueue_prompt_rows(m, tokens, n, start)) {
       hipStreamSynchronize(s);
@@ -1835,7 +1853,7 @@ int32_t ss_hip_embed(ss_hip_model_t* m, const int32_t* tokens, int32_t n, float*
   HIP_TRY(hipMemsetAsync(m->emb, 0, sizeof(float) * m->d, s));
   m->host_pos = -1;   // the cache holds positions 0..n-1, but no token to continue from
   int32_t rc = 0;
-  if (m->kv_type == 0 && m->pf_min >= 0) {
+  if (m->kv_type == 0 && m->pf_min >= 0 && !m->any_q4k) {
     int T = 0;
     rc = prefill_setup(m);
     if (!rc) rc = enqueue_rows(m, n, 0, true, &T);

@@ -16,10 +16,15 @@ enum Epi : int {
   EPI_LOGITS = 4,  // y[r] = W x, plus one first-max argmax candidate per workgroup in part[]
 };
 
-// A packed Q4_0/Q8_0 matrix on the device: code plane then scale plane.
+// ggml type of the K-quant with 4-bit codes (256-weight super-blocks)
+constexpr int kQ4K = 12;
+
+// A packed Q4_0/Q8_0/Q4_K matrix on the device: code plane, scale plane
+// and, for Q4_K, a super-block plane (see ss_gemv.hip).
 struct PackedMat {
   const uint8_t* qs;
   const uint16_t* ds;
+  const uint32_t* su = nullptr;
 };
 
 struct GemvArgs {
@@ -135,8 +140,8 @@ int attn_round_positions(int head_dim, int group);
 // attention workgroups of this shape resident on one compute unit (0: unknown)
 int attn_resident_groups(int head_dim, int group, int kv_type);
 
-hipError_t launch_pack(int type, const uint8_t* src, uint8_t* qs, uint16_t* ds, int64_t nblocks,
-                       int nb, int64_t row_off, hipStream_t s);
+hipError_t launch_pack(int type, const uint8_t* src, PackedMat dst, int64_t nblocks, int nb, int64_t row_off,
+                       hipStream_t s);
 // With xr set, also the x records of row * nw (xrec_words(cols) words).
 hipError_t launch_embed(int type, PackedMat t, int cols, const int* tokens, const int* dpos,
                         int token, float* out, const float* nw, uint32_t* xr, hipStream_t s);

@@ -17,8 +17,10 @@
 
 namespace ssk {
 
-// Weights and cache of one decoder layer on the device.
-struct SweepLayer {
+// Weights and cache of one decoder layer on the device. 16-byte aligned:
+// the kernel copies the descriptors into shared memory in 16-byte units and
+// reads them back as an array, so the array stride must be such a multiple.
+struct alignas(16) SweepLayer {
   PackedMat qkv, o, gate, up, down;   // [Wq;Wk;Wv] packed as one matrix
   const float* attn_norm;
   const float* ffn_norm;

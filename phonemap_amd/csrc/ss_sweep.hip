@@ -75,6 +75,8 @@ __host__ __device__ constexpr int attn_rows_per_lane_s(int group) {
 // saturated.
 constexpr int kArgWords = ((int)sizeof(SweepArgs) + 15) / 16 * 4;
 constexpr int kLayerWords = ((int)sizeof(SweepLayer) + 15) / 16 * 4;
+static_assert(kLayerWords * 4 == (int)sizeof(SweepLayer), "descriptor copy stride != SweepLayer array stride");
+static_assert(kArgWords * 4 >= (int)sizeof(SweepArgs), "argument block larger than its shared-memory slot");
 
 struct LdsPlan {
   int params, x, red, hrow;   // words

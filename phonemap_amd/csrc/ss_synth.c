@@ -20,6 +20,7 @@
 #define T_F32 0
 #define T_Q4_0 2
 #define T_Q8_0 8
+#define T_Q4_K 12
 #define CHUNK_BLOCKS (1u << 18)   /* 256 Ki blocks per work item */
 
 typedef struct {
@@ -143,7 +144,13 @@ typedef struct {
     int failed;
 } job_t;
 
-static uint64_t tensor_blocks(const syn_tensor_t *t) { return t->dims[0] * t->dims[1] / 32; }
+/* quantisation blocks of a matrix: 32 weights (Q4_0, Q8_0) or 256 (Q4_K) */
+static uint64_t tensor_blocks(const syn_tensor_t *t) {
+    return t->dims[0] * t->dims[1] / (t->type == T_Q4_K ? 256 : 32);
+}
+static size_t block_bytes(int32_t type) { return type == T_Q4_0 ? 18 : type == T_Q8_0 ? 34 : 144; }
+/* blocks per work item: Q4_K super-blocks are 8 blocks of 32 weights */
+static uint64_t chunk_blocks(int32_t type) { return type == T_Q4_K ? CHUNK_BLOCKS / 8 : CHUNK_BLOCKS; }
 
 static void gen_item(job_t *j, uint64_t it, uint8_t *buf) {
     const syn_tensor_t *t = &j->t[j->item_tensor[it]];
@@ -170,21 +177,52 @@ static void gen_item(job_t *j, uint64_t it, uint8_t *buf) {
         for (uint64_t i = 0; i < ne; i++) f[i] = (float)(1.0 + j->norm_sigma * xo_normal(&x));
         n = ne * 4;
     } else {
-        uint64_t nb = tensor_blocks(t), b0 = chunk * CHUNK_BLOCKS;
-        uint64_t b1 = b0 + CHUNK_BLOCKS < nb ? b0 + CHUNK_BLOCKS : nb;
-        size_t bb = t->type == T_Q4_0 ? 18 : 34;
+        const uint64_t cb = chunk_blocks(t->type);
+        uint64_t nb = tensor_blocks(t), b0 = chunk * cb;
+        uint64_t b1 = b0 + cb < nb ? b0 + cb : nb;
+        size_t bb = block_bytes(t->type);
         /* mode 0: int8 codes spread 16 times as wide as nibbles, so both
          * types give weights of the same spread. mode 1: signed d with the
          * weights' standard deviation 1/sqrt(cols), the RMS of the codes
          * being sqrt(21.5) for Q4_0 (nibble - 8) and sqrt(127*128/3) for
          * uniform int8 in [-127, 127]. */
         double sigma;
-        if (j->scale_mode == 1)
+        if (t->type == T_Q4_K) {
+            /* weight d*sc*q - dmin*m with sc, m uniform 0..63 and q 0..15:
+             * RMS sigma * sqrt(E[sc^2] (E[q^2] + 1)) = sigma * 323.5 */
+            sigma = j->scale_mode == 1 ? 1.0 / (323.5 * sqrt((double)t->dims[0])) : j->scale_sigma / 64.0;
+        } else if (j->scale_mode == 1) {
             sigma = 1.0 / ((t->type == T_Q4_0 ? sqrt(21.5) : sqrt(127.0 * 128.0 / 3.0)) *
                            sqrt((double)t->dims[0]));
-        else
+        } else {
             sigma = t->type == T_Q4_0 ? j->scale_sigma : j->scale_sigma / 16.0;
-        for (uint64_t b = b0; b < b1; b++) {
+        }
+        for (uint64_t b = b0; b < b1 && t->type == T_Q4_K; b++) {
+            /* Q4_K super-block: d, dmin, 8 random 6-bit scales and mins in
+             * the 12-byte K-quant packing, 128 bytes of random nibbles */
+            uint8_t *p = buf + (b - b0) * bb;
+            const double dv = sigma * xo_normal(&x), mv = sigma * xo_normal(&x);
+            const uint16_t d = to_f16((float)(j->scale_mode == 1 ? dv : fabs(dv)));
+            const uint16_t dm = to_f16((float)(j->scale_mode == 1 ? mv : fabs(mv)));
+            memcpy(p, &d, 2);
+            memcpy(p + 2, &dm, 2);
+            uint8_t sc[8], mn[8];
+            const uint64_t rs = xo_next(&x), rm = xo_next(&x);
+            for (int i = 0; i < 8; i++) {
+                sc[i] = (uint8_t)((rs >> (6 * i)) & 63);
+                mn[i] = (uint8_t)((rm >> (6 * i)) & 63);
+            }
+            for (int i = 0; i < 4; i++) {
+                p[4 + i] = (uint8_t)((sc[i] & 63) | ((sc[4 + i] >> 4) << 6));
+                p[8 + i] = (uint8_t)((mn[i] & 63) | ((mn[4 + i] >> 4) << 6));
+                p[12 + i] = (uint8_t)((sc[4 + i] & 15) | ((mn[4 + i] & 15) << 4));
+            }
+            for (int i = 0; i < 16; i++) {
+                const uint64_t q = xo_next(&x);
+                memcpy(p + 16 + 8 * i, &q, 8);
+            }
+        }
+        for (uint64_t b = b0; b < b1 && t->type != T_Q4_K; b++) {
             uint8_t *p = buf + (b - b0) * bb;
             const double dv = sigma * xo_normal(&x);
             uint16_t d = to_f16((float)(j->scale_mode == 1 ? dv : fabs(dv)));
@@ -230,9 +268,12 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
     if (s->n_layers <= 0 || s->hidden <= 0 || s->n_heads <= 0 || s->n_kv_heads <= 0 ||
         s->head_dim <= 0 || s->ffn <= 0 || s->vocab <= 3 || s->hidden % 32 || s->ffn % 32 ||
         (s->n_heads * s->head_dim) % 32 || (s->n_kv_heads * s->head_dim) % 32 ||
-        (s->layer_type != T_Q4_0 && s->layer_type != T_Q8_0) ||
-        (s->embd_type != T_Q4_0 && s->embd_type != T_Q8_0) ||
-        (s->out_type != -1 && s->out_type != T_Q4_0 && s->out_type != T_Q8_0) ||
+        (s->layer_type != T_Q4_0 && s->layer_type != T_Q8_0 && s->layer_type != T_Q4_K) ||
+        (s->embd_type != T_Q4_0 && s->embd_type != T_Q8_0 && s->embd_type != T_Q4_K) ||
+        (s->out_type != -1 && s->out_type != T_Q4_0 && s->out_type != T_Q8_0 && s->out_type != T_Q4_K) ||
+        /* Q4_K rows are whole super-blocks of 256 */
+        (s->layer_type == T_Q4_K && (s->hidden % 256 || s->ffn % 256 || (s->n_heads * s->head_dim) % 256)) ||
+        ((s->embd_type == T_Q4_K || s->out_type == T_Q4_K) && s->hidden % 256) ||
         s->arch < 0 || s->arch > 1 || s->qkv_bias < 0 || s->qkv_bias > 2 || s->scale_mode < 0 ||
         s->scale_mode > 1)
         return -5;
@@ -258,6 +299,7 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
         t[k].sid = (isnorm) == 2 ? 0x100000u + (uint64_t)k : sid++;                 \
         t[k].bytes = (isnorm) == 2 ? (uint64_t)(cols) * ((type_) == T_F16 ? 2 : 4)   \
                      : (isnorm) ? (uint64_t)(cols) * 4                               \
+                     : (type_) == T_Q4_K ? (uint64_t)(cols) * (rows) / 256 * 144     \
                                 : (uint64_t)(cols) * (rows) / 32 * ((type_) == T_Q4_0 ? 18 : 34); \
         k++;                                                                         \
     } while (0)
@@ -374,13 +416,13 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
     j.nt = nt;
     uint64_t items = 0;
     for (int i = 0; i < nt; i++)
-        items += t[i].norm ? 1 : (tensor_blocks(&t[i]) + CHUNK_BLOCKS - 1) / CHUNK_BLOCKS;
+        items += t[i].norm ? 1 : (tensor_blocks(&t[i]) + chunk_blocks(t[i].type) - 1) / chunk_blocks(t[i].type);
     j.item_tensor = (uint64_t *)malloc(items * 8);
     j.item_chunk = (uint64_t *)malloc(items * 8);
     if (!j.item_tensor || !j.item_chunk) rc = -3;
     uint64_t it = 0;
     for (int i = 0; rc == 0 && i < nt; i++) {
-        uint64_t nc = t[i].norm ? 1 : (tensor_blocks(&t[i]) + CHUNK_BLOCKS - 1) / CHUNK_BLOCKS;
+        uint64_t nc = t[i].norm ? 1 : (tensor_blocks(&t[i]) + chunk_blocks(t[i].type) - 1) / chunk_blocks(t[i].type);
         for (uint64_t c = 0; c < nc; c++) { j.item_tensor[it] = (uint64_t)i; j.item_chunk[it] = c; it++; }
     }
     j.n_items = items;

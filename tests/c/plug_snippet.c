@@ -19,6 +19,7 @@
 
 #define GGML_TYPE_Q4_0 2
 #define GGML_TYPE_Q8_0 8
+#define GGML_TYPE_Q4_K 12
 
 typedef struct { ss_hip_ctx_t *hip_ctx; } sched_t;
 
@@ -32,7 +33,7 @@ static void cpu_dequant_matvec(float *out, int32_t rows) {
 static void matmul_dispatch(sched_t *sched, float *out, const void *mat, const float *vec, int32_t rows,
                             int32_t cols, int32_t type) {
     if (sched->hip_ctx && ss_hip_should_use_gpu(rows, cols) &&
-        (type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0)) {
+        (type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0 || type == GGML_TYPE_Q4_K)) {
         /* true (nonzero) = out holds the result, as gpu_success for Metal */
         bool gpu_success = ss_hip_matvec_host(sched->hip_ctx, out, mat, vec, rows, cols, type) != 0;
         if (gpu_success) return;         /* else fall through to the CPU path */

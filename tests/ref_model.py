@@ -38,8 +38,7 @@ def _matrix(raw, data, dims, ttype, off):
     cols, rows = int(dims[0]), int(dims[1])
     if ttype in (0, 1):
         return _vector(raw, data, dims, ttype, off).reshape(rows, cols)
-    bb = {2: 18, 8: 34}[ttype]
-    nbytes = rows * (cols // 32) * bb
+    nbytes = rows * cols // 256 * 144 if ttype == 12 else rows * (cols // 32) * {2: 18, 8: 34}[ttype]
     blocks = np.frombuffer(raw, np.uint8, nbytes, data + off)
     return dequant_np(blocks, rows, cols, ttype)
 

@@ -45,6 +45,7 @@ VARIANTS = {
     "qwen2_f32_bias": dict(arch=1, qkv_bias=1, seed=25),
     "qwen2_f16_bias_fused": dict(arch=1, qkv_bias=2, fused_qkv=1, seed=26),
     "mha_hd64": dict(n_heads=4, n_kv_heads=4, head_dim=64, seed=27),
+    "q4_k": dict(layer_type=12, embd_type=12, out_type=12, seed=28),
 }
 
 

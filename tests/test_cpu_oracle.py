@@ -349,3 +349,74 @@ def test_sample_uniform_draw_index():
         j = int(np.floor(r * V))
         if abs(r * V - round(r * V)) > 1e-3:   # away from a cell boundary
             assert i == j
+
+
+# ---------------------------------------------------------------- Q4_K
+def _q4k_expected(d, dmin, sc, mn, q):
+    """The reference's fp32 arithmetic for one super-block (quantize.c:287-307):
+    d1 = d * sc, m1 = dmin * m, weight = d1 * q - m1, each rounded to fp32."""
+    out = np.zeros(256, np.float32)
+    df, mf = np.float32(np.float16(d)), np.float32(np.float16(dmin))
+    for k in range(8):
+        d1 = np.float32(df * np.float32(sc[k]))
+        m1 = np.float32(mf * np.float32(mn[k]))
+        for l in range(32):
+            out[32 * k + l] = np.float32(np.float32(d1 * np.float32(q[k][l])) - m1)
+    return out
+
+
+@pytest.mark.parametrize("case", range(6))
+def test_q4_K_dequant_known_blocks(case):
+    """Hand-built super-blocks (packed from chosen scales, mins and nibbles by
+    the format definition, tests/util.q4k_pack_scales) dequantise to exactly
+    d*sc*q - dmin*m: every scale and min bit position is exercised (values
+    0, 63, and patterns whose top two bits differ)."""
+    from tests.util import q4k_block
+    rng = np.random.default_rng(case)
+    scs = [[1] * 8, [63] * 8, [0, 63, 16, 47, 32, 15, 48, 31], list(rng.integers(0, 64, 8)),
+           [5, 9, 17, 33, 48, 60, 2, 40], list(rng.integers(0, 64, 8))]
+    mns = [[0] * 8, [63] * 8, [63, 0, 47, 16, 31, 48, 15, 32], list(rng.integers(0, 64, 8)),
+           [40, 2, 60, 48, 33, 17, 9, 5], list(rng.integers(0, 64, 8))]
+    ds = [1.0, 0.5, -0.0078125, 0.0123, -2.0, 6.1e-5]
+    dms = [0.0, 0.25, 0.001, -0.5, 0.0625, -3.0e-5]
+    q = [[(k * 5 + l) % 16 for l in range(32)] for k in range(8)] if case % 2 == 0 else \
+        [list(rng.integers(0, 16, 32)) for _ in range(8)]
+    blk = q4k_block(ds[case], dms[case], scs[case], mns[case], q)
+    got = oracle.dequantize(blk, 256, 12)
+    want = _q4k_expected(ds[case], dms[case], scs[case], mns[case], q)
+    assert np.array_equal(got, want)
+
+
+def test_q4_K_identity_block():
+    """d = 1, every scale 1 and min 0: the weights are the nibbles themselves,
+    sub-block 2j from the low and 2j+1 from the high nibbles of bytes 32j.."""
+    from tests.util import q4k_block
+    q = [[(3 * k + l) % 16 for l in range(32)] for k in range(8)]
+    blk = q4k_block(1.0, 0.0, [1] * 8, [0] * 8, q)
+    got = oracle.dequantize(blk, 256, 12)
+    assert np.array_equal(got, np.array(q, np.float32).reshape(-1))
+    # the raw bytes: low nibble of byte 16 + l is weight l of sub-block 0
+    assert (blk[16] & 15) == q[0][0] and (blk[16] >> 4) == q[1][0]
+
+
+def test_q4_K_scale_unpack_round_trip():
+    from tests.util import q4k_pack_scales, q4k_unpack_scales
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        sc, mn = rng.integers(0, 64, 8), rng.integers(0, 64, 8)
+        s2, m2 = q4k_unpack_scales(q4k_pack_scales(sc, mn))
+        assert np.array_equal(s2, sc) and np.array_equal(m2, mn)
+
+
+@pytest.mark.parametrize("rows,cols", [(3, 256), (37, 1024), (16, 4096)])
+def test_q4_K_matvec_fp64(rows, cols):
+    from tests.util import Q4_K, dequant_np, make_q4_k
+    rng = np.random.default_rng(rows)
+    w = make_q4_k(rows, cols, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = oracle.matvec(w, x, rows, cols, Q4_K)
+    want = dequant_np(w, rows, cols, Q4_K) @ x.astype(np.float64)
+    assert np.max(np.abs(got - want)) / np.max(np.abs(want)) < 1e-5
+    # the numpy decoder is the oracle's dequantisation, value for value
+    deq = oracle.dequantize(w[:144], 256, Q4_K)
+    assert np.allclose(deq, dequant_np(w[:144], 1, 256, Q4_K)[0], rtol=1e-6, atol=1e-9)

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.util import Q4_0, Q8_0, make_blocks, rel_err
+from tests.util import Q4_0, Q4_K, Q8_0, make_blocks, rel_err
 
 pytestmark = pytest.mark.gpu
 EXE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c", "plug_snippet")
@@ -27,7 +27,8 @@ def _run(tmp_path, w, x, rows, cols, qtype):
     return int(r.stdout.split()[-1]), np.fromfile(yp, np.float32)
 
 
-@pytest.mark.parametrize("qtype,rows,cols", [(Q4_0, 512, 4096), (Q8_0, 1000, 2048), (Q4_0, 33, 96)])
+@pytest.mark.parametrize("qtype,rows,cols", [(Q4_0, 512, 4096), (Q8_0, 1000, 2048), (Q4_0, 33, 96),
+                                             (Q4_K, 700, 4096), (Q4_K, 33, 256)])
 def test_plug_snippet_matches_oracle(tmp_path, qtype, rows, cols):
     rng = np.random.default_rng(rows + cols)
     w = make_blocks(qtype, rows, cols, rng)
@@ -37,8 +38,10 @@ def test_plug_snippet_matches_oracle(tmp_path, qtype, rows, cols):
     assert rel_err(y, oracle.matvec(w, x, rows, cols, qtype)) <= 1e-3
 
 
-def test_plug_snippet_rejected_shape_falls_back(tmp_path):
-    rows, cols = 64, 40          # not a whole number of 32-weight blocks: the plug says false
-    fallbacks, y = _run(tmp_path, np.zeros(rows * 2 * 18, np.uint8), np.ones(cols, np.float32), rows, cols, Q4_0)
+@pytest.mark.parametrize("qtype,cols", [(Q4_0, 40), (Q4_K, 288)])
+def test_plug_snippet_rejected_shape_falls_back(tmp_path, qtype, cols):
+    # not a whole number of blocks (32 weights) or super-blocks (256): the plug says false
+    rows = 64
+    fallbacks, y = _run(tmp_path, np.zeros(rows * 10 * 18, np.uint8), np.ones(cols, np.float32), rows, cols, qtype)
     assert fallbacks == 2
     assert np.all(y == -1.0)

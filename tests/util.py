@@ -4,7 +4,7 @@ import ctypes as C
 
 import numpy as np
 
-Q4_0, Q8_0 = 2, 8
+Q4_0, Q8_0, Q4_K = 2, 8, 12
 
 
 def _vp(a):
@@ -35,8 +35,68 @@ def make_q8_0(rows, cols, rng, sigma=0.02):
     return blk.reshape(-1)
 
 
+def q4k_pack_scales(sc, mn):
+    """The 12-byte scale array of a Q4_K super-block from eight 6-bit scales
+    and mins, laid out as the GGML K-quant format defines it: bytes 0-3 hold
+    scales 0-3 in their low 6 bits and the top 2 bits of scales 4-7 above
+    them; bytes 4-7 the same for the mins; bytes 8-11 hold scale 4+i in the
+    low nibble and min 4+i in the high nibble (their low 4 bits)."""
+    b = np.zeros(12, np.uint8)
+    for i in range(4):
+        b[i] = (sc[i] & 63) | ((sc[4 + i] >> 4) << 6)
+        b[4 + i] = (mn[i] & 63) | ((mn[4 + i] >> 4) << 6)
+        b[8 + i] = (sc[4 + i] & 15) | ((mn[4 + i] & 15) << 4)
+    return b
+
+
+def q4k_block(d, dmin, sc, mn, q):
+    """One 144-byte Q4_K super-block: fp16 d and dmin, 8 scales and mins
+    (0..63), q[8][32] nibbles: sub-block 2j in the low and 2j+1 in the high
+    nibbles of bytes 32j..32j+31."""
+    blk = np.zeros(144, np.uint8)
+    blk[0:2] = np.array([d], np.float16).view(np.uint8)
+    blk[2:4] = np.array([dmin], np.float16).view(np.uint8)
+    blk[4:16] = q4k_pack_scales(sc, mn)
+    q = np.asarray(q, np.uint8)
+    for j in range(4):
+        blk[16 + 32 * j:16 + 32 * j + 32] = (q[2 * j] & 15) | ((q[2 * j + 1] & 15) << 4)
+    return blk
+
+
+def make_q4_k(rows, cols, rng, sigma=0.02):
+    """GGUF Q4_K super-blocks: d, dmin = fp16(N(0, sigma / 32)), random 6-bit
+    scales and mins, uniform nibbles."""
+    nsb = rows * (cols // 256)
+    out = np.zeros((nsb, 144), np.uint8)
+    d = f16_bits(rng.normal(0.0, sigma / 32, nsb))
+    dm = f16_bits(rng.normal(0.0, sigma / 32, nsb))
+    out[:, 0:2] = d.view(np.uint8).reshape(nsb, 2)
+    out[:, 2:4] = dm.view(np.uint8).reshape(nsb, 2)
+    sc = rng.integers(0, 64, (nsb, 8))
+    mn = rng.integers(0, 64, (nsb, 8))
+    for i in range(nsb):
+        out[i, 4:16] = q4k_pack_scales(sc[i], mn[i])
+    out[:, 16:] = rng.integers(0, 256, (nsb, 128), dtype=np.uint8)
+    return out.reshape(-1)
+
+
 def make_blocks(qtype, rows, cols, rng, sigma=0.02):
+    if qtype == Q4_K:
+        return make_q4_k(rows, cols, rng, sigma)
     return make_q4_0(rows, cols, rng, sigma) if qtype == Q4_0 else make_q8_0(rows, cols, rng, sigma)
+
+
+def q4k_unpack_scales(b):
+    """Inverse of q4k_pack_scales (per the format definition): (sc[8], mn[8])."""
+    b = np.asarray(b, np.int64)
+    sc = np.zeros(8, np.int64)
+    mn = np.zeros(8, np.int64)
+    for i in range(4):
+        sc[i] = b[i] & 63
+        mn[i] = b[4 + i] & 63
+        sc[4 + i] = (b[8 + i] & 15) | ((b[i] >> 6) << 4)
+        mn[4 + i] = (b[8 + i] >> 4) | ((b[4 + i] >> 6) << 4)
+    return sc, mn
 
 
 def dequant_np(blocks, rows, cols, qtype):
@@ -49,10 +109,22 @@ def dequant_np(blocks, rows, cols, qtype):
         lo = (q & 0xF).astype(np.int64) - 8
         hi = (q >> 4).astype(np.int64) - 8
         w = np.concatenate([lo, hi], axis=1) * d[:, None]
-    else:
+    elif qtype == Q8_0:
         b = blocks.reshape(rows * nb, 34)
         d = b[:, 0:2].copy().view(np.float16).astype(np.float64).reshape(-1)
         w = b[:, 2:].view(np.int8).astype(np.float64) * d[:, None]
+    else:   # Q4_K super-blocks of 256
+        nsb = rows * (cols // 256)
+        b = blocks.reshape(nsb, 144)
+        d = b[:, 0:2].copy().view(np.float16).astype(np.float64).reshape(-1)
+        dm = b[:, 2:4].copy().view(np.float16).astype(np.float64).reshape(-1)
+        w = np.zeros((nsb, 256))
+        for i in range(nsb):
+            sc, mn = q4k_unpack_scales(b[i, 4:16])
+            q = b[i, 16:].astype(np.int64)
+            for k in range(8):
+                nib = (q[32 * (k // 2):32 * (k // 2) + 32] >> (4 * (k % 2))) & 15
+                w[i, 32 * k:32 * k + 32] = d[i] * sc[k] * nib - dm[i] * mn[k]
     return w.reshape(rows, cols)
 
 
