@@ -56,6 +56,10 @@ typedef struct {
                            * of two); 0 = 32, the only alignment the reference reads */
     int32_t scale_mode;   /* block scale distribution, see above: 0 |N(0, scale_sigma)|,
                            * 1 signed fan-in scaled */
+    int32_t vocab_tokens; /* with with_vocab: tokenizer strings written, when in [1, vocab)
+                           * (0 = vocab). Fewer than vocab leaves token_embd/output rows past
+                           * the vocabulary, as padded tables do; the loaders clamp the
+                           * vocabulary to the tokenizer (layer_scheduler.c:186-197). */
 } ss_synth_spec_t;
 
 /* Returns 0, or a negative ss_error_t value (-5 bad spec, -1 cannot write). */

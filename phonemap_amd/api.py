@@ -51,7 +51,8 @@ class SynthSpec(C.Structure):         # ss_synth.h
                 ("rope_theta", _f32), ("rms_eps", _f32), ("layer_type", _i32), ("embd_type", _i32),
                 ("out_type", _i32), ("seed", _u64), ("scale_sigma", _f32), ("norm_sigma", _f32),
                 ("with_vocab", _i32), ("n_threads", _i32), ("arch", _i32), ("fused_qkv", _i32),
-                ("fused_up", _i32), ("qkv_bias", _i32), ("alignment", _i32), ("scale_mode", _i32)]
+                ("fused_up", _i32), ("qkv_bias", _i32), ("alignment", _i32), ("scale_mode", _i32),
+                ("vocab_tokens", _i32)]
 
     def __init__(self, **kw):
         d = dict(rope_theta=10000.0, rms_eps=1e-5, layer_type=2, embd_type=2, out_type=2, seed=0,

@@ -888,6 +888,11 @@ hipError_t timed(ss_hip_model* m, int cls, double bytes, F&& launch) {
   return e;
 }
 
+// Rows the LM-head table was packed with: the embedding's (tied, possibly
+// more than the vocabulary) or the vocabulary (output.weight is packed
+// clamped). The packed planes' offsets depend on it.
+int out_rows(const ss_hip_model* m) { return m->out == m->embd ? m->embd_rows : m->vocab; }
+
 int q_class(int type) { return type == SS_HIP_Q8_0 ? PC_Q8 : PC_Q4; }   // 4-bit codes: Q4_0 and Q4_K
 
 // Algorithmic HBM bytes of one token at context ctx: every weight byte once
@@ -921,7 +926,7 @@ int32_t sweep_setup(ss_hip_model* m) {
   ssk::SweepArgs& a = m->sw;
   memset(&a, 0, sizeof(a));
   a.embd = view(m->embd, m->t_embd, m->embd_rows, m->d);
-  a.out = view(m->out, m->t_out, m->out == m->embd ? m->embd_rows : m->vocab, m->d);
+  a.out = view(m->out, m->t_out, out_rows(m), m->d);
   a.embd_type = m->t_embd;
   a.out_norm = m->out_norm;
   a.rope_cs = m->rope_cs;
@@ -1135,6 +1140,7 @@ int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden,
 int32_t enqueue_head(ss_hip_model* m, const float* hidden, const uint32_t* xr) {
   hipStream_t s = m->ctx->stream;
   ssk::GemvArgs h = gemv_args(m->out, hidden, m->logits, m->vocab, m->d, m->t_out);
+  h.w = view(m->out, m->t_out, out_rows(m), m->d);   // the first vocab rows of the table
   h.nw = m->out_norm;
   h.eps = m->eps;
   h.xr = xr;

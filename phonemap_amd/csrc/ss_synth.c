@@ -82,6 +82,11 @@ static uint16_t to_f16(float f) {    /* IEEE binary16, round to nearest even */
     return (uint16_t)(sign | h);
 }
 
+/* tokenizer strings written: vocab_tokens when set (a table with rows past the vocabulary) */
+static int32_t n_tokens(const ss_synth_spec_t *s) {
+    return s->vocab_tokens > 0 && s->vocab_tokens < s->vocab ? s->vocab_tokens : s->vocab;
+}
+
 /* ---- synthetic SentencePiece-style vocabulary ---- */
 static void word_of(uint64_t n, char *out) {   /* bijective base-26: a..z, aa, ab, ... */
     char tmp[16];
@@ -368,17 +373,18 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
     kv_f32(&b, AK("attention.layer_norm_rms_epsilon"), s->rms_eps > 0 ? s->rms_eps : 1e-5f);
     if (s->with_vocab) {
         char vb[64];
+        const int32_t nv = n_tokens(s);
         kv_str(&b, "tokenizer.ggml.model", "llama");
         wb_str(&b, "tokenizer.ggml.tokens");
         wb_u32(&b, 9);
         wb_u32(&b, 8);
-        wb_u64(&b, (uint64_t)s->vocab);
-        for (int i = 0; i < s->vocab; i++) wb_str(&b, ss_synth_vocab_string(s->vocab, i, vb, sizeof(vb)));
+        wb_u64(&b, (uint64_t)nv);
+        for (int i = 0; i < nv; i++) wb_str(&b, ss_synth_vocab_string(nv, i, vb, sizeof(vb)));
         wb_str(&b, "tokenizer.ggml.scores");
         wb_u32(&b, 9);
         wb_u32(&b, 6);
-        wb_u64(&b, (uint64_t)s->vocab);
-        for (int i = 0; i < s->vocab; i++) wb_f32(&b, i < 259 ? 0.0f : -(float)(i - 259) * 0.01f);
+        wb_u64(&b, (uint64_t)nv);
+        for (int i = 0; i < nv; i++) wb_f32(&b, i < 259 ? 0.0f : -(float)(i - 259) * 0.01f);
     }
 #undef AK
     for (int i = 0; i < nt;) {

@@ -46,6 +46,9 @@ VARIANTS = {
     "qwen2_f16_bias_fused": dict(arch=1, qkv_bias=2, fused_qkv=1, seed=26),
     "mha_hd64": dict(n_heads=4, n_kv_heads=4, head_dim=64, seed=27),
     "q4_k": dict(layer_type=12, embd_type=12, out_type=12, seed=28),
+    # tokenizer shorter than the tables: the vocabulary is clamped to it
+    "padded_tied": dict(embd_type=2, out_type=-1, vocab_tokens=360, seed=29),
+    "padded_out": dict(vocab_tokens=370, seed=30),
 }
 
 
@@ -86,6 +89,19 @@ def test_oracle_forward_and_prefill_match_fp64_restatement(tmp_path, name, kv):
     worst, same = _run(path, kv, ref)
     assert worst <= BAR[kv], worst
     assert same
+
+
+@pytest.mark.parametrize("name", ["padded_tied", "padded_out"])
+def test_vocab_clamped_to_the_tokenizer(tmp_path, name):
+    """layer_scheduler.c:186-197: the vocabulary is the tokenizer's size when
+    the embedding/output tables have more rows; logits cover it only."""
+    path = str(tmp_path / (name + ".gguf"))
+    api.write_synthetic_gguf(path, _spec(**VARIANTS[name]))
+    ref = RefModel(path, 64)
+    assert ref.vocab == VARIANTS[name]["vocab_tokens"] < ref.embd.shape[0] == 400
+    om = oracle.Model(path, 64)
+    assert om.forward(5, 0).shape == (ref.vocab,)
+    om.close()
 
 
 @pytest.mark.parametrize("kv", ["f16", "int8"])

@@ -173,6 +173,40 @@ def test_streaming_matches_resident(spec, kv):
     om.close()
 
 
+PADDED_TIED = dict(TINY, vocab=560, vocab_tokens=500, out_type=-1, seed=5)
+PADDED_OUT = dict(TINY, vocab=560, vocab_tokens=510, seed=6)
+
+
+@pytest.mark.parametrize("launch", ["sweep", "graph"])
+@pytest.mark.parametrize("spec", ["padded_tied", "padded_out"])
+def test_tables_with_rows_past_the_vocabulary(spec, launch):
+    """Embedding/output tables with more rows than the tokenizer has strings:
+    the vocabulary is clamped (layer_scheduler.c:186-197), the LM head reads
+    the first vocab rows of the table as packed, and logits and greedy tokens
+    match the oracle's."""
+    kw = {"padded_tied": PADDED_TIED, "padded_out": PADDED_OUT}[spec]
+    path = _model_file(spec, **kw)
+    print("model", spec, launch, flush=True)
+    prompt = np.random.default_rng(8).integers(3, kw["vocab_tokens"], 10).tolist()
+    om = oracle.Model(path, 128)
+    with api.Model(path, max_context=128, launch=launch) as m:
+        assert m.vocab == kw["vocab_tokens"]
+        assert _launch_in_effect(m) == api.LAUNCH[launch]
+        lg, am = m.eval_prompt(prompt, 0)
+        olg = om.prefill(prompt, 0)
+        assert lg.shape == olg.shape == (kw["vocab_tokens"],)
+        assert rel_err(lg, olg) <= TOL
+        assert am == oracle.argmax(olg)
+        tok, pos = am, len(prompt)
+        for _ in range(12):
+            lg, am = m.eval_token(tok, pos)
+            olg = om.forward(tok, pos)
+            assert rel_err(lg, olg) <= TOL, pos
+            assert am == oracle.argmax(olg), pos
+            tok, pos = am, pos + 1
+    om.close()
+
+
 def test_kv_injection_matches_oracle():
     """KV pre-filled with random fp16 N(0,1) through ss_kv_write, then decode."""
     path = _model_file("gqa8", **GQA8)
