@@ -242,7 +242,7 @@ def main():
         roof = profile_classes(m, prof_steps)
         roof["timed_as"] = "eager replay; start/stop events recorded by each kernel's dispatch" 
         if args.config == "llama2-7b" and args.kv == "f16" and args.prompt_len is None:
-            roof["traffic"] = measured_traffic(roof["kernel_id"])   # counter runs of this workload
+            roof["traffic"], roof["traffic_from"] = measured_traffic(roof["kernel_id"])
     except Exception as e:   # profiling is optional for the headline number
         log("profiling failed: %s" % e)
 
@@ -396,20 +396,42 @@ def bench_matvec(args):
 TRAFFIC_FILES = {"sweep": "traffic_llama2-7b_sweep.md", "q4_0": "traffic_llama2-7b_q4_0_matvec.md"}
 
 
+def kernel_source_hash():
+    """sha256 (first 16 hex digits) of the HIP sources and headers of the
+    library (phonemap_amd/csrc/*.hip, *.h, sorted by name): the kernels a
+    counter profile was measured on."""
+    import hashlib
+    h = hashlib.sha256()
+    d = os.path.join(ROOT, "phonemap_amd", "csrc")
+    for name in sorted(os.listdir(d)):
+        if name.endswith((".hip", ".h")):
+            h.update(name.encode())
+            h.update(open(os.path.join(d, name), "rb").read())
+    return h.hexdigest()[:16]
+
+
 def measured_traffic(kernel_id):
     """HBM bytes per launch of the dominant kernel from the committed
     FETCH_SIZE/WRITE_SIZE counter runs (scaled by a copy kernel of known
-    size), or None."""
+    size), and the profile it came from; None when there is no profile or
+    it was measured on other library sources than these."""
     if kernel_id not in TRAFFIC_FILES:
-        return None
+        return None, None
     path = os.path.join(ROOT, "profiles", TRAFFIC_FILES[kernel_id])
+    fields = {}
     try:
         for line in open(path):
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":")[1])
+            k, sep, v = line.partition(":")
+            if sep and k in ("traffic_bytes_per_launch", "source_hash"):
+                fields[k] = v.strip()
     except OSError:
-        pass
-    return None
+        return None, None
+    name = "profiles/" + TRAFFIC_FILES[kernel_id]
+    if fields.get("source_hash") != kernel_source_hash():
+        return None, name + " (measured on other library sources: not used)"
+    if "traffic_bytes_per_launch" not in fields:
+        return None, None
+    return int(fields["traffic_bytes_per_launch"]), name + " (source_hash %s)" % fields["source_hash"]
 
 
 def profile_classes(m, n_steps):
