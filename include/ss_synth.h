@@ -21,8 +21,9 @@
  * gives every Q4_0 block the mean -d/2 (nibbles average 7.5 - 8): a shared
  * direction that, compounded over the layers, makes deep models emit nearly
  * the same logits for any input; mode 1 models respond to their input.
- * Norm weights are fp32 1 + N(0, norm_sigma); q/k/v biases (when asked for)
- * are N(0, 0.1).
+ * Norm weights are fp32 1 + N(0, norm_sigma) (Gemma: N(0, norm_sigma), the
+ * file format's weight minus one); q/k/v biases (when asked for) are
+ * N(0, 0.1).
  * The bytes depend only on the spec (seed included), not on n_threads.
  */
 #ifndef SS_SYNTH_H
@@ -48,7 +49,10 @@ typedef struct {
     int32_t n_threads;    /* 0 = hardware concurrency */
     /* Architecture variants. A variant changes no weight: a fused or biased
      * file holds the same matrices as the plain one with the same seed. */
-    int32_t arch;         /* 0: "llama"; 1: "qwen2" (NeoX RoPE, layer_scheduler.c:145-149) */
+    int32_t arch;         /* 0: "llama"; 1: "qwen2" (NeoX RoPE, layer_scheduler.c:145-149);
+                           * 2: "gemma" (norm weights N(0, norm_sigma), applied as 1 + w);
+                           * 3: "gemma2" (as 2, plus blk.N.post_attention_norm and
+                           * blk.N.post_ffw_norm, layer_scheduler.c:309-310) */
     int32_t fused_qkv;    /* blk.N.attn_qkv.weight = [Wq; Wk; Wv] in place of three tensors */
     int32_t fused_up;     /* blk.N.ffn_up.weight = [Wgate; Wup] (2 * ffn rows), no ffn_gate */
     int32_t qkv_bias;     /* blk.N.attn_q/k/v.bias: 0 none, 1 F32, 2 F16; values N(0, 0.1) */
@@ -60,6 +64,8 @@ typedef struct {
                            * (0 = vocab). Fewer than vocab leaves token_embd/output rows past
                            * the vocabulary, as padded tables do; the loaders clamp the
                            * vocabulary to the tokenizer (layer_scheduler.c:186-197). */
+    float attn_softcap;   /* > 0: <arch>.attn_logit_softcapping (layer_scheduler.c:446-448) */
+    float final_softcap;  /* > 0: <arch>.final_logit_softcapping (:674-676) */
 } ss_synth_spec_t;
 
 /* Returns 0, or a negative ss_error_t value (-5 bad spec, -1 cannot write). */

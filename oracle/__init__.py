@@ -43,6 +43,9 @@ def lib():
         "orc_rmsnorm": (None, [_vp, _vp, _vp, _i32, C.c_float]),
         "orc_softmax": (None, [_vp, _i32]),
         "orc_silu_mul": (C.c_float, [C.c_float, C.c_float]),
+        "orc_gemma_rmsnorm": (None, [_vp, _vp, _vp, _i32, C.c_float]),
+        "orc_gelu": (C.c_float, [C.c_float]),
+        "orc_softcap": (None, [_vp, _i32, C.c_float]),
         "orc_rope": (None, [_vp, _vp, _i32, _i32, _i32, _i32, _i32, C.c_float, _i32]),
         "orc_rope_table": (None, [_vp, _i32, _i32, C.c_float]),
         "orc_argmax": (_i32, [_vp, _i32]),
@@ -84,6 +87,8 @@ def ref():
     L.ss_neon_dot.argtypes = [_vp, _vp, _i32]
     L.ss_neon_rmsnorm.restype = None
     L.ss_neon_rmsnorm.argtypes = [_vp, _vp, _vp, _i32, C.c_float]
+    L.ss_neon_gemma_rmsnorm.restype = None
+    L.ss_neon_gemma_rmsnorm.argtypes = [_vp, _vp, _vp, _i32, C.c_float]
     L.ss_neon_silu.restype = None
     L.ss_neon_silu.argtypes = [_vp, _i32]
     L.ss_neon_matvec.restype = None
@@ -122,6 +127,25 @@ def rmsnorm(x, w, eps):
     out = np.zeros_like(x)
     lib().orc_rmsnorm(_ptr(out), _ptr(x), _ptr(w), x.size, eps)
     return out
+
+
+def gemma_rmsnorm(x, w, eps):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.zeros_like(x)
+    lib().orc_gemma_rmsnorm(_ptr(out), _ptr(x), _ptr(w), x.size, eps)
+    return out
+
+
+def gelu(x):
+    f = lib().orc_gelu
+    return np.array([f(float(v)) for v in np.asarray(x, np.float32).ravel()], np.float32)
+
+
+def softcap(x, cap):
+    x = np.array(x, np.float32)
+    lib().orc_softcap(_ptr(x), x.size, cap)
+    return x
 
 
 def rope(q, k, n_heads, n_kv_heads, head_dim, rope_dim, pos, theta, neox=False):

@@ -20,10 +20,15 @@
  *    are rounded to binary16 when appended and widened when read, inside the
  *    fp32 KV structure of layer_scheduler.c.orig:289-342.
  *  - The llama block and the branches the reference takes by tensor name or
- *    by architecture outside Gemma are restated: fused attn_qkv and fused
- *    ffn_up (layer_scheduler.c:337-347,518-524), q/k/v biases (:367-402) and
- *    NeoX RoPE pairs for qwen/falcon/phi/deepseek (:144-149). Gemma files
- *    are rejected.
+ *    by architecture are restated: fused attn_qkv and fused ffn_up
+ *    (layer_scheduler.c:337-347,518-524), q/k/v biases (:367-402), NeoX RoPE
+ *    pairs for qwen/falcon/phi/deepseek (:144-149), and for "gemma" files the
+ *    (1 + w) RMSNorm (tensor.c:133-152), the sqrt(d) embedding scale
+ *    (:597-602), GeGLU (:529-531, tensor.c:181-190) and the 1/sqrt(d) logit
+ *    scale (:667-672); post-attention / post-FFN norms wherever those
+ *    tensors exist (:474-481,553-560) and the attention / final logit
+ *    softcaps wherever the GGUF keys are set (:446-448,674-676,
+ *    tensor.c:194-200), as the reference applies them, for any architecture.
  *
  * Parity unpinned: the summation order of Apple vDSP_dotpr / cblas_saxpy
  * (system frameworks, no version pin; orc_dot's order is checked against the
@@ -231,6 +236,30 @@ void orc_softmax(float *x, int32_t n) {
 
 /* layer_scheduler.c:540-547: up * (g / (1 + exp(-g))) */
 float orc_silu_mul(float g, float u) { return u * (g / (1.0f + expf(-g))); }
+
+/* cpu_neon.c:153-158 (scalar branch of ss_neon_gemma_rmsnorm, reached through
+ * tensor.c:133-137 for F32 weights): the weight is applied as (w + 1). */
+void orc_gemma_rmsnorm(float *out, const float *x, const float *w, int32_t n, float eps) {
+    float ss = 0.0f;
+    for (int32_t i = 0; i < n; i++) ss += x[i] * x[i];
+    float scale = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int32_t i = 0; i < n; i++) out[i] = x[i] * scale * (w[i] + 1.0f);
+}
+
+/* tensor.c:181-190: tanh-form GELU, in place */
+float orc_gelu(float v) {
+    const float sqrt_2_over_pi = 0.7978845608028654f;
+    float cube = v * v * v;
+    float inner = sqrt_2_over_pi * (v + 0.044715f * cube);
+    return 0.5f * v * (1.0f + tanhf(inner));
+}
+
+/* tensor.c:194-200 */
+void orc_softcap(float *x, int32_t n, float cap) {
+    if (cap <= 0.0f) return;
+    float inv_cap = 1.0f / cap;
+    for (int32_t i = 0; i < n; i++) x[i] = cap * tanhf(x[i] * inv_cap);
+}
 
 /* tensor.c:220-275 */
 void orc_rope(float *q, float *k, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
@@ -659,6 +688,7 @@ typedef struct {
 typedef struct {
     const orc_tensor_t *attn_norm, *wq, *wk, *wv, *wo, *ffn_norm, *wg, *wu, *wd;
     const orc_tensor_t *wqkv, *bq, *bk, *bv;   /* fused [Wq;Wk;Wv]; Qwen biases (optional) */
+    const orc_tensor_t *post_attn_norm, *post_ffn_norm;   /* Gemma 2 (optional, :309-310) */
 } orc_layer_t;
 
 struct orc_model {
@@ -671,8 +701,8 @@ struct orc_model {
     const orc_tensor_t *embd, *out_norm, *out;
     char arch[64];
     uint32_t n_layers, d, n_heads, n_kv_heads, vocab_meta, ctx_len, ffn, key_len, rope_dim_meta;
-    float theta, eps;
-    int32_t hd, rope_dim, vocab, max_seq, kv_mode, kv_dim, neox;
+    float theta, eps, attn_softcap, final_softcap;
+    int32_t hd, rope_dim, vocab, max_seq, kv_mode, kv_dim, neox, gemma;
     /* KV cache, [L][max_seq][kv_dim] (+ per-(L,pos) scales in int8 mode) */
     int8_t *kq, *vq;
     float *ks, *vs;
@@ -830,6 +860,10 @@ static int parse_gguf(orc_model_t *m) {
             m->key_len = rd_u32(&r);
         } else if (key_ends(k, kl, ".rope.dimension_count") && vt == 4) {
             m->rope_dim_meta = rd_u32(&r);
+        } else if (key_ends(k, kl, ".attn_logit_softcapping") && vt == 6) {   /* gguf_loader.c:314-317 */
+            m->attn_softcap = rd_f32(&r);
+        } else if (key_ends(k, kl, ".final_logit_softcapping") && vt == 6) {
+            m->final_softcap = rd_f32(&r);
         } else if (key_is(k, kl, "tokenizer.ggml.tokens") && vt == 9) {
             uint32_t at = rd_u32(&r);
             uint64_t n = rd_u64(&r);
@@ -923,10 +957,7 @@ orc_model_t *orc_model_open(const char *path, int32_t max_seq, int32_t kv_mode) 
     if (m->base == MAP_FAILED) { m->base = NULL; orc_model_close(m); return NULL; }
     if (parse_gguf(m) != 0) { orc_model_close(m); return NULL; }
 
-    if (strstr(m->arch, "gemma")) {
-        orc_model_close(m);   /* the Gemma branches are not restated */
-        return NULL;
-    }
+    m->gemma = strstr(m->arch, "gemma") != NULL;                   /* :152-155 */
     /* layer_scheduler.c:144-149 */
     m->neox = strstr(m->arch, "qwen") || strstr(m->arch, "falcon") || strstr(m->arch, "phi") ||
               strstr(m->arch, "deepseek");
@@ -986,6 +1017,8 @@ orc_model_t *orc_model_open(const char *path, int32_t max_seq, int32_t kv_mode) 
         ly->bq = find_suffix(m, l, "attn_q.bias");
         ly->bk = find_suffix(m, l, "attn_k.bias");
         ly->bv = find_suffix(m, l, "attn_v.bias");
+        ly->post_attn_norm = find_suffix(m, l, "post_attention_norm.weight");
+        ly->post_ffn_norm = find_suffix(m, l, "post_ffw_norm.weight");
         int qkv_ok = ly->wqkv ? matrix_ok(ly->wqkv, qdim + 2 * (uint64_t)m->kv_dim, d)
                               : matrix_ok(ly->wq, qdim, d) && matrix_ok(ly->wk, m->kv_dim, d) &&
                                     matrix_ok(ly->wv, m->kv_dim, d);
@@ -994,7 +1027,9 @@ orc_model_t *orc_model_open(const char *path, int32_t max_seq, int32_t kv_mode) 
         if (!vector_ok(ly->attn_norm, d) || !qkv_ok || !matrix_ok(ly->wo, d, qdim) ||
             !vector_ok(ly->ffn_norm, d) || !ffn_ok || !matrix_ok(ly->wd, d, ffn) ||
             (ly->bq && !bias_ok(ly->bq, qdim)) || (ly->bk && !bias_ok(ly->bk, m->kv_dim)) ||
-            (ly->bv && !bias_ok(ly->bv, m->kv_dim))) {
+            (ly->bv && !bias_ok(ly->bv, m->kv_dim)) ||
+            (ly->post_attn_norm && !vector_ok(ly->post_attn_norm, d)) ||
+            (ly->post_ffn_norm && !vector_ok(ly->post_ffn_norm, d))) {
             orc_model_close(m);
             return NULL;
         }
@@ -1089,6 +1124,7 @@ static void attend(const orc_model_t *m, int32_t layer, int32_t seq_len, int32_t
         kv_read(m, 0, layer, t, kvh, tmp);
         scores[t] = orc_dot(q, tmp, hd) * scale;
     }
+    orc_softcap(scores, seq_len, m->attn_softcap);                  /* :446-448 */
     orc_softmax(scores, seq_len);
     memset(dst, 0, (size_t)hd * sizeof(float));
     for (int32_t t = 0; t < seq_len; t++) {
@@ -1108,12 +1144,35 @@ static void attn_head(void *arg, int32_t h) {
            m->attn_out + (size_t)h * m->hd);
 }
 
-/* layer_scheduler.c:291-567 (llama branch) */
+/* the pre-norms: (1 + w) for Gemma (:328-334, 492-498), w otherwise */
+static void norm_in(const orc_model_t *m, float *out, const float *x, const orc_tensor_t *w) {
+    if (m->gemma)
+        orc_gemma_rmsnorm(out, x, (const float *)tdata(m, w), (int32_t)m->d, m->eps);
+    else
+        orc_rmsnorm(out, x, (const float *)tdata(m, w), (int32_t)m->d, m->eps);
+}
+
+/* :474-481, 553-560: a post norm (always the (1 + w) form) on the
+ * projection's output, before the residual, when the tensor exists */
+static void post_norm(const orc_model_t *m, float *x, const orc_tensor_t *w) {
+    if (w) orc_gemma_rmsnorm(x, x, (const float *)tdata(m, w), (int32_t)m->d, m->eps);
+}
+
+/* :529-549: up * GELU(gate) for Gemma (ss_geglu then ss_elementwise_mul),
+ * up * SiLU(gate) otherwise; u is overwritten */
+static void ffn_act(const orc_model_t *m, const float *g, float *u, int32_t n) {
+    if (m->gemma)
+        for (int32_t i = 0; i < n; i++) u[i] = u[i] * orc_gelu(g[i]);
+    else
+        for (int32_t i = 0; i < n; i++) u[i] = orc_silu_mul(g[i], u[i]);
+}
+
+/* layer_scheduler.c:291-567 */
 static void process_layer(orc_model_t *m, int32_t l, int32_t pos) {
     const orc_layer_t *ly = &m->layers[l];
     int32_t d = (int32_t)m->d, ffn = (int32_t)m->ffn;
     memcpy(m->residual, m->hidden, (size_t)d * 4);
-    orc_rmsnorm(m->hidden, m->residual, (const float *)tdata(m, ly->attn_norm), d, m->eps);
+    norm_in(m, m->hidden, m->residual, ly->attn_norm);
     int32_t qdim = (int32_t)m->n_heads * m->hd, kvd = m->kv_dim;
     if (ly->wqkv) {   /* :337-347: one product, then split (attn_qkv.bias is never applied) */
         float *qkv = (float *)malloc((size_t)(qdim + 2 * kvd) * 4);
@@ -1141,10 +1200,11 @@ static void process_layer(orc_model_t *m, int32_t l, int32_t pos) {
     pool_run(attn_head, &j, (int32_t)m->n_heads);
 
     matvec_t(m, m->hidden, ly->wo, m->attn_out);
+    post_norm(m, m->hidden, ly->post_attn_norm);
     for (int32_t i = 0; i < d; i++) m->hidden[i] = m->hidden[i] + m->residual[i];   /* :484 */
 
     memcpy(m->residual, m->hidden, (size_t)d * 4);
-    orc_rmsnorm(m->hidden, m->residual, (const float *)tdata(m, ly->ffn_norm), d, m->eps);
+    norm_in(m, m->hidden, m->residual, ly->ffn_norm);
     if (ly->wg) {
         matvec_t(m, m->ffn_gate, ly->wg, m->hidden);
         matvec_t(m, m->ffn_buf, ly->wu, m->hidden);
@@ -1156,8 +1216,9 @@ static void process_layer(orc_model_t *m, int32_t l, int32_t pos) {
         memcpy(m->ffn_buf, gu + ffn, (size_t)ffn * 4);
         free(gu);
     }
-    for (int32_t i = 0; i < ffn; i++) m->ffn_buf[i] = orc_silu_mul(m->ffn_gate[i], m->ffn_buf[i]);
+    ffn_act(m, m->ffn_gate, m->ffn_buf, ffn);
     matvec_t(m, m->hidden, ly->wd, m->ffn_buf);
+    post_norm(m, m->hidden, ly->post_ffn_norm);
     for (int32_t i = 0; i < d; i++) m->hidden[i] = m->hidden[i] + m->residual[i];   /* :566 */
 }
 
@@ -1172,10 +1233,11 @@ static void process_layer(orc_model_t *m, int32_t l, int32_t pos) {
  * per layer; kv_read's widening is exact or one fp32 product, so the rows
  * hold the values attend() reads) */
 static void attend_rows(const float *K, const float *V, size_t ld, int32_t seq_len, int32_t hd, float scale,
-                        const float *q, float *dst) {
+                        float softcap, const float *q, float *dst) {
     float *scores = (float *)malloc((size_t)seq_len * sizeof(float));
     if (!scores) abort();
     for (int32_t t = 0; t < seq_len; t++) scores[t] = orc_dot(q, K + t * ld, hd) * scale;
+    orc_softcap(scores, seq_len, softcap);
     orc_softmax(scores, seq_len);
     memset(dst, 0, (size_t)hd * sizeof(float));
     for (int32_t t = 0; t < seq_len; t++) {
@@ -1199,7 +1261,7 @@ static void attn_batch_task(void *arg, int32_t task) {
     const orc_model_t *m = j->m;
     int32_t H = (int32_t)m->n_heads, i = task / H, h = task % H, hd = m->hd;
     size_t qdim = (size_t)H * hd, koff = (size_t)(h / j->heads_per_kv) * hd;
-    attend_rows(j->K + koff, j->V + koff, (size_t)m->kv_dim, j->start + i + 1, hd, j->scale,
+    attend_rows(j->K + koff, j->V + koff, (size_t)m->kv_dim, j->start + i + 1, hd, j->scale, m->attn_softcap,
                 j->q + i * qdim + (size_t)h * hd, j->out + i * qdim + (size_t)h * hd);
 }
 
@@ -1213,7 +1275,7 @@ static void layer_batch(orc_model_t *m, int32_t l, int32_t start, int32_t n, flo
     if (!res || !xn || !qkv || !att || !gu) abort();
     for (int32_t i = 0; i < n; i++) {
         memcpy(res + (size_t)i * d, X + (size_t)i * d, (size_t)d * 4);
-        orc_rmsnorm(xn + (size_t)i * d, res + (size_t)i * d, (const float *)tdata(m, ly->attn_norm), d, m->eps);
+        norm_in(m, xn + (size_t)i * d, res + (size_t)i * d, ly->attn_norm);
     }
     /* [q | k | v] per token, from one fused product or three */
     if (ly->wqkv) {
@@ -1249,10 +1311,11 @@ static void layer_batch(orc_model_t *m, int32_t l, int32_t start, int32_t n, flo
     free(K);
     dequant_matmul(X, d, tdata(m, ly->wo), att, qdim, n, (int32_t)ly->wo->dims[1], (int32_t)ly->wo->dims[0],
                    ly->wo->type);
+    for (int32_t i = 0; i < n; i++) post_norm(m, X + (size_t)i * d, ly->post_attn_norm);
     for (size_t e = 0; e < (size_t)n * d; e++) X[e] = X[e] + res[e];                 /* :484 */
     for (int32_t i = 0; i < n; i++) {
         memcpy(res + (size_t)i * d, X + (size_t)i * d, (size_t)d * 4);
-        orc_rmsnorm(xn + (size_t)i * d, res + (size_t)i * d, (const float *)tdata(m, ly->ffn_norm), d, m->eps);
+        norm_in(m, xn + (size_t)i * d, res + (size_t)i * d, ly->ffn_norm);
     }
     /* gate | up per token: two products, or the fused [gate; up] (:518-524) */
     if (ly->wg) {
@@ -1263,10 +1326,11 @@ static void layer_batch(orc_model_t *m, int32_t l, int32_t start, int32_t n, flo
     }
     for (int32_t i = 0; i < n; i++) {
         float *g = gu + (size_t)i * 2 * ffn, *u = g + ffn;
-        for (int32_t k = 0; k < ffn; k++) u[k] = orc_silu_mul(g[k], u[k]);
+        ffn_act(m, g, u, ffn);
     }
     dequant_matmul(X, d, tdata(m, ly->wd), gu + ffn, 2 * ffn, n, (int32_t)ly->wd->dims[1], (int32_t)ly->wd->dims[0],
                    ly->wd->type);
+    for (int32_t i = 0; i < n; i++) post_norm(m, X + (size_t)i * d, ly->post_ffn_norm);
     for (size_t e = 0; e < (size_t)n * d; e++) X[e] = X[e] + res[e];                 /* :566 */
     free(q);
     free(gu);
@@ -1276,16 +1340,24 @@ static void layer_batch(orc_model_t *m, int32_t l, int32_t start, int32_t n, flo
     free(res);
 }
 
-static void embed_row(orc_model_t *m, int32_t token, float *dst) {   /* :584-595 */
+static void embed_row(orc_model_t *m, int32_t token, float *dst) {   /* :584-602 */
     size_t rb = orc_row_bytes((int32_t)m->d, m->embd->type);
     const uint8_t *row = (const uint8_t *)tdata(m, m->embd) + (size_t)token * rb;
     orc_dequantize(row, dst, (int32_t)m->d, m->embd->type);
+    if (m->gemma) {
+        float sq = sqrtf((float)m->d);
+        for (int32_t i = 0; i < (int32_t)m->d; i++) dst[i] *= sq;
+    }
 }
 
-static void head(orc_model_t *m) {                                   /* :634-662 */
-    if (m->out_norm)
-        orc_rmsnorm(m->hidden, m->hidden, (const float *)tdata(m, m->out_norm), (int32_t)m->d, m->eps);
+static void head(orc_model_t *m) {                                   /* :634-676 */
+    if (m->out_norm) norm_in(m, m->hidden, m->hidden, m->out_norm);
     orc_dequant_matvec(m->logits, tdata(m, m->out), m->hidden, m->vocab, (int32_t)m->d, m->out->type);
+    if (m->gemma) {
+        float inv_sq = 1.0f / sqrtf((float)m->d);
+        for (int32_t i = 0; i < m->vocab; i++) m->logits[i] *= inv_sq;
+    }
+    orc_softcap(m->logits, m->vocab, m->final_softcap);
 }
 
 const float *orc_forward(orc_model_t *m, int32_t token, int32_t pos) {
@@ -1359,9 +1431,7 @@ int32_t orc_embed(orc_model_t *m, const int32_t *tokens, int32_t n, float *out) 
     if (!batch) return -1;
     layers_batched(m, 0, n, batch);
     if (m->out_norm)
-        for (int32_t i = 0; i < n; i++)
-            orc_rmsnorm(batch + (size_t)i * d, batch + (size_t)i * d,
-                        (const float *)tdata(m, m->out_norm), d, m->eps);
+        for (int32_t i = 0; i < n; i++) norm_in(m, batch + (size_t)i * d, batch + (size_t)i * d, m->out_norm);
     memset(out, 0, (size_t)d * 4);
     for (int32_t i = 0; i < n; i++)
         for (int32_t j = 0; j < d; j++) out[j] += batch[(size_t)i * d + j];

@@ -35,6 +35,9 @@ void     orc_dequant_matvec(float *out, const void *w, const float *x,
 void     orc_rmsnorm(float *out, const float *x, const float *w, int32_t n, float eps); /* cpu_neon.c:109-115 */
 void     orc_softmax(float *x, int32_t n);           /* tensor.c:154-173 */
 float    orc_silu_mul(float g, float u);             /* layer_scheduler.c:533-549 */
+void     orc_gemma_rmsnorm(float *out, const float *x, const float *w, int32_t n, float eps); /* cpu_neon.c:153-158 */
+float    orc_gelu(float v);                          /* tensor.c:181-190 (one element) */
+void     orc_softcap(float *x, int32_t n, float cap);  /* tensor.c:194-200 */
 void     orc_rope(float *q, float *k, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                   int32_t rope_dim, int32_t pos, float theta, int32_t is_neox); /* tensor.c:220-275 */
 void     orc_rope_table(float *cs, int32_t rope_dim, int32_t n_pos, float theta); /* cos/sin of tensor.c:250-254 */

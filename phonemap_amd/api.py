@@ -52,7 +52,7 @@ class SynthSpec(C.Structure):         # ss_synth.h
                 ("out_type", _i32), ("seed", _u64), ("scale_sigma", _f32), ("norm_sigma", _f32),
                 ("with_vocab", _i32), ("n_threads", _i32), ("arch", _i32), ("fused_qkv", _i32),
                 ("fused_up", _i32), ("qkv_bias", _i32), ("alignment", _i32), ("scale_mode", _i32),
-                ("vocab_tokens", _i32)]
+                ("vocab_tokens", _i32), ("attn_softcap", _f32), ("final_softcap", _f32)]
 
     def __init__(self, **kw):
         d = dict(rope_theta=10000.0, rms_eps=1e-5, layer_type=2, embd_type=2, out_type=2, seed=0,

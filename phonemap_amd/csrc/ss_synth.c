@@ -30,7 +30,8 @@ typedef struct {
     int32_t type;
     uint64_t offset;   /* relative to the data section */
     uint64_t bytes;
-    int norm;          /* 1: norm weight 1 + N(0, norm_sigma); 2: bias N(0, kBiasSigma) */
+    int norm;          /* 1: norm weight 1 + N(0, norm_sigma); 2: bias N(0, kBiasSigma);
+                        * 3: Gemma norm weight N(0, norm_sigma) (applied as 1 + w) */
     uint64_t sid;      /* seed id of the random stream: the tensor's index in the unfused,
                         * bias-free layout, so fused and biased files keep every weight */
     int join_next;     /* the next tensor continues this one's rows (one fused GGUF tensor) */
@@ -179,7 +180,8 @@ static void gen_item(job_t *j, uint64_t it, uint8_t *buf) {
     } else if (t->type == T_F32) {
         uint64_t ne = t->dims[0] * (t->n_dims > 1 ? t->dims[1] : 1);
         float *f = (float *)buf;
-        for (uint64_t i = 0; i < ne; i++) f[i] = (float)(1.0 + j->norm_sigma * xo_normal(&x));
+        const double one = t->norm == 3 ? 0.0 : 1.0;
+        for (uint64_t i = 0; i < ne; i++) f[i] = (float)(one + j->norm_sigma * xo_normal(&x));
         n = ne * 4;
     } else {
         const uint64_t cb = chunk_blocks(t->type);
@@ -279,16 +281,19 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
         /* Q4_K rows are whole super-blocks of 256 */
         (s->layer_type == T_Q4_K && (s->hidden % 256 || s->ffn % 256 || (s->n_heads * s->head_dim) % 256)) ||
         ((s->embd_type == T_Q4_K || s->out_type == T_Q4_K) && s->hidden % 256) ||
-        s->arch < 0 || s->arch > 1 || s->qkv_bias < 0 || s->qkv_bias > 2 || s->scale_mode < 0 ||
+        s->arch < 0 || s->arch > 3 || s->attn_softcap < 0 || s->final_softcap < 0 || s->qkv_bias < 0 || s->qkv_bias > 2 || s->scale_mode < 0 ||
         s->scale_mode > 1)
         return -5;
-    const char *arch = s->arch == 1 ? "qwen2" : "llama";
+    static const char *const kArch[4] = {"llama", "qwen2", "gemma", "gemma2"};
+    const char *arch = kArch[s->arch];
+    const int gemma = s->arch >= 2, post_norms = s->arch == 3;
+    const int nk = gemma ? 3 : 1;   /* norm kind */
     const uint64_t align = s->alignment > 0 ? (uint64_t)s->alignment : 32;
     if (align & (align - 1)) return -5;
     const int L = s->n_layers;
     const uint64_t d = (uint64_t)s->hidden, q = (uint64_t)s->n_heads * s->head_dim,
                    kv = (uint64_t)s->n_kv_heads * s->head_dim, f = (uint64_t)s->ffn;
-    int nt = 1 + 9 * L + 1 + (s->out_type >= 0 ? 1 : 0) + (s->qkv_bias ? 3 * L : 0);
+    int nt = 1 + 9 * L + 1 + (s->out_type >= 0 ? 1 : 0) + (s->qkv_bias ? 3 * L : 0) + (post_norms ? 2 * L : 0);
     syn_tensor_t *t = (syn_tensor_t *)calloc((size_t)nt, sizeof(syn_tensor_t));
     if (!t) return -3;
     int k = 0;
@@ -311,7 +316,7 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
     ADD("token_embd.weight", s->embd_type, d, (uint64_t)s->vocab, 0);
     char nm[64];
     for (int l = 0; l < L; l++) {
-        snprintf(nm, sizeof(nm), "blk.%d.attn_norm.weight", l); ADD(nm, T_F32, d, 1, 1);
+        snprintf(nm, sizeof(nm), "blk.%d.attn_norm.weight", l); ADD(nm, T_F32, d, 1, nk);
         /* fused: one tensor [Wq; Wk; Wv] (layer_scheduler.c:337-347) of the same parts */
         snprintf(nm, sizeof(nm), "blk.%d.%s.weight", l, s->fused_qkv ? "attn_qkv" : "attn_q");
         ADD(nm, s->layer_type, d, q, 0);
@@ -326,15 +331,25 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
             snprintf(nm, sizeof(nm), "blk.%d.attn_v.bias", l); ADD(nm, bt, kv, 1, 2);
         }
         snprintf(nm, sizeof(nm), "blk.%d.attn_output.weight", l); ADD(nm, s->layer_type, q, d, 0);
-        snprintf(nm, sizeof(nm), "blk.%d.ffn_norm.weight", l); ADD(nm, T_F32, d, 1, 1);
+        if (post_norms) {   /* Gemma 2 (layer_scheduler.c:309-310); own seed range, like biases */
+            snprintf(nm, sizeof(nm), "blk.%d.post_attention_norm.weight", l); ADD(nm, T_F32, d, 1, 3);
+            t[k - 1].sid = 0x200000u + (uint64_t)(k - 1);
+            sid--;   /* the matrices keep the seed ids of the file without post norms */
+        }
+        snprintf(nm, sizeof(nm), "blk.%d.ffn_norm.weight", l); ADD(nm, T_F32, d, 1, nk);
         /* fused: ffn_up = [Wgate; Wup], 2 * ffn rows (layer_scheduler.c:518-524) */
         snprintf(nm, sizeof(nm), "blk.%d.%s.weight", l, s->fused_up ? "ffn_up" : "ffn_gate");
         ADD(nm, s->layer_type, d, f, 0);
         t[k - 1].join_next = s->fused_up;
         snprintf(nm, sizeof(nm), "blk.%d.ffn_up.weight", l); ADD(nm, s->layer_type, d, f, 0);
         snprintf(nm, sizeof(nm), "blk.%d.ffn_down.weight", l); ADD(nm, s->layer_type, f, d, 0);
+        if (post_norms) {
+            snprintf(nm, sizeof(nm), "blk.%d.post_ffw_norm.weight", l); ADD(nm, T_F32, d, 1, 3);
+            t[k - 1].sid = 0x200000u + (uint64_t)(k - 1);
+            sid--;   /* the matrices keep the seed ids of the file without post norms */
+        }
     }
-    ADD("output_norm.weight", T_F32, d, 1, 1);
+    ADD("output_norm.weight", T_F32, d, 1, nk);
     if (s->out_type >= 0) ADD("output.weight", s->out_type, d, (uint64_t)s->vocab, 0);
 #undef ADD
     /* the parts of a fused tensor are contiguous; tensors start aligned */
@@ -351,7 +366,7 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
     const uint64_t data_bytes = off;
 
     wbuf_t b = {0};
-    const uint32_t n_kv = 12 + (s->with_vocab ? 3 : 0);
+    const uint32_t n_kv = 12 + (s->with_vocab ? 3 : 0) + (s->attn_softcap > 0) + (s->final_softcap > 0);
     wb_u32(&b, 0x46554747u);
     wb_u32(&b, 3);
     wb_u64(&b, (uint64_t)n_phys);
@@ -371,6 +386,8 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
     kv_u32(&b, AK("rope.dimension_count"), (uint32_t)s->head_dim);
     kv_f32(&b, AK("rope.freq_base"), s->rope_theta > 0 ? s->rope_theta : 10000.0f);
     kv_f32(&b, AK("attention.layer_norm_rms_epsilon"), s->rms_eps > 0 ? s->rms_eps : 1e-5f);
+    if (s->attn_softcap > 0) kv_f32(&b, AK("attn_logit_softcapping"), s->attn_softcap);   /* gguf_loader.c:314-317 */
+    if (s->final_softcap > 0) kv_f32(&b, AK("final_logit_softcapping"), s->final_softcap);
     if (s->with_vocab) {
         char vb[64];
         const int32_t nv = n_tokens(s);

@@ -6,7 +6,10 @@ dequantised by tests/util.dequant_np.
 It pins the oracle's whole-model functions: orc_forward
 (ss_scheduler_forward, layer_scheduler.c:571-679, with process_layer
 :291-567), orc_prefill (ss_scheduler_prefill :681-803) and orc_embed
-(ss_scheduler_embed :805-911). Everything is computed in fp64 apart from the
+(ss_scheduler_embed :805-911), with the Gemma branches: the (1 + w) norm
+(tensor.c:133-152), the sqrt(d) embedding and 1/sqrt(d) logit scales
+(:597-602, 667-672), GeGLU (:529-531, tensor.c:181-190), the post norms
+(:474-481, 553-560) and the softcaps (:446-448, 674-676, tensor.c:194-200). Everything is computed in fp64 apart from the
 two KV cache encodings, which round as the reference stores: binary16 for
 the fp16 cache, and the absmax int8 codes of kv_turboquant_encode
 (:101-118, one scale per (layer, position) over all KV heads) for the int8
@@ -48,9 +51,10 @@ class RefModel:
         _, meta, tensors, data, raw = parse_gguf(path)
         arch = meta["general.architecture"]
         self.neox = any(s in arch for s in NEOX_ARCHS)
-        if "gemma" in arch:
-            raise ValueError("gemma branches are not restated here")
+        self.gemma = "gemma" in arch                                   # :152-155
         g = lambda k, dflt=None: meta.get("%s.%s" % (arch, k), dflt)
+        self.attn_softcap = float(g("attn_logit_softcapping", 0.0))
+        self.final_softcap = float(g("final_logit_softcapping", 0.0))
         self.L = int(g("block_count"))
         self.d = int(g("embedding_length"))
         self.H = int(g("attention.head_count"))
@@ -104,6 +108,8 @@ class RefModel:
             for b in ("q", "k", "v"):                  # biases (:367-402); attn_qkv.bias is never applied
                 n = p + "attn_%s.bias" % b
                 ly["b" + b] = self._vec(n) if n in info else None
+            for k, n in (("post_attn", "post_attention_norm.weight"), ("post_ffn", "post_ffw_norm.weight")):
+                ly[k] = self._vec(p + n) if p + n in info else None
             self.layers.append(ly)
         self.reset()
 
@@ -121,8 +127,17 @@ class RefModel:
         self.vc = np.zeros((self.L, self.max_seq, kvd))
 
     # ---- pieces, each restating one reference function ----
-    def rmsnorm(self, x, w):                          # tensor.c:114-131
-        return x / np.sqrt(np.mean(x * x) + self.eps) * w
+    def rmsnorm(self, x, w, gemma=None):              # tensor.c:114-152
+        gemma = self.gemma if gemma is None else gemma
+        return x / np.sqrt(np.mean(x * x) + self.eps) * (w + 1.0 if gemma else w)
+
+    def ffn_act(self, gt, up):
+        if self.gemma:                                # :529-531, tensor.c:181-190
+            return up * 0.5 * gt * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (gt + 0.044715 * gt ** 3)))
+        return up * (gt / (1.0 + np.exp(-gt)))        # :533-549
+
+    def softcap(self, x, cap):                        # tensor.c:194-200
+        return cap * np.tanh(x / cap) if cap > 0 else x
 
     def rope(self, v, n_heads, pos):                  # tensor.c:220-275
         v = v.reshape(n_heads, self.hd).copy()
@@ -173,36 +188,47 @@ class RefModel:
             kvh = hh // G
             K = self.kc[l, :n, kvh * hd:(kvh + 1) * hd]
             V = self.vc[l, :n, kvh * hd:(kvh + 1) * hd]
-            sc = K @ q[hh * hd:(hh + 1) * hd] / np.sqrt(hd)
+            sc = self.softcap(K @ q[hh * hd:(hh + 1) * hd] / np.sqrt(hd), self.attn_softcap)
             p = np.exp(sc - sc.max())
             p /= p.sum()
             att[hh * hd:(hh + 1) * hd] = p @ V
-        x = x + ly["wo"] @ att                        # :471-484
+        o = ly["wo"] @ att                            # :471-484
+        if ly["post_attn"] is not None:
+            o = self.rmsnorm(o, ly["post_attn"], gemma=True)
+        x = x + o
         h = self.rmsnorm(x, ly["ffn_norm"])
-        gt, up = ly["wg"] @ h, ly["wu"] @ h
-        f = up * (gt / (1.0 + np.exp(-gt)))           # :533-549
-        return x + ly["wd"] @ f                       # :552-566
+        o = ly["wd"] @ self.ffn_act(ly["wg"] @ h, ly["wu"] @ h)   # :552-566
+        if ly["post_ffn"] is not None:
+            o = self.rmsnorm(o, ly["post_ffn"], gemma=True)
+        return x + o
 
-    def head(self, x):                                # :634-662
+    def head(self, x):                                # :634-676
         if self.out_norm is not None:
             x = self.rmsnorm(x, self.out_norm)
         self.hidden = x
-        return self.out[:self.vocab] @ x
+        y = self.out[:self.vocab] @ x
+        if self.gemma:
+            y = y / np.sqrt(self.d)
+        return self.softcap(y, self.final_softcap)
+
+    def embed_row(self, token):                       # :578-602
+        x = self.embd[token].copy()
+        return x * np.sqrt(self.d) if self.gemma else x
 
     def forward(self, token, pos):                    # ss_scheduler_forward, :571-679
-        x = self.embd[token].copy()
+        x = self.embed_row(token)
         for l in range(self.L):
             x = self.layer(l, x, pos)
         return self.head(x)
 
     def prefill(self, tokens, start_pos):             # ss_scheduler_prefill, :681-803 (layer-major)
-        xs = [self.embd[t].copy() for t in tokens]
+        xs = [self.embed_row(t) for t in tokens]
         for l in range(self.L):
             xs = [self.layer(l, x, start_pos + i) for i, x in enumerate(xs)]
         return self.head(xs[-1])
 
     def embed(self, tokens):                          # ss_scheduler_embed, :805-911
-        xs = [self.embd[t].copy() for t in tokens]
+        xs = [self.embed_row(t) for t in tokens]
         for l in range(self.L):
             xs = [self.layer(l, x, i) for i, x in enumerate(xs)]
         if self.out_norm is not None:

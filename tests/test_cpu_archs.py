@@ -159,12 +159,41 @@ def test_qwen2_and_llama_agree_at_position_zero_only(tmp_path):
         mq.close()
 
 
-def test_gemma_is_still_rejected(tmp_path):
-    path = str(tmp_path / "g.gguf")
-    api.write_synthetic_gguf(path, tiny_spec())
-    b = bytearray(open(path, "rb").read())
-    i = b.find(b"llama", 0)          # general.architecture's value comes first
-    b[i:i + 5] = b"gemma"
-    open(path, "wb").write(bytes(b))
-    with pytest.raises(RuntimeError):
-        oracle.Model(path, 16)
+def test_gemma_files_hold_the_llama_matrices(tmp_path):
+    """arch 3 ("gemma2") changes no matrix of the llama file with the same
+    seed; its norm weights are the llama ones minus one (the format's 1 + w),
+    and it adds the two post norms per layer and the softcap keys."""
+    plain, gem = str(tmp_path / "p.gguf"), str(tmp_path / "g.gguf")
+    api.write_synthetic_gguf(plain, tiny_spec())
+    api.write_synthetic_gguf(gem, tiny_spec(arch=3, attn_softcap=50.0, final_softcap=30.0))
+    mp, tp, _, _ = _tensors(plain)
+    mg, tg, _, _ = _tensors(gem)
+    assert mg["general.architecture"] == "gemma2"
+    assert mg["gemma2.attn_logit_softcapping"] == 50.0 and mg["gemma2.final_logit_softcapping"] == 30.0
+    for name, (dims, t, data) in tp.items():
+        if name.endswith("norm.weight"):
+            lw = np.frombuffer(data, np.float32)
+            gw = np.frombuffer(tg[name][2], np.float32)
+            assert np.max(np.abs((gw + np.float32(1)) - lw)) <= 2.4e-7, name
+        else:
+            assert tg[name][2] == data, name
+    for l in range(2):
+        for n in ("post_attention_norm.weight", "post_ffw_norm.weight"):
+            dims, t, data = tg["blk.%d.%s" % (l, n)]
+            w = np.frombuffer(data, np.float32)
+            assert t == 0 and dims == [64] and abs(float(np.mean(w))) < 0.01 and 0 < np.std(w) < 0.02
+
+
+def test_huge_softcaps_change_nothing_and_small_ones_do(tmp_path):
+    """cap * tanh(x / cap) -> x as cap grows: llama logits with caps of 1e6
+    equal the uncapped ones to fp32 rounding; caps of the scores' size move
+    them (tensor.c:194-200 applied at layer_scheduler.c:446-448, 674-676)."""
+    paths = {}
+    for name, kw in (("none", {}), ("huge", dict(attn_softcap=1e6, final_softcap=1e6)),
+                     ("small", dict(attn_softcap=0.5, final_softcap=0.5))):
+        paths[name] = str(tmp_path / (name + ".gguf"))
+        api.write_synthetic_gguf(paths[name], tiny_spec(**kw))
+    base, huge, small = (_trace(paths[n]) for n in ("none", "huge", "small"))
+    assert np.max(np.abs(huge - base)) <= 1e-5 * np.max(np.abs(base))
+    assert np.max(np.abs(small)) <= 0.5
+    assert np.max(np.abs(small - base)) > 0.1 * np.max(np.abs(base))

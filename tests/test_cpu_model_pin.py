@@ -4,7 +4,8 @@ from SlipStream/src/core/layer_scheduler.c:291-911 over the independent
 Python GGUF parser: the two share no code, so a mistake in the oracle's
 wiring (a norm weight on the wrong matvec, a wrong KV head for a query head,
 a rope pair mix-up, a fused tensor split at the wrong row, a bias on the
-wrong projection) shows as an O(1) difference.
+wrong projection, a Gemma branch missing or misplaced) shows as an O(1)
+difference.
 
 Bars (measured worst cases in brackets): the int8 cache rounds K/V to one
 of 255 levels per (layer, position), coarse enough that fp32 and fp64 land
@@ -49,6 +50,12 @@ VARIANTS = {
     # tokenizer shorter than the tables: the vocabulary is clamped to it
     "padded_tied": dict(embd_type=2, out_type=-1, vocab_tokens=360, seed=29),
     "padded_out": dict(vocab_tokens=370, seed=30),
+    # Gemma: (1 + w) norms, sqrt(d) embedding, GeGLU, 1/sqrt(d) logits, tied head
+    "gemma": dict(arch=2, embd_type=8, out_type=-1, seed=31),
+    # Gemma 2: post norms, and softcaps small enough to bend the scores and logits
+    "gemma2_softcap": dict(arch=3, embd_type=8, out_type=-1, attn_softcap=1.5, final_softcap=0.4, seed=32),
+    # the softcaps apply to any architecture that sets the keys
+    "llama_softcap": dict(attn_softcap=1.0, final_softcap=3.0, seed=33),
 }
 
 
@@ -105,7 +112,7 @@ def test_vocab_clamped_to_the_tokenizer(tmp_path, name):
 
 
 @pytest.mark.parametrize("kv", ["f16", "int8"])
-@pytest.mark.parametrize("name", ["llama_gqa", "qwen2_f16_bias_fused"])
+@pytest.mark.parametrize("name", ["llama_gqa", "qwen2_f16_bias_fused", "gemma2_softcap"])
 def test_oracle_embed_matches_fp64_restatement(tmp_path, name, kv):
     path = str(tmp_path / (name + ".gguf"))
     api.write_synthetic_gguf(path, _spec(**VARIANTS[name]))
@@ -161,8 +168,43 @@ def test_fp64_restatement_detects_miswiring(tmp_path):
         assert bad > 20 * BAR["f16"], (cls.__name__, bad)
 
 
+def test_fp64_restatement_detects_gemma_miswiring(tmp_path):
+    """The Gemma branches are each visible: dropping any one of them from
+    the fp64 model (SiLU for GeGLU, no post norms, no softcaps, w for 1 + w)
+    misses the oracle by far more than the bar."""
+    path = str(tmp_path / "g.gguf")
+    api.write_synthetic_gguf(path, _spec(**VARIANTS["gemma2_softcap"]))
+
+    class SiluNotGelu(RefModel):
+        def ffn_act(self, gt, up):
+            return up * (gt / (1.0 + np.exp(-gt)))
+
+    class NoPostNorms(RefModel):
+        def layer(self, l, x, pos):
+            ly = self.layers[l]
+            self.layers[l] = dict(ly, post_attn=None, post_ffn=None)
+            try:
+                return RefModel.layer(self, l, x, pos)
+            finally:
+                self.layers[l] = ly
+
+    class NoSoftcaps(RefModel):
+        def softcap(self, x, cap):
+            return x
+
+    class PlainNorms(RefModel):
+        def rmsnorm(self, x, w, gemma=None):
+            return RefModel.rmsnorm(self, x, w, gemma=False)
+
+    good, _ = _run(path, "f16", RefModel(path, 64, "f16"))
+    assert good <= BAR["f16"]
+    for cls in (SiluNotGelu, NoPostNorms, NoSoftcaps, PlainNorms):
+        bad, _ = _run(path, "f16", cls(path, 64, "f16"))
+        assert bad > 20 * BAR["f16"], (cls.__name__, bad)
+
+
 @pytest.mark.parametrize("kv", ["f16", "int8"])
-@pytest.mark.parametrize("name", ["llama_gqa", "tied_q8", "fused_qkv_up", "qwen2_f16_bias_fused"])
+@pytest.mark.parametrize("name", ["llama_gqa", "tied_q8", "fused_qkv_up", "qwen2_f16_bias_fused", "gemma2_softcap"])
 def test_batched_prefill_is_bit_identical_to_token_serial(tmp_path, name, kv):
     """orc_prefill runs each layer's tokens together (rows dequantised once);
     orc_prefill_serial is the reference's token-by-token loop

@@ -145,6 +145,49 @@ def test_rmsnorm_bit_exact_vs_reference(n):
     assert np.array_equal(oracle.rmsnorm(x, w, 1e-5), ref)
 
 
+def test_gemma_rmsnorm_known_answer():
+    """tensor.c:133-152: x * (1 / sqrt(mean(x^2) + eps)) * (w + 1); w = 0 is
+    the plain RMSNorm with unit weights."""
+    x = np.array([1.0, 2.0, 3.0, 4.0], np.float32)
+    s = 1.0 / math.sqrt((1 + 4 + 9 + 16) / 4.0 + 1e-5)
+    assert np.allclose(oracle.gemma_rmsnorm(x, np.zeros(4, np.float32), 1e-5), x * s, rtol=1e-6)
+    assert np.allclose(oracle.gemma_rmsnorm(x, np.full(4, 0.5, np.float32), 1e-5), 1.5 * x * s, rtol=1e-6)
+    assert np.array_equal(oracle.gemma_rmsnorm(x, np.zeros(4, np.float32), 1e-5),
+                          oracle.rmsnorm(x, np.ones(4, np.float32), 1e-5))
+
+
+@needs_ref
+@pytest.mark.parametrize("n", [4, 2304, 3584])
+def test_gemma_rmsnorm_bit_exact_vs_reference(n):
+    rng = np.random.default_rng(n + 1)
+    x = (5 * rng.standard_normal(n)).astype(np.float32)
+    w = (0.1 * rng.standard_normal(n)).astype(np.float32)
+    ref = np.zeros(n, np.float32)
+    REF.ss_neon_gemma_rmsnorm(p(ref), p(x), p(w), n, 1e-6)
+    assert np.array_equal(oracle.gemma_rmsnorm(x, w, 1e-6), ref)
+
+
+def test_gelu_closed_form_and_limits():
+    """tensor.c:181-190, the tanh form: 0 at 0, odd part x/2, -> x for large
+    x and -> 0 for large negative x; GELU(1) = 0.841192 (tanh form)."""
+    v = oracle.gelu([0.0, 1.0, -1.0, 10.0, -10.0, 3.0])
+    assert v[0] == 0.0
+    assert abs(v[1] - 0.8411920) < 1e-6 and abs(v[1] - v[2] - 1.0) < 1e-6   # gelu(x) - gelu(-x) = x
+    assert abs(v[3] - 10.0) < 1e-6 and abs(v[4]) < 1e-6
+    x = 3.0
+    want = 0.5 * x * (1 + math.tanh(math.sqrt(2 / math.pi) * (x + 0.044715 * x ** 3)))
+    assert abs(v[5] - want) < 1e-6
+
+
+def test_softcap_closed_form():
+    """tensor.c:194-200: cap * tanh(x / cap); cap <= 0 leaves x."""
+    x = np.array([0.0, 1.0, -1.0, 100.0, -100.0, 2.5], np.float32)
+    out = oracle.softcap(x, 5.0)
+    assert np.allclose(out, 5.0 * np.tanh(x / 5.0), rtol=1e-6, atol=1e-7)
+    assert out[3] <= 5.0 and out[4] >= -5.0 and out[0] == 0.0
+    assert np.array_equal(oracle.softcap(x, 0.0), x)
+
+
 def test_silu_known_answers():
     for g, want in GOLD["silu"]["cases"]:
         assert abs(L.orc_silu_mul(g, 1.0) - want) < GOLD["silu"]["tol"]
