@@ -232,6 +232,20 @@ typedef struct {
      * a layer has none), added to the projections before RoPE
      * (layer_scheduler.c:367-402). */
     const ss_hip_tensor_t *qkv_bias;
+    /* Gemma ("gemma" in the architecture name, layer_scheduler.c:152-155):
+     * nonzero applies attn_norm, ffn_norm and output_norm in the (1 + w) form
+     * (tensor.c:133-152), scales the embedding by sqrt(hidden) (:597-602)
+     * and the logits by 1/sqrt(hidden) (:667-672), and uses GeGLU (the
+     * tanh-form GELU of the gate, :529-531, tensor.c:181-190) for SwiGLU. */
+    int32_t gemma;
+    /* > 0: cap * tanh(x / cap) on the attention scores before the softmax
+     * (:446-448) and on the logits (:674-676), for any architecture */
+    float attn_softcap, final_softcap;
+    /* NULL, or n_layers * 2 norm vectors (post_attention_norm, post_ffw_norm;
+     * F32 or F16; data NULL where a layer has none), applied in the (1 + w)
+     * form to the Wo and down outputs before the residual (:474-481,
+     * 553-560) */
+    const ss_hip_tensor_t *post_norms;
 } ss_hip_model_desc_t;
 
 /* ss_scheduler_init (layer_scheduler.h:95-96): upload + pack all weights,

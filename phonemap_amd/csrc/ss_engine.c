@@ -162,12 +162,7 @@ ss_model_t *ss_model_load_ex(const char *path, const ss_model_config_t *config,
     m->tok = ss_tok_create(g->vocab, g->vocab_scores, g->vocab ? g->vocab_size : 0, g->merges,
                            g->n_merges, g->arch);
 
-    if (strstr(g->arch, "gemma")) {
-        fprintf(stderr, "SlipStream: architecture '%s' is not supported by the HIP path\n", g->arch);
-        ss_model_free(m);
-        set_err(SS_ERROR_BACKEND);
-        return NULL;
-    }
+    const int gemma = strstr(g->arch, "gemma") != NULL;   /* layer_scheduler.c:152-155 */
     /* layer_scheduler.c:144-149 */
     const int neox = strstr(g->arch, "qwen") || strstr(g->arch, "falcon") || strstr(g->arch, "phi") ||
                      strstr(g->arch, "deepseek");
@@ -212,21 +207,21 @@ ss_model_t *ss_model_load_ex(const char *path, const ss_model_config_t *config,
     }
     ss_hip_tensor_t *lt = (ss_hip_tensor_t *)calloc((size_t)L * SS_HIP_LAYER_TENSORS, sizeof(ss_hip_tensor_t));
     ss_hip_tensor_t *bias = (ss_hip_tensor_t *)calloc((size_t)L * 3, sizeof(ss_hip_tensor_t));
+    ss_hip_tensor_t *post = (ss_hip_tensor_t *)calloc((size_t)L * 2, sizeof(ss_hip_tensor_t));
     void **owned = (void **)calloc((size_t)L * 4 + 1, sizeof(void *));   /* NeoX-ordered copies */
-    int n_owned = 0, any_bias = 0;
+    int n_owned = 0, any_bias = 0, any_post = 0;
     ss_error_t err = SS_OK;
-    if (!lt || !bias || !owned) err = SS_ERROR_OUT_OF_MEMORY;
+    if (!lt || !bias || !post || !owned) err = SS_ERROR_OUT_OF_MEMORY;
     static const char *sfx[SS_HIP_LAYER_TENSORS] = {
         "attn_norm.weight", "attn_q.weight", "attn_k.weight", "attn_v.weight", "attn_output.weight",
         "ffn_norm.weight", "ffn_gate.weight", "ffn_up.weight", "ffn_down.weight"};
     static const char *bsfx[3] = {"attn_q.bias", "attn_k.bias", "attn_v.bias"};
     for (uint32_t l = 0; l < L && err == SS_OK; l++) {
         ss_hip_tensor_t *t = lt + (size_t)l * SS_HIP_LAYER_TENSORS;
-        if (ss_gguf_find_in_layer(g, l, "post_attention_norm.weight")) {
-            fprintf(stderr, "SlipStream: blk.%u uses post norms (not supported)\n", l);
-            err = SS_ERROR_BACKEND;
-            break;
-        }
+        /* Gemma 2 post norms, wherever they exist (layer_scheduler.c:309-310) */
+        fill_tensor(&post[l * 2], g, ss_gguf_find_in_layer(g, l, "post_attention_norm.weight"));
+        fill_tensor(&post[l * 2 + 1], g, ss_gguf_find_in_layer(g, l, "post_ffw_norm.weight"));
+        if (post[l * 2].data || post[l * 2 + 1].data) any_post = 1;
         const ss_gguf_tensor_t *wqkv = ss_gguf_find_in_layer(g, l, "attn_qkv.weight");
         const ss_gguf_tensor_t *wgate = ss_gguf_find_in_layer(g, l, "ffn_gate.weight");
         for (int k = 0; k < SS_HIP_LAYER_TENSORS && err == SS_OK; k++) {
@@ -291,6 +286,7 @@ ss_model_t *ss_model_load_ex(const char *path, const ss_model_config_t *config,
     if (err != SS_OK) {
         for (int i = 0; i < n_owned; i++) free(owned[i]);
         free(owned);
+        free(post);
         free(bias);
         free(lt);
         ss_model_free(m);
@@ -318,12 +314,17 @@ ss_model_t *ss_model_load_ex(const char *path, const ss_model_config_t *config,
     fill_tensor(&desc.output, g, ss_gguf_find(g, "output.weight"));
     desc.layers = lt;
     desc.qkv_bias = any_bias ? bias : NULL;
+    desc.gemma = gemma;
+    desc.attn_softcap = g->attn_logit_softcapping;   /* gguf_loader.c:314-317 */
+    desc.final_softcap = g->final_logit_softcapping;
+    desc.post_norms = any_post ? post : NULL;
 
     m->ctx = ss_hip_init(m->ext.device);
     if (!m->ctx) {
         fprintf(stderr, "SlipStream: HIP backend unavailable: %s\n", ss_hip_last_error());
         for (int i = 0; i < n_owned; i++) free(owned[i]);
         free(owned);
+        free(post);
         free(bias);
         free(lt);
         ss_model_free(m);
@@ -333,6 +334,7 @@ ss_model_t *ss_model_load_ex(const char *path, const ss_model_config_t *config,
     m->hm = ss_hip_model_create(m->ctx, &desc);
     for (int i = 0; i < n_owned; i++) free(owned[i]);
     free(owned);
+    free(post);
     free(bias);
     free(lt);
     if (!m->hm) {

@@ -303,7 +303,13 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int row, bool own, c
     float out;
     if constexpr (EPI == EPI_SWIGLU) {
       const float g = v[0], u = v[NMAT - 1];
-      out = u * (g / (1.0f + expf(-g)));                               // layer_scheduler.c:540-547
+      if (a.act == 1) {   // GeGLU (layer_scheduler.c:529-531): up * GELU(gate), tensor.c:181-190
+        const float cube = g * g * g;
+        const float inner = 0.7978845608028654f * (g + 0.044715f * cube);
+        out = u * (0.5f * g * (1.0f + tanhf(inner)));
+      } else {
+        out = u * (g / (1.0f + expf(-g)));                             // layer_scheduler.c:540-547
+      }
     } else {
       out = EPI == EPI_ADD ? v[0] + pre.y : v[0];                       // layer_scheduler.c:484,566
     }
@@ -345,11 +351,15 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int row, bool own, c
       }
     }
   } else if constexpr (EPI == EPI_LOGITS) {
+    // Gemma's 1/sqrt(d) (layer_scheduler.c:667-672), then the final softcap
+    // (:674-676, tensor.c:194-200), before the argmax sees the logit
+    float y = v[0] * a.out_scale;
+    if (a.softcap > 0.f) y = a.softcap * tanhf(y * a.softcap_inv);
     float bv = -INFINITY;
     int bi = 0x7fffffff;
     if (valid) {
-      a.y[row] = v[0];
-      bv = v[0];
+      a.y[row] = y;
+      bv = y;
       bi = row;
     }
     wave_best(bv, bi);
@@ -544,13 +554,16 @@ __device__ __forceinline__ float embed_value(const PackedMat& t, int tok, int nt
 // encoded in the same pass (every lane of a wave takes part in enc16).
 template <int QT>
 __global__ void __launch_bounds__(256) k_embed(PackedMat t, int cols, const int* tokens, const int* dpos,
-                                               int token, float* out, const float* nw, uint32_t* xr) {
+                                               int token, float* out, const float* nw, uint32_t* xr,
+                                               float scale) {
   const int tok = tokens ? tokens[*dpos + blockIdx.y] : token;
   out += (size_t)blockIdx.y * cols;
   const int ntk = (cols / 32 + kTB - 1) / kTB;
   const int j = blockIdx.x * blockDim.x + threadIdx.x;
   const bool in = j < cols;
-  const float v = in ? embed_value<QT>(t, tok, ntk, j) : 0.f;
+  // the dequantised value, then (Gemma) times sqrt(d): two roundings, as
+  // layer_scheduler.c:584-602 (scale 1 is exact)
+  const float v = in ? __fmul_rn(embed_value<QT>(t, tok, ntk, j), scale) : 0.f;
   if (in) out[j] = v;
   if (!xr) return;
   const Enc e = enc16(in ? v * nw[j] : 0.f, v);
@@ -625,7 +638,7 @@ hipError_t launch_qkv(const GemvArgs& a, hipStream_t s) {
 template <int QT>
 hipError_t launch_q(int epi, const GemvArgs& a, hipStream_t s) {
   switch (epi) {
-    case EPI_STORE: return launch_x<QT, 1, EPI_STORE>(a, s);
+    case EPI_STORE: return a.att_o ? launch_t<QT, 1, EPI_STORE, true>(a, s) : launch_x<QT, 1, EPI_STORE>(a, s);
     case EPI_ADD: return a.att_o ? launch_t<QT, 1, EPI_ADD, true>(a, s) : launch_x<QT, 1, EPI_ADD>(a, s);
     case EPI_SWIGLU: return launch_x<QT, 2, EPI_SWIGLU>(a, s);
     case EPI_QKV: return launch_qkv<QT>(a, s);
@@ -697,7 +710,7 @@ PackedMat packed_view(const void* base, int type, int64_t rows, int cols) {
 hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t s) {
   if (a.att_o && a.xr) return hipErrorInvalidValue;
   if (a.xr_out && epi != EPI_STORE && epi != EPI_ADD && epi != EPI_SWIGLU) return hipErrorInvalidValue;
-  if (a.att_o && (epi != EPI_ADD || !a.att_ml || !a.dpos || a.att_ns < 1 || a.att_ns > kMergeSplits ||
+  if (a.att_o && ((epi != EPI_ADD && epi != EPI_STORE) || !a.att_ml || !a.dpos || a.att_ns < 1 || a.att_ns > kMergeSplits ||
                   a.att_group < 1 || a.head_dim < 32 || a.head_dim % 32 || a.cols % a.head_dim))
     return hipErrorInvalidValue;
   if (a.type == 2) return launch_q<2>(epi, a, s);
@@ -730,34 +743,34 @@ hipError_t launch_pack(int type, const uint8_t* src, PackedMat dst, int64_t nblo
 }
 
 hipError_t launch_embed(int type, PackedMat t, int cols, const int* tokens, const int* dpos,
-                        int token, float* out, const float* nw, uint32_t* xr, hipStream_t s) {
+                        int token, float* out, const float* nw, uint32_t* xr, float scale, hipStream_t s) {
   if (xr && !nw) return hipErrorInvalidValue;
   if (type == 2)
     hipLaunchKernelGGL(k_embed<2>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out, nw,
-                       xr);
+                       xr, scale);
   else if (type == 8)
     hipLaunchKernelGGL(k_embed<8>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out, nw,
-                       xr);
+                       xr, scale);
   else if (type == kQ4K)
     hipLaunchKernelGGL(k_embed<kQ4K>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out,
-                       nw, xr);
+                       nw, xr, scale);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
 hipError_t launch_embed_rows(int type, PackedMat t, int cols, const int* tokens, const int* dpos, int n,
-                             float* out, hipStream_t s) {
+                             float* out, float scale, hipStream_t s) {
   if (n <= 0 || !tokens || !dpos) return hipErrorInvalidValue;
   if (type == 2)
     hipLaunchKernelGGL(k_embed<2>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
-                       nullptr, nullptr);
+                       nullptr, nullptr, scale);
   else if (type == 8)
     hipLaunchKernelGGL(k_embed<8>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
-                       nullptr, nullptr);
+                       nullptr, nullptr, scale);
   else if (type == kQ4K)
     hipLaunchKernelGGL(k_embed<kQ4K>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
-                       nullptr, nullptr);
+                       nullptr, nullptr, scale);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();

@@ -358,6 +358,7 @@ static ssk::GemvArgs gemv_args(const void* w, const float* x, float* y, int rows
   a.cols = cols;
   a.type = type;
   a.n_cu = g_n_cu;
+  a.out_scale = 1.f;
   return a;
 }
 
@@ -614,7 +615,7 @@ int32_t ss_hip_embed_row(ss_hip_ctx_t* c, float* out, const void* table, int32_t
   if (!c || !out || !table || token < 0 || token >= rows) return fail(kErrParams, "embed: bad argument");
   if (int32_t rc = check_mv(rows, cols, type)) return rc;
   HIP_TRY(ssk::launch_embed(type, view(table, type, rows, cols), cols, nullptr, nullptr, token, out, nullptr,
-                            nullptr, pick(c, stream)));
+                            nullptr, 1.f, pick(c, stream)));
   return 0;
 }
 
@@ -672,6 +673,8 @@ struct DevLayer {
   void* wu = nullptr;
   void* wd = nullptr;
   int t_qkv = 0, t_o = 0, t_gu = 0, t_d = 0;
+  float* post_attn = nullptr;   // Gemma 2 post norms as (1 + w), or nullptr
+  float* post_ffn = nullptr;
 };
 
 enum ProfClass { PC_Q4 = 0, PC_Q8 = 1, PC_ATTN = 2, PC_OTHER = 3, PC_SWEEP = 4, PC_N = 5 };
@@ -697,6 +700,17 @@ struct ss_hip_model {
   void* out = nullptr;   // == embd when tied
   int t_out = 0;
   bool any_q4k = false;   // some matrix is Q4_K: prompts run token by token
+  // Gemma and the optional branches (layer_scheduler.c:446-448, 474-481,
+  // 529-531, 553-560, 597-602, 667-676); the (1 + w) norms are uploaded as 1 + w
+  bool gemma = false;
+  float emb_scale = 1.f;     // sqrt(d) for Gemma
+  float logit_scale = 1.f;   // 1/sqrt(d) for Gemma
+  float attn_softcap = 0.f, final_softcap = 0.f;
+  bool any_post = false;     // some layer has a post norm
+  float* post_y = nullptr;   // [d]: a projection's output before its post norm
+  // prompts run token by token (the prompt products have none of: Q4_K,
+  // the Gemma branches, post norms, softcaps, head_dim 256)
+  bool token_only = false;
   float* out_norm = nullptr;
   // KV cache: [L][KVH][max_seq][hd] (+ [L][max_seq] scales for int8)
   void* kc = nullptr;
@@ -778,9 +792,14 @@ int32_t m_alloc(ss_hip_model* m, void** p, size_t bytes, bool zero = true) {
 // An F32 or F16 vector of n elements widened to fp32 into h.
 int32_t host_f32(const ss_hip_tensor_t& t, int n, const char* what, float* h);
 
-int32_t upload_vec(ss_hip_model* m, float** dst, const ss_hip_tensor_t& t, int n, const char* what) {
+// An F32/F16 vector widened to fp32, plus add (1 for the (1 + w) norms of
+// tensor.c:133-152: the one fp32 rounding of w + 1.0f done once here).
+int32_t upload_vec(ss_hip_model* m, float** dst, const ss_hip_tensor_t& t, int n, const char* what,
+                   float add = 0.f) {
   std::vector<float> h((size_t)n);
   if (int32_t rc = host_f32(t, n, what, h.data())) return rc;
+  if (add != 0.f)
+    for (float& v : h) v = v + add;
   if (int32_t rc = m_alloc(m, (void**)dst, sizeof(float) * n, false)) return rc;
   HIP_TRY(hipMemcpy(*dst, h.data(), sizeof(float) * n, hipMemcpyHostToDevice));
   return 0;
@@ -921,6 +940,7 @@ int32_t sweep_setup(ss_hip_model* m) {
     if (ly.t_qkv != lt || ly.t_o != lt || ly.t_gu != lt || ly.t_d != lt) return 1;
   if (!ssk::sweep_supported(m->hd, m->group, lt, m->t_out)) return 1;
   if (m->t_embd != SS_HIP_Q4_0 && m->t_embd != SS_HIP_Q8_0) return 1;   // the sweep stages Q4_0/Q8_0 rows only
+  if (m->gemma || m->any_post || m->attn_softcap > 0.f || m->final_softcap > 0.f) return 1;   // llama blocks only
   int nwg = m->ctx->n_cu < ssk::kSweepMaxWg ? m->ctx->n_cu : ssk::kSweepMaxWg;
   if (m->KVH > nwg) return 1;
   ssk::SweepArgs& a = m->sw;
@@ -1025,7 +1045,7 @@ int32_t enqueue_embed(ss_hip_model* m, const int* dpos, float* hidden, uint32_t*
   hipStream_t s = m->ctx->stream;
   HIP_TRY(timed(m, PC_OTHER, 0, [&] {
     return ssk::launch_embed(m->t_embd, view(m->embd, m->t_embd, m->embd_rows, m->d), m->d, m->tokens,
-                             dpos, 0, hidden, m->layers[0].attn_norm, xr, s);
+                             dpos, 0, hidden, m->layers[0].attn_norm, xr, m->emb_scale, s);
   }));
   return 0;
 }
@@ -1085,6 +1105,8 @@ int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden,
   at.ns = m->ns;
   at.n_kv_heads = m->KVH;
   at.scale = 1.0f / sqrtf((float)m->hd);
+  at.softcap = m->attn_softcap;
+  at.softcap_inv = m->attn_softcap > 0.f ? 1.0f / m->attn_softcap : 0.f;
   at.out = m->attn;
   at.part_o = m->att_o;
   at.part_ml = m->att_ml;
@@ -1097,7 +1119,8 @@ int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden,
   HIP_TRY(timed(m, PC_ATTN, 0, [&] { return ssk::launch_attention(m->hd, m->group, m->kv_type, at, s); }));
 
   // 3. hidden += Wo attn                                         (:470-484)
-  ssk::GemvArgs o = gemv_args(ly.wo, m->attn, hidden, m->d, m->qdim, ly.t_o);
+  // (with a post norm: y = Wo attn, then hidden += y * (1 + w) / rms(y), :474-481)
+  ssk::GemvArgs o = gemv_args(ly.wo, m->attn, ly.post_attn ? m->post_y : hidden, m->d, m->qdim, ly.t_o);
   if (fused) {
     o.att_o = m->att_o;
     o.att_ml = m->att_ml;
@@ -1108,10 +1131,18 @@ int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden,
   } else {
     o.xr = m->xr_att;
   }
-  o.xr_out = m->xr_hid;
-  o.nw_out = ly.ffn_norm;
-  HIP_TRY(timed(m, q_class(ly.t_o), matvec_bytes(ly.t_o, m->d, m->qdim, 1),
-                [&] { return ssk::launch_gemv(ssk::EPI_ADD, o, s); }));
+  if (ly.post_attn) {
+    HIP_TRY(timed(m, q_class(ly.t_o), matvec_bytes(ly.t_o, m->d, m->qdim, 1),
+                  [&] { return ssk::launch_gemv(ssk::EPI_STORE, o, s); }));
+    HIP_TRY(timed(m, PC_OTHER, 0, [&] {
+      return ssk::launch_post_norm(hidden, m->post_y, ly.post_attn, m->d, m->eps, m->xr_hid, ly.ffn_norm, s);
+    }));
+  } else {
+    o.xr_out = m->xr_hid;
+    o.nw_out = ly.ffn_norm;
+    HIP_TRY(timed(m, q_class(ly.t_o), matvec_bytes(ly.t_o, m->d, m->qdim, 1),
+                  [&] { return ssk::launch_gemv(ssk::EPI_ADD, o, s); }));
+  }
 
   // 4. rmsnorm(ffn_norm) -> gate, up -> silu(gate) * up           (:486-550)
   ssk::GemvArgs gu = gemv_args(ly.wg, hidden, m->ffn_act, m->ffn, m->d, ly.t_gu);
@@ -1120,16 +1151,27 @@ int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden,
   gu.eps = m->eps;
   gu.xr = m->xr_hid;
   gu.xr_out = m->xr_ffn;
+  gu.act = m->gemma ? 1 : 0;   // GeGLU for Gemma (:529-531)
   HIP_TRY(timed(m, q_class(ly.t_gu), matvec_bytes(ly.t_gu, m->ffn, m->d, 2),
                 [&] { return ssk::launch_gemv(ssk::EPI_SWIGLU, gu, s); }));
 
   // 5. hidden += Wdown act                                       (:552-566)
-  ssk::GemvArgs dn = gemv_args(ly.wd, m->ffn_act, hidden, m->d, m->ffn, ly.t_d);
+  // (with a post norm, as for Wo: :553-560)
+  ssk::GemvArgs dn = gemv_args(ly.wd, m->ffn_act, ly.post_ffn ? m->post_y : hidden, m->d, m->ffn, ly.t_d);
   dn.xr = m->xr_ffn;
-  dn.xr_out = xr;
-  dn.nw_out = l + 1 < m->L ? m->layers[l + 1].attn_norm : m->out_norm;
-  HIP_TRY(timed(m, q_class(ly.t_d), matvec_bytes(ly.t_d, m->d, m->ffn, 1),
-                [&] { return ssk::launch_gemv(ssk::EPI_ADD, dn, s); }));
+  const float* nw_next = l + 1 < m->L ? m->layers[l + 1].attn_norm : m->out_norm;
+  if (ly.post_ffn) {
+    HIP_TRY(timed(m, q_class(ly.t_d), matvec_bytes(ly.t_d, m->d, m->ffn, 1),
+                  [&] { return ssk::launch_gemv(ssk::EPI_STORE, dn, s); }));
+    HIP_TRY(timed(m, PC_OTHER, 0, [&] {
+      return ssk::launch_post_norm(hidden, m->post_y, ly.post_ffn, m->d, m->eps, xr, nw_next, s);
+    }));
+  } else {
+    dn.xr_out = xr;
+    dn.nw_out = nw_next;
+    HIP_TRY(timed(m, q_class(ly.t_d), matvec_bytes(ly.t_d, m->d, m->ffn, 1),
+                  [&] { return ssk::launch_gemv(ssk::EPI_ADD, dn, s); }));
+  }
   return 0;
 }
 
@@ -1145,6 +1187,9 @@ int32_t enqueue_head(ss_hip_model* m, const float* hidden, const uint32_t* xr) {
   h.eps = m->eps;
   h.xr = xr;
   h.part = m->lm_part;
+  h.out_scale = m->logit_scale;   // Gemma 1/sqrt(d) (:667-672), then the final softcap (:674-676)
+  h.softcap = m->final_softcap;
+  h.softcap_inv = m->final_softcap > 0.f ? 1.0f / m->final_softcap : 0.f;
   HIP_TRY(timed(m, q_class(m->t_out), matvec_bytes(m->t_out, m->vocab, m->d, 1),
                 [&] { return ssk::launch_gemv(ssk::EPI_LOGITS, h, s); }));
   HIP_TRY(timed(m, PC_OTHER, 0, [&] {
@@ -1392,7 +1437,7 @@ int32_t enqueue_rows(ss_hip_model* m, int n, int start, bool pool, int* last) {
     const int p0 = start + c0;
     HIP_TRY(timed(m, PC_OTHER, 0, [&] {
       return ssk::launch_embed_rows(m->t_embd, view(m->embd, m->t_embd, m->embd_rows, m->d), m->d, m->tokens,
-                                    m->pos_iota + p0, T, m->pf_h, s);
+                                    m->pos_iota + p0, T, m->pf_h, m->emb_scale, s);
     }));
     for (int l = 0; l < m->L; l++) {
       if (m->cancel && *m->cancel) return fail(kErrCancel, "cancelled");
@@ -1596,6 +1641,18 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
   m->any_q4k = d->token_embd.type == SS_HIP_Q4_K || (d->output.data && d->output.type == SS_HIP_Q4_K);
   for (int i = 0; i < m->L * SS_HIP_LAYER_TENSORS; i++)
     if (d->layers[i].data && d->layers[i].type == SS_HIP_Q4_K) m->any_q4k = true;
+  m->gemma = d->gemma != 0;
+  m->emb_scale = m->gemma ? sqrtf((float)m->d) : 1.f;                       // layer_scheduler.c:597-602
+  m->logit_scale = m->gemma ? 1.0f / sqrtf((float)m->d) : 1.f;              // :667-672
+  m->attn_softcap = d->attn_softcap > 0.f ? d->attn_softcap : 0.f;
+  m->final_softcap = d->final_softcap > 0.f ? d->final_softcap : 0.f;
+  if (d->post_norms)
+    for (int i = 0; i < 2 * m->L; i++)
+      if (d->post_norms[i].data) m->any_post = true;
+  // (and head_dim 256: the prompt attention kernel covers 64 and 128)
+  m->token_only = m->any_q4k || m->gemma || m->any_post || m->attn_softcap > 0.f || m->final_softcap > 0.f ||
+                  m->hd > 128;
+  const float norm_add = m->gemma ? 1.f : 0.f;   // (1 + w) norms, tensor.c:133-152
   if (!d->token_embd.data || d->token_embd.cols != m->d || d->token_embd.rows < m->vocab) {
     fail(kErrParams, "model: token_embd must be [>= vocab x hidden]");
     return bail();
@@ -1615,7 +1672,7 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
     m->out = m->embd;   // tied embeddings, layer_scheduler.c:652-655
     m->t_out = m->t_embd;
   }
-  if (d->output_norm.data && upload_vec(m, &m->out_norm, d->output_norm, m->d, "output_norm"))
+  if (d->output_norm.data && upload_vec(m, &m->out_norm, d->output_norm, m->d, "output_norm", norm_add))
     return bail();
   m->layers.resize(m->L);
   if (m->streaming && stream_setup(m, d)) return bail();
@@ -1631,9 +1688,17 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
     }
     char what[64];
     snprintf(what, sizeof(what), "blk.%d attn_norm", l);
-    if (upload_vec(m, &ly.attn_norm, t[SS_HIP_ATTN_NORM], m->d, what)) return bail();
+    if (upload_vec(m, &ly.attn_norm, t[SS_HIP_ATTN_NORM], m->d, what, norm_add)) return bail();
     snprintf(what, sizeof(what), "blk.%d ffn_norm", l);
-    if (upload_vec(m, &ly.ffn_norm, t[SS_HIP_FFN_NORM], m->d, what)) return bail();
+    if (upload_vec(m, &ly.ffn_norm, t[SS_HIP_FFN_NORM], m->d, what, norm_add)) return bail();
+    if (d->post_norms) {   // always the (1 + w) form (layer_scheduler.c:474-481, 553-560)
+      for (int k = 0; k < 2; k++) {
+        const ss_hip_tensor_t& pn = d->post_norms[(size_t)l * 2 + k];
+        if (!pn.data) continue;
+        snprintf(what, sizeof(what), "blk.%d %s", l, k ? "post_ffw_norm" : "post_attention_norm");
+        if (upload_vec(m, k ? &ly.post_ffn : &ly.post_attn, pn, m->d, what, 1.f)) return bail();
+      }
+    }
     snprintf(what, sizeof(what), "blk.%d attn_q/k/v", l);
     if (upload_mat(m, &ly.wqkv, t + SS_HIP_WQ, 3, m->qdim + 2 * m->kvdim, m->d, &ly.t_qkv, what,
                    blk ? blk + off[0] : nullptr))
@@ -1710,7 +1775,8 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
       m_alloc(m, (void**)&m->xr_hid, sizeof(uint32_t) * ssk::xrec_words(m->d)) ||
       m_alloc(m, (void**)&m->xr_ffn, sizeof(uint32_t) * ssk::xrec_words(m->ffn)) ||
       m_alloc(m, (void**)&m->xr_att, sizeof(uint32_t) * ssk::xrec_words(m->qdim)) ||
-      m_alloc(m, (void**)&m->emb, sizeof(float) * (2 * (size_t)m->d + 64)))
+      m_alloc(m, (void**)&m->emb, sizeof(float) * (2 * (size_t)m->d + 64)) ||
+      (m->any_post && m_alloc(m, (void**)&m->post_y, sizeof(float) * m->d)))
     return bail();
   // RoPE (cos, sin) table for every position, computed with the host libm
   // exactly as tensor.c:250-254 computes each pair.
@@ -1812,7 +1878,7 @@ int32_t ss_hip_eval_prompt(ss_hip_model_t* m, const int32_t* tokens, int32_t n, 
   HIP_TRY(hipMemcpy(m->tokens + start, tokens, sizeof(int) * n, hipMemcpyHostToDevice));
   HIP_TRY(ssk::launch_set_state(m->dpos, m->tokens, start, tokens[0], s));
   const int pf_min = m->pf_min > 0 ? m->pf_min : kPrefillMin;
-  if (m->kv_type == 0 && m->pf_min >= 0 && n >= pf_min && !m->any_q4k) {
+  if (m->kv_type == 0 && m->pf_min >= 0 && n >= pf_min && !m->token_only) {
     if (int32_t rc = prefill_setup(m)) return rc;
     if (int32_t rc = enqueue_prompt_rows(m, tokens, n, start)) {
       hipStreamSynchronize(s);
@@ -1859,7 +1925,7 @@ int32_t ss_hip_embed(ss_hip_model_t* m, const int32_t* tokens, int32_t n, float*
   HIP_TRY(hipMemsetAsync(m->emb, 0, sizeof(float) * m->d, s));
   m->host_pos = -1;   // the cache holds positions 0..n-1, but no token to continue from
   int32_t rc = 0;
-  if (m->kv_type == 0 && m->pf_min >= 0 && !m->any_q4k) {
+  if (m->kv_type == 0 && m->pf_min >= 0 && !m->token_only) {
     int T = 0;
     rc = prefill_setup(m);
     if (!rc) rc = enqueue_rows(m, n, 0, true, &T);

@@ -45,6 +45,9 @@ struct GemvArgs {
   float* kv_f32;             // kv_type 1: fp32 K,V staging [2*kvdim]
   // EPI_LOGITS
   float2* part;              // one (value, index bits) candidate per workgroup
+  float out_scale;           // EPI_LOGITS: y = (W x) * out_scale (1: none; Gemma 1/sqrt(d))
+  float softcap, softcap_inv;  // EPI_LOGITS: then y = softcap * tanh(y * softcap_inv) when softcap > 0
+  int act;                   // EPI_SWIGLU: 0 up * SiLU(gate), 1 up * GELU(gate) (tanh form, GeGLU)
   // x = the attention output merged from its splits while staging (x unused):
   // the attention split merge folded into the Wo matvec; needs att_ns <= kMergeSplits
   const float* att_o;        // [kvh][ns][G][head_dim] partial outputs, or nullptr
@@ -91,6 +94,7 @@ struct AttnArgs {
   const int* dpos;           // ctx = *dpos + 1 when set, else seq_len
   int seq_len, max_seq, ns, n_kv_heads;
   float scale;
+  float softcap, softcap_inv;  // > 0: scores = softcap * tanh(scores * softcap_inv) before the softmax
   float* out;                // [n_heads][hd]
   float* part_o;             // [kvh][ns][G][hd]
   float* part_ml;            // [kvh][ns][G][2]
@@ -142,12 +146,18 @@ int attn_resident_groups(int head_dim, int group, int kv_type);
 
 hipError_t launch_pack(int type, const uint8_t* src, PackedMat dst, int64_t nblocks, int nb, int64_t row_off,
                        hipStream_t s);
-// With xr set, also the x records of row * nw (xrec_words(cols) words).
+// The row times scale (1: none; Gemma sqrt(d)). With xr set, also the x
+// records of row * nw (xrec_words(cols) words).
 hipError_t launch_embed(int type, PackedMat t, int cols, const int* tokens, const int* dpos,
-                        int token, float* out, const float* nw, uint32_t* xr, hipStream_t s);
-// Rows tokens[*dpos + z], z < n, of the table into out[z][cols].
+                        int token, float* out, const float* nw, uint32_t* xr, float scale, hipStream_t s);
+// Rows tokens[*dpos + z], z < n, of the table (times scale) into out[z][cols].
 hipError_t launch_embed_rows(int type, PackedMat t, int cols, const int* tokens, const int* dpos, int n,
-                             float* out, hipStream_t s);
+                             float* out, float scale, hipStream_t s);
+// Post norm (layer_scheduler.c:474-481, 553-560): hidden += y * w / rms(y),
+// w the (1 + weight) vector; with xr set, also the x records of the new
+// hidden * nw_out (nw_out may be nullptr). One workgroup; n a multiple of 16.
+hipError_t launch_post_norm(float* hidden, const float* y, const float* w, int n, float eps, uint32_t* xr,
+                            const float* nw_out, hipStream_t s);
 hipError_t launch_rmsnorm(float* out, const float* x, const float* w, int n, float eps,
                           hipStream_t s);
 hipError_t launch_rope(float* q, float* k, int n_heads, int n_kv_heads, int head_dim,

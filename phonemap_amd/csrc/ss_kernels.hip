@@ -58,6 +58,12 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a, int& ctx, int& chu
   attn_chunks(ctx, a.ns, chunk, active);
 }
 
+// The attention softcap (layer_scheduler.c:446-448, tensor.c:194-200) of a
+// scaled score: cap * tanh(score / cap), or the score when no cap is set.
+__device__ __forceinline__ float softcap(float d, const AttnArgs& a) {
+  return a.softcap > 0.f ? a.softcap * tanhf(d * a.softcap_inv) : d;
+}
+
 // Sum over aligned groups of N (4, 8 or 16) lanes, result in every lane.
 template <int N>
 __device__ __forceinline__ float sum_lanes(float v) {
@@ -65,6 +71,7 @@ __device__ __forceinline__ float sum_lanes(float v) {
   v += dpp<0x4e>(v);                           // quad_perm [2,3,0,1]
   if constexpr (N >= 8) v += dpp<0x141>(v);    // row_half_mirror
   if constexpr (N >= 16) v += dpp<0x140>(v);   // row_mirror
+  if constexpr (N >= 32) v += __shfl_xor(v, 16, kWave);   // the neighbouring 16-lane row
   return v;
 }
 
@@ -301,7 +308,7 @@ __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
         float d = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) d = fmaf(q[g][e], kv[e], d);
-        d = sum_lanes<kLpr>(d) * a.scale;        // (q . k) * (1/sqrt(hd)), layer_scheduler.c:442-446
+        d = softcap(sum_lanes<kLpr>(d) * a.scale, a);   // (q . k) / sqrt(hd), layer_scheduler.c:442-448
         sc[g][k] = live ? d : -INFINITY;
       }
     }
@@ -475,7 +482,7 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
       float d = 0.f;
 #pragma unroll
       for (int i = 0; i < kDpl; ++i) d = fmaf(q[i], bt.k[j].get(i, bt.ks[j]), d);
-      d = sum_lanes<kLph>(d) * a.scale;   // (q . k) * (1/sqrt(hd)), layer_scheduler.c:442-446
+      d = softcap(sum_lanes<kLph>(d) * a.scale, a);   // (q . k) / sqrt(hd), layer_scheduler.c:442-448
       sc[j] = pb + j < p1 ? d : -INFINITY;
     }
     float bm = sc[0];                      // live: pb < p1
@@ -593,7 +600,7 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_rows(const AttnArgs a) {
       float d = 0.f;
 #pragma unroll
       for (int i = 0; i < kDpl; ++i) d = fmaf(q[i], bt.k[r].get(i, 1.f), d);
-      d = sum_lanes<kLph>(d) * a.scale;   // (q . k) * (1/sqrt(hd)), layer_scheduler.c:442-446
+      d = softcap(sum_lanes<kLph>(d) * a.scale, a);   // (q . k) / sqrt(hd), layer_scheduler.c:442-448
       sc[r] = pb + r < p1 && pb + r <= lim ? d : -INFINITY;
     }
     float bm = sc[0];
@@ -815,6 +822,42 @@ __global__ void k_kv_append(void* kc, void* vc, float* ksc, float* vsc, const fl
   if (threadIdx.x == 0) (is_v ? vsc : ksc)[pos] = s;
 }
 
+// Post norm (layer_scheduler.c:474-481, 553-560: ss_gemma_rmsnorm of the
+// projection's output y, then the residual add): hidden[i] += y[i] * s * w[i]
+// with s = 1 / sqrt(mean(y^2) + eps) and w already 1 + weight. With xr set,
+// also the x records of the new hidden * nw_out (nw_out null: weight 1) for
+// the next matvec. One workgroup; every iteration of the element loop runs
+// in all threads, so the 16 lanes of a record encode together (n % 16 == 0).
+__global__ void __launch_bounds__(1024) k_post_norm(float* hidden, const float* y, const float* w, int n,
+                                                   float eps, uint32_t* xr, const float* nw_out) {
+  __shared__ float red[16];
+  const int tid = threadIdx.x;
+  float ss = 0.f;
+  for (int i = tid; i < n; i += 1024) {
+    const float v = y[i];
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  float t = 0.f;
+  for (int k = 0; k < 16; ++k) t += red[k];
+  const float sc = 1.0f / sqrtf(t / (float)n + eps);
+  for (int i0 = 0; i0 < n; i0 += 1024) {
+    const int i = i0 + tid;
+    const bool in = i < n;
+    float out = 0.f;
+    if (in) {
+      out = hidden[i] + y[i] * sc * w[i];
+      hidden[i] = out;
+    }
+    if (xr) {
+      const Enc e = enc16(in ? out * (nw_out ? nw_out[i] : 1.f) : 0.f, out);
+      if (in) put_rec_lds(xr + (size_t)(i >> 4) * kRW, e, i & 15);
+    }
+  }
+}
+
 __global__ void k_swiglu(float* out, const float* g, const float* u, int n) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
     const float gv = g[i];
@@ -923,7 +966,8 @@ const void* attn_kernel_hd(int group, int kv_type) {
 
 int attn_resident_groups(int head_dim, int group, int kv_type) {
   const void* f = head_dim == 64 ? attn_kernel_hd<64>(group, kv_type)
-                : head_dim == 128 ? attn_kernel_hd<128>(group, kv_type) : nullptr;
+                : head_dim == 128 ? attn_kernel_hd<128>(group, kv_type)
+                : head_dim == 256 ? attn_kernel_hd<256>(group, kv_type) : nullptr;
   if (!f) return 0;
   const int threads = (group >= 4 ? kHgWaves : kAttnWaves) * kWave;
   int n = 0;
@@ -938,7 +982,7 @@ int attn_round_positions(int head_dim, int group) {
 }
 
 bool attention_supported(int head_dim, int group) {
-  return (head_dim == 64 || head_dim == 128) &&
+  return (head_dim == 64 || head_dim == 128 || head_dim == 256) &&
          (group == 1 || group == 2 || group == 4 || group == 8);
 }
 
@@ -946,6 +990,7 @@ hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs
   if (a.ns < 1 || a.ns > kMaxSplits) return hipErrorInvalidValue;   // merge weights: kMaxSplits per head
   if (head_dim == 64) return launch_attn_hd<64>(group, kv_type, a, s);
   if (head_dim == 128) return launch_attn_hd<128>(group, kv_type, a, s);
+  if (head_dim == 256) return launch_attn_hd<256>(group, kv_type, a, s);   // Gemma
   return hipErrorInvalidValue;
 }
 
@@ -1001,6 +1046,13 @@ hipError_t launch_rope_kv_rows(float* qkv, const float* bias, int ld, int qdim, 
   const int gx = (npairs + 255) / 256;
   hipLaunchKernelGGL(k_rope_kv_rows, dim3(gx, n), dim3(256), 0, s, qkv, bias, ld, qdim, kvdim, head_dim, rope_dim,
                      cs, dpos, kc, vc, max_seq);
+  return hipGetLastError();
+}
+
+hipError_t launch_post_norm(float* hidden, const float* y, const float* w, int n, float eps, uint32_t* xr,
+                            const float* nw_out, hipStream_t s) {
+  if (n <= 0 || n % 16 || !hidden || !y || !w) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_post_norm, dim3(1), dim3(1024), 0, s, hidden, y, w, n, eps, xr, nw_out);
   return hipGetLastError();
 }
 
