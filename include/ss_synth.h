@@ -17,7 +17,9 @@
  * standard deviation 1/sqrt(cols) and zero mean. Q4_K super-blocks have
  * random 6-bit scales and mins and uniform nibbles, with d and dmin drawn as
  * the Q4_0 d (mode 1: weight spread 1/sqrt(cols) again; mode 0:
- * |N(0, scale_sigma / 64)|). Mode 0 with positive d
+ * |N(0, scale_sigma / 64)|). Q2_K, Q3_K, Q5_K and Q6_K super-blocks have
+ * every code and scale byte uniformly random and d (and dmin) drawn so that
+ * the weights spread 1/sqrt(cols) in mode 1. Mode 0 with positive d
  * gives every Q4_0 block the mean -d/2 (nibbles average 7.5 - 8): a shared
  * direction that, compounded over the layers, makes deep models emit nearly
  * the same logits for any input; mode 1 models respond to their input.
@@ -38,8 +40,9 @@ extern "C" {
 typedef struct {
     int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, context_length;
     float rope_theta, rms_eps;
-    int32_t layer_type;   /* ggml type of the layer matrices: 2 (Q4_0), 8 (Q8_0) or 12 (Q4_K:
-                           * hidden, ffn and n_heads * head_dim multiples of 256) */
+    int32_t layer_type;   /* ggml type of the layer matrices: 2 (Q4_0), 8 (Q8_0) or a K-quant,
+                           * 10 (Q2_K), 11 (Q3_K), 12 (Q4_K), 13 (Q5_K), 14 (Q6_K) (hidden, ffn
+                           * and n_heads * head_dim multiples of 256) */
     int32_t embd_type;    /* token_embd.weight */
     int32_t out_type;     /* output.weight; -1 = tied to token_embd (no output.weight) */
     uint64_t seed;

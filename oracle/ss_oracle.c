@@ -183,6 +183,113 @@ void orc_dequantize(const void *src, float *dst, int32_t n, int32_t type) {
             }
         }
         break;
+    case ORC_Q2_K:
+        /* quantize.c:180-215: 84 bytes: 16 scale bytes (low nibble scale,
+         * high nibble min, one per 16 weights), 64 bytes of 2-bit codes, d,
+         * dmin. Weights 128h + 32j + l (l < 32, h < 2, j < 4) take bits
+         * 2j..2j+1 of byte 32h + l; weight = d*sc * q - dmin*m with the
+         * scale byte 8h + 2j + l/16. */
+        for (int32_t b = 0; b < n / 256; b++) {
+            const uint8_t *blk = p + (size_t)b * 84;
+            uint16_t dh, mh;
+            memcpy(&dh, blk + 80, 2);
+            memcpy(&mh, blk + 82, 2);
+            const float d = orc_f16_to_f32(dh), dmin = orc_f16_to_f32(mh);
+            for (int32_t h = 0; h < 2; h++)
+                for (int32_t j = 0; j < 4; j++)
+                    for (int32_t l = 0; l < 32; l++) {
+                        const uint8_t sc = blk[8 * h + 2 * j + l / 16];
+                        const float dl = d * (float)(sc & 0xF), ml = dmin * (float)(sc >> 4);
+                        const int32_t q = (blk[16 + 32 * h + l] >> (2 * j)) & 3;
+                        dst[b * 256 + 128 * h + 32 * j + l] = dl * (float)q - ml;
+                    }
+        }
+        break;
+    case ORC_Q3_K: {
+        /* quantize.c:219-263: 110 bytes: 32 bytes of high bits, 64 bytes of
+         * 2-bit codes, 12 bytes of 6-bit scales, d. Weights 128h + 32j + l
+         * take bits 2j..2j+1 of byte 32h + l, minus 4 unless bit 4h + j of
+         * hmask byte l is set; weight = d * (scale - 32) * q with scale
+         * 8h + 2j + l/16. The 16 scales: low nibbles of bytes 0..7 (scales
+         * 0..7) and high nibbles of bytes 0..7 (8..15), each with two more
+         * bits from byte 8 + i%4, at bit 2*(i/4). */
+        for (int32_t b = 0; b < n / 256; b++) {
+            const uint8_t *blk = p + (size_t)b * 110;
+            uint16_t dh;
+            memcpy(&dh, blk + 108, 2);
+            const float d = orc_f16_to_f32(dh);
+            const uint8_t *hm = blk, *qs = blk + 32, *sb = blk + 96;
+            int32_t scl[16];
+            for (int32_t i = 0; i < 16; i++) {
+                const int32_t low = i < 8 ? sb[i] & 0xF : sb[i - 8] >> 4;
+                const int32_t high = (sb[8 + i % 4] >> (2 * (i / 4))) & 3;
+                scl[i] = low | (high << 4);
+            }
+            for (int32_t h = 0; h < 2; h++)
+                for (int32_t j = 0; j < 4; j++)
+                    for (int32_t l = 0; l < 32; l++) {
+                        const float dl = d * (float)(scl[8 * h + 2 * j + l / 16] - 32);
+                        const int32_t q = ((qs[32 * h + l] >> (2 * j)) & 3) - ((hm[l] >> (4 * h + j)) & 1 ? 0 : 4);
+                        dst[b * 256 + 128 * h + 32 * j + l] = dl * (float)q;
+                    }
+        }
+        break;
+    }
+    case ORC_Q5_K:
+        /* quantize.c:312-346: 176 bytes: d, dmin, 12 bytes of 6-bit scales
+         * and mins (as Q4_K), 32 bytes of fifth bits, 128 bytes of nibbles.
+         * Sub-block k (32 weights) takes the low (k even) or high nibbles of
+         * bytes 32(k/2)..+31 plus 16 times bit k of qh byte l; weight =
+         * d*sc * q - dmin*m. */
+        for (int32_t b = 0; b < n / 256; b++) {
+            const uint8_t *blk = p + (size_t)b * 176;
+            uint16_t dh, mh;
+            memcpy(&dh, blk, 2);
+            memcpy(&mh, blk + 2, 2);
+            const float d = orc_f16_to_f32(dh), dmin = orc_f16_to_f32(mh);
+            const uint8_t *sc = blk + 4, *qh = blk + 16, *qs = blk + 48;
+            for (int32_t k = 0; k < 8; k++) {
+                uint8_t s6, m6;
+                if (k < 4) {
+                    s6 = sc[k] & 63;
+                    m6 = sc[k + 4] & 63;
+                } else {
+                    s6 = (uint8_t)((sc[k + 4] & 0xF) | ((sc[k - 4] >> 6) << 4));
+                    m6 = (uint8_t)((sc[k + 4] >> 4) | ((sc[k] >> 6) << 4));
+                }
+                const float d1 = d * (float)s6, m1 = dmin * (float)m6;
+                for (int32_t l = 0; l < 32; l++) {
+                    const uint8_t byte = qs[32 * (k / 2) + l];
+                    const int32_t q = (k % 2 ? byte >> 4 : byte & 0xF) + ((qh[l] >> k) & 1 ? 16 : 0);
+                    dst[b * 256 + k * 32 + l] = d1 * (float)q - m1;
+                }
+            }
+        }
+        break;
+    case ORC_Q6_K:
+        /* quantize.c:350-383: 210 bytes: 128 bytes of low nibbles, 64 bytes
+         * of high 2-bit pairs, 16 int8 scales (one per 16 weights), d.
+         * Weight 128h + 32c + l (c < 4, l < 32): low nibble of byte
+         * 64h + l (c = 0), 64h + 32 + l (1), high nibbles of the same (2,
+         * 3); high bits 2c..2c+1 of qh byte 32h + l; minus 32; weight =
+         * d * scale[8h + 2c + l/16] * q. */
+        for (int32_t b = 0; b < n / 256; b++) {
+            const uint8_t *blk = p + (size_t)b * 210;
+            uint16_t dh;
+            memcpy(&dh, blk + 208, 2);
+            const float d = orc_f16_to_f32(dh);
+            const uint8_t *ql = blk, *qh = blk + 128;
+            const int8_t *sc = (const int8_t *)(blk + 192);
+            for (int32_t h = 0; h < 2; h++)
+                for (int32_t c = 0; c < 4; c++)
+                    for (int32_t l = 0; l < 32; l++) {
+                        const uint8_t lb = ql[64 * h + 32 * (c & 1) + l];
+                        const int32_t lo = c < 2 ? lb & 0xF : lb >> 4;
+                        const int32_t q = (lo | (((qh[32 * h + l] >> (2 * c)) & 3) << 4)) - 32;
+                        dst[b * 256 + 128 * h + 32 * c + l] = d * (float)sc[8 * h + 2 * c + l / 16] * (float)q;
+                    }
+        }
+        break;
     default:
         memset(dst, 0, (size_t)n * sizeof(float));
         break;
@@ -195,7 +302,11 @@ static size_t orc_row_bytes(int32_t cols, int32_t type) {
     case ORC_F16: return (size_t)cols * 2;
     case ORC_Q4_0: return (size_t)(cols / 32) * 18;
     case ORC_Q8_0: return (size_t)(cols / 32) * 34;
+    case ORC_Q2_K: return (size_t)(cols / 256) * 84;
+    case ORC_Q3_K: return (size_t)(cols / 256) * 110;
     case ORC_Q4_K: return (size_t)(cols / 256) * 144;
+    case ORC_Q5_K: return (size_t)(cols / 256) * 176;
+    case ORC_Q6_K: return (size_t)(cols / 256) * 210;
     default: return 0;
     }
 }
@@ -773,8 +884,9 @@ static int key_ends(const char *k, uint64_t kl, const char *s) {
 }
 
 /* gguf_loader.c:22-62: weights per block and bytes per block */
+static int is_kquant(int32_t t) { return t >= ORC_Q2_K && t <= ORC_Q6_K; }
 static uint32_t type_block(int32_t t) {
-    return (t == ORC_Q4_0 || t == ORC_Q8_0) ? 32 : t == ORC_Q4_K ? 256 : 1;
+    return (t == ORC_Q4_0 || t == ORC_Q8_0) ? 32 : is_kquant(t) ? 256 : 1;
 }
 static uint32_t type_size(int32_t t) {
     switch (t) {
@@ -782,7 +894,11 @@ static uint32_t type_size(int32_t t) {
     case ORC_F16: return 2;
     case ORC_Q4_0: return 18;
     case ORC_Q8_0: return 34;
+    case ORC_Q2_K: return 84;
+    case ORC_Q3_K: return 110;
     case ORC_Q4_K: return 144;
+    case ORC_Q5_K: return 176;
+    case ORC_Q6_K: return 210;
     default: return 0;
     }
 }
@@ -927,7 +1043,7 @@ void orc_model_close(orc_model_t *m) {
 static int matrix_ok(const orc_tensor_t *t, uint64_t rows, uint64_t cols) {
     return t && t->n_dims == 2 && t->dims[0] == cols && t->dims[1] == rows &&
            (t->type == ORC_Q4_0 || t->type == ORC_Q8_0 || t->type == ORC_F32 || t->type == ORC_F16 ||
-            (t->type == ORC_Q4_K && cols % 256 == 0));
+            (is_kquant(t->type) && cols % 256 == 0));
 }
 static int vector_ok(const orc_tensor_t *t, uint64_t n) {
     return t && t->type == ORC_F32 && t->dims[0] == n;

@@ -21,6 +21,15 @@
 #define T_Q4_0 2
 #define T_Q8_0 8
 #define T_Q4_K 12
+#define T_Q2_K 10
+#define T_Q3_K 11
+#define T_Q5_K 13
+#define T_Q6_K 14
+/* the K-quants: super-blocks of 256 weights */
+static int is_k(int32_t type) { return type >= T_Q2_K && type <= T_Q6_K; }
+static size_t k_bytes(int32_t type) {
+    return type == T_Q2_K ? 84 : type == T_Q3_K ? 110 : type == T_Q4_K ? 144 : type == T_Q5_K ? 176 : 210;
+}
 #define CHUNK_BLOCKS (1u << 18)   /* 256 Ki blocks per work item */
 
 typedef struct {
@@ -152,11 +161,11 @@ typedef struct {
 
 /* quantisation blocks of a matrix: 32 weights (Q4_0, Q8_0) or 256 (Q4_K) */
 static uint64_t tensor_blocks(const syn_tensor_t *t) {
-    return t->dims[0] * t->dims[1] / (t->type == T_Q4_K ? 256 : 32);
+    return t->dims[0] * t->dims[1] / (is_k(t->type) ? 256 : 32);
 }
-static size_t block_bytes(int32_t type) { return type == T_Q4_0 ? 18 : type == T_Q8_0 ? 34 : 144; }
+static size_t block_bytes(int32_t type) { return type == T_Q4_0 ? 18 : type == T_Q8_0 ? 34 : k_bytes(type); }
 /* blocks per work item: Q4_K super-blocks are 8 blocks of 32 weights */
-static uint64_t chunk_blocks(int32_t type) { return type == T_Q4_K ? CHUNK_BLOCKS / 8 : CHUNK_BLOCKS; }
+static uint64_t chunk_blocks(int32_t type) { return is_k(type) ? CHUNK_BLOCKS / 8 : CHUNK_BLOCKS; }
 
 static void gen_item(job_t *j, uint64_t it, uint8_t *buf) {
     const syn_tensor_t *t = &j->t[j->item_tensor[it]];
@@ -198,6 +207,15 @@ static void gen_item(job_t *j, uint64_t it, uint8_t *buf) {
             /* weight d*sc*q - dmin*m with sc, m uniform 0..63 and q 0..15:
              * RMS sigma * sqrt(E[sc^2] (E[q^2] + 1)) = sigma * 323.5 */
             sigma = j->scale_mode == 1 ? 1.0 / (323.5 * sqrt((double)t->dims[0])) : j->scale_sigma / 64.0;
+        } else if (is_k(t->type)) {
+            /* the RMS of a weight per unit d (every field uniform): Q2_K
+             * d*sc*q - dmin*m, sc, m < 16, q < 4: sqrt(77.5 * (3.5 + 1));
+             * Q3_K d*(s - 32)*q, q in [-4, 3]: sqrt(341.5 * 5.5); Q5_K
+             * d*sc*q - dmin*m, sc, m < 64, q < 32: sqrt(1333.5 * (325.5 + 1));
+             * Q6_K d*sc*q, sc int8, q in [-32, 31]: sqrt(5461.5 * 341.5) */
+            const double rms = t->type == T_Q2_K ? 18.675 : t->type == T_Q3_K ? 43.34
+                             : t->type == T_Q5_K ? 659.8 : 1365.7;
+            sigma = j->scale_mode == 1 ? 1.0 / (rms * sqrt((double)t->dims[0])) : j->scale_sigma * 4.6 / rms;
         } else if (j->scale_mode == 1) {
             sigma = 1.0 / ((t->type == T_Q4_0 ? sqrt(21.5) : sqrt(127.0 * 128.0 / 3.0)) *
                            sqrt((double)t->dims[0]));
@@ -229,7 +247,23 @@ static void gen_item(job_t *j, uint64_t it, uint8_t *buf) {
                 memcpy(p + 16 + 8 * i, &q, 8);
             }
         }
-        for (uint64_t b = b0; b < b1 && t->type != T_Q4_K; b++) {
+        for (uint64_t b = b0; b < b1 && is_k(t->type) && t->type != T_Q4_K; b++) {
+            /* Q2_K, Q3_K, Q5_K, Q6_K: every code and scale byte random, then
+             * d (and dmin) */
+            uint8_t *p = buf + (b - b0) * bb;
+            for (size_t i = 0; i + 8 <= bb; i += 8) {
+                const uint64_t r = xo_next(&x);
+                memcpy(p + i, &r, 8);
+            }
+            for (size_t i = bb / 8 * 8; i < bb; i++) p[i] = (uint8_t)xo_next(&x);
+            const double dv = sigma * xo_normal(&x), mv = sigma * xo_normal(&x);
+            const uint16_t d = to_f16((float)(j->scale_mode == 1 ? dv : fabs(dv)));
+            const uint16_t dm = to_f16((float)(j->scale_mode == 1 ? mv : fabs(mv)));
+            const size_t od = t->type == T_Q2_K ? 80 : t->type == T_Q3_K ? 108 : t->type == T_Q5_K ? 0 : 208;
+            memcpy(p + od, &d, 2);
+            if (t->type == T_Q2_K || t->type == T_Q5_K) memcpy(p + od + 2, &dm, 2);
+        }
+        for (uint64_t b = b0; b < b1 && !is_k(t->type); b++) {
             uint8_t *p = buf + (b - b0) * bb;
             const double dv = sigma * xo_normal(&x);
             uint16_t d = to_f16((float)(j->scale_mode == 1 ? dv : fabs(dv)));
@@ -275,12 +309,12 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
     if (s->n_layers <= 0 || s->hidden <= 0 || s->n_heads <= 0 || s->n_kv_heads <= 0 ||
         s->head_dim <= 0 || s->ffn <= 0 || s->vocab <= 3 || s->hidden % 32 || s->ffn % 32 ||
         (s->n_heads * s->head_dim) % 32 || (s->n_kv_heads * s->head_dim) % 32 ||
-        (s->layer_type != T_Q4_0 && s->layer_type != T_Q8_0 && s->layer_type != T_Q4_K) ||
-        (s->embd_type != T_Q4_0 && s->embd_type != T_Q8_0 && s->embd_type != T_Q4_K) ||
-        (s->out_type != -1 && s->out_type != T_Q4_0 && s->out_type != T_Q8_0 && s->out_type != T_Q4_K) ||
-        /* Q4_K rows are whole super-blocks of 256 */
-        (s->layer_type == T_Q4_K && (s->hidden % 256 || s->ffn % 256 || (s->n_heads * s->head_dim) % 256)) ||
-        ((s->embd_type == T_Q4_K || s->out_type == T_Q4_K) && s->hidden % 256) ||
+        (s->layer_type != T_Q4_0 && s->layer_type != T_Q8_0 && !is_k(s->layer_type)) ||
+        (s->embd_type != T_Q4_0 && s->embd_type != T_Q8_0 && !is_k(s->embd_type)) ||
+        (s->out_type != -1 && s->out_type != T_Q4_0 && s->out_type != T_Q8_0 && !is_k(s->out_type)) ||
+        /* K-quant rows are whole super-blocks of 256 */
+        (is_k(s->layer_type) && (s->hidden % 256 || s->ffn % 256 || (s->n_heads * s->head_dim) % 256)) ||
+        ((is_k(s->embd_type) || is_k(s->out_type)) && s->hidden % 256) ||
         s->arch < 0 || s->arch > 3 || s->attn_softcap < 0 || s->final_softcap < 0 || s->qkv_bias < 0 || s->qkv_bias > 2 || s->scale_mode < 0 ||
         s->scale_mode > 1)
         return -5;
@@ -309,7 +343,7 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
         t[k].sid = (isnorm) == 2 ? 0x100000u + (uint64_t)k : sid++;                 \
         t[k].bytes = (isnorm) == 2 ? (uint64_t)(cols) * ((type_) == T_F16 ? 2 : 4)   \
                      : (isnorm) ? (uint64_t)(cols) * 4                               \
-                     : (type_) == T_Q4_K ? (uint64_t)(cols) * (rows) / 256 * 144     \
+                     : is_k(type_) ? (uint64_t)(cols) * (rows) / 256 * k_bytes(type_) \
                                 : (uint64_t)(cols) * (rows) / 32 * ((type_) == T_Q4_0 ? 18 : 34); \
         k++;                                                                         \
     } while (0)

@@ -47,6 +47,10 @@ VARIANTS = {
     "qwen2_f16_bias_fused": dict(arch=1, qkv_bias=2, fused_qkv=1, seed=26),
     "mha_hd64": dict(n_heads=4, n_kv_heads=4, head_dim=64, seed=27),
     "q4_k": dict(layer_type=12, embd_type=12, out_type=12, seed=28),
+    "q2_k_q6_head": dict(layer_type=10, embd_type=10, out_type=14, seed=34),
+    "q3_k_q5_head": dict(layer_type=11, embd_type=13, out_type=13, seed=35),
+    "q5_k": dict(layer_type=13, embd_type=14, out_type=-1, seed=36),
+    "q6_k": dict(layer_type=14, embd_type=14, out_type=14, seed=37),
     # tokenizer shorter than the tables: the vocabulary is clamped to it
     "padded_tied": dict(embd_type=2, out_type=-1, vocab_tokens=360, seed=29),
     "padded_out": dict(vocab_tokens=370, seed=30),

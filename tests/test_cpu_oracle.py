@@ -463,3 +463,89 @@ def test_q4_K_matvec_fp64(rows, cols):
     # the numpy decoder is the oracle's dequantisation, value for value
     deq = oracle.dequantize(w[:144], 256, Q4_K)
     assert np.allclose(deq, dequant_np(w[:144], 1, 256, Q4_K)[0], rtol=1e-6, atol=1e-9)
+
+
+# ---------------------------------------------------------------- Q2_K, Q3_K, Q5_K, Q6_K
+@pytest.mark.parametrize("qtype", [10, 11, 13, 14])
+def test_kquant_dequant_matches_independent_numpy(qtype):
+    """quantize.c:180-263, 310-383 against the vectorised fp64 numpy reading
+    of the GGML layouts in tests/util.py (for Q3_K through the 32-bit-word
+    scale unpacking): equal on random super-blocks (every product involved
+    is exact in fp32 or rounds once the same way)."""
+    from tests.util import KQ_BYTES, dequant_np, make_kq
+    rng = np.random.default_rng(qtype)
+    rows, cols = 5, 1024
+    w = make_kq(qtype, rows, cols, rng)
+    want = dequant_np(w, rows, cols, qtype)
+    rb = cols // 256 * KQ_BYTES[qtype]
+    got = np.stack([oracle.dequantize(w[r * rb:(r + 1) * rb], cols, qtype) for r in range(rows)])
+    assert np.max(np.abs(got - want)) <= 1e-7 * np.max(np.abs(want))
+
+
+def test_q2_K_closed_form():
+    """Bits 2j..2j+1 of byte 32h + l for weight 128h + 32j + l; scale byte
+    8h + 2j + l/16 = sc | m << 4: every byte 0b11100100 gives q = j."""
+    blk = np.zeros(84, np.uint8)
+    blk[0:16] = [(s % 16) | (((s * 3) % 16) << 4) for s in range(16)]
+    blk[16:80] = 0xE4
+    blk[80:82] = np.array([0.5], np.float16).view(np.uint8)
+    blk[82:84] = np.array([0.25], np.float16).view(np.uint8)
+    got = oracle.dequantize(blk, 256, 10)
+    for i in range(256):
+        h, j, l = i // 128, (i % 128) // 32, i % 32
+        s = 8 * h + 2 * j + l // 16
+        assert got[i] == np.float32(0.5 * (s % 16) * j - 0.25 * ((s * 3) % 16)), i
+
+
+def test_q3_K_closed_form():
+    """Zero scale bytes give scale 0 - 32; q = bits 2j..2j+1 (0b11100100: j),
+    minus 4 where the hmask bit 4h + j is clear (odd bits set here)."""
+    blk = np.zeros(110, np.uint8)
+    blk[0:32] = 0xAA                       # bits 1, 3, 5, 7 set
+    blk[32:96] = 0xE4
+    blk[108:110] = np.array([0.125], np.float16).view(np.uint8)
+    got = oracle.dequantize(blk, 256, 11)
+    for i in range(256):
+        h, j, l = i // 128, (i % 128) // 32, i % 32
+        q = j - (0 if (0xAA >> (4 * h + j)) & 1 else 4)
+        assert got[i] == np.float32(0.125 * -32 * q), i
+
+
+def test_q5_K_closed_form():
+    """Sub-block k: nibble (low for even k) plus 16 times bit k of qh byte l."""
+    from tests.util import q4k_pack_scales
+    sc, mn = np.arange(8) * 7 + 1, np.arange(8) * 5
+    blk = np.zeros(176, np.uint8)
+    blk[0:2] = np.array([0.5], np.float16).view(np.uint8)
+    blk[2:4] = np.array([0.25], np.float16).view(np.uint8)
+    blk[4:16] = q4k_pack_scales(sc, mn)
+    blk[16:48] = 0x55                      # bits 0, 2, 4, 6: even sub-blocks get +16
+    blk[48:176] = [(l % 16) | (((l * 3) % 16) << 4) for l in range(32)] * 4
+    got = oracle.dequantize(blk, 256, 13)
+    for i in range(256):
+        k, l = i // 32, i % 32
+        q = (l % 16 if k % 2 == 0 else (l * 3) % 16) + (16 if k % 2 == 0 else 0)
+        assert got[i] == np.float32(np.float32(0.5 * sc[k]) * q - np.float32(0.25 * mn[k])), i
+
+
+def test_q6_K_closed_form():
+    """Low nibbles 0 and high pairs 0 give q = -32; scale 8h + 2c + l/16."""
+    blk = np.zeros(210, np.uint8)
+    blk[192:208] = (np.arange(16) - 8).astype(np.int8).view(np.uint8)
+    blk[208:210] = np.array([0.5], np.float16).view(np.uint8)
+    got = oracle.dequantize(blk, 256, 14)
+    for i in range(256):
+        h, c, l = i // 128, (i % 128) // 32, i % 32
+        assert got[i] == np.float32(0.5 * (8 * h + 2 * c + l // 16 - 8) * -32), i
+
+
+@pytest.mark.parametrize("qtype", [10, 11, 13, 14])
+def test_kquant_matvec_fp64(qtype):
+    from tests.util import dequant_np, make_kq
+    rng = np.random.default_rng(qtype + 100)
+    rows, cols = 16, 2048
+    w = make_kq(qtype, rows, cols, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = oracle.matvec(w, x, rows, cols, qtype)
+    want = dequant_np(w, rows, cols, qtype) @ x.astype(np.float64)
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))

@@ -5,6 +5,8 @@ import ctypes as C
 import numpy as np
 
 Q4_0, Q8_0, Q4_K = 2, 8, 12
+Q2_K, Q3_K, Q5_K, Q6_K = 10, 11, 13, 14
+KQ_BYTES = {Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}   # per 256 weights
 
 
 def _vp(a):
@@ -80,9 +82,37 @@ def make_q4_k(rows, cols, rng, sigma=0.02):
     return out.reshape(-1)
 
 
+def _f16_into(out, lo, vals):
+    out[:, lo:lo + 2] = f16_bits(vals).view(np.uint8).reshape(-1, 2)
+
+
+def make_kq(qtype, rows, cols, rng, sigma=0.02):
+    """GGUF Q2_K / Q3_K / Q5_K / Q6_K super-blocks with every code and scale
+    field uniformly random, d (and dmin) = fp16(N(0, s)) with s chosen so that
+    the weights spread about sigma."""
+    nsb = rows * (cols // 256)
+    nbytes = KQ_BYTES[qtype]
+    out = rng.integers(0, 256, (nsb, nbytes), dtype=np.uint8)
+    if qtype == Q2_K:     # w = d*sc*q - dmin*m, sc, m < 16, q < 4
+        _f16_into(out, 80, rng.normal(0.0, sigma / 18.7, nsb))
+        _f16_into(out, 82, rng.normal(0.0, sigma / 18.7, nsb))
+    elif qtype == Q3_K:   # w = d*(s - 32)*q, q in [-4, 3]
+        _f16_into(out, 108, rng.normal(0.0, sigma / 43.3, nsb))
+    elif qtype == Q5_K:   # w = d*sc*q - dmin*m, sc, m < 64, q < 32
+        _f16_into(out, 0, rng.normal(0.0, sigma / 660.0, nsb))
+        _f16_into(out, 2, rng.normal(0.0, sigma / 660.0, nsb))
+    elif qtype == Q6_K:   # w = d*sc*q, sc int8, q in [-32, 31]
+        _f16_into(out, 208, rng.normal(0.0, sigma / 1366.0, nsb))
+    else:
+        raise ValueError(qtype)
+    return out.reshape(-1)
+
+
 def make_blocks(qtype, rows, cols, rng, sigma=0.02):
     if qtype == Q4_K:
         return make_q4_k(rows, cols, rng, sigma)
+    if qtype in (Q2_K, Q3_K, Q5_K, Q6_K):
+        return make_kq(qtype, rows, cols, rng, sigma)
     return make_q4_0(rows, cols, rng, sigma) if qtype == Q4_0 else make_q8_0(rows, cols, rng, sigma)
 
 
@@ -113,6 +143,8 @@ def dequant_np(blocks, rows, cols, qtype):
         b = blocks.reshape(rows * nb, 34)
         d = b[:, 0:2].copy().view(np.float16).astype(np.float64).reshape(-1)
         w = b[:, 2:].view(np.int8).astype(np.float64) * d[:, None]
+    elif qtype in (Q2_K, Q3_K, Q5_K, Q6_K):
+        w = _dequant_kq(blocks, rows, cols, qtype)
     else:   # Q4_K super-blocks of 256
         nsb = rows * (cols // 256)
         b = blocks.reshape(nsb, 144)
@@ -126,6 +158,53 @@ def dequant_np(blocks, rows, cols, qtype):
                 nib = (q[32 * (k // 2):32 * (k // 2) + 32] >> (4 * (k % 2))) & 15
                 w[i, 32 * k:32 * k + 32] = d[i] * sc[k] * nib - dm[i] * mn[k]
     return w.reshape(rows, cols)
+
+
+def _f16_col(b, lo):
+    return b[:, lo:lo + 2].copy().view(np.float16).astype(np.float64).reshape(-1)
+
+
+def _dequant_kq(blocks, rows, cols, qtype):
+    """Q2_K / Q3_K / Q5_K / Q6_K in fp64, vectorised over the 256 weights of a
+    super-block from the GGML block layouts (weight index i = 128h + 32j + l
+    for the 2-bit-plane formats and Q6_K; sub-block i // 32 for Q5_K)."""
+    nsb = rows * (cols // 256)
+    b = blocks.reshape(nsb, KQ_BYTES[qtype]).astype(np.int64)
+    i = np.arange(256)
+    h, j, l = i // 128, (i % 128) // 32, i % 32
+    if qtype == Q2_K:
+        q = (b[:, 16 + 32 * h + l] >> (2 * j)) & 3
+        sb = b[:, 8 * h + 2 * j + l // 16]
+        return (_f16_col(b.astype(np.uint8), 80)[:, None] * (sb & 15) * q
+                - _f16_col(b.astype(np.uint8), 82)[:, None] * (sb >> 4))
+    if qtype == Q3_K:
+        # the 16 6-bit scales from the 12 packed bytes, as 32-bit words
+        w32 = b[:, 96:108].astype(np.uint8).copy().view("<u4").astype(np.int64)
+        a0, a1, t = w32[:, 0], w32[:, 1], w32[:, 2]
+        m2, m1 = 0x0F0F0F0F, 0x03030303
+        aux = np.stack([(a0 & m2) | (((t >> 0) & m1) << 4), (a1 & m2) | (((t >> 2) & m1) << 4),
+                        ((a0 >> 4) & m2) | (((t >> 4) & m1) << 4), ((a1 >> 4) & m2) | (((t >> 6) & m1) << 4)],
+                       axis=1).astype("<u4")
+        scales = aux.view(np.uint8).astype(np.int64).reshape(nsb, 16)
+        hbit = (b[:, l] >> (4 * h + j)) & 1
+        q = ((b[:, 32 + 32 * h + l] >> (2 * j)) & 3) - np.where(hbit == 1, 0, 4)
+        return _f16_col(b.astype(np.uint8), 108)[:, None] * (scales[:, 8 * h + 2 * j + l // 16] - 32) * q
+    if qtype == Q5_K:
+        k = i // 32
+        sc = np.zeros((nsb, 8), np.int64)
+        mn = np.zeros((nsb, 8), np.int64)
+        for s in range(nsb):
+            sc[s], mn[s] = q4k_unpack_scales(b[s, 4:16])
+        byte = b[:, 48 + 32 * (k // 2) + l]
+        q = np.where(k % 2 == 1, byte >> 4, byte & 15) + 16 * ((b[:, 16 + l] >> k) & 1)
+        return (_f16_col(b.astype(np.uint8), 0)[:, None] * sc[:, k] * q
+                - _f16_col(b.astype(np.uint8), 2)[:, None] * mn[:, k])
+    # Q6_K
+    lb = b[:, 64 * h + 32 * (j & 1) + l]
+    lo = np.where(j < 2, lb & 15, lb >> 4)
+    q = (lo | (((b[:, 128 + 32 * h + l] >> (2 * j)) & 3) << 4)) - 32
+    sc = b[:, 192:208].astype(np.uint8).view(np.int8).astype(np.int64)
+    return _f16_col(b.astype(np.uint8), 208)[:, None] * sc[:, 8 * h + 2 * j + l // 16] * q
 
 
 def rel_err(got, want):
