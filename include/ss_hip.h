@@ -47,6 +47,10 @@ typedef struct ss_hip_model ss_hip_model_t;
 #define SS_HIP_Q4_0 2
 #define SS_HIP_Q8_0 8
 #define SS_HIP_Q4_K 12   /* 256-weight super-blocks (cols a multiple of 256) */
+#define SS_HIP_Q2_K 10   /* the other K-quants, also 256-weight super-blocks */
+#define SS_HIP_Q3_K 11
+#define SS_HIP_Q5_K 13
+#define SS_HIP_Q6_K 14
 
 /* token launch modes (match SS_LAUNCH_* in slipstream.h): per-kernel eager,
  * per-kernel replayed from a HIP graph, or one persistent launch per token

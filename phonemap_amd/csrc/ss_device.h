@@ -158,6 +158,26 @@ struct QTraits<12> {           // Q4_K: a 32-weight sub-block packs like a Q4_0 
   static constexpr int kQB = 16;
   static constexpr int kGgufBytes = 144;   // per 256-weight super-block
 };
+template <>
+struct QTraits<10> {           // Q2_K: 2-bit codes in nibbles
+  static constexpr int kQB = 16;
+  static constexpr int kGgufBytes = 84;
+};
+template <>
+struct QTraits<11> {           // Q3_K: 3-bit codes + 4 in nibbles
+  static constexpr int kQB = 16;
+  static constexpr int kGgufBytes = 110;
+};
+template <>
+struct QTraits<13> {           // Q5_K: 5-bit codes as int8
+  static constexpr int kQB = 32;
+  static constexpr int kGgufBytes = 176;
+};
+template <>
+struct QTraits<14> {           // Q6_K: 6-bit codes - 32 as int8
+  static constexpr int kQB = 32;
+  static constexpr int kGgufBytes = 210;
+};
 
 
 // ------------------------------------------------------------ x records
@@ -324,6 +344,81 @@ __device__ __forceinline__ float q4k_dot(const uint4 q, const uint32_t* ra, cons
   const float qx = fmaf((float)a, sa, (float)b * sb);
   const float sx = fmaf((float)((int)ta.x >> 3), sa, (float)((int)tb.x >> 3) * sb);
   return fmaf(dsc, qx, -dmn * sx);
+}
+
+// The K-quants other than Q4_K: a 32-weight block is two 16-weight groups,
+// each with weight = A * c - B (A = d * scale, B = dmin * min, or B = 4 A for
+// Q3_K's codes stored + 4, B = 0 for Q6_K; all exact in fp32). The block's
+// scale entry e and super-block word sup = d | dmin << 16 give A and B:
+//   Q2_K (quantize.c:180-215)  e = scale byte of each group (scale | min << 4)
+//   Q3_K (:219-263)            e = the groups' 6-bit scales; A = d (s - 32)
+//   Q5_K (:312-346)            e = scale | min << 8, one pair for the block
+//   Q6_K (:350-383)            e = the groups' int8 scales
+template <int QT>
+__device__ __forceinline__ void kq_affine(uint32_t e, uint32_t sup, float (&A)[2], float (&B)[2]) {
+  const float d = h2f((uint16_t)(sup & 0xffffu)), dm = h2f((uint16_t)(sup >> 16));
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const uint32_t b = (e >> (8 * g)) & 0xffu;
+    if constexpr (QT == 10) {
+      A[g] = d * (float)(b & 15u);
+      B[g] = dm * (float)(b >> 4);
+    } else if constexpr (QT == 11) {
+      A[g] = d * (float)((int)b - 32);
+      B[g] = 4.0f * A[g];
+    } else if constexpr (QT == 13) {
+      A[g] = d * (float)(e & 0xffu);
+      B[g] = dm * (float)(e >> 8);
+    } else {
+      A[g] = d * (float)(int8_t)b;
+      B[g] = 0.f;
+    }
+  }
+}
+
+// sum over one 16-value record of code * X, exact: X = 16384 q1 + 128 q2 + q3
+// from the record's three int8 levels; nibble codes (w[i] & 0x0F0F0F0F or
+// >> 4) or int8 codes (|code| <= 32 keeps the sum inside int32)
+template <bool NIB, bool HIGH>
+__device__ __forceinline__ int rec_sum(const uint32_t (&w)[4], const uint32_t* r) {
+  int a = 0;
+#pragma unroll
+  for (int l = 0; l < 3; ++l) {
+    const uint4 x = *reinterpret_cast<const uint4*>(r + 4 * l);
+    if (l) a <<= 7;
+    const uint32_t xs[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t c = NIB ? (HIGH ? (w[i] >> 4) & 0x0F0F0F0Fu : w[i] & 0x0F0F0F0Fu) : w[i];
+      a = sdot4(c, (int)xs[i], a);
+    }
+  }
+  return a;
+}
+
+// One 32-weight block of a K-quant other than Q4_K: sum over both groups of
+// A * (sum c X) s3 - B * (sum X) s3, sum X being the record's word 12 / 8.
+template <int QT>
+__device__ __forceinline__ float kq_dot(const uint4 qa, const uint4 qb, const uint32_t* ra, const uint32_t* rb,
+                                        uint32_t e, uint32_t sup) {
+  float A[2], B[2];
+  kq_affine<QT>(e, sup, A, B);
+  int a, b;
+  if constexpr (QT == 10 || QT == 11) {   // nibbles: weight j low, j + 16 high
+    const uint32_t w[4] = {qa.x, qa.y, qa.z, qa.w};
+    a = rec_sum<true, false>(w, ra);
+    b = rec_sum<true, true>(w, rb);
+  } else {                                // int8 codes: 16 per record
+    const uint32_t wa[4] = {qa.x, qa.y, qa.z, qa.w}, wb[4] = {qb.x, qb.y, qb.z, qb.w};
+    a = rec_sum<false, false>(wa, ra);
+    b = rec_sum<false, false>(wb, rb);
+  }
+  const uint2 ta = *reinterpret_cast<const uint2*>(ra + 12);
+  const uint2 tb = *reinterpret_cast<const uint2*>(rb + 12);
+  const float sa = __uint_as_float(ta.y), sb = __uint_as_float(tb.y);
+  const float qx = fmaf(A[0], (float)a * sa, A[1] * ((float)b * sb));
+  const float sx = fmaf(B[0], (float)((int)ta.x >> 3) * sa, B[1] * ((float)((int)tb.x >> 3) * sb));
+  return qx - sx;
 }
 
 // Q8_0 block (quantize.c:139-149: 32 int8 codes, value d * code); levels 1-2

@@ -187,7 +187,7 @@ struct Round {
   static constexpr int kNV = QTraits<QT>::kQB / 16;
   uint4 q[NMAT][UT][kNV];
   uint32_t sc[NMAT][UT / 2];   // the unit's binary16 scales (Q4_K: scale | min << 8), tile order
-  uint32_t su[NMAT][QT == kQ4K ? UT / 2 : 1];   // Q4_K: (d, dmin) of the unit's super-blocks
+  uint32_t su[NMAT][is_kq(QT) ? UT / 2 : 1];   // K-quants: (d, dmin) of the unit's super-blocks
 };
 
 template <int QT, int NMAT, int UT>
@@ -209,7 +209,7 @@ __device__ __forceinline__ void load_round(Round<QT, NMAT, UT>& f, const GemvArg
     } else {
       f.sc[m][0] = *sp;
     }
-    if constexpr (QT == kQ4K) {   // a unit (an even number of tiles) covers UT / 2 super-blocks
+    if constexpr (is_kq(QT)) {   // a unit (an even number of tiles) covers UT / 2 super-blocks
       const int nsb = ntk / 2;
 #pragma unroll
       for (int j = 0; j < UT / 2; ++j)
@@ -245,6 +245,8 @@ __device__ __forceinline__ void fma_round(float (&acc)[NMAT], const Round<QT, NM
         const float dsc = h2f((uint16_t)(sup & 0xffffu)) * (float)(e & 0xffu);   // exact
         const float dmn = h2f((uint16_t)(sup >> 16)) * (float)(e >> 8);
         acc[m] += q4k_dot(f.q[m][k][0], ra, ra + kRW, dsc, dmn);
+      } else if constexpr (is_kq(QT)) {
+        acc[m] += kq_dot<QT>(f.q[m][k][0], f.q[m][k][Round<QT, NMAT, UT>::kNV - 1], ra, ra + kRW, e, f.su[m][k / 2]);
       } else {
         float s;
         if constexpr (QT == 2)
@@ -370,7 +372,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int row, bool own, c
 // Q8_0 and two-matrix rounds hold 64 VGPRs of codes: at most 8 waves, so
 // 256 VGPRs are available to them.
 template <int QT, int NMAT>
-constexpr int gemv_max_waves() { return QT == 8 || NMAT == 2 || (QT == kQ4K) ? 8 : 16; }
+constexpr int gemv_max_waves() { return QT == 8 || NMAT == 2 || is_kq(QT) ? 8 : 16; }
 
 template <int QT, int NMAT, int EPI, int UT, bool MERGE, bool PX>
 __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(const GemvArgs a) {
@@ -520,6 +522,90 @@ __global__ void k_pack_q4k(const uint8_t* __restrict__ src, uint8_t* __restrict_
         (uint32_t)(sb[0] | (sb[1] << 8)) | ((uint32_t)(sb[2] | (sb[3] << 8)) << 16);
 }
 
+// GGUF Q2_K / Q3_K / Q5_K / Q6_K super-blocks -> tiled planes: thread i
+// takes 32-weight block b = i % nb (k = b % 8 within its super-block, weights
+// 128h + 32j + l with h = k / 4, j = k % 4) of row row_off + i / nb. Its 32
+// codes go to the code plane (nibbles in Q4_0 order for Q2_K and Q3_K, the
+// latter + 4; int8 for Q5_K and Q6_K, the latter - 32), its scale entry (see
+// kq_affine) to the scale plane and, with block 0, the super-block's d and
+// dmin to the third plane. Field offsets: quantize.h:61-99.
+template <int QT>
+__global__ void k_pack_kq(const uint8_t* __restrict__ src, uint8_t* __restrict__ qs, uint16_t* __restrict__ ds,
+                          uint32_t* __restrict__ su, int64_t nblk, int nb, int64_t row_off) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nblk) return;
+  constexpr int kBytes = QTraits<QT>::kGgufBytes;
+  const int64_t r = i / nb;
+  const int b = (int)(i % nb), k = b % 8, nsb = nb / 8, h = k / 4, j = k % 4;
+  const int64_t row = row_off + r;
+  const uint8_t* sb = src + (r * nsb + b / 8) * kBytes;
+  int c[32];
+  uint32_t e, d, dm = 0;
+  if constexpr (QT == kQ2K) {   // quantize.c:180-215
+#pragma unroll
+    for (int l = 0; l < 32; ++l) c[l] = (sb[16 + 32 * h + l] >> (2 * j)) & 3;
+    e = sb[8 * h + 2 * j] | ((uint32_t)sb[8 * h + 2 * j + 1] << 8);
+    d = sb[80] | ((uint32_t)sb[81] << 8);
+    dm = sb[82] | ((uint32_t)sb[83] << 8);
+  } else if constexpr (QT == kQ3K) {   // :219-263, the code + 4 (0..7)
+#pragma unroll
+    for (int l = 0; l < 32; ++l)
+      c[l] = ((sb[32 + 32 * h + l] >> (2 * j)) & 3) | (((sb[l] >> (4 * h + j)) & 1) << 2);
+    uint32_t sv[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int si = 8 * h + 2 * j + g;
+      const uint32_t low = si < 8 ? sb[96 + si] & 15u : sb[96 + si - 8] >> 4;
+      sv[g] = low | (((uint32_t)(sb[104 + si % 4] >> (2 * (si / 4))) & 3u) << 4);
+    }
+    e = sv[0] | (sv[1] << 8);
+    d = sb[108] | ((uint32_t)sb[109] << 8);
+  } else if constexpr (QT == kQ5K) {   // :312-346
+    const uint8_t* sc = sb + 4;
+    uint32_t s6, m6;
+    if (k < 4) {
+      s6 = sc[k] & 63u;
+      m6 = sc[k + 4] & 63u;
+    } else {
+      s6 = (sc[k + 4] & 0xFu) | ((uint32_t)(sc[k - 4] >> 6) << 4);
+      m6 = (sc[k + 4] >> 4) | ((uint32_t)(sc[k] >> 6) << 4);
+    }
+#pragma unroll
+    for (int l = 0; l < 32; ++l) {
+      const uint32_t byte = sb[48 + 32 * (k / 2) + l];
+      c[l] = (int)(k % 2 ? byte >> 4 : byte & 15u) + 16 * ((sb[16 + l] >> k) & 1);
+    }
+    e = s6 | (m6 << 8);
+    d = sb[0] | ((uint32_t)sb[1] << 8);
+    dm = sb[2] | ((uint32_t)sb[3] << 8);
+  } else {   // Q6_K, :350-383
+#pragma unroll
+    for (int l = 0; l < 32; ++l) {
+      const uint32_t lb = sb[64 * h + 32 * (j & 1) + l];
+      const uint32_t lo = j < 2 ? lb & 15u : lb >> 4;
+      c[l] = (int)(lo | (((sb[128 + 32 * h + l] >> (2 * j)) & 3u) << 4)) - 32;
+    }
+    e = sb[192 + 8 * h + 2 * j] | ((uint32_t)sb[192 + 8 * h + 2 * j + 1] << 8);
+    d = sb[208] | ((uint32_t)sb[209] << 8);
+  }
+  const int ntk = (nb + kTB - 1) / kTB, g = (int)(row / kRG), tl = tile_lane((int)(row % kRG), b);
+  uint8_t* dst = qs + tile_idx(g, ntk, b / kTB, tl) * QTraits<QT>::kQB;
+  if constexpr (QTraits<QT>::kQB == 16) {
+    uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int m = 0; m < 16; ++m) w[m / 4] |= ((uint32_t)(c[m] & 15) | ((uint32_t)(c[m + 16] & 15) << 4)) << (8 * (m % 4));
+    *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+  } else {
+    uint32_t w[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int m = 0; m < 32; ++m) w[m / 4] |= ((uint32_t)c[m] & 0xffu) << (8 * (m % 4));
+    reinterpret_cast<uint4*>(dst)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    reinterpret_cast<uint4*>(dst)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+  }
+  ds[scale_idx(g, ntk, b / kTB, tl)] = (uint16_t)e;
+  if (k == 0) su[((size_t)g * nsb + b / 8) * kRG + row % kRG] = d | (dm << 16);
+}
+
 // Row `token` of a packed table, dequantised exactly as quantize.c:60-72 /
 // 139-149 (one fp32 multiply per weight). With tokens set, workgroup row z
 // writes row tokens[*dpos + z] to out + z * cols (a prompt's rows at once).
@@ -544,6 +630,26 @@ __device__ __forceinline__ float embed_value(const PackedMat& t, int tok, int nt
     const float d1 = h2f((uint16_t)(sup & 0xffffu)) * (float)(e & 0xffu);
     const float m1 = h2f((uint16_t)(sup >> 16)) * (float)(e >> 8);
     return __fsub_rn(__fmul_rn(d1, (float)(p < 16 ? v & 0xF : v >> 4)), m1);
+  } else if constexpr (is_kq(QT)) {
+    // the reference's per-weight expressions (quantize.c:180-383), each
+    // product and difference rounded once
+    const uint32_t e = t.ds[scale_idx(tok / kRG, ntk, b / kTB, l)];
+    const uint32_t sup = t.su[((size_t)(tok / kRG) * (ntk / 2) + b / 8) * kRG + tok % kRG];
+    const float dd = h2f((uint16_t)(sup & 0xffffu)), dm = h2f((uint16_t)(sup >> 16));
+    const uint32_t sg = (e >> (8 * (p / 16))) & 0xffu;   // the group's scale byte
+    if constexpr (QT == kQ2K || QT == kQ3K) {
+      const uint8_t v = q[p & 15];
+      const int nib = p < 16 ? v & 0xF : v >> 4;
+      if constexpr (QT == kQ2K)
+        return __fsub_rn(__fmul_rn(__fmul_rn(dd, (float)(sg & 15u)), (float)nib), __fmul_rn(dm, (float)(sg >> 4)));
+      else
+        return __fmul_rn(__fmul_rn(dd, (float)((int)sg - 32)), (float)(nib - 4));
+    } else if constexpr (QT == kQ5K) {
+      return __fsub_rn(__fmul_rn(__fmul_rn(dd, (float)(e & 0xffu)), (float)(int8_t)q[p]),
+                       __fmul_rn(dm, (float)(e >> 8)));
+    } else {
+      return __fmul_rn(__fmul_rn(dd, (float)(int8_t)sg), (float)(int8_t)q[p]);
+    }
   } else {
     return d * (float)(int8_t)q[p];
   }
@@ -662,7 +768,7 @@ GemvPlan gemv_plan(int rows, int cols, int type, int nmat, int unit) {
   GemvPlan p;
   const int groups = (rows + kRG - 1) / kRG;
   const int ntk = (cols / 32 + kTB - 1) / kTB;
-  const int smax = type == 8 || type == kQ4K || nmat == 2 ? gemv_max_waves<8, 1>() : gemv_max_waves<2, 1>();
+  const int smax = type == 8 || is_kq(type) || nmat == 2 ? gemv_max_waves<8, 1>() : gemv_max_waves<2, 1>();
   const int ut = unit;
   const int nu = (ntk + ut - 1) / ut;
   const int S = nu < smax ? nu : smax;
@@ -681,11 +787,11 @@ static void packed_sizes(int type, int64_t rows, int cols, size_t* code, size_t*
   const size_t groups = (size_t)((rows + kRG - 1) / kRG);
   const int ntk = (cols / 32 + kTB - 1) / kTB;
   const int nu = (ntk + kUT - 1) / kUT;
-  const int kqb = type == 2 || type == kQ4K ? 16 : type == 8 ? 32 : 0;
+  const int kqb = code_bytes_of(type);
   *code = ((groups * ntk * kWave * kqb) + 255) & ~(size_t)255;
   *scales = groups * nu * kWave * kUT * 2;
   *sup = 0;
-  if (type == kQ4K) {
+  if (is_kq(type)) {
     *scales = (*scales + 255) & ~(size_t)255;
     *sup = groups * (size_t)(cols / 256) * kRG * 4;
   }
@@ -716,6 +822,10 @@ hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t s) {
   if (a.type == 2) return launch_q<2>(epi, a, s);
   if (a.type == 8) return launch_q<8>(epi, a, s);
   if (a.type == kQ4K) return launch_q<kQ4K>(epi, a, s);
+  if (a.type == kQ2K) return launch_q<kQ2K>(epi, a, s);
+  if (a.type == kQ3K) return launch_q<kQ3K>(epi, a, s);
+  if (a.type == kQ5K) return launch_q<kQ5K>(epi, a, s);
+  if (a.type == kQ6K) return launch_q<kQ6K>(epi, a, s);
   return hipErrorInvalidValue;
 }
 
@@ -737,6 +847,18 @@ hipError_t launch_pack(int type, const uint8_t* src, PackedMat dst, int64_t nblo
   else if (type == kQ4K && dst.su && nb % 8 == 0)
     hipLaunchKernelGGL(k_pack_q4k, dim3((unsigned)grid), dim3(256), 0, s, src, qs, ds, const_cast<uint32_t*>(dst.su),
                        nblocks, nb, row_off);
+  else if (type == kQ2K && dst.su && nb % 8 == 0)
+    hipLaunchKernelGGL(k_pack_kq<kQ2K>, dim3((unsigned)grid), dim3(256), 0, s, src, qs, ds,
+                       const_cast<uint32_t*>(dst.su), nblocks, nb, row_off);
+  else if (type == kQ3K && dst.su && nb % 8 == 0)
+    hipLaunchKernelGGL(k_pack_kq<kQ3K>, dim3((unsigned)grid), dim3(256), 0, s, src, qs, ds,
+                       const_cast<uint32_t*>(dst.su), nblocks, nb, row_off);
+  else if (type == kQ5K && dst.su && nb % 8 == 0)
+    hipLaunchKernelGGL(k_pack_kq<kQ5K>, dim3((unsigned)grid), dim3(256), 0, s, src, qs, ds,
+                       const_cast<uint32_t*>(dst.su), nblocks, nb, row_off);
+  else if (type == kQ6K && dst.su && nb % 8 == 0)
+    hipLaunchKernelGGL(k_pack_kq<kQ6K>, dim3((unsigned)grid), dim3(256), 0, s, src, qs, ds,
+                       const_cast<uint32_t*>(dst.su), nblocks, nb, row_off);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -754,6 +876,18 @@ hipError_t launch_embed(int type, PackedMat t, int cols, const int* tokens, cons
   else if (type == kQ4K)
     hipLaunchKernelGGL(k_embed<kQ4K>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out,
                        nw, xr, scale);
+  else if (type == kQ2K)
+    hipLaunchKernelGGL(k_embed<kQ2K>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out,
+                       nw, xr, scale);
+  else if (type == kQ3K)
+    hipLaunchKernelGGL(k_embed<kQ3K>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out,
+                       nw, xr, scale);
+  else if (type == kQ5K)
+    hipLaunchKernelGGL(k_embed<kQ5K>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out,
+                       nw, xr, scale);
+  else if (type == kQ6K)
+    hipLaunchKernelGGL(k_embed<kQ6K>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out,
+                       nw, xr, scale);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
@@ -770,6 +904,18 @@ hipError_t launch_embed_rows(int type, PackedMat t, int cols, const int* tokens,
                        nullptr, nullptr, scale);
   else if (type == kQ4K)
     hipLaunchKernelGGL(k_embed<kQ4K>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
+                       nullptr, nullptr, scale);
+  else if (type == kQ2K)
+    hipLaunchKernelGGL(k_embed<kQ2K>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
+                       nullptr, nullptr, scale);
+  else if (type == kQ3K)
+    hipLaunchKernelGGL(k_embed<kQ3K>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
+                       nullptr, nullptr, scale);
+  else if (type == kQ5K)
+    hipLaunchKernelGGL(k_embed<kQ5K>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
+                       nullptr, nullptr, scale);
+  else if (type == kQ6K)
+    hipLaunchKernelGGL(k_embed<kQ6K>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
                        nullptr, nullptr, scale);
   else
     return hipErrorInvalidValue;

@@ -52,13 +52,23 @@ int32_t fail(int32_t code, const char* fmt, ...) {
 
 size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 
-int code_bytes(int type) { return type == SS_HIP_Q4_0 || type == SS_HIP_Q4_K ? 16 : type == SS_HIP_Q8_0 ? 32 : 0; }
-// GGUF bytes per 32 weights (a Q4_K super-block of 256 is 144 bytes: 18 per 32)
-int gguf_block_bytes(int type) { return type == SS_HIP_Q4_0 || type == SS_HIP_Q4_K ? 18 : type == SS_HIP_Q8_0 ? 34 : 0; }
+// GGUF bytes of a row of cols weights (gguf_loader.c:22-62 block sizes)
+size_t gguf_row_bytes(int type, int64_t cols) {
+  switch (type) {
+    case SS_HIP_Q4_0: return (size_t)cols / 32 * 18;
+    case SS_HIP_Q8_0: return (size_t)cols / 32 * 34;
+    case SS_HIP_Q2_K: return (size_t)cols / 256 * 84;
+    case SS_HIP_Q3_K: return (size_t)cols / 256 * 110;
+    case SS_HIP_Q4_K: return (size_t)cols / 256 * 144;
+    case SS_HIP_Q5_K: return (size_t)cols / 256 * 176;
+    case SS_HIP_Q6_K: return (size_t)cols / 256 * 210;
+    default: return 0;
+  }
+}
 
-bool quant_type_ok(int type) { return type == SS_HIP_Q4_0 || type == SS_HIP_Q8_0 || type == SS_HIP_Q4_K; }
+bool quant_type_ok(int type) { return type == SS_HIP_Q4_0 || type == SS_HIP_Q8_0 || ssk::is_kq(type); }
 // columns a row of this type must be a multiple of (whole blocks, or super-blocks)
-int col_unit(int type) { return type == SS_HIP_Q4_K ? 256 : 32; }
+int col_unit(int type) { return ssk::is_kq(type) ? 256 : 32; }
 
 ssk::PackedMat view(const void* base, int type, int64_t rows, int cols) {
   return ssk::packed_view(base, type, rows, cols);
@@ -67,7 +77,7 @@ ssk::PackedMat view(const void* base, int type, int64_t rows, int cols) {
 // Algorithmic HBM bytes of one matvec launch: packed weights (18 or 34 bytes
 // per 32 weights) + x + y.
 double matvec_bytes(int type, int64_t rows, int cols, int nmat) {
-  return (double)nmat * rows * (cols / 32) * gguf_block_bytes(type) + 4.0 * cols + 4.0 * rows;
+  return (double)nmat * rows * gguf_row_bytes(type, cols) + 4.0 * cols + 4.0 * rows;
 }
 
 }  // namespace
@@ -147,7 +157,7 @@ int32_t set_device(ss_hip_ctx* c) {
 int32_t pack_rows(ss_hip_ctx* c, void* dst, int64_t total_rows, int64_t row_off,
                   const void* src, int type, int64_t rows, int cols) {
   const int nb = cols / 32;
-  const size_t row_bytes = (size_t)nb * gguf_block_bytes(type);
+  const size_t row_bytes = gguf_row_bytes(type, cols);
   const size_t chunk_target = 64u << 20;
   int64_t chunk_rows = (int64_t)(chunk_target / row_bytes);
   if (chunk_rows < 1) chunk_rows = 1;
@@ -341,7 +351,7 @@ int32_t ss_hip_pack_matrix(ss_hip_ctx_t* c, void* dst, const void* src, int32_t 
 
 // ============================================================== single ops
 static int32_t check_mv(int32_t rows, int32_t cols, int32_t type) {
-  if (!quant_type_ok(type)) return fail(kErrParams, "matvec: type %d is not Q4_0/Q8_0/Q4_K", type);
+  if (!quant_type_ok(type)) return fail(kErrParams, "matvec: type %d is not Q4_0/Q8_0/Q2_K..Q6_K", type);
   if (rows <= 0 || cols <= 0 || cols % col_unit(type))
     return fail(kErrParams, "matvec: bad shape %dx%d (cols must be a multiple of %d)", rows, cols, col_unit(type));
   return 0;
@@ -369,7 +379,7 @@ int32_t ss_hip_matvec(ss_hip_ctx_t* c, float* y, const void* w, const float* x, 
 
 int32_t ss_hip_gemm(ss_hip_ctx_t* c, float* y, const void* w, const float* x, const float* nw, float eps,
                     int32_t accumulate, int32_t rows, int32_t cols, int32_t n_tokens, int32_t type, void* stream) {
-  // the MFMA products take Q4_0 and Q8_0 (Q4_K prompts run token by token)
+  // the MFMA products take Q4_0 and Q8_0 (K-quant prompts run token by token)
   if (!c || !y || !w || !x || rows <= 0 || cols <= 0 || cols % 32 || n_tokens <= 0 ||
       (type != SS_HIP_Q4_0 && type != SS_HIP_Q8_0))
     return fail(kErrParams, "gemm: bad argument (rows %d cols %d tokens %d type %d)", rows, cols, n_tokens, type);
@@ -699,7 +709,7 @@ struct ss_hip_model {
   int t_embd = 0;
   void* out = nullptr;   // == embd when tied
   int t_out = 0;
-  bool any_q4k = false;   // some matrix is Q4_K: prompts run token by token
+  bool any_kq = false;    // some matrix is a K-quant: prompts run token by token
   // Gemma and the optional branches (layer_scheduler.c:446-448, 474-481,
   // 529-531, 553-560, 597-602, 667-676); the (1 + w) norms are uploaded as 1 + w
   bool gemma = false;
@@ -708,7 +718,7 @@ struct ss_hip_model {
   float attn_softcap = 0.f, final_softcap = 0.f;
   bool any_post = false;     // some layer has a post norm
   float* post_y = nullptr;   // [d]: a projection's output before its post norm
-  // prompts run token by token (the prompt products have none of: Q4_K,
+  // prompts run token by token (the prompt products have none of: K-quants,
   // the Gemma branches, post norms, softcaps, head_dim 256)
   bool token_only = false;
   float* out_norm = nullptr;
@@ -851,7 +861,7 @@ int32_t upload_mat(ss_hip_model* m, void** dst, const ss_hip_tensor_t* parts, in
     total += parts[i].rows;
   }
   if (!quant_type_ok(type))
-    return fail(kErrParams, "model: %s has type %d; Q4_0, Q8_0 and Q4_K are supported", what, type);
+    return fail(kErrParams, "model: %s has type %d; Q4_0, Q8_0 and Q2_K..Q6_K are supported", what, type);
   if (total != rows_expect_total) return fail(kErrParams, "model: %s has %lld rows, %d expected", what, (long long)total, rows_expect_total);
   if (cols % col_unit(type))
     return fail(kErrParams, "model: %s columns %d not a multiple of %d", what, cols, col_unit(type));
@@ -912,7 +922,8 @@ hipError_t timed(ss_hip_model* m, int cls, double bytes, F&& launch) {
 // clamped). The packed planes' offsets depend on it.
 int out_rows(const ss_hip_model* m) { return m->out == m->embd ? m->embd_rows : m->vocab; }
 
-int q_class(int type) { return type == SS_HIP_Q8_0 ? PC_Q8 : PC_Q4; }   // 4-bit codes: Q4_0 and Q4_K
+// 8-bit codes on the device (Q8_0, Q5_K, Q6_K), or 4-bit (the rest)
+int q_class(int type) { return ssk::code_bytes_of(type) == 32 ? PC_Q8 : PC_Q4; }
 
 // Algorithmic HBM bytes of one token at context ctx: every weight byte once
 // (GGUF block sizes), the fp16 K/V read and appended, the norm weights.
@@ -924,7 +935,7 @@ double token_bytes(const ss_hip_model* m, int ctx, bool with_head) {
     b += 2.0 * 2 * ((double)ctx * m->kvdim + m->kvdim) + 2.0 * 4 * m->d;
   }
   if (with_head) b += matvec_bytes(m->t_out, m->vocab, m->d, 1) + 4.0 * m->d;
-  b += (double)m->d / 32 * gguf_block_bytes(m->t_embd);
+  b += (double)gguf_row_bytes(m->t_embd, m->d);
   return b;
 }
 
@@ -1517,8 +1528,8 @@ int32_t stream_setup(ss_hip_model* m, const ss_hip_model_desc_t* d) {
     size_t o = 0;
     for (int i = 0; i < 5; i++) {
       if (!quant_type_ok(types[i]))
-        return fail(kErrParams, "model: blk.%d matrix %d has type %d; Q4_0, Q8_0 and Q4_K are supported", l, i,
-                    types[i]);
+        return fail(kErrParams, "model: blk.%d matrix %d has type %d; Q4_0, Q8_0 and Q2_K..Q6_K are supported", l,
+                    i, types[i]);
       m->layer_off[(size_t)l * 5 + i] = o;
       o += align256(ss_hip_packed_bytes(types[i], rows[i], cols[i]));
     }
@@ -1638,9 +1649,9 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
   };
 
   // weights
-  m->any_q4k = d->token_embd.type == SS_HIP_Q4_K || (d->output.data && d->output.type == SS_HIP_Q4_K);
+  m->any_kq = ssk::is_kq(d->token_embd.type) || (d->output.data && ssk::is_kq(d->output.type));
   for (int i = 0; i < m->L * SS_HIP_LAYER_TENSORS; i++)
-    if (d->layers[i].data && d->layers[i].type == SS_HIP_Q4_K) m->any_q4k = true;
+    if (d->layers[i].data && ssk::is_kq(d->layers[i].type)) m->any_kq = true;
   m->gemma = d->gemma != 0;
   m->emb_scale = m->gemma ? sqrtf((float)m->d) : 1.f;                       // layer_scheduler.c:597-602
   m->logit_scale = m->gemma ? 1.0f / sqrtf((float)m->d) : 1.f;              // :667-672
@@ -1650,7 +1661,7 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
     for (int i = 0; i < 2 * m->L; i++)
       if (d->post_norms[i].data) m->any_post = true;
   // (and head_dim 256: the prompt attention kernel covers 64 and 128)
-  m->token_only = m->any_q4k || m->gemma || m->any_post || m->attn_softcap > 0.f || m->final_softcap > 0.f ||
+  m->token_only = m->any_kq || m->gemma || m->any_post || m->attn_softcap > 0.f || m->final_softcap > 0.f ||
                   m->hd > 128;
   const float norm_add = m->gemma ? 1.f : 0.f;   // (1 + w) norms, tensor.c:133-152
   if (!d->token_embd.data || d->token_embd.cols != m->d || d->token_embd.rows < m->vocab) {

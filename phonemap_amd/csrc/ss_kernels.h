@@ -16,8 +16,14 @@ enum Epi : int {
   EPI_LOGITS = 4,  // y[r] = W x, plus one first-max argmax candidate per workgroup in part[]
 };
 
-// ggml type of the K-quant with 4-bit codes (256-weight super-blocks)
-constexpr int kQ4K = 12;
+// ggml types of the K-quants (256-weight super-blocks)
+constexpr int kQ2K = 10, kQ3K = 11, kQ4K = 12, kQ5K = 13, kQ6K = 14;
+__host__ __device__ constexpr bool is_kq(int t) { return t >= kQ2K && t <= kQ6K; }
+// device code width of a 32-weight block: nibbles (Q4_0 and the 2-, 3- and
+// 4-bit K-quants) or int8 codes (Q8_0, Q5_K, Q6_K)
+__host__ __device__ constexpr int code_bytes_of(int t) {
+  return t == 2 || t == kQ2K || t == kQ3K || t == kQ4K ? 16 : t == 8 || t == kQ5K || t == kQ6K ? 32 : 0;
+}
 
 // A packed Q4_0/Q8_0/Q4_K matrix on the device: code plane, scale plane
 // and, for Q4_K, a super-block plane (see ss_gemv.hip).
