@@ -154,6 +154,18 @@ int32_t ss_hip_attention(ss_hip_ctx_t *ctx, float *out_dev, const float *q_dev,
                          int32_t head_dim, int32_t max_seq, int32_t seq_len, int32_t kv_type,
                          void *stream);
 
+/* Causal attention of n_tokens prompt rows on MFMA: token t (query
+ * q[t][n_heads*head_dim], output out[t][n_heads*head_dim]) attends to
+ * positions 0..pos0+t of one layer's fp16 cache, whose rows pos0 ..
+ * pos0+n_tokens-1 already hold the tokens' own K and V. The per-token
+ * attention of layer_scheduler.c:415-468 for every token of a layer-major
+ * prompt (ss_scheduler_prefill, layer_scheduler.c:681-803) in one launch;
+ * head_dim 64 or 128. */
+int32_t ss_hip_attention_rows(ss_hip_ctx_t *ctx, float *out_dev, const float *q_dev,
+                              const void *k_cache, const void *v_cache, int32_t n_heads,
+                              int32_t n_kv_heads, int32_t head_dim, int32_t max_seq, int32_t pos0,
+                              int32_t n_tokens, void *stream);
+
 /* ss_hip_attention with no device allocation. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under HIP graph capture, tight serving loops, harnesses that forbid

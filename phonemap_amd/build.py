@@ -14,7 +14,7 @@ CSRC = os.path.join(HERE, "csrc")
 OBJ = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libslipstream_hip.so")
 
-HIP_SOURCES = ["ss_gemv.hip", "ss_kernels.hip", "ss_gemm.hip", "ss_sweep.hip", "ss_sample.hip", "ss_hip.hip"]
+HIP_SOURCES = ["ss_gemv.hip", "ss_kernels.hip", "ss_gemm.hip", "ss_flash.hip", "ss_sweep.hip", "ss_sample.hip", "ss_hip.hip"]
 C_SOURCES = ["ss_gguf.c", "ss_tokenizer.c", "ss_engine.c", "ss_synth.c"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

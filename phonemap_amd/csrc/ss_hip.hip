@@ -547,6 +547,34 @@ int32_t ss_hip_attention(ss_hip_ctx_t* c, float* out, const float* q, const void
   return 0;
 }
 
+int32_t ss_hip_attention_rows(ss_hip_ctx_t* c, float* out, const float* q, const void* kc, const void* vc,
+                              int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, int32_t max_seq,
+                              int32_t pos0, int32_t n_tokens, void* stream) {
+  if (!c || !out || !q || !kc || !vc || n_kv_heads <= 0 || n_heads % n_kv_heads || pos0 < 0 || n_tokens <= 0 ||
+      (int64_t)pos0 + n_tokens > max_seq)
+    return fail(kErrParams, "attention_rows: bad argument (pos0 %d, %d tokens, max_seq %d)", pos0, n_tokens,
+                max_seq);
+  const int group = n_heads / n_kv_heads;
+  if ((head_dim != 64 && head_dim != 128) || !ssk::attention_supported(head_dim, group))
+    return fail(kErrParams, "attention_rows: head_dim %d / group %d not supported", head_dim, group);
+  if (set_device(c)) return kErrBackend;
+  ssk::AttnArgs a;
+  memset(&a, 0, sizeof(a));
+  a.q = q;
+  a.kc = kc;
+  a.vc = vc;
+  a.max_seq = max_seq;
+  a.ns = 1;
+  a.n_kv_heads = n_kv_heads;
+  a.scale = 1.0f / sqrtf((float)head_dim);
+  a.out = out;
+  a.n_tok = n_tokens;
+  a.pos0 = pos0;
+  a.tok_q = a.tok_o = n_heads * head_dim;
+  HIP_TRY(ssk::launch_attention_rows(head_dim, group, a, pick(c, stream)));
+  return 0;
+}
+
 int32_t ss_hip_attention_noalloc(ss_hip_ctx_t* c, float* out, const float* q, const void* kc,
                                  const void* vc, const float* ksc, const float* vsc, int32_t n_heads,
                                  int32_t n_kv_heads, int32_t head_dim, int32_t max_seq, int32_t seq_len,

@@ -108,9 +108,16 @@ struct AttnArgs {
                              // split merges into out; nullptr: the splits stay in part_o/part_ml
                              // for a merging consumer (ns <= kMergeSplits)
   uint32_t* xr_out;          // with cnt set: also the output as x records (xrec_words(n_heads * hd))
-  int n_tok;                 // prompt rows (launch_attention_rows): token z at position dpos[z],
+  int n_tok;                 // prompt rows (launch_attention_rows): token z at position dpos[z]
+  int pos0;                  // (or pos0 + z when dpos is null),
   int tok_q, tok_o;          // its query at q + z*tok_q, its output at out + z*tok_o
 };
+
+// The attention softcap (layer_scheduler.c:446-448, tensor.c:194-200) of a
+// scaled score: cap * tanh(score / cap), or the score when no cap is set.
+__device__ __forceinline__ float softcap(float d, const AttnArgs& a) {
+  return a.softcap > 0.f ? a.softcap * tanhf(d * a.softcap_inv) : d;
+}
 
 // Profiling: when start is set, the next matvec or attention launch on this
 // thread passes start/stop to hipExtLaunchKernel, so the dispatch records them
@@ -135,7 +142,8 @@ hipError_t launch_argmax_merge(const float2* part, int n, const float* y, int* o
                                int* dpos, hipStream_t s);
 hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, hipStream_t s);
 // Causal attention of a.n_tok prompt rows (token z: query a.q + z*a.tok_q,
-// positions 0..a.dpos[z], output a.out + z*a.tok_o), fp16 cache.
+// positions 0..a.dpos[z] (or a.pos0 + z), output a.out + z*a.tok_o), fp16
+// cache, head_dim 64 or 128, on MFMA (ss_flash.hip).
 hipError_t launch_attention_rows(int head_dim, int group, const AttnArgs& a, hipStream_t s);
 // ssq[t] = sum of x[t][c]^2 (x [T][cols])
 hipError_t launch_sumsq(const float* x, int cols, int T, float* ssq, hipStream_t s);

@@ -58,12 +58,6 @@ __device__ __forceinline__ void attn_split(const AttnArgs& a, int& ctx, int& chu
   attn_chunks(ctx, a.ns, chunk, active);
 }
 
-// The attention softcap (layer_scheduler.c:446-448, tensor.c:194-200) of a
-// scaled score: cap * tanh(score / cap), or the score when no cap is set.
-__device__ __forceinline__ float softcap(float d, const AttnArgs& a) {
-  return a.softcap > 0.f ? a.softcap * tanhf(d * a.softcap_inv) : d;
-}
-
 // Sum over aligned groups of N (4, 8 or 16) lanes, result in every lane.
 template <int N>
 __device__ __forceinline__ float sum_lanes(float v) {
@@ -525,162 +519,6 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
   attn_finish<HD, G, kHgWaves>(a, kvh, active, wm, wl, wo, tid);
 }
 
-// ------------------------------------------------------------ attention of prompt rows
-// A prompt's tokens attend to their own prefixes (token z to positions
-// 0..dpos[z], causal). One workgroup serves TQ = 8/G consecutive tokens of
-// one KV head, so the K/V rows are loaded once for 8 (token, head) pairs:
-// the heads-on-lanes layout of k_attn_hg with virtual heads v = (token
-// v / G, head v % G), 8 lanes each, and a per-lane causal limit. The 8 waves
-// take contiguous shares of positions 0..(last token's position); each wave
-// keeps an online softmax per virtual head and the waves are merged in LDS.
-// fp16 cache only; same fp32 arithmetic as the decode kernels.
-template <int HD, int G>
-__global__ void __launch_bounds__(kHgWaves * 64) k_attn_rows(const AttnArgs a) {
-  constexpr int kVH = 8;                   // virtual heads per workgroup
-  constexpr int kTQ = kVH / G;             // tokens per workgroup
-  constexpr int kLph = kWave / kVH;        // 8 lanes per virtual head
-  constexpr int kDpl = HD / kLph;          // dims per lane
-  constexpr int kB = hg_batch(HD, kVH);
-  using Row = KvRow<0, kDpl>;
-
-  __shared__ float wm[kHgWaves][kVH], wl[kHgWaves][kVH];
-  __shared__ float wo[kHgWaves][kVH][HD];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int kvh = blockIdx.y;
-  const int z0 = blockIdx.x * kTQ;
-  const int vh = lane / kLph, c = lane % kLph;
-  const int j = vh / G, h = vh % G;
-  const int z = z0 + j;
-  const int zc = min(z, a.n_tok - 1);
-  const int lim = z < a.n_tok ? a.dpos[zc] : -1;   // last position this lane's token sees
-  int ctx = 0;
-#pragma unroll
-  for (int t = 0; t < kTQ; ++t) ctx = max(ctx, a.dpos[min(z0 + t, a.n_tok - 1)] + 1);
-  const int per = (ctx + kHgWaves - 1) / kHgWaves;
-  const int p0 = wave * per;
-  const int p1 = min(ctx, p0 + per);
-
-  const size_t head_base = (size_t)kvh * a.max_seq;
-  const uint8_t* kb = static_cast<const uint8_t*>(a.kc) + (head_base * HD + c * kDpl) * 2;
-  const uint8_t* vb = static_cast<const uint8_t*>(a.vc) + (head_base * HD + c * kDpl) * 2;
-
-  float q[kDpl], o[kDpl];
-  {
-    const float4* qp =
-        reinterpret_cast<const float4*>(a.q + (size_t)zc * a.tok_q + ((size_t)kvh * G + h) * HD + c * kDpl);
-#pragma unroll
-    for (int i = 0; i < kDpl / 4; ++i) {
-      const float4 x = qp[i];
-      q[4 * i] = x.x;
-      q[4 * i + 1] = x.y;
-      q[4 * i + 2] = x.z;
-      q[4 * i + 3] = x.w;
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < kDpl; ++i) o[i] = 0.f;
-  float m = -INFINITY, l = 0.f;
-
-  struct Batch {
-    Row k[kB], v[kB];
-  };
-  auto load = [&](Batch& bt, int pb) {   // rows past p1 reload p1 - 1 (masked in use)
-#pragma unroll
-    for (int r = 0; r < kB; ++r) {
-      const int p = min(pb + r, p1 - 1);
-      bt.k[r].load(kb + (size_t)p * HD * 2);
-      bt.v[r].load(vb + (size_t)p * HD * 2);
-    }
-  };
-  auto use = [&](const Batch& bt, int pb) {
-    float sc[kB];
-#pragma unroll
-    for (int r = 0; r < kB; ++r) {
-      float d = 0.f;
-#pragma unroll
-      for (int i = 0; i < kDpl; ++i) d = fmaf(q[i], bt.k[r].get(i, 1.f), d);
-      d = softcap(sum_lanes<kLph>(d) * a.scale, a);   // (q . k) / sqrt(hd), layer_scheduler.c:442-448
-      sc[r] = pb + r < p1 && pb + r <= lim ? d : -INFINITY;
-    }
-    float bm = sc[0];
-#pragma unroll
-    for (int r = 1; r < kB; ++r) bm = fmaxf(bm, sc[r]);
-    const float mn = fmaxf(m, bm);
-    const float ms = mn == -INFINITY ? 0.f : mn;   // nothing seen yet: weights stay 0
-    const float corr = expf(m - ms);
-    l *= corr;
-#pragma unroll
-    for (int i = 0; i < kDpl; ++i) o[i] *= corr;
-#pragma unroll
-    for (int r = 0; r < kB; ++r) {
-      const float pj = expf(sc[r] - ms);
-      l += pj;
-#pragma unroll
-      for (int i = 0; i < kDpl; ++i) o[i] = fmaf(pj, bt.v[r].get(i, 1.f), o[i]);
-    }
-    m = mn;
-  };
-  if (p0 < p1) {
-    Batch A, B;
-    load(A, p0);
-    for (int pb = p0;; pb += 2 * kB) {
-      load(B, pb + kB);
-      use(A, pb);
-      if (pb + kB >= p1) break;
-      load(A, pb + 2 * kB);
-      use(B, pb + kB);
-      if (pb + 2 * kB >= p1) break;
-    }
-  }
-  if (c == 0) {
-    wm[wave][vh] = m;   // -inf and 0 where this wave saw none of the token's positions
-    wl[wave][vh] = l;
-  }
-#pragma unroll
-  for (int i = 0; i < kDpl; ++i) wo[wave][vh][c * kDpl + i] = o[i];
-  __syncthreads();
-  // merge the waves (wave 0 holds position 0, seen by every token)
-  for (int i = tid; i < kVH * HD; i += kHgWaves * 64) {
-    const int v = i / HD, d = i % HD;
-    const int zt = z0 + v / G;
-    if (zt >= a.n_tok) continue;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kHgWaves; ++w) M = fmaxf(M, wm[w][v]);
-    float so = 0.f, sl = 0.f;
-#pragma unroll
-    for (int w = 0; w < kHgWaves; ++w) {
-      const float f = expf(wm[w][v] - M);
-      so = fmaf(f, wo[w][v][d], so);
-      sl = fmaf(f, wl[w][v], sl);
-    }
-    a.out[(size_t)zt * a.tok_o + ((size_t)kvh * G + v % G) * HD + d] = so * (1.0f / sl);
-  }
-}
-
-template <int HD>
-hipError_t launch_attn_rows_hd(int group, const AttnArgs& a, hipStream_t s) {
-  const dim3 block(kHgWaves * 64);
-  switch (group) {
-    case 1:
-      hipLaunchKernelGGL((k_attn_rows<HD, 1>), dim3((a.n_tok + 7) / 8, a.n_kv_heads), block, 0, s, a);
-      break;
-    case 2:
-      hipLaunchKernelGGL((k_attn_rows<HD, 2>), dim3((a.n_tok + 3) / 4, a.n_kv_heads), block, 0, s, a);
-      break;
-    case 4:
-      hipLaunchKernelGGL((k_attn_rows<HD, 4>), dim3((a.n_tok + 1) / 2, a.n_kv_heads), block, 0, s, a);
-      break;
-    case 8:
-      hipLaunchKernelGGL((k_attn_rows<HD, 8>), dim3(a.n_tok, a.n_kv_heads), block, 0, s, a);
-      break;
-    default:
-      return hipErrorInvalidValue;
-  }
-  return hipGetLastError();
-}
-
 // ------------------------------------------------------------ embedding of a prompt
 // ss_scheduler_embed (layer_scheduler.c:864-911): every token's final hidden
 // state through the output norm (x * k_t * w, k_t = 1/sqrt(ssq_t/d + eps)),
@@ -991,13 +829,6 @@ hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs
   if (head_dim == 64) return launch_attn_hd<64>(group, kv_type, a, s);
   if (head_dim == 128) return launch_attn_hd<128>(group, kv_type, a, s);
   if (head_dim == 256) return launch_attn_hd<256>(group, kv_type, a, s);   // Gemma
-  return hipErrorInvalidValue;
-}
-
-hipError_t launch_attention_rows(int head_dim, int group, const AttnArgs& a, hipStream_t s) {
-  if (a.n_tok < 1 || !a.dpos || !a.q || !a.out) return hipErrorInvalidValue;
-  if (head_dim == 64) return launch_attn_rows_hd<64>(group, a, s);
-  if (head_dim == 128) return launch_attn_rows_hd<128>(group, a, s);
   return hipErrorInvalidValue;
 }
 
