@@ -40,7 +40,8 @@ extern "C" {
 typedef struct {
     int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, ffn, vocab, context_length;
     float rope_theta, rms_eps;
-    int32_t layer_type;   /* ggml type of the layer matrices: 2 (Q4_0), 8 (Q8_0) or a K-quant,
+    int32_t layer_type;   /* ggml type of the layer matrices: 0 (F32), 1 (F16), 2 (Q4_0),
+                           * 3 (Q4_1), 6 (Q5_0), 7 (Q5_1), 8 (Q8_0), 9 (Q8_1) or a K-quant,
                            * 10 (Q2_K), 11 (Q3_K), 12 (Q4_K), 13 (Q5_K), 14 (Q6_K) (hidden, ffn
                            * and n_heads * head_dim multiples of 256) */
     int32_t embd_type;    /* token_embd.weight */

@@ -149,6 +149,63 @@ void orc_dequantize(const void *src, float *dst, int32_t n, int32_t type) {
                 dst[b * 32 + i] = scale * (float)(int8_t)blk[2 + i];
         }
         break;
+    case ORC_Q4_1:
+        /* quantize.c:76-91: fp16 d, fp16 m, 16 bytes of nibbles (20 B,
+         * quantize.h:20-24); weight j = d * nibble + m, low nibbles first. */
+        for (int32_t b = 0; b < n / 32; b++) {
+            const uint8_t *blk = p + (size_t)b * 20;
+            uint16_t dh, mh;
+            memcpy(&dh, blk, 2);
+            memcpy(&mh, blk + 2, 2);
+            float d = orc_f16_to_f32(dh), m = orc_f16_to_f32(mh);
+            for (int32_t i = 0; i < 16; i++) {
+                uint8_t byte = blk[4 + i];
+                dst[b * 32 + i] = d * (float)(byte & 0xF) + m;
+                dst[b * 32 + i + 16] = d * (float)(byte >> 4) + m;
+            }
+        }
+        break;
+    case ORC_Q5_0:
+    case ORC_Q5_1: {
+        /* quantize.c:93-137: 5-bit codes, the low 4 bits in nibbles (weight
+         * i low, i + 16 high) and bit 4 of weight i in bit i of the 32-bit
+         * little-endian qh. Q5_0 (22 B: d, qh, qs): (q - 16) * d. Q5_1
+         * (24 B: d, m, qh, qs): q * d + m (quantize.h:26-41). */
+        const int one = type == ORC_Q5_1;
+        const size_t bytes = one ? 24 : 22;
+        for (int32_t b = 0; b < n / 32; b++) {
+            const uint8_t *blk = p + (size_t)b * bytes;
+            uint16_t dh, mh = 0;
+            uint32_t qh;
+            memcpy(&dh, blk, 2);
+            if (one) memcpy(&mh, blk + 2, 2);
+            memcpy(&qh, blk + (one ? 4 : 2), 4);
+            const uint8_t *qs = blk + (one ? 8 : 6);
+            float d = orc_f16_to_f32(dh), m = orc_f16_to_f32(mh);
+            for (int32_t i = 0; i < 16; i++) {
+                int32_t q0 = (qs[i] & 0xF) | (int32_t)(((qh >> i) & 1u) << 4);
+                int32_t q1 = (qs[i] >> 4) | (int32_t)(((qh >> (i + 16)) & 1u) << 4);
+                if (one) {
+                    dst[b * 32 + i] = (float)q0 * d + m;
+                    dst[b * 32 + i + 16] = (float)q1 * d + m;
+                } else {
+                    dst[b * 32 + i] = (float)(q0 - 16) * d;
+                    dst[b * 32 + i + 16] = (float)(q1 - 16) * d;
+                }
+            }
+        }
+        break;
+    }
+    case ORC_Q8_1:
+        /* quantize.c:153-163: fp32 d, fp32 s (unused), 32 int8 (40 B,
+         * quantize.h:49-53); weight = d * q. */
+        for (int32_t b = 0; b < n / 32; b++) {
+            const uint8_t *blk = p + (size_t)b * 40;
+            float d;
+            memcpy(&d, blk, 4);
+            for (int32_t i = 0; i < 32; i++) dst[b * 32 + i] = d * (float)(int8_t)blk[8 + i];
+        }
+        break;
     case ORC_Q4_K:
         /* quantize.c:265-310: super-blocks of 256 weights, 144 bytes: d and
          * dmin (binary16), 12 bytes of packed 6-bit sub-block scales and
@@ -302,6 +359,10 @@ static size_t orc_row_bytes(int32_t cols, int32_t type) {
     case ORC_F16: return (size_t)cols * 2;
     case ORC_Q4_0: return (size_t)(cols / 32) * 18;
     case ORC_Q8_0: return (size_t)(cols / 32) * 34;
+    case ORC_Q4_1: return (size_t)(cols / 32) * 20;
+    case ORC_Q5_0: return (size_t)(cols / 32) * 22;
+    case ORC_Q5_1: return (size_t)(cols / 32) * 24;
+    case ORC_Q8_1: return (size_t)(cols / 32) * 40;
     case ORC_Q2_K: return (size_t)(cols / 256) * 84;
     case ORC_Q3_K: return (size_t)(cols / 256) * 110;
     case ORC_Q4_K: return (size_t)(cols / 256) * 144;
@@ -885,8 +946,11 @@ static int key_ends(const char *k, uint64_t kl, const char *s) {
 
 /* gguf_loader.c:22-62: weights per block and bytes per block */
 static int is_kquant(int32_t t) { return t >= ORC_Q2_K && t <= ORC_Q6_K; }
+static int is_legacy(int32_t t) {
+    return t == ORC_Q4_0 || t == ORC_Q4_1 || t == ORC_Q5_0 || t == ORC_Q5_1 || t == ORC_Q8_0 || t == ORC_Q8_1;
+}
 static uint32_t type_block(int32_t t) {
-    return (t == ORC_Q4_0 || t == ORC_Q8_0) ? 32 : is_kquant(t) ? 256 : 1;
+    return is_legacy(t) ? 32 : is_kquant(t) ? 256 : 1;
 }
 static uint32_t type_size(int32_t t) {
     switch (t) {
@@ -894,6 +958,10 @@ static uint32_t type_size(int32_t t) {
     case ORC_F16: return 2;
     case ORC_Q4_0: return 18;
     case ORC_Q8_0: return 34;
+    case ORC_Q4_1: return 20;
+    case ORC_Q5_0: return 22;
+    case ORC_Q5_1: return 24;
+    case ORC_Q8_1: return 40;
     case ORC_Q2_K: return 84;
     case ORC_Q3_K: return 110;
     case ORC_Q4_K: return 144;
@@ -1042,7 +1110,7 @@ void orc_model_close(orc_model_t *m) {
 
 static int matrix_ok(const orc_tensor_t *t, uint64_t rows, uint64_t cols) {
     return t && t->n_dims == 2 && t->dims[0] == cols && t->dims[1] == rows &&
-           (t->type == ORC_Q4_0 || t->type == ORC_Q8_0 || t->type == ORC_F32 || t->type == ORC_F16 ||
+           ((is_legacy(t->type) && cols % 32 == 0) || t->type == ORC_F32 || t->type == ORC_F16 ||
             (is_kquant(t->type) && cols % 256 == 0));
 }
 static int vector_ok(const orc_tensor_t *t, uint64_t n) {

@@ -19,8 +19,8 @@ extern "C" {
 #endif
 
 /* ggml tensor types used on the path (src/core/gguf_loader.h:41-55) */
-enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q8_0 = 8, ORC_Q2_K = 10, ORC_Q3_K = 11, ORC_Q4_K = 12,
-       ORC_Q5_K = 13, ORC_Q6_K = 14 };
+enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q5_0 = 6, ORC_Q5_1 = 7, ORC_Q8_0 = 8,
+       ORC_Q8_1 = 9, ORC_Q2_K = 10, ORC_Q3_K = 11, ORC_Q4_K = 12, ORC_Q5_K = 13, ORC_Q6_K = 14 };
 
 /* KV cache storage modes */
 enum { ORC_KV_INT8 = 0,   /* reference: per-(layer,pos) absmax int8, layer_scheduler.c:101-125 */

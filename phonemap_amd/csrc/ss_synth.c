@@ -18,8 +18,13 @@
 #include <unistd.h>
 
 #define T_F32 0
+#define T_F16 1
 #define T_Q4_0 2
+#define T_Q4_1 3
+#define T_Q5_0 6
+#define T_Q5_1 7
 #define T_Q8_0 8
+#define T_Q8_1 9
 #define T_Q4_K 12
 #define T_Q2_K 10
 #define T_Q3_K 11
@@ -30,7 +35,13 @@ static int is_k(int32_t type) { return type >= T_Q2_K && type <= T_Q6_K; }
 static size_t k_bytes(int32_t type) {
     return type == T_Q2_K ? 84 : type == T_Q3_K ? 110 : type == T_Q4_K ? 144 : type == T_Q5_K ? 176 : 210;
 }
+/* the matrix types the writer makes: float, 32-weight blocks, K-quants */
+static int matrix_type_ok(int32_t type) {
+    return type == T_F32 || type == T_F16 || type == T_Q4_0 || type == T_Q4_1 || type == T_Q5_0 || type == T_Q5_1 ||
+           type == T_Q8_0 || type == T_Q8_1 || is_k(type);
+}
 #define CHUNK_BLOCKS (1u << 18)   /* 256 Ki blocks per work item */
+#define MAX_BLOCK_BYTES 128       /* F32: 32 weights */
 
 typedef struct {
     char name[64];
@@ -46,7 +57,6 @@ typedef struct {
     int join_next;     /* the next tensor continues this one's rows (one fused GGUF tensor) */
 } syn_tensor_t;
 
-#define T_F16 1
 static const double kBiasSigma = 0.1;
 
 /* ---- random numbers ---- */
@@ -163,7 +173,19 @@ typedef struct {
 static uint64_t tensor_blocks(const syn_tensor_t *t) {
     return t->dims[0] * t->dims[1] / (is_k(t->type) ? 256 : 32);
 }
-static size_t block_bytes(int32_t type) { return type == T_Q4_0 ? 18 : type == T_Q8_0 ? 34 : k_bytes(type); }
+static size_t block_bytes(int32_t type) {
+    switch (type) {
+    case T_F32: return 128;   /* matrices are generated in 32-weight pieces */
+    case T_F16: return 64;
+    case T_Q4_0: return 18;
+    case T_Q4_1: return 20;
+    case T_Q5_0: return 22;
+    case T_Q5_1: return 24;
+    case T_Q8_0: return 34;
+    case T_Q8_1: return 40;
+    default: return k_bytes(type);
+    }
+}
 /* blocks per work item: Q4_K super-blocks are 8 blocks of 32 weights */
 static uint64_t chunk_blocks(int32_t type) { return is_k(type) ? CHUNK_BLOCKS / 8 : CHUNK_BLOCKS; }
 
@@ -186,7 +208,7 @@ static void gen_item(job_t *j, uint64_t it, uint8_t *buf) {
             }
         }
         n = ne * (t->type == T_F16 ? 2 : 4);
-    } else if (t->type == T_F32) {
+    } else if (t->norm) {   /* norm weight vectors (F32) */
         uint64_t ne = t->dims[0] * (t->n_dims > 1 ? t->dims[1] : 1);
         float *f = (float *)buf;
         const double one = t->norm == 3 ? 0.0 : 1.0;
@@ -215,6 +237,16 @@ static void gen_item(job_t *j, uint64_t it, uint8_t *buf) {
              * Q6_K d*sc*q, sc int8, q in [-32, 31]: sqrt(5461.5 * 341.5) */
             const double rms = t->type == T_Q2_K ? 18.675 : t->type == T_Q3_K ? 43.34
                              : t->type == T_Q5_K ? 659.8 : 1365.7;
+            sigma = j->scale_mode == 1 ? 1.0 / (rms * sqrt((double)t->dims[0])) : j->scale_sigma * 4.6 / rms;
+        } else if (t->type != T_Q4_0 && t->type != T_Q8_0) {
+            /* the RMS of a weight per unit d: F16 / F32 weights are sigma *
+             * N(0, 1); Q4_1 d*q + m with m = 8 d' (d' another N(0, 1) draw),
+             * q < 16: sqrt(77.5 + 64); Q5_0 (q - 16) d: sqrt(85.5); Q5_1
+             * d*q + m with m = 16 d', q < 32: sqrt(325.5 + 256); Q8_1 as
+             * Q8_0. Mode 0 spreads the weights like Q4_0's. */
+            const double rms = t->type == T_F32 || t->type == T_F16 ? 1.0
+                             : t->type == T_Q4_1 ? sqrt(141.5) : t->type == T_Q5_0 ? sqrt(85.5)
+                             : t->type == T_Q5_1 ? sqrt(581.5) : sqrt(127.0 * 128.0 / 3.0);
             sigma = j->scale_mode == 1 ? 1.0 / (rms * sqrt((double)t->dims[0])) : j->scale_sigma * 4.6 / rms;
         } else if (j->scale_mode == 1) {
             sigma = 1.0 / ((t->type == T_Q4_0 ? sqrt(21.5) : sqrt(127.0 * 128.0 / 3.0)) *
@@ -263,7 +295,55 @@ static void gen_item(job_t *j, uint64_t it, uint8_t *buf) {
             memcpy(p + od, &d, 2);
             if (t->type == T_Q2_K || t->type == T_Q5_K) memcpy(p + od + 2, &dm, 2);
         }
-        for (uint64_t b = b0; b < b1 && !is_k(t->type); b++) {
+        for (uint64_t b = b0; b < b1 && (t->type == T_F32 || t->type == T_F16); b++) {
+            uint8_t *p = buf + (b - b0) * bb;
+            for (int i = 0; i < 32; i++) {
+                const float v = (float)(sigma * xo_normal(&x));
+                if (t->type == T_F32) {
+                    memcpy(p + 4 * i, &v, 4);
+                } else {
+                    const uint16_t h = to_f16(v);
+                    memcpy(p + 2 * i, &h, 2);
+                }
+            }
+        }
+        for (uint64_t b = b0; b < b1 && (t->type == T_Q4_1 || t->type == T_Q5_0 || t->type == T_Q5_1); b++) {
+            /* d (and m) binary16, then random high bits (Q5) and nibbles */
+            uint8_t *p = buf + (b - b0) * bb;
+            const double dv = sigma * xo_normal(&x), mv = sigma * xo_normal(&x);
+            const uint16_t d = to_f16((float)(j->scale_mode == 1 ? dv : fabs(dv)));
+            const uint16_t m = to_f16((float)((t->type == T_Q5_1 ? -16.0 : -8.0) * mv));
+            memcpy(p, &d, 2);
+            size_t o = 2;
+            if (t->type != T_Q5_0) {
+                memcpy(p + 2, &m, 2);
+                o = 4;
+            }
+            if (t->type != T_Q4_1) {
+                const uint32_t qh = (uint32_t)(xo_next(&x) >> 32);
+                memcpy(p + o, &qh, 4);
+                o += 4;
+            }
+            uint64_t r0 = xo_next(&x), r1 = xo_next(&x);
+            memcpy(p + o, &r0, 8);
+            memcpy(p + o + 8, &r1, 8);
+        }
+        for (uint64_t b = b0; b < b1 && t->type == T_Q8_1; b++) {
+            /* fp32 d, fp32 s = d * sum q (the field the reference ignores), 32 int8 */
+            uint8_t *p = buf + (b - b0) * bb;
+            const float d = (float)(sigma * xo_normal(&x));
+            int sum = 0;
+            for (int i = 0; i < 32; i++) {
+                uint32_t r = (uint32_t)(xo_next(&x) >> 32);
+                const int q = (int)(((uint64_t)r * 255u) >> 32) - 127;
+                p[8 + i] = (uint8_t)(int8_t)q;
+                sum += q;
+            }
+            const float sv = d * (float)sum;
+            memcpy(p, &d, 4);
+            memcpy(p + 4, &sv, 4);
+        }
+        for (uint64_t b = b0; b < b1 && (t->type == T_Q4_0 || t->type == T_Q8_0); b++) {
             uint8_t *p = buf + (b - b0) * bb;
             const double dv = sigma * xo_normal(&x);
             uint16_t d = to_f16((float)(j->scale_mode == 1 ? dv : fabs(dv)));
@@ -288,11 +368,11 @@ static void gen_item(job_t *j, uint64_t it, uint8_t *buf) {
 
 static void *worker(void *arg) {
     job_t *j = (job_t *)arg;
-    uint8_t *buf = (uint8_t *)malloc((size_t)CHUNK_BLOCKS * 34 + (1u << 20));
+    uint8_t *buf = (uint8_t *)malloc((size_t)CHUNK_BLOCKS * MAX_BLOCK_BYTES + (1u << 20));
     uint64_t max_vec = 0;
     for (int i = 0; i < j->nt; i++)
         if (j->t[i].norm && j->t[i].bytes > max_vec) max_vec = j->t[i].bytes;
-    uint8_t *vbuf = max_vec > (size_t)CHUNK_BLOCKS * 34 ? (uint8_t *)malloc(max_vec) : NULL;
+    uint8_t *vbuf = max_vec > (size_t)CHUNK_BLOCKS * MAX_BLOCK_BYTES ? (uint8_t *)malloc(max_vec) : NULL;
     if (!buf) { __atomic_store_n(&j->failed, 1, __ATOMIC_RELAXED); return NULL; }
     for (;;) {
         uint64_t it = __atomic_fetch_add(&j->next, 1, __ATOMIC_RELAXED);
@@ -309,9 +389,8 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
     if (s->n_layers <= 0 || s->hidden <= 0 || s->n_heads <= 0 || s->n_kv_heads <= 0 ||
         s->head_dim <= 0 || s->ffn <= 0 || s->vocab <= 3 || s->hidden % 32 || s->ffn % 32 ||
         (s->n_heads * s->head_dim) % 32 || (s->n_kv_heads * s->head_dim) % 32 ||
-        (s->layer_type != T_Q4_0 && s->layer_type != T_Q8_0 && !is_k(s->layer_type)) ||
-        (s->embd_type != T_Q4_0 && s->embd_type != T_Q8_0 && !is_k(s->embd_type)) ||
-        (s->out_type != -1 && s->out_type != T_Q4_0 && s->out_type != T_Q8_0 && !is_k(s->out_type)) ||
+        !matrix_type_ok(s->layer_type) || !matrix_type_ok(s->embd_type) ||
+        (s->out_type != -1 && !matrix_type_ok(s->out_type)) ||
         /* K-quant rows are whole super-blocks of 256 */
         (is_k(s->layer_type) && (s->hidden % 256 || s->ffn % 256 || (s->n_heads * s->head_dim) % 256)) ||
         ((is_k(s->embd_type) || is_k(s->out_type)) && s->hidden % 256) ||
@@ -344,7 +423,7 @@ int32_t ss_synth_gguf_write(const char *path, const ss_synth_spec_t *s) {
         t[k].bytes = (isnorm) == 2 ? (uint64_t)(cols) * ((type_) == T_F16 ? 2 : 4)   \
                      : (isnorm) ? (uint64_t)(cols) * 4                               \
                      : is_k(type_) ? (uint64_t)(cols) * (rows) / 256 * k_bytes(type_) \
-                                : (uint64_t)(cols) * (rows) / 32 * ((type_) == T_Q4_0 ? 18 : 34); \
+                                : (uint64_t)(cols) * (rows) / 32 * block_bytes(type_);           \
         k++;                                                                         \
     } while (0)
     ADD("token_embd.weight", s->embd_type, d, (uint64_t)s->vocab, 0);

@@ -22,7 +22,7 @@ Test infrastructure only.
 import numpy as np
 
 from tests.test_cpu_host import parse_gguf
-from tests.util import KQ_BYTES, dequant_np
+from tests.util import B32_BYTES, KQ_BYTES, dequant_np
 
 NEOX_ARCHS = ("qwen", "falcon", "phi", "deepseek")       # layer_scheduler.c:144-149
 
@@ -41,7 +41,7 @@ def _matrix(raw, data, dims, ttype, off):
     cols, rows = int(dims[0]), int(dims[1])
     if ttype in (0, 1):
         return _vector(raw, data, dims, ttype, off).reshape(rows, cols)
-    nbytes = rows * cols // 256 * KQ_BYTES[ttype] if ttype in KQ_BYTES else rows * (cols // 32) * {2: 18, 8: 34}[ttype]
+    nbytes = rows * cols // 256 * KQ_BYTES[ttype] if ttype in KQ_BYTES else rows * (cols // 32) * B32_BYTES[ttype]
     blocks = np.frombuffer(raw, np.uint8, nbytes, data + off)
     return dequant_np(blocks, rows, cols, ttype)
 

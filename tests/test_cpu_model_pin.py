@@ -51,6 +51,12 @@ VARIANTS = {
     "q3_k_q5_head": dict(layer_type=11, embd_type=13, out_type=13, seed=35),
     "q5_k": dict(layer_type=13, embd_type=14, out_type=-1, seed=36),
     "q6_k": dict(layer_type=14, embd_type=14, out_type=14, seed=37),
+    # the other 32-weight block types and float matrices (quantize.c:74-176)
+    "q4_1_q8_1_head": dict(layer_type=3, embd_type=3, out_type=9, seed=38),
+    "q5_0_f16_head": dict(layer_type=6, embd_type=6, out_type=1, seed=39),
+    "q5_1_tied": dict(layer_type=7, embd_type=7, out_type=-1, seed=40),
+    "f16": dict(layer_type=1, embd_type=1, out_type=1, seed=41),
+    "f32_q8_1": dict(layer_type=0, embd_type=9, out_type=0, seed=42),
     # tokenizer shorter than the tables: the vocabulary is clamped to it
     "padded_tied": dict(embd_type=2, out_type=-1, vocab_tokens=360, seed=29),
     "padded_out": dict(vocab_tokens=370, seed=30),

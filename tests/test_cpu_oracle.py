@@ -549,3 +549,94 @@ def test_kquant_matvec_fp64(qtype):
     got = oracle.matvec(w, x, rows, cols, qtype)
     want = dequant_np(w, rows, cols, qtype) @ x.astype(np.float64)
     assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))
+
+
+# ---------------------------------------------------------------- Q4_1, Q5_0, Q5_1, Q8_1, F16, F32
+MORE = [0, 1, 3, 6, 7, 9]
+
+
+@pytest.mark.parametrize("qtype", MORE)
+def test_more_dequant_matches_independent_numpy(qtype):
+    """quantize.c:74-176 against the vectorised fp64 numpy reading of the
+    GGML layouts in tests/util.py: equal on random blocks (each weight is one
+    exact product plus at most one fp32 rounding)."""
+    from tests.util import B32_BYTES, dequant_np, make_more
+    rng = np.random.default_rng(qtype + 50)
+    rows, cols = 5, 256
+    w = make_more(qtype, rows, cols, rng)
+    want = dequant_np(w, rows, cols, qtype)
+    rb = cols // 32 * B32_BYTES[qtype]
+    got = np.stack([oracle.dequantize(w[r * rb:(r + 1) * rb], cols, qtype) for r in range(rows)])
+    assert np.max(np.abs(got - want)) <= 1e-7 * np.max(np.abs(want))
+
+
+def _nibble_block():
+    return np.array([j | ((15 - j) << 4) for j in range(16)], np.uint8)   # weight j: j, weight j+16: 15-j
+
+
+def test_q4_1_closed_form():
+    """d * nibble + m, weight j in the low nibble of byte j, j + 16 in the high."""
+    blk = np.zeros(20, np.uint8)
+    blk[0:2] = np.array([0.5], np.float16).view(np.uint8)
+    blk[2:4] = np.array([-1.25], np.float16).view(np.uint8)
+    blk[4:20] = _nibble_block()
+    got = oracle.dequantize(blk, 32, 3)
+    want = [0.5 * j - 1.25 for j in range(16)] + [0.5 * (15 - j) - 1.25 for j in range(16)]
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+def test_q5_0_closed_form():
+    """(q - 16) * d with q = nibble | bit j of the little-endian qh << 4."""
+    qh = 0xF0F0F00F
+    blk = np.zeros(22, np.uint8)
+    blk[0:2] = np.array([0.25], np.float16).view(np.uint8)
+    blk[2:6] = np.array([qh], np.uint32).view(np.uint8)
+    blk[6:22] = _nibble_block()
+    got = oracle.dequantize(blk, 32, 6)
+    nib = list(range(16)) + [15 - j for j in range(16)]
+    want = [((nib[j] | (((qh >> j) & 1) << 4)) - 16) * 0.25 for j in range(32)]
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+def test_q5_1_closed_form():
+    """q * d + m; qh 0x0000FFFF lifts the first 16 weights by 16."""
+    blk = np.zeros(24, np.uint8)
+    blk[0:2] = np.array([0.5], np.float16).view(np.uint8)
+    blk[2:4] = np.array([0.75], np.float16).view(np.uint8)
+    blk[4:8] = np.array([0x0000FFFF], np.uint32).view(np.uint8)
+    blk[8:24] = _nibble_block()
+    got = oracle.dequantize(blk, 32, 7)
+    want = [(j + 16) * 0.5 + 0.75 for j in range(16)] + [(15 - j) * 0.5 + 0.75 for j in range(16)]
+    assert np.array_equal(got, np.array(want, np.float32))
+
+
+def test_q8_1_closed_form():
+    """fp32 d (0.1 has no binary16 form: the whole fp32 word is read) times
+    the int8 code; the sum field s is ignored."""
+    blk = np.zeros(40, np.uint8)
+    blk[0:4] = np.array([0.1], np.float32).view(np.uint8)
+    blk[4:8] = np.array([123.0], np.float32).view(np.uint8)
+    blk[8:40] = (np.arange(32) - 16).astype(np.int8).view(np.uint8)
+    got = oracle.dequantize(blk, 32, 9)
+    assert np.array_equal(got, np.float32(0.1) * (np.arange(32) - 16).astype(np.float32))
+
+
+def test_f16_f32_rows_are_the_weights():
+    """quantize.c:167-172 (F16 widened exactly, subnormals and signed zero
+    included) and :391-393 (F32 copied)."""
+    h = np.array([0.0, -0.0, 1.0, -2.5, 6.1e-5, 5.96e-8, 65504.0, 0.333], np.float16)
+    assert np.array_equal(oracle.dequantize(h.view(np.uint8), h.size, 1), h.astype(np.float32))
+    f = np.array([1e-40, -3.25, 7.0, 1e30], np.float32)
+    assert np.array_equal(oracle.dequantize(f.view(np.uint8), f.size, 0), f)
+
+
+@pytest.mark.parametrize("qtype", MORE)
+def test_more_matvec_fp64(qtype):
+    from tests.util import dequant_np, make_more
+    rng = np.random.default_rng(qtype + 150)
+    rows, cols = 16, 2048
+    w = make_more(qtype, rows, cols, rng)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = oracle.matvec(w, x, rows, cols, qtype)
+    want = dequant_np(w, rows, cols, qtype) @ x.astype(np.float64)
+    assert np.max(np.abs(got - want)) <= 1e-5 * np.max(np.abs(want))

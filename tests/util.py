@@ -6,7 +6,10 @@ import numpy as np
 
 Q4_0, Q8_0, Q4_K = 2, 8, 12
 Q2_K, Q3_K, Q5_K, Q6_K = 10, 11, 13, 14
+F32, F16, Q4_1, Q5_0, Q5_1, Q8_1 = 0, 1, 3, 6, 7, 9
 KQ_BYTES = {Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}   # per 256 weights
+# per 32 weights (GGML block sizes; float matrices counted in 32-weight pieces)
+B32_BYTES = {Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q8_0: 34, Q8_1: 40, F16: 64, F32: 128}
 
 
 def _vp(a):
@@ -108,7 +111,32 @@ def make_kq(qtype, rows, cols, rng, sigma=0.02):
     return out.reshape(-1)
 
 
+def make_more(qtype, rows, cols, rng, sigma=0.02):
+    """F32 / F16 matrices (weights N(0, 4.6 sigma), the spread of make_q4_0's)
+    and GGUF Q4_1 / Q5_0 / Q5_1 / Q8_1 blocks: random codes and high bits,
+    d = |N(0, s)| (fp32 for Q8_1), m = -(centre code) d + noise."""
+    if qtype in (F32, F16):
+        w = rng.normal(0.0, 4.6 * sigma, rows * cols)
+        return (w.astype(np.float32) if qtype == F32 else w.astype(np.float16)).view(np.uint8)
+    nb = rows * (cols // 32)
+    out = rng.integers(0, 256, (nb, B32_BYTES[qtype]), dtype=np.uint8)
+    if qtype == Q8_1:
+        d = np.abs(rng.normal(0.0, sigma / 16.0, nb)).astype(np.float32)
+        out[:, 0:4] = d.view(np.uint8).reshape(nb, 4)
+        out[:, 4:8] = rng.normal(0.0, 1.0, nb).astype(np.float32).view(np.uint8).reshape(nb, 4)   # s, unused
+        out[:, 8:40] = rng.integers(-127, 128, (nb, 32), dtype=np.int16).astype(np.int8).view(np.uint8)
+        return out.reshape(-1)
+    centre, rms = {Q4_1: (7.5, 4.6), Q5_0: (0.0, 9.25), Q5_1: (15.5, 9.2)}[qtype]
+    d = np.abs(rng.normal(0.0, 4.6 * sigma / rms, nb))
+    _f16_into(out, 0, d)
+    if qtype != Q5_0:
+        _f16_into(out, 2, -centre * d + rng.normal(0.0, 0.5 * sigma, nb))
+    return out.reshape(-1)
+
+
 def make_blocks(qtype, rows, cols, rng, sigma=0.02):
+    if qtype in B32_BYTES and qtype not in (Q4_0, Q8_0):
+        return make_more(qtype, rows, cols, rng, sigma)
     if qtype == Q4_K:
         return make_q4_k(rows, cols, rng, sigma)
     if qtype in (Q2_K, Q3_K, Q5_K, Q6_K):
@@ -145,6 +173,8 @@ def dequant_np(blocks, rows, cols, qtype):
         w = b[:, 2:].view(np.int8).astype(np.float64) * d[:, None]
     elif qtype in (Q2_K, Q3_K, Q5_K, Q6_K):
         w = _dequant_kq(blocks, rows, cols, qtype)
+    elif qtype in (F32, F16, Q4_1, Q5_0, Q5_1, Q8_1):
+        w = _dequant_more(blocks, rows, cols, qtype)
     else:   # Q4_K super-blocks of 256
         nsb = rows * (cols // 256)
         b = blocks.reshape(nsb, 144)
@@ -157,6 +187,33 @@ def dequant_np(blocks, rows, cols, qtype):
             for k in range(8):
                 nib = (q[32 * (k // 2):32 * (k // 2) + 32] >> (4 * (k % 2))) & 15
                 w[i, 32 * k:32 * k + 32] = d[i] * sc[k] * nib - dm[i] * mn[k]
+    return w.reshape(rows, cols)
+
+
+def _dequant_more(blocks, rows, cols, qtype):
+    """F32 / F16 and Q4_1 / Q5_0 / Q5_1 / Q8_1 in fp64 from the GGML block
+    layouts: Q4_1 = d, m, 16 nibble bytes (weight j low, j + 16 high), d q + m;
+    Q5_0 = d, qh, nibbles, (q - 16) d; Q5_1 = d, m, qh, nibbles, d q + m, with
+    bit j of the little-endian qh as bit 4 of weight j; Q8_1 = fp32 d, fp32 s,
+    32 int8, d q."""
+    raw = np.ascontiguousarray(blocks, np.uint8)
+    if qtype == F32:
+        return raw.view(np.float32).astype(np.float64).reshape(rows, cols)
+    if qtype == F16:
+        return raw.view(np.float16).astype(np.float64).reshape(rows, cols)
+    b = raw.reshape(rows * (cols // 32), B32_BYTES[qtype])
+    if qtype == Q8_1:
+        d = b[:, 0:4].copy().view(np.float32).astype(np.float64).reshape(-1)
+        return (b[:, 8:].view(np.int8).astype(np.float64) * d[:, None]).reshape(rows, cols)
+    d = _f16_col(b, 0)
+    m = _f16_col(b, 2) if qtype != Q5_0 else 0.0
+    qs = b[:, {Q4_1: 4, Q5_0: 6, Q5_1: 8}[qtype]:].astype(np.int64)
+    q = np.concatenate([qs & 15, qs >> 4], axis=1)
+    if qtype != Q4_1:
+        o = 2 if qtype == Q5_0 else 4
+        qh = b[:, o:o + 4].copy().view(np.uint32).astype(np.int64).reshape(-1)
+        q = q | (((qh[:, None] >> np.arange(32)[None, :]) & 1) << 4)
+    w = (q - 16) * d[:, None] if qtype == Q5_0 else q * d[:, None] + m[:, None]
     return w.reshape(rows, cols)
 
 
