@@ -26,7 +26,11 @@
  * uses the same tiles for its 32-weight sub-blocks (nibbles without offset,
  * scale-plane entry = 6-bit scale | 6-bit min << 8), then at the next
  * 256-byte boundary a third plane with each row's super-block (d, dmin)
- * binary16 pairs, [row group][super-block][16 rows].
+ * binary16 pairs, [row group][super-block][16 rows]. The other 32-weight
+ * block types use the same tiles: Q4_1 nibbles and Q5_1 / Q8_1 int8 codes
+ * with a 32-bit scale entry per block (d | m << 16 as binary16, or Q8_1's
+ * fp32 d), Q5_0 as Q8_0 (codes q - 16); F16 and F32 matrices store each
+ * block's 32 weights (64 or 128 bytes) and have no scale plane.
  */
 #ifndef SS_HIP_H
 #define SS_HIP_H
@@ -42,10 +46,14 @@ typedef struct ss_hip_ctx ss_hip_ctx_t;
 typedef struct ss_hip_model ss_hip_model_t;
 
 /* ggml tensor types accepted (src/core/gguf_loader.h:41-55) */
-#define SS_HIP_F32 0
+#define SS_HIP_F32 0     /* float matrices: 32-weight chunks, no scales */
 #define SS_HIP_F16 1
 #define SS_HIP_Q4_0 2
+#define SS_HIP_Q4_1 3    /* 32-bit (d, m) scale entries */
+#define SS_HIP_Q5_0 6    /* stored as Q8_0: code q - 16, the same d */
+#define SS_HIP_Q5_1 7    /* int8 codes, 32-bit (d, m) scale entries */
 #define SS_HIP_Q8_0 8
+#define SS_HIP_Q8_1 9    /* int8 codes, 32-bit (fp32 d) scale entries */
 #define SS_HIP_Q4_K 12   /* 256-weight super-blocks (cols a multiple of 256) */
 #define SS_HIP_Q2_K 10   /* the other K-quants, also 256-weight super-blocks */
 #define SS_HIP_Q3_K 11

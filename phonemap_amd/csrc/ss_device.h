@@ -154,6 +154,36 @@ struct QTraits<8> {            // Q8_0
   static constexpr int kGgufBytes = 34;
 };
 template <>
+struct QTraits<3> {             // Q4_1: nibbles as Q4_0's, (d, m) scale entry
+  static constexpr int kQB = 16;
+  static constexpr int kGgufBytes = 20;
+};
+template <>
+struct QTraits<6> {             // Q5_0 (packed into the Q8_0 format)
+  static constexpr int kQB = 32;
+  static constexpr int kGgufBytes = 22;
+};
+template <>
+struct QTraits<7> {             // Q5_1: 5-bit codes as int8, (d, m) scale entry
+  static constexpr int kQB = 32;
+  static constexpr int kGgufBytes = 24;
+};
+template <>
+struct QTraits<9> {             // Q8_1: int8 codes, fp32 d
+  static constexpr int kQB = 32;
+  static constexpr int kGgufBytes = 40;
+};
+template <>
+struct QTraits<1> {             // F16: 32 binary16 weights per block chunk
+  static constexpr int kQB = 64;
+  static constexpr int kGgufBytes = 64;
+};
+template <>
+struct QTraits<0> {             // F32: 32 fp32 weights per block chunk
+  static constexpr int kQB = 128;
+  static constexpr int kGgufBytes = 128;
+};
+template <>
 struct QTraits<12> {           // Q4_K: a 32-weight sub-block packs like a Q4_0 block
   static constexpr int kQB = 16;
   static constexpr int kGgufBytes = 144;   // per 256-weight super-block
@@ -449,6 +479,19 @@ __device__ __forceinline__ float q8_dot(const uint4 qa, const uint4 qb, const ui
   }
   const float sa3 = __uint_as_float(ra[13]), sb3 = __uint_as_float(rb[13]);
   return fmaf(fmaf((float)a12, 128.0f, (float)a3), sa3, fmaf((float)b12, 128.0f, (float)b3) * sb3);
+}
+
+// Q5_1 block (quantize.c:114-137: weight = q * d + m, q = 0..31, stored as
+// int8 codes): d * sum q X s3 + m * sum X s3 per 16-value record, sum X
+// being the records' [12] / 8.
+__device__ __forceinline__ float q51_dot(const uint4 qa, const uint4 qb, const uint32_t* ra, const uint32_t* rb,
+                                         float d, float m) {
+  const float qx = q8_dot(qa, qb, ra, rb);
+  const uint2 ta = *reinterpret_cast<const uint2*>(ra + 12);
+  const uint2 tb = *reinterpret_cast<const uint2*>(rb + 12);
+  const float sx = fmaf((float)((int)ta.x >> 3), __uint_as_float(ta.y),
+                        (float)((int)tb.x >> 3) * __uint_as_float(tb.y));
+  return fmaf(d, qx, m * sx);
 }
 
 

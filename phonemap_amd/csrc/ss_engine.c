@@ -97,7 +97,11 @@ static size_t row_bytes(int32_t type, int32_t cols) {
     case SS_HIP_F32: return (size_t)cols * 4;
     case SS_HIP_F16: return (size_t)cols * 2;
     case SS_HIP_Q4_0: return (size_t)cols / 32 * 18;
+    case SS_HIP_Q4_1: return (size_t)cols / 32 * 20;
+    case SS_HIP_Q5_0: return (size_t)cols / 32 * 22;
+    case SS_HIP_Q5_1: return (size_t)cols / 32 * 24;
     case SS_HIP_Q8_0: return (size_t)cols / 32 * 34;
+    case SS_HIP_Q8_1: return (size_t)cols / 32 * 40;
     case SS_HIP_Q2_K: return (size_t)cols / 256 * 84;
     case SS_HIP_Q3_K: return (size_t)cols / 256 * 110;
     case SS_HIP_Q4_K: return (size_t)cols / 256 * 144;

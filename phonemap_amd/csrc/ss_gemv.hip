@@ -179,6 +179,74 @@ __device__ __forceinline__ void mput(MSlice<UT>& p, int* xw, int u, int nb, int 
   }
 }
 
+// F16 / F32 matrices take x as fp32 values: the unit's records in this wave's
+// LDS slice become v = s3 * (16384 q1 + 128 q2 + q3) in place, value j of a
+// block at word j of its kXW (every lane reads all its record words before
+// any lane writes; one wave owns the slice). Lanes read words other lanes
+// wrote (a record's s3), so wavefront fences order the accesses: without
+// them the compiler may hoist a lane's read of s3 above the write another
+// lane makes on the other side of a branch.
+template <int UT>
+__device__ __forceinline__ void rec_to_float(int* xw, int lane) {
+  constexpr int kN = UT * kTB * 8 / kWave;   // groups of 4 values per lane
+  uint32_t q1[kN], q2[kN], q3[kN];
+  float s3[kN];
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");   // the staged records are written
+#pragma unroll
+  for (int i = 0; i < kN; ++i) {
+    const int gi = i * kWave + lane, grp = gi & 7;
+    const int* rp = xw + (gi >> 3) * kXW + (grp >> 2) * kRW;
+    q1[i] = (uint32_t)rp[grp & 3];
+    q2[i] = (uint32_t)rp[4 + (grp & 3)];
+    q3[i] = (uint32_t)rp[8 + (grp & 3)];
+    s3[i] = __int_as_float(rp[13]);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");   // all reads before the first write
+#pragma unroll
+  for (int i = 0; i < kN; ++i) {
+    const int gi = i * kWave + lane;
+    float v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int X = 16384 * (int)(int8_t)(q1[i] >> (8 * k)) + 128 * (int)(int8_t)(q2[i] >> (8 * k)) +
+                    (int)(int8_t)(q3[i] >> (8 * k));
+      v[k] = s3[i] * (float)X;
+    }
+    *reinterpret_cast<float4*>(xw + (gi >> 3) * kXW + 4 * (gi & 7)) = make_float4(v[0], v[1], v[2], v[3]);
+  }
+}
+
+// One F16 / F32 block chunk (32 weights in column order) against its 32 fp32
+// x values, in four interleaved partial sums.
+template <int QT>
+__device__ __forceinline__ float float_dot(const uint4 (&q)[QTraits<QT>::kQB / 16], const float* xv) {
+  float s[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int v = 0; v < 8; ++v) {   // values 4v .. 4v+3
+    const float4 x = *reinterpret_cast<const float4*>(xv + 4 * v);
+    float w[4];
+    if constexpr (QT == kF16) {
+      const uint4 c = q[v / 2];
+      const uint32_t lo = v & 1 ? c.z : c.x, hi = v & 1 ? c.w : c.y;
+      w[0] = h2f((uint16_t)(lo & 0xffffu));
+      w[1] = h2f((uint16_t)(lo >> 16));
+      w[2] = h2f((uint16_t)(hi & 0xffffu));
+      w[3] = h2f((uint16_t)(hi >> 16));
+    } else {
+      const uint4 c = q[v];
+      w[0] = __uint_as_float(c.x);
+      w[1] = __uint_as_float(c.y);
+      w[2] = __uint_as_float(c.z);
+      w[3] = __uint_as_float(c.w);
+    }
+    s[0] = fmaf(w[0], x.x, s[0]);
+    s[1] = fmaf(w[1], x.y, s[1]);
+    s[2] = fmaf(w[2], x.z, s[2]);
+    s[3] = fmaf(w[3], x.w, s[3]);
+  }
+  return (s[0] + s[1]) + (s[2] + s[3]);
+}
+
 // One wave's share per round: a unit of UT (2, 4 or 8) consecutive tiles
 // (those < ntk), every chunk of it requested before any is used. A unit lies
 // inside one 8-tile scale group, whose 16 bytes per lane it reads UT/2 words of.
@@ -186,7 +254,9 @@ template <int QT, int NMAT, int UT>
 struct Round {
   static constexpr int kNV = QTraits<QT>::kQB / 16;
   uint4 q[NMAT][UT][kNV];
-  uint32_t sc[NMAT][UT / 2];   // the unit's binary16 scales (Q4_K: scale | min << 8), tile order
+  // the unit's scale entries, tile order: binary16 pairs (Q4_K: scale | min
+  // << 8), or one 32-bit entry per tile (Q4_1, Q5_1: d | m << 16; Q8_1: fp32 d)
+  uint32_t sc[NMAT][is_wide(QT) ? UT : UT / 2];
   uint32_t su[NMAT][is_kq(QT) ? UT / 2 : 1];   // K-quants: (d, dmin) of the unit's super-blocks
 };
 
@@ -199,15 +269,29 @@ __device__ __forceinline__ void load_round(Round<QT, NMAT, UT>& f, const GemvArg
 #pragma unroll
   for (int m = 0; m < NMAT; ++m) {
     const PackedMat& w = m == 0 ? a.w : a.w2;
-    const uint32_t* sp = reinterpret_cast<const uint32_t*>(w.ds + scale_idx(g, ntk, t0, lane));
-    if constexpr (UT == 8) {
-      const uint4 v = *reinterpret_cast<const uint4*>(sp);
-      f.sc[m][0] = v.x; f.sc[m][1] = v.y; f.sc[m][2] = v.z; f.sc[m][3] = v.w;
-    } else if constexpr (UT == 4) {
-      const uint2 v = *reinterpret_cast<const uint2*>(sp);
-      f.sc[m][0] = v.x; f.sc[m][1] = v.y;
-    } else {
-      f.sc[m][0] = *sp;
+    if constexpr (is_wide(QT)) {   // 32-bit entries: 4 bytes per tile
+      const uint32_t* sp = reinterpret_cast<const uint32_t*>(w.ds) + scale_idx(g, ntk, t0, lane);
+#pragma unroll
+      for (int k = 0; k < UT; k += 4) {
+        if constexpr (UT >= 4) {
+          const uint4 v = *reinterpret_cast<const uint4*>(sp + k);
+          f.sc[m][k] = v.x; f.sc[m][k + 1] = v.y; f.sc[m][k + 2] = v.z; f.sc[m][k + 3] = v.w;
+        } else {
+          const uint2 v = *reinterpret_cast<const uint2*>(sp);
+          f.sc[m][0] = v.x; f.sc[m][1] = v.y;
+        }
+      }
+    } else if constexpr (!is_float(QT)) {   // F16 / F32 have no scales
+      const uint32_t* sp = reinterpret_cast<const uint32_t*>(w.ds + scale_idx(g, ntk, t0, lane));
+      if constexpr (UT == 8) {
+        const uint4 v = *reinterpret_cast<const uint4*>(sp);
+        f.sc[m][0] = v.x; f.sc[m][1] = v.y; f.sc[m][2] = v.z; f.sc[m][3] = v.w;
+      } else if constexpr (UT == 4) {
+        const uint2 v = *reinterpret_cast<const uint2*>(sp);
+        f.sc[m][0] = v.x; f.sc[m][1] = v.y;
+      } else {
+        f.sc[m][0] = *sp;
+      }
     }
     if constexpr (is_kq(QT)) {   // a unit (an even number of tiles) covers UT / 2 super-blocks
       const int nsb = ntk / 2;
@@ -238,9 +322,18 @@ __device__ __forceinline__ void fma_round(float (&acc)[NMAT], const Round<QT, NM
     const uint32_t* ra = reinterpret_cast<const uint32_t*>(xs + (k * kTB + kb) * kXW);
 #pragma unroll
     for (int m = 0; m < NMAT; ++m) {
-      const uint32_t sw = f.sc[m][k / 2];
-      const uint32_t e = k & 1 ? sw >> 16 : sw & 0xffffu;
-      if constexpr (QT == kQ4K) {
+      const uint32_t sw = f.sc[m][is_wide(QT) ? k : k / 2];
+      const uint32_t e = is_wide(QT) ? sw : k & 1 ? sw >> 16 : sw & 0xffffu;
+      if constexpr (is_float(QT)) {
+        acc[m] += float_dot<QT>(f.q[m][k], reinterpret_cast<const float*>(ra));
+      } else if constexpr (QT == kQ4_1) {   // d * q + m: Q4_K's dot with dsc = d, dmn = -m
+        acc[m] += q4k_dot(f.q[m][k][0], ra, ra + kRW, h2f((uint16_t)(e & 0xffffu)), -h2f((uint16_t)(e >> 16)));
+      } else if constexpr (QT == kQ5_1) {
+        acc[m] += q51_dot(f.q[m][k][0], f.q[m][k][1], ra, ra + kRW, h2f((uint16_t)(e & 0xffffu)),
+                          h2f((uint16_t)(e >> 16)));
+      } else if constexpr (QT == kQ8_1) {
+        acc[m] = fmaf(__uint_as_float(e), q8_dot(f.q[m][k][0], f.q[m][k][1], ra, ra + kRW), acc[m]);
+      } else if constexpr (QT == kQ4K) {
         const uint32_t sup = f.su[m][k / 2];
         const float dsc = h2f((uint16_t)(sup & 0xffffu)) * (float)(e & 0xffu);   // exact
         const float dmn = h2f((uint16_t)(sup >> 16)) * (float)(e >> 8);
@@ -372,7 +465,7 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int row, bool own, c
 // Q8_0 and two-matrix rounds hold 64 VGPRs of codes: at most 8 waves, so
 // 256 VGPRs are available to them.
 template <int QT, int NMAT>
-constexpr int gemv_max_waves() { return QT == 8 || NMAT == 2 || is_kq(QT) ? 8 : 16; }
+constexpr int gemv_max_waves() { return QT == 2 && NMAT == 1 ? 16 : 8; }
 
 template <int QT, int NMAT, int EPI, int UT, bool MERGE, bool PX>
 __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(const GemvArgs a) {
@@ -418,6 +511,7 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
       load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
       ssq += xput<UT>(xp, xw, a.nw, u, nb, lane);
     }
+    if constexpr (is_float(QT)) rec_to_float<UT>(xw, lane);
     // the slice is written and read by this wave only: LDS operations of a
     // wave complete in order, the fence keeps the compiler from reordering
     __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -606,6 +700,64 @@ __global__ void k_pack_kq(const uint8_t* __restrict__ src, uint8_t* __restrict__
   if (k == 0) su[((size_t)g * nsb + b / 8) * kRG + row % kRG] = d | (dm << 16);
 }
 
+// GGUF Q4_1 / Q5_0 / Q5_1 / Q8_1 blocks (quantize.h:20-53) and F16 / F32
+// rows -> tiled planes; thread i takes 32-weight block b = i % nb of row
+// row_off + i / nb. Q4_1: its 16 nibble bytes as they are (Q4_0 order) and
+// d | m << 16. Q5_0 (into the Q8_0 format): int8 codes q - 16 in weight order
+// (q = nibble | bit j of qh << 4; weight j < 16 the low nibble of byte j,
+// weight j + 16 the high one, quantize.c:93-112) and d. Q5_1: int8 codes q
+// (0..31) and d | m << 16. Q8_1: its 32 int8 codes and the fp32 bits of d.
+// F16 / F32: the block's 32 weights.
+template <int QT>
+__global__ void k_pack_more(const uint8_t* __restrict__ src, uint8_t* __restrict__ qs, uint16_t* __restrict__ ds,
+                            int64_t nblocks, int nb, int64_t row_off) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= nblocks) return;
+  constexpr int kBytes = QTraits<QT>::kGgufBytes;
+  constexpr int DT = dev_type(QT);
+  constexpr int kQB = code_bytes_of(DT);
+  const int64_t row = row_off + i / nb;
+  const int b = (int)(i % nb);
+  const int ntk = (nb + kTB - 1) / kTB, g = (int)(row / kRG), l = tile_lane((int)(row % kRG), b);
+  const uint8_t* sb = src + i * kBytes;
+  uint8_t* dst = qs + tile_idx(g, ntk, b / kTB, l) * kQB;
+  auto u16 = [&](int o) { return (uint32_t)sb[o] | ((uint32_t)sb[o + 1] << 8); };
+  auto u32 = [&](int o) { return u16(o) | (u16(o + 2) << 16); };
+  if constexpr (is_float(QT)) {
+#pragma unroll
+    for (int v = 0; v < kQB / 16; ++v)
+      reinterpret_cast<uint4*>(dst)[v] = make_uint4(u32(16 * v), u32(16 * v + 4), u32(16 * v + 8), u32(16 * v + 12));
+    return;
+  } else {
+    uint32_t w[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+    if constexpr (QT == kQ4_1) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w[k] = u32(4 + 4 * k);
+      reinterpret_cast<uint32_t*>(ds)[scale_idx(g, ntk, b / kTB, l)] = u16(0) | (u16(2) << 16);
+    } else if constexpr (QT == kQ8_1) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) w[k] = u32(8 + 4 * k);
+      reinterpret_cast<uint32_t*>(ds)[scale_idx(g, ntk, b / kTB, l)] = u32(0);
+    } else {   // Q5_0, Q5_1
+      constexpr bool one = QT == kQ5_1;
+      const uint32_t qh = u32(one ? 4 : 2);
+      const uint8_t* q = sb + (one ? 8 : 6);
+#pragma unroll
+      for (int j = 0; j < 32; ++j) {
+        const uint32_t nib = j < 16 ? q[j] & 15u : q[j - 16] >> 4;
+        const int c = (int)(nib | (((qh >> j) & 1u) << 4)) - (one ? 0 : 16);
+        w[j / 4] |= ((uint32_t)c & 0xffu) << (8 * (j % 4));
+      }
+      if constexpr (one)
+        reinterpret_cast<uint32_t*>(ds)[scale_idx(g, ntk, b / kTB, l)] = u16(0) | (u16(2) << 16);
+      else
+        ds[scale_idx(g, ntk, b / kTB, l)] = (uint16_t)u16(0);
+    }
+    reinterpret_cast<uint4*>(dst)[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    if constexpr (kQB == 32) reinterpret_cast<uint4*>(dst)[1] = make_uint4(w[4], w[5], w[6], w[7]);
+  }
+}
+
 // Row `token` of a packed table, dequantised exactly as quantize.c:60-72 /
 // 139-149 (one fp32 multiply per weight). With tokens set, workgroup row z
 // writes row tokens[*dpos + z] to out + z * cols (a prompt's rows at once).
@@ -617,8 +769,23 @@ __device__ __forceinline__ float embed_value(const PackedMat& t, int tok, int nt
   const int b = j >> 5, p = j & 31;
   const int l = tile_lane(tok % kRG, b);
   const uint8_t* q = t.qs + tile_idx(tok / kRG, ntk, b / kTB, l) * kQB;
-  const float d = h2f(t.ds[scale_idx(tok / kRG, ntk, b / kTB, l)]);
-  if constexpr (QT == 2) {
+  if constexpr (QT == kF16) {   // quantize.c:167-172
+    return h2f(reinterpret_cast<const uint16_t*>(q)[p]);
+  } else if constexpr (QT == kF32) {
+    return reinterpret_cast<const float*>(q)[p];
+  } else if constexpr (is_wide(QT)) {
+    const uint32_t e = reinterpret_cast<const uint32_t*>(t.ds)[scale_idx(tok / kRG, ntk, b / kTB, l)];
+    const float d = h2f((uint16_t)(e & 0xffffu)), m = h2f((uint16_t)(e >> 16));
+    if constexpr (QT == kQ4_1) {   // quantize.c:76-91: d * q + m
+      const uint8_t v = q[p & 15];
+      return __fadd_rn(__fmul_rn(d, (float)(p < 16 ? v & 0xF : v >> 4)), m);
+    } else if constexpr (QT == kQ5_1) {   // :114-137: q * d + m
+      return __fadd_rn(__fmul_rn((float)q[p], d), m);
+    } else {   // Q8_1, :153-163: fp32 d * q
+      return __fmul_rn(__uint_as_float(e), (float)(int8_t)q[p]);
+    }
+  } else if constexpr (QT == 2) {
+    const float d = h2f(t.ds[scale_idx(tok / kRG, ntk, b / kTB, l)]);
     const uint8_t v = q[p & 15];
     return d * (float)((int)(p < 16 ? v & 0xF : v >> 4) - 8);
   } else if constexpr (QT == kQ4K) {
@@ -650,8 +817,8 @@ __device__ __forceinline__ float embed_value(const PackedMat& t, int tok, int nt
     } else {
       return __fmul_rn(__fmul_rn(dd, (float)(int8_t)sg), (float)(int8_t)q[p]);
     }
-  } else {
-    return d * (float)(int8_t)q[p];
+  } else {   // Q8_0, and Q5_0 in the Q8_0 format: (q - 16) * d, quantize.c:93-112
+    return h2f(t.ds[scale_idx(tok / kRG, ntk, b / kTB, l)]) * (float)(int8_t)q[p];
   }
 }
 
@@ -768,7 +935,7 @@ GemvPlan gemv_plan(int rows, int cols, int type, int nmat, int unit) {
   GemvPlan p;
   const int groups = (rows + kRG - 1) / kRG;
   const int ntk = (cols / 32 + kTB - 1) / kTB;
-  const int smax = type == 8 || is_kq(type) || nmat == 2 ? gemv_max_waves<8, 1>() : gemv_max_waves<2, 1>();
+  const int smax = dev_type(type) == 2 && nmat == 1 ? gemv_max_waves<2, 1>() : gemv_max_waves<8, 1>();
   const int ut = unit;
   const int nu = (ntk + ut - 1) / ut;
   const int S = nu < smax ? nu : smax;
@@ -784,12 +951,14 @@ GemvPlan gemv_plan(int rows, int cols, int type, int nmat, int unit) {
 // matrix; the scale plane starts at a 256-byte boundary, and so does the
 // super-block plane
 static void packed_sizes(int type, int64_t rows, int cols, size_t* code, size_t* scales, size_t* sup) {
+  type = dev_type(type);
   const size_t groups = (size_t)((rows + kRG - 1) / kRG);
   const int ntk = (cols / 32 + kTB - 1) / kTB;
   const int nu = (ntk + kUT - 1) / kUT;
   const int kqb = code_bytes_of(type);
   *code = ((groups * ntk * kWave * kqb) + 255) & ~(size_t)255;
-  *scales = groups * nu * kWave * kUT * 2;
+  // 16-bit entries, 32-bit for Q4_1 / Q5_1 / Q8_1, none for F16 / F32
+  *scales = is_float(type) ? 0 : groups * nu * kWave * kUT * (is_wide(type) ? 4 : 2);
   *sup = 0;
   if (is_kq(type)) {
     *scales = (*scales + 255) & ~(size_t)255;
@@ -819,14 +988,21 @@ hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t s) {
   if (a.att_o && ((epi != EPI_ADD && epi != EPI_STORE) || !a.att_ml || !a.dpos || a.att_ns < 1 || a.att_ns > kMergeSplits ||
                   a.att_group < 1 || a.head_dim < 32 || a.head_dim % 32 || a.cols % a.head_dim))
     return hipErrorInvalidValue;
-  if (a.type == 2) return launch_q<2>(epi, a, s);
-  if (a.type == 8) return launch_q<8>(epi, a, s);
-  if (a.type == kQ4K) return launch_q<kQ4K>(epi, a, s);
-  if (a.type == kQ2K) return launch_q<kQ2K>(epi, a, s);
-  if (a.type == kQ3K) return launch_q<kQ3K>(epi, a, s);
-  if (a.type == kQ5K) return launch_q<kQ5K>(epi, a, s);
-  if (a.type == kQ6K) return launch_q<kQ6K>(epi, a, s);
-  return hipErrorInvalidValue;
+  switch (dev_type(a.type)) {
+    case 2: return launch_q<2>(epi, a, s);
+    case 8: return launch_q<8>(epi, a, s);
+    case kQ4K: return launch_q<kQ4K>(epi, a, s);
+    case kQ2K: return launch_q<kQ2K>(epi, a, s);
+    case kQ3K: return launch_q<kQ3K>(epi, a, s);
+    case kQ5K: return launch_q<kQ5K>(epi, a, s);
+    case kQ6K: return launch_q<kQ6K>(epi, a, s);
+    case kQ4_1: return launch_q<kQ4_1>(epi, a, s);
+    case kQ5_1: return launch_q<kQ5_1>(epi, a, s);
+    case kQ8_1: return launch_q<kQ8_1>(epi, a, s);
+    case kF16: return launch_q<kF16>(epi, a, s);
+    case kF32: return launch_q<kF32>(epi, a, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_argmax_merge(const float2* part, int n, const float* y, int* out_idx, int* tokens,
@@ -859,67 +1035,60 @@ hipError_t launch_pack(int type, const uint8_t* src, PackedMat dst, int64_t nblo
   else if (type == kQ6K && dst.su && nb % 8 == 0)
     hipLaunchKernelGGL(k_pack_kq<kQ6K>, dim3((unsigned)grid), dim3(256), 0, s, src, qs, ds,
                        const_cast<uint32_t*>(dst.su), nblocks, nb, row_off);
+  else if (type == kQ4_1)
+    hipLaunchKernelGGL(k_pack_more<kQ4_1>, dim3((unsigned)grid), dim3(256), 0, s, src, qs, ds, nblocks, nb, row_off);
+  else if (type == kQ5_0)
+    hipLaunchKernelGGL(k_pack_more<kQ5_0>, dim3((unsigned)grid), dim3(256), 0, s, src, qs, ds, nblocks, nb, row_off);
+  else if (type == kQ5_1)
+    hipLaunchKernelGGL(k_pack_more<kQ5_1>, dim3((unsigned)grid), dim3(256), 0, s, src, qs, ds, nblocks, nb, row_off);
+  else if (type == kQ8_1)
+    hipLaunchKernelGGL(k_pack_more<kQ8_1>, dim3((unsigned)grid), dim3(256), 0, s, src, qs, ds, nblocks, nb, row_off);
+  else if (type == kF16)
+    hipLaunchKernelGGL(k_pack_more<kF16>, dim3((unsigned)grid), dim3(256), 0, s, src, qs, ds, nblocks, nb, row_off);
+  else if (type == kF32)
+    hipLaunchKernelGGL(k_pack_more<kF32>, dim3((unsigned)grid), dim3(256), 0, s, src, qs, ds, nblocks, nb, row_off);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
+}
+
+template <int QT>
+static hipError_t embed_t(const PackedMat& t, int cols, const int* tokens, const int* dpos, int token, float* out,
+                          const float* nw, uint32_t* xr, float scale, int n, hipStream_t s) {
+  hipLaunchKernelGGL(k_embed<QT>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, token, out, nw,
+                     xr, scale);
+  return hipGetLastError();
+}
+
+static hipError_t embed_any(int type, const PackedMat& t, int cols, const int* tokens, const int* dpos, int token,
+                            float* out, const float* nw, uint32_t* xr, float scale, int n, hipStream_t s) {
+  switch (dev_type(type)) {
+    case 2: return embed_t<2>(t, cols, tokens, dpos, token, out, nw, xr, scale, n, s);
+    case 8: return embed_t<8>(t, cols, tokens, dpos, token, out, nw, xr, scale, n, s);
+    case kQ4K: return embed_t<kQ4K>(t, cols, tokens, dpos, token, out, nw, xr, scale, n, s);
+    case kQ2K: return embed_t<kQ2K>(t, cols, tokens, dpos, token, out, nw, xr, scale, n, s);
+    case kQ3K: return embed_t<kQ3K>(t, cols, tokens, dpos, token, out, nw, xr, scale, n, s);
+    case kQ5K: return embed_t<kQ5K>(t, cols, tokens, dpos, token, out, nw, xr, scale, n, s);
+    case kQ6K: return embed_t<kQ6K>(t, cols, tokens, dpos, token, out, nw, xr, scale, n, s);
+    case kQ4_1: return embed_t<kQ4_1>(t, cols, tokens, dpos, token, out, nw, xr, scale, n, s);
+    case kQ5_1: return embed_t<kQ5_1>(t, cols, tokens, dpos, token, out, nw, xr, scale, n, s);
+    case kQ8_1: return embed_t<kQ8_1>(t, cols, tokens, dpos, token, out, nw, xr, scale, n, s);
+    case kF16: return embed_t<kF16>(t, cols, tokens, dpos, token, out, nw, xr, scale, n, s);
+    case kF32: return embed_t<kF32>(t, cols, tokens, dpos, token, out, nw, xr, scale, n, s);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t launch_embed(int type, PackedMat t, int cols, const int* tokens, const int* dpos,
                         int token, float* out, const float* nw, uint32_t* xr, float scale, hipStream_t s) {
   if (xr && !nw) return hipErrorInvalidValue;
-  if (type == 2)
-    hipLaunchKernelGGL(k_embed<2>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out, nw,
-                       xr, scale);
-  else if (type == 8)
-    hipLaunchKernelGGL(k_embed<8>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out, nw,
-                       xr, scale);
-  else if (type == kQ4K)
-    hipLaunchKernelGGL(k_embed<kQ4K>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out,
-                       nw, xr, scale);
-  else if (type == kQ2K)
-    hipLaunchKernelGGL(k_embed<kQ2K>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out,
-                       nw, xr, scale);
-  else if (type == kQ3K)
-    hipLaunchKernelGGL(k_embed<kQ3K>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out,
-                       nw, xr, scale);
-  else if (type == kQ5K)
-    hipLaunchKernelGGL(k_embed<kQ5K>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out,
-                       nw, xr, scale);
-  else if (type == kQ6K)
-    hipLaunchKernelGGL(k_embed<kQ6K>, dim3((cols + 255) / 256), dim3(256), 0, s, t, cols, tokens, dpos, token, out,
-                       nw, xr, scale);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  return embed_any(type, t, cols, tokens, dpos, token, out, nw, xr, scale, 1, s);
 }
 
 hipError_t launch_embed_rows(int type, PackedMat t, int cols, const int* tokens, const int* dpos, int n,
                              float* out, float scale, hipStream_t s) {
   if (n <= 0 || !tokens || !dpos) return hipErrorInvalidValue;
-  if (type == 2)
-    hipLaunchKernelGGL(k_embed<2>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
-                       nullptr, nullptr, scale);
-  else if (type == 8)
-    hipLaunchKernelGGL(k_embed<8>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
-                       nullptr, nullptr, scale);
-  else if (type == kQ4K)
-    hipLaunchKernelGGL(k_embed<kQ4K>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
-                       nullptr, nullptr, scale);
-  else if (type == kQ2K)
-    hipLaunchKernelGGL(k_embed<kQ2K>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
-                       nullptr, nullptr, scale);
-  else if (type == kQ3K)
-    hipLaunchKernelGGL(k_embed<kQ3K>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
-                       nullptr, nullptr, scale);
-  else if (type == kQ5K)
-    hipLaunchKernelGGL(k_embed<kQ5K>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
-                       nullptr, nullptr, scale);
-  else if (type == kQ6K)
-    hipLaunchKernelGGL(k_embed<kQ6K>, dim3((cols + 255) / 256, n), dim3(256), 0, s, t, cols, tokens, dpos, 0, out,
-                       nullptr, nullptr, scale);
-  else
-    return hipErrorInvalidValue;
-  return hipGetLastError();
+  return embed_any(type, t, cols, tokens, dpos, 0, out, nullptr, nullptr, scale, n, s);
 }
 
 }  // namespace ssk

@@ -55,8 +55,14 @@ size_t align256(size_t n) { return (n + 255) & ~(size_t)255; }
 // GGUF bytes of a row of cols weights (gguf_loader.c:22-62 block sizes)
 size_t gguf_row_bytes(int type, int64_t cols) {
   switch (type) {
+    case SS_HIP_F32: return (size_t)cols * 4;
+    case SS_HIP_F16: return (size_t)cols * 2;
     case SS_HIP_Q4_0: return (size_t)cols / 32 * 18;
+    case SS_HIP_Q4_1: return (size_t)cols / 32 * 20;
+    case SS_HIP_Q5_0: return (size_t)cols / 32 * 22;
+    case SS_HIP_Q5_1: return (size_t)cols / 32 * 24;
     case SS_HIP_Q8_0: return (size_t)cols / 32 * 34;
+    case SS_HIP_Q8_1: return (size_t)cols / 32 * 40;
     case SS_HIP_Q2_K: return (size_t)cols / 256 * 84;
     case SS_HIP_Q3_K: return (size_t)cols / 256 * 110;
     case SS_HIP_Q4_K: return (size_t)cols / 256 * 144;
@@ -66,7 +72,11 @@ size_t gguf_row_bytes(int type, int64_t cols) {
   }
 }
 
-bool quant_type_ok(int type) { return type == SS_HIP_Q4_0 || type == SS_HIP_Q8_0 || ssk::is_kq(type); }
+// every matrix type of the reference's dequantiser (quantize.c:389-442)
+bool quant_type_ok(int type) { return gguf_row_bytes(type, 256) > 0; }
+// the prompt products take Q4_0 and Q8_0 device formats (Q5_0 is stored as Q8_0)
+bool product_type(int type) { return ssk::dev_type(type) == SS_HIP_Q4_0 || ssk::dev_type(type) == SS_HIP_Q8_0; }
+constexpr const char* kTypesSupported = "F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1 and Q2_K..Q6_K";
 // columns a row of this type must be a multiple of (whole blocks, or super-blocks)
 int col_unit(int type) { return ssk::is_kq(type) ? 256 : 32; }
 
@@ -351,7 +361,7 @@ int32_t ss_hip_pack_matrix(ss_hip_ctx_t* c, void* dst, const void* src, int32_t 
 
 // ============================================================== single ops
 static int32_t check_mv(int32_t rows, int32_t cols, int32_t type) {
-  if (!quant_type_ok(type)) return fail(kErrParams, "matvec: type %d is not Q4_0/Q8_0/Q2_K..Q6_K", type);
+  if (!quant_type_ok(type)) return fail(kErrParams, "matvec: type %d is not one of %s", type, kTypesSupported);
   if (rows <= 0 || cols <= 0 || cols % col_unit(type))
     return fail(kErrParams, "matvec: bad shape %dx%d (cols must be a multiple of %d)", rows, cols, col_unit(type));
   return 0;
@@ -737,7 +747,9 @@ struct ss_hip_model {
   int t_embd = 0;
   void* out = nullptr;   // == embd when tied
   int t_out = 0;
-  bool any_kq = false;    // some matrix is a K-quant: prompts run token by token
+  // some layer matrix has no prompt-product kernel (a type other than Q4_0,
+  // Q8_0 and Q5_0, which is stored as Q8_0): prompts run token by token
+  bool no_products = false;
   // Gemma and the optional branches (layer_scheduler.c:446-448, 474-481,
   // 529-531, 553-560, 597-602, 667-676); the (1 + w) norms are uploaded as 1 + w
   bool gemma = false;
@@ -746,8 +758,9 @@ struct ss_hip_model {
   float attn_softcap = 0.f, final_softcap = 0.f;
   bool any_post = false;     // some layer has a post norm
   float* post_y = nullptr;   // [d]: a projection's output before its post norm
-  // prompts run token by token (the prompt products have none of: K-quants,
-  // the Gemma branches, post norms, softcaps, head_dim 256)
+  // prompts run token by token (the prompt products have none of: matrix
+  // types other than Q4_0 / Q8_0 / Q5_0, the Gemma branches, post norms,
+  // softcaps, head_dim 256)
   bool token_only = false;
   float* out_norm = nullptr;
   // KV cache: [L][KVH][max_seq][hd] (+ [L][max_seq] scales for int8)
@@ -889,7 +902,7 @@ int32_t upload_mat(ss_hip_model* m, void** dst, const ss_hip_tensor_t* parts, in
     total += parts[i].rows;
   }
   if (!quant_type_ok(type))
-    return fail(kErrParams, "model: %s has type %d; Q4_0, Q8_0 and Q2_K..Q6_K are supported", what, type);
+    return fail(kErrParams, "model: %s has type %d; %s are supported", what, type, kTypesSupported);
   if (total != rows_expect_total) return fail(kErrParams, "model: %s has %lld rows, %d expected", what, (long long)total, rows_expect_total);
   if (cols % col_unit(type))
     return fail(kErrParams, "model: %s columns %d not a multiple of %d", what, cols, col_unit(type));
@@ -1404,7 +1417,7 @@ ssk::GemmArgs gemm_args(ss_hip_model* m, const void* w, int type, int rows, int 
   a.rows = rows;
   a.cols = cols;
   a.T = T;
-  a.type = type;
+  a.type = ssk::dev_type(type);
   return a;
 }
 
@@ -1556,8 +1569,8 @@ int32_t stream_setup(ss_hip_model* m, const ss_hip_model_desc_t* d) {
     size_t o = 0;
     for (int i = 0; i < 5; i++) {
       if (!quant_type_ok(types[i]))
-        return fail(kErrParams, "model: blk.%d matrix %d has type %d; Q4_0, Q8_0 and Q2_K..Q6_K are supported", l,
-                    i, types[i]);
+        return fail(kErrParams, "model: blk.%d matrix %d has type %d; %s are supported", l,
+                    i, types[i], kTypesSupported);
       m->layer_off[(size_t)l * 5 + i] = o;
       o += align256(ss_hip_packed_bytes(types[i], rows[i], cols[i]));
     }
@@ -1677,9 +1690,12 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
   };
 
   // weights
-  m->any_kq = ssk::is_kq(d->token_embd.type) || (d->output.data && ssk::is_kq(d->output.type));
-  for (int i = 0; i < m->L * SS_HIP_LAYER_TENSORS; i++)
-    if (d->layers[i].data && ssk::is_kq(d->layers[i].type)) m->any_kq = true;
+  for (int i = 0; i < m->L * SS_HIP_LAYER_TENSORS; i++) {
+    const int slot = i % SS_HIP_LAYER_TENSORS;
+    if (slot != SS_HIP_ATTN_NORM && slot != SS_HIP_FFN_NORM && d->layers[i].data &&
+        !product_type(d->layers[i].type))
+      m->no_products = true;
+  }
   m->gemma = d->gemma != 0;
   m->emb_scale = m->gemma ? sqrtf((float)m->d) : 1.f;                       // layer_scheduler.c:597-602
   m->logit_scale = m->gemma ? 1.0f / sqrtf((float)m->d) : 1.f;              // :667-672
@@ -1689,7 +1705,7 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
     for (int i = 0; i < 2 * m->L; i++)
       if (d->post_norms[i].data) m->any_post = true;
   // (and head_dim 256: the prompt attention kernel covers 64 and 128)
-  m->token_only = m->any_kq || m->gemma || m->any_post || m->attn_softcap > 0.f || m->final_softcap > 0.f ||
+  m->token_only = m->no_products || m->gemma || m->any_post || m->attn_softcap > 0.f || m->final_softcap > 0.f ||
                   m->hd > 128;
   const float norm_add = m->gemma ? 1.f : 0.f;   // (1 + w) norms, tensor.c:133-152
   if (!d->token_embd.data || d->token_embd.cols != m->d || d->token_embd.rows < m->vocab) {

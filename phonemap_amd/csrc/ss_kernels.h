@@ -16,17 +16,32 @@ enum Epi : int {
   EPI_LOGITS = 4,  // y[r] = W x, plus one first-max argmax candidate per workgroup in part[]
 };
 
-// ggml types of the K-quants (256-weight super-blocks)
+// ggml types: the K-quants (256-weight super-blocks), the other 32-weight
+// block types and the float matrices
 constexpr int kQ2K = 10, kQ3K = 11, kQ4K = 12, kQ5K = 13, kQ6K = 14;
+constexpr int kF32 = 0, kF16 = 1, kQ4_1 = 3, kQ5_0 = 6, kQ5_1 = 7, kQ8_1 = 9;
 __host__ __device__ constexpr bool is_kq(int t) { return t >= kQ2K && t <= kQ6K; }
-// device code width of a 32-weight block: nibbles (Q4_0 and the 2-, 3- and
-// 4-bit K-quants) or int8 codes (Q8_0, Q5_K, Q6_K)
+__host__ __device__ constexpr bool is_float(int t) { return t == kF32 || t == kF16; }
+// a 32-bit scale entry per block: the (d, m) binary16 pair of Q4_1 / Q5_1,
+// or Q8_1's fp32 d
+__host__ __device__ constexpr bool is_wide(int t) { return t == kQ4_1 || t == kQ5_1 || t == kQ8_1; }
+// The device format a GGUF type is packed into: Q5_0 blocks ((q - 16) * d,
+// quantize.c:93-112) become Q8_0 blocks with code q - 16 and the same d, an
+// exact restatement; every other type keeps its own format.
+__host__ __device__ constexpr int dev_type(int t) { return t == kQ5_0 ? 8 : t; }
+// device code bytes of a 32-weight block: nibbles (Q4_0, Q4_1 and the 2-, 3-
+// and 4-bit K-quants), int8 codes (Q8_0, Q5_1, Q8_1, Q5_K, Q6_K), or the
+// weights themselves (F16, F32)
 __host__ __device__ constexpr int code_bytes_of(int t) {
-  return t == 2 || t == kQ2K || t == kQ3K || t == kQ4K ? 16 : t == 8 || t == kQ5K || t == kQ6K ? 32 : 0;
+  return t == 2 || t == kQ4_1 || t == kQ2K || t == kQ3K || t == kQ4K         ? 16
+         : t == 8 || t == kQ5_1 || t == kQ8_1 || t == kQ5K || t == kQ6K ? 32
+         : t == kF16                                                      ? 64
+         : t == kF32                                                      ? 128
+                                                                          : 0;
 }
 
-// A packed Q4_0/Q8_0/Q4_K matrix on the device: code plane, scale plane
-// and, for Q4_K, a super-block plane (see ss_gemv.hip).
+// A packed matrix on the device: code plane, scale plane (none for F16 and
+// F32) and, for the K-quants, a super-block plane (see ss_gemv.hip).
 struct PackedMat {
   const uint8_t* qs;
   const uint16_t* ds;

@@ -5,7 +5,7 @@
  * ss_dequant_matvec and only counts that it ran. Test infrastructure.
  *
  * usage: plug_snippet W.bin x.bin y.bin rows cols type
- * W.bin holds GGUF blocks, x.bin cols fp32 values; y.bin receives rows fp32
+ * W.bin holds GGUF blocks (or F32 rows), x.bin cols fp32 values; y.bin receives rows fp32
  * values (two dispatches of the same matrix: the second reuses the upload).
  * Prints "fallbacks N".
  */
@@ -17,6 +17,7 @@
 
 #include "ss_hip.h"
 
+#define GGML_TYPE_F32 0
 #define GGML_TYPE_Q4_0 2
 #define GGML_TYPE_Q8_0 8
 #define GGML_TYPE_Q4_K 12
@@ -33,7 +34,7 @@ static void cpu_dequant_matvec(float *out, int32_t rows) {
 static void matmul_dispatch(sched_t *sched, float *out, const void *mat, const float *vec, int32_t rows,
                             int32_t cols, int32_t type) {
     if (sched->hip_ctx && ss_hip_should_use_gpu(rows, cols) &&
-        (type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0 || type == GGML_TYPE_Q4_K)) {
+        (type == GGML_TYPE_Q4_0 || type == GGML_TYPE_Q8_0 || type == GGML_TYPE_Q4_K || type == GGML_TYPE_F32)) {
         /* true (nonzero) = out holds the result, as gpu_success for Metal */
         bool gpu_success = ss_hip_matvec_host(sched->hip_ctx, out, mat, vec, rows, cols, type) != 0;
         if (gpu_success) return;         /* else fall through to the CPU path */

@@ -11,7 +11,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.util import Q4_0, Q4_K, Q8_0, make_blocks, rel_err
+from tests.util import F32, Q4_0, Q4_K, Q8_0, make_blocks, rel_err
 
 pytestmark = pytest.mark.gpu
 EXE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c", "plug_snippet")
@@ -28,7 +28,7 @@ def _run(tmp_path, w, x, rows, cols, qtype):
 
 
 @pytest.mark.parametrize("qtype,rows,cols", [(Q4_0, 512, 4096), (Q8_0, 1000, 2048), (Q4_0, 33, 96),
-                                             (Q4_K, 700, 4096), (Q4_K, 33, 256)])
+                                             (Q4_K, 700, 4096), (Q4_K, 33, 256), (F32, 300, 1024)])
 def test_plug_snippet_matches_oracle(tmp_path, qtype, rows, cols):
     rng = np.random.default_rng(rows + cols)
     w = make_blocks(qtype, rows, cols, rng)
