@@ -18,6 +18,15 @@
 // su[(g * nsb + sb) * 16 + row % 16], nsb = cols / 256. 18.5 bytes per 32
 // weights against the GGUF format's 18.
 //
+// The other 32-weight block types use the same tiles. Q4_1 (d * q + m)
+// stores its nibbles as Q4_0 does, Q5_1 its 5-bit codes as int8 and Q8_1
+// its int8 codes, each with a 32-bit scale-plane entry per block (d | m << 16
+// as binary16, or Q8_1's fp32 d; a lane's 8 tiles in 32 contiguous bytes).
+// Q5_0 ((q - 16) * d) is packed into the Q8_0 format. F16 and F32 matrices
+// store each block's 32 weights (64 or 128 bytes per lane chunk) and have no
+// scale plane; their dot products take x as fp32 values decoded from the
+// staged records.
+//
 // k_gemv: workgroup = one 16-row group; wave s takes units (UT consecutive
 // tiles) s, s+S, ... of it. A wave requests its x slice, then every chunk and
 // scale of its unit, before using any; it encodes its own slice of x into its
