@@ -383,6 +383,7 @@ __device__ __forceinline__ float q4k_dot(const uint4 q, const uint32_t* ra, cons
 //   Q2_K (quantize.c:180-215)  e = scale byte of each group (scale | min << 4)
 //   Q3_K (:219-263)            e = the groups' 6-bit scales; A = d (s - 32)
 //   Q5_K (:312-346)            e = scale | min << 8, one pair for the block
+//   Q4_K (:265-310)            as Q5_K (the prompt products; the matvec uses q4k_dot)
 //   Q6_K (:350-383)            e = the groups' int8 scales
 template <int QT>
 __device__ __forceinline__ void kq_affine(uint32_t e, uint32_t sup, float (&A)[2], float (&B)[2]) {
@@ -396,7 +397,7 @@ __device__ __forceinline__ void kq_affine(uint32_t e, uint32_t sup, float (&A)[2
     } else if constexpr (QT == 11) {
       A[g] = d * (float)((int)b - 32);
       B[g] = 4.0f * A[g];
-    } else if constexpr (QT == 13) {
+    } else if constexpr (QT == 13 || QT == 12) {   // Q5_K, Q4_K: one pair for the block
       A[g] = d * (float)(e & 0xffu);
       B[g] = dm * (float)(e >> 8);
     } else {

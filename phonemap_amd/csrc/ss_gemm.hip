@@ -15,9 +15,11 @@
 // and B[l/16][l%16] and receives D[4*(l/16) + i][l%16], i = 0..3.
 //
 // The fast path (k_gemm_h, with a split-x scratch) runs the same products on
-// v_mfma_f32_16x16x32_f16: the codes are exact fp16 integers, x is split into
-// two fp16 parts, and d scales each block's fp32 result (see below): eight
-// times the fp32 MFMA rate per product, with x kept to 2^-22.
+// v_mfma_f32_16x16x32_f16 for every block format (Q4_0, Q8_0, Q4_1, Q5_1,
+// Q8_1, the K-quants; Q5_0 as Q8_0): the codes are exact fp16 integers, x is
+// split into two fp16 parts, and each block's (or 16-weight group's) fp32
+// result is scaled by its A, with B times the sum of x subtracted (see
+// below): eight times the fp32 MFMA rate per product, with x kept to 2^-22.
 
 #include <hip/hip_runtime.h>
 #include <math.h>
@@ -241,6 +243,8 @@ constexpr int kHChunks = 16;              // 16-byte chunks of one token's 128 c
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef __attribute__((address_space(1))) void* gbl_ptr_t;
 
+constexpr v8h kOnes = {1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16, 1.0f16};
+
 template <int QT>
 __host__ __device__ constexpr int slot_col(int s) {   // column within the block of slot s (s < 32)
   return QT == 2 ? 4 * (s >> 3) + 2 * (s & 1) + ((s >> 2) & 1) + 16 * ((s >> 1) & 1)
@@ -312,13 +316,33 @@ __global__ void __launch_bounds__(256) k_split_x(const float* __restrict__ x, in
   }
 }
 
-// A lane's 8 codes of one block as exact fp16 values in slot order (Q4_0:
-// w0 = 32-bit word kq of the block; Q8_0: w0, w1 = words 2kq, 2kq+1).
+// The weight formats of the products. Every 32-weight block is
+// sum_g (A_g * sum c x - B_g * sum x) over its two 16-weight groups g, c
+// being the stored code (an exact fp16 integer) and A, B exact fp32:
+//   Q4_0, Q8_0: A = d, B = 0 (Q4_0 codes are nibble - 8)
+//   Q4_1, Q5_1: A = d, B = -m (nibbles; 5-bit codes as int8)
+//   Q8_1:       A = fp32 d, B = 0
+//   K-quants:   kq_affine (Q4_K and Q5_K one (A, B) pair per block; Q2_K,
+//               Q3_K and Q6_K one per 16-weight group)
+// kLay: the code layout, and so the slot order of the split x (2: nibbles
+// as Q4_0's, 8: int8 codes as Q8_0's).
+template <int QT>
+struct PQ {
+  static constexpr int kLay = code_bytes_of(QT) == 16 ? 2 : 8;
+  static constexpr bool kGroups = QT == kQ2K || QT == kQ3K || QT == kQ6K;
+  static constexpr bool kMin =
+      QT == kQ4_1 || QT == kQ5_1 || QT == kQ2K || QT == kQ3K || QT == kQ4K || QT == kQ5K;
+  static constexpr float kNibOff = QT == 2 ? -1032.0f : -1024.0f;   // 0x6400 | u is 1024 + u
+};
+
+// A lane's 8 codes of one block as exact fp16 values in slot order (nibble
+// layout: w0 = 32-bit word kq of the block; int8 layout: w0, w1 = words 2kq,
+// 2kq+1).
 template <int QT>
 __device__ __forceinline__ v8h codes_f16(uint32_t w0, uint32_t w1) {
   v4u r;
-  if constexpr (QT == 2) {
-    const h2 off = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  if constexpr (PQ<QT>::kLay == 2) {
+    const h2 off = {(_Float16)PQ<QT>::kNibOff, (_Float16)PQ<QT>::kNibOff};
 #pragma unroll
     for (int k = 0; k < 4; ++k)
       r[k] = __builtin_bit_cast(uint32_t,
@@ -332,6 +356,44 @@ __device__ __forceinline__ v8h codes_f16(uint32_t w0, uint32_t w1) {
     r[3] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(h2, ((u1 >> 8) & 0x00FF00FFu) | 0x64006400u) + off);
   }
   return __builtin_bit_cast(v8h, r);
+}
+
+// (A_g, B_g) of a block from its scale entry e (16 bits, or 32 for Q4_1 /
+// Q5_1 / Q8_1) and, for the K-quants, its super-block word sup.
+template <int QT>
+__device__ __forceinline__ void block_affine(uint32_t e, uint32_t sup, float (&A)[2], float (&B)[2]) {
+  if constexpr (QT == 2 || QT == 8) {
+    A[0] = A[1] = h2f((uint16_t)e);
+    B[0] = B[1] = 0.f;
+  } else if constexpr (QT == kQ4_1 || QT == kQ5_1) {
+    A[0] = A[1] = h2f((uint16_t)(e & 0xffffu));
+    B[0] = B[1] = -h2f((uint16_t)(e >> 16));
+  } else if constexpr (QT == kQ8_1) {
+    A[0] = A[1] = __uint_as_float(e);
+    B[0] = B[1] = 0.f;
+  } else {
+    kq_affine<QT>(e, sup, A, B);
+  }
+}
+
+// The slots of 16-weight group g among a lane's 8 (slot order above): nibble
+// layout, slots 2, 3, 6, 7 are the block's weights 16..31 (pairs 1 and 3 of
+// the four fp16 pairs); int8 layout, lane groups kq 2 and 3 hold them.
+template <int QT>
+__device__ __forceinline__ v8h group_part(v8h v, int g, int kq) {
+  if constexpr (PQ<QT>::kLay == 2) {
+    v4u r = __builtin_bit_cast(v4u, v);
+    if (g == 0) {
+      r[1] = 0u;
+      r[3] = 0u;
+    } else {
+      r[0] = 0u;
+      r[2] = 0u;
+    }
+    return __builtin_bit_cast(v8h, r);
+  } else {
+    return (kq >= 2) == (g == 1) ? v : v8h{};
+  }
 }
 
 // Workgroup: 4 waves x kHRG row groups of 16 rows x 64 tokens. Per packed tile
@@ -351,7 +413,7 @@ __global__ void __launch_bounds__(kHWaves * 64, 2) k_gemm_h(const GemmArgs a, in
   const int ntk = (nb + kTB - 1) / kTB;
   const int t0 = blockIdx.y * kHTok;
   const int n = lane & 15, kq = lane >> 4;
-  constexpr int kQW = QT == 2 ? 1 : 2;   // code words per lane per block
+  constexpr int kQW = PQ<QT>::kLay == 2 ? 1 : 2;   // code words per lane per block
   const uint16_t* xlo = a.xs + (size_t)a.T * ldxs;
   const float* xinv = reinterpret_cast<const float*>(a.xs + 2 * (size_t)a.T * ldxs);
 
@@ -367,27 +429,33 @@ __global__ void __launch_bounds__(kHWaves * 64, 2) k_gemm_h(const GemmArgs a, in
       __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)&xs[buf][part][4 * (R & 15)][0], 16, 0, 0);
     }
   };
+  // per block: codes, the raw scale entry; per tile: the K-quants' super-block word
   uint32_t wq[NMAT][kHRG][kTB][kQW];
-  float wd[NMAT][kHRG][kTB];
-  auto load_w = [&](int tk, uint32_t (&q)[NMAT][kHRG][kTB][kQW], float (&d)[NMAT][kHRG][kTB]) {
+  uint32_t we[NMAT][kHRG][kTB];
+  uint32_t wsu[NMAT][kHRG];
+  auto load_w = [&](int tk, uint32_t (&q)[NMAT][kHRG][kTB][kQW], uint32_t (&e)[NMAT][kHRG][kTB],
+                    uint32_t (&su)[NMAT][kHRG]) {
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
       for (int r = 0; r < kHRG; ++r) {
-        const uint8_t* qs = mt == 0 ? a.w.qs : a.w2.qs;
-        const uint16_t* ds = mt == 0 ? a.w.ds : a.w2.ds;
+        const PackedMat& w = mt == 0 ? a.w : a.w2;
         const int g = min(g0 + r, ngroups - 1);
 #pragma unroll
         for (int b = 0; b < kTB; ++b) {
           const int tl = tile_lane(n, b);
           const uint32_t* p =
-              reinterpret_cast<const uint32_t*>(qs + tile_idx(g, ntk, tk, tl) * QTraits<QT>::kQB) + kQW * kq;
+              reinterpret_cast<const uint32_t*>(w.qs + tile_idx(g, ntk, tk, tl) * QTraits<QT>::kQB) + kQW * kq;
 #pragma unroll
           for (int k = 0; k < kQW; ++k) q[mt][r][b][k] = p[k];
-          // blocks past the row (the last tile's padding) are read and weighted 0
-          const float dv = h2f(ds[scale_idx(g, ntk, tk, tl)]);
-          d[mt][r][b] = tk * kTB + b < nb ? dv : 0.f;
+          // blocks past the row (the last tile's padding of a 32-weight type)
+          // are read and weighted 0 (entry 0: A = B = 0)
+          const uint32_t ev = is_wide(QT) ? reinterpret_cast<const uint32_t*>(w.ds)[scale_idx(g, ntk, tk, tl)]
+                                          : (uint32_t)w.ds[scale_idx(g, ntk, tk, tl)];
+          e[mt][r][b] = tk * kTB + b < nb ? ev : 0u;
         }
+        // K-quants: the 4 blocks of a tile lie in super-block tk / 2 (nb is a multiple of 8)
+        su[mt][r] = is_kq(QT) ? w.su[((size_t)g * (ntk / 2) + tk / 2) * kRG + n] : 0u;
       }
   };
 
@@ -400,7 +468,7 @@ __global__ void __launch_bounds__(kHWaves * 64, 2) k_gemm_h(const GemmArgs a, in
       for (int tt = 0; tt < kHTiles; ++tt) acc[mt][r][tt] = v4f{0.f, 0.f, 0.f, 0.f};
 
   stage_x(0, 0);
-  load_w(0, wq, wd);
+  load_w(0, wq, we, wsu);
   vm_drain();
   __syncthreads();
 #pragma unroll 1
@@ -410,43 +478,69 @@ __global__ void __launch_bounds__(kHWaves * 64, 2) k_gemm_h(const GemmArgs a, in
     // the idle buffer: branch-free, read by no one)
     const int tn = min(tk + 1, ntk - 1);
     uint32_t nq[NMAT][kHRG][kTB][kQW];
-    float nd[NMAT][kHRG][kTB];
+    uint32_t ne[NMAT][kHRG][kTB];
+    uint32_t nsu[NMAT][kHRG];
     stage_x(tn, buf ^ 1);
-    load_w(tn, nq, nd);
+    load_w(tn, nq, ne, nsu);
 #pragma unroll
     for (int b = 0; b < kTB; ++b) {
-      v8h wc[NMAT][kHRG];
+      constexpr int NG = PQ<QT>::kGroups ? 2 : 1;   // codes split by 16-weight group
+      v8h wc[NMAT][kHRG][NG];
+      float A[NMAT][kHRG][2], B[NMAT][kHRG][2];
 #pragma unroll
       for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-        for (int r = 0; r < kHRG; ++r) wc[mt][r] = codes_f16<QT>(wq[mt][r][b][0], wq[mt][r][b][kQW - 1]);
+        for (int r = 0; r < kHRG; ++r) {
+          const v8h c = codes_f16<QT>(wq[mt][r][b][0], wq[mt][r][b][kQW - 1]);
+#pragma unroll
+          for (int gg = 0; gg < NG; ++gg) wc[mt][r][gg] = NG == 1 ? c : group_part<QT>(c, gg, kq);
+          block_affine<QT>(we[mt][r][b], wsu[mt][r], A[mt][r], B[mt][r]);
+        }
 #pragma unroll
       for (int tt = 0; tt < kHTiles; ++tt) {
         const v8h xh = __builtin_bit_cast(v8h, xs[buf][0][tt * 16 + n][(4 * b + kq) ^ n]);
         const v8h xl = __builtin_bit_cast(v8h, xs[buf][1][tt * 16 + n][(4 * b + kq) ^ n]);
+        v4f sx[NG];   // sum of x over the block (or group), for the B terms
+        if constexpr (PQ<QT>::kMin) {
+#pragma unroll
+          for (int gg = 0; gg < NG; ++gg) {
+            const v8h one = NG == 1 ? kOnes : group_part<QT>(kOnes, gg, kq);
+            sx[gg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, one, v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            sx[gg] = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, one, sx[gg], 0, 0, 0);
+          }
+        }
 #pragma unroll
         for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-          for (int r = 0; r < kHRG; ++r) {
-            v4f c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, wc[mt][r], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, wc[mt][r], c, 0, 0, 0);
-            const float d = wd[mt][r][b];
+          for (int r = 0; r < kHRG; ++r)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[mt][r][tt][i] = fmaf(d, c[i], acc[mt][r][tt][i]);
-          }
+            for (int gg = 0; gg < NG; ++gg) {
+              v4f c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xh, wc[mt][r][gg], v4f{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+              c = __builtin_amdgcn_mfma_f32_16x16x32_f16(xl, wc[mt][r][gg], c, 0, 0, 0);
+              const float ag = A[mt][r][gg];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) acc[mt][r][tt][i] = fmaf(ag, c[i], acc[mt][r][tt][i]);
+              if constexpr (PQ<QT>::kMin) {
+                const float bg = -B[mt][r][gg];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[mt][r][tt][i] = fmaf(bg, sx[gg][i], acc[mt][r][tt][i]);
+              }
+            }
       }
       __builtin_amdgcn_sched_barrier(0);   // one block's operands live at a time
     }
 #pragma unroll
     for (int mt = 0; mt < NMAT; ++mt)
 #pragma unroll
-      for (int r = 0; r < kHRG; ++r)
+      for (int r = 0; r < kHRG; ++r) {
 #pragma unroll
         for (int b = 0; b < kTB; ++b) {
 #pragma unroll
           for (int k = 0; k < kQW; ++k) wq[mt][r][b][k] = nq[mt][r][b][k];
-          wd[mt][r][b] = nd[mt][r][b];
+          we[mt][r][b] = ne[mt][r][b];
         }
+        wsu[mt][r] = nsu[mt][r];
+      }
     vm_drain();   // this wave's direct LDS loads of the next tile have landed
     __syncthreads();
   }
@@ -554,25 +648,38 @@ hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t s) {
       (a.nw && !a.ssq))
     return hipErrorInvalidValue;
   if (epi != EPI_STORE && epi != EPI_ADD && epi != EPI_SWIGLU) return hipErrorInvalidValue;
-  if (a.xs && (a.type == 2 || a.type == 8)) {
+  const int t = dev_type(a.type);
+  if (a.xs && product_format(t)) {
+    if (is_kq(t) && a.cols % 256) return hipErrorInvalidValue;   // whole super-blocks
     const int ldxs = (a.cols + 127) / 128 * 128;
     uint16_t* xl = a.xs + (size_t)a.T * ldxs;
     float* xinv = reinterpret_cast<float*>(a.xs + 2 * (size_t)a.T * ldxs);
     float* ssq = a.nw ? a.ssq : nullptr;
-    if (a.type == 2)
+    if (code_bytes_of(t) == 16)   // nibble layouts: Q4_0's slot order
       hipLaunchKernelGGL(k_split_x<2>, dim3(a.T), dim3(256), 0, s, a.x, a.ldx, a.nw, a.cols, ssq, a.xs, xl, xinv, ldxs);
     else
       hipLaunchKernelGGL(k_split_x<8>, dim3(a.T), dim3(256), 0, s, a.x, a.ldx, a.nw, a.cols, ssq, a.xs, xl, xinv, ldxs);
     if (hipError_t e = hipGetLastError()) return e;
     const int n_cu = device_cus();
-    return a.type == 2 ? launch_gemm_h<2>(epi, a, ldxs, n_cu, s) : launch_gemm_h<8>(epi, a, ldxs, n_cu, s);
+    switch (t) {
+      case 2: return launch_gemm_h<2>(epi, a, ldxs, n_cu, s);
+      case 8: return launch_gemm_h<8>(epi, a, ldxs, n_cu, s);
+      case kQ4_1: return launch_gemm_h<kQ4_1>(epi, a, ldxs, n_cu, s);
+      case kQ5_1: return launch_gemm_h<kQ5_1>(epi, a, ldxs, n_cu, s);
+      case kQ8_1: return launch_gemm_h<kQ8_1>(epi, a, ldxs, n_cu, s);
+      case kQ2K: return launch_gemm_h<kQ2K>(epi, a, ldxs, n_cu, s);
+      case kQ3K: return launch_gemm_h<kQ3K>(epi, a, ldxs, n_cu, s);
+      case kQ4K: return launch_gemm_h<kQ4K>(epi, a, ldxs, n_cu, s);
+      case kQ5K: return launch_gemm_h<kQ5K>(epi, a, ldxs, n_cu, s);
+      default: return launch_gemm_h<kQ6K>(epi, a, ldxs, n_cu, s);
+    }
   }
   if (a.nw) {
     hipLaunchKernelGGL(k_sumsq, dim3(a.T), dim3(256), 0, s, a.x, a.ldx, a.cols, a.ssq);
     if (hipError_t e = hipGetLastError()) return e;
   }
-  if (a.type == 2) return launch_gemm_q<2>(epi, a, s);
-  if (a.type == 8) return launch_gemm_q<8>(epi, a, s);
+  if (t == 2) return launch_gemm_q<2>(epi, a, s);
+  if (t == 8) return launch_gemm_q<8>(epi, a, s);
   return hipErrorInvalidValue;
 }
 

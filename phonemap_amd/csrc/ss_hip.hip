@@ -74,8 +74,8 @@ size_t gguf_row_bytes(int type, int64_t cols) {
 
 // every matrix type of the reference's dequantiser (quantize.c:389-442)
 bool quant_type_ok(int type) { return gguf_row_bytes(type, 256) > 0; }
-// the prompt products take Q4_0 and Q8_0 device formats (Q5_0 is stored as Q8_0)
-bool product_type(int type) { return ssk::dev_type(type) == SS_HIP_Q4_0 || ssk::dev_type(type) == SS_HIP_Q8_0; }
+// the prompt products take every block format (Q5_0 is stored as Q8_0), not F16 / F32
+bool product_type(int type) { return ssk::product_format(ssk::dev_type(type)); }
 constexpr const char* kTypesSupported = "F32, F16, Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q8_1 and Q2_K..Q6_K";
 // columns a row of this type must be a multiple of (whole blocks, or super-blocks)
 int col_unit(int type) { return ssk::is_kq(type) ? 256 : 32; }
@@ -389,9 +389,9 @@ int32_t ss_hip_matvec(ss_hip_ctx_t* c, float* y, const void* w, const float* x, 
 
 int32_t ss_hip_gemm(ss_hip_ctx_t* c, float* y, const void* w, const float* x, const float* nw, float eps,
                     int32_t accumulate, int32_t rows, int32_t cols, int32_t n_tokens, int32_t type, void* stream) {
-  // the MFMA products take Q4_0 and Q8_0 (K-quant prompts run token by token)
-  if (!c || !y || !w || !x || rows <= 0 || cols <= 0 || cols % 32 || n_tokens <= 0 ||
-      (type != SS_HIP_Q4_0 && type != SS_HIP_Q8_0))
+  // the MFMA products take every block type (F16 / F32 prompts run token by token)
+  if (!c || !y || !w || !x || rows <= 0 || cols <= 0 || cols % col_unit(type) || n_tokens <= 0 ||
+      !quant_type_ok(type) || !product_type(type))
     return fail(kErrParams, "gemm: bad argument (rows %d cols %d tokens %d type %d)", rows, cols, n_tokens, type);
   if (set_device(c)) return kErrBackend;
   int32_t rc = ensure(c, (void**)&c->g_ssq, &c->g_ssq_bytes, sizeof(float) * n_tokens, false);
@@ -747,8 +747,8 @@ struct ss_hip_model {
   int t_embd = 0;
   void* out = nullptr;   // == embd when tied
   int t_out = 0;
-  // some layer matrix has no prompt-product kernel (a type other than Q4_0,
-  // Q8_0 and Q5_0, which is stored as Q8_0): prompts run token by token
+  // some layer matrix has no prompt-product kernel (F16 or F32): prompts run
+  // token by token
   bool no_products = false;
   // Gemma and the optional branches (layer_scheduler.c:446-448, 474-481,
   // 529-531, 553-560, 597-602, 667-676); the (1 + w) norms are uploaded as 1 + w
@@ -758,9 +758,8 @@ struct ss_hip_model {
   float attn_softcap = 0.f, final_softcap = 0.f;
   bool any_post = false;     // some layer has a post norm
   float* post_y = nullptr;   // [d]: a projection's output before its post norm
-  // prompts run token by token (the prompt products have none of: matrix
-  // types other than Q4_0 / Q8_0 / Q5_0, the Gemma branches, post norms,
-  // softcaps, head_dim 256)
+  // prompts run token by token (the prompt products have none of: F16 / F32
+  // layer matrices, the Gemma branches, post norms, softcaps, head_dim 256)
   bool token_only = false;
   float* out_norm = nullptr;
   // KV cache: [L][KVH][max_seq][hd] (+ [L][max_seq] scales for int8)

@@ -29,6 +29,10 @@ __host__ __device__ constexpr bool is_wide(int t) { return t == kQ4_1 || t == kQ
 // quantize.c:93-112) become Q8_0 blocks with code q - 16 and the same d, an
 // exact restatement; every other type keeps its own format.
 __host__ __device__ constexpr int dev_type(int t) { return t == kQ5_0 ? 8 : t; }
+// device formats the fp16-MFMA prompt products take (all but F16 / F32)
+__host__ __device__ constexpr bool product_format(int t) {
+  return t == 2 || t == 8 || t == kQ4_1 || t == kQ5_1 || t == kQ8_1 || is_kq(t);
+}
 // device code bytes of a 32-weight block: nibbles (Q4_0, Q4_1 and the 2-, 3-
 // and 4-bit K-quants), int8 codes (Q8_0, Q5_1, Q8_1, Q5_K, Q6_K), or the
 // weights themselves (F16, F32)

@@ -12,8 +12,9 @@ against the CPU oracle, through the C-ABI and the public API.
   tokens equal to the oracle's and logits within 1e-3 (fp16 cache; 5e-2
   int8) at every step, or, at a step where the oracle's own fp16 cache
   rounds a value across a binary16 midpoint the other way than fp64 does,
-  within 1e-3 of the fp64 model of tests/ref_model.py. Prompts run token by
-  token; streaming equals resident bit for bit.
+  within 1e-3 of the fp64 model of tests/ref_model.py. The 10-token prompts
+  run as fp16-MFMA products (fp16 cache) or token by token (int8 cache);
+  streaming equals resident bit for bit.
 """
 import ctypes as C
 

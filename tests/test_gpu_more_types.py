@@ -10,9 +10,9 @@ public API.
   greedy tokens equal to the oracle's and logits within 1e-3 (fp16 cache;
   5e-2 int8) at every step, or, at a step where the oracle's own fp16 cache
   rounds a value across a binary16 midpoint the other way than fp64 does,
-  within 1e-3 of the fp64 model of tests/ref_model.py. Q5_0 layers (stored
-  in the Q8_0 format) take the prompt products; the other types run prompts
-  token by token. Streaming equals resident bit for bit.
+  within 1e-3 of the fp64 model of tests/ref_model.py. Block types take the
+  prompt products (Q5_0 as Q8_0-format products); F16 / F32 layers run
+  prompts token by token. Streaming equals resident bit for bit.
 """
 import ctypes as C
 
