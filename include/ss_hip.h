@@ -168,7 +168,7 @@ int32_t ss_hip_attention(ss_hip_ctx_t *ctx, float *out_dev, const float *q_dev,
  * pos0+n_tokens-1 already hold the tokens' own K and V. The per-token
  * attention of layer_scheduler.c:415-468 for every token of a layer-major
  * prompt (ss_scheduler_prefill, layer_scheduler.c:681-803) in one launch;
- * head_dim 64 or 128. */
+ * head_dim 64, 128 or 256. */
 int32_t ss_hip_attention_rows(ss_hip_ctx_t *ctx, float *out_dev, const float *q_dev,
                               const void *k_cache, const void *v_cache, int32_t n_heads,
                               int32_t n_kv_heads, int32_t head_dim, int32_t max_seq, int32_t pos0,

@@ -41,6 +41,14 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// The FFN activations of layer_scheduler.c:529-547: SiLU (g / (1 + e^-g))
+// and the tanh form of GELU for Gemma's GeGLU (tensor.c:181-190).
+__device__ __forceinline__ float silu(float g) { return g / (1.0f + expf(-g)); }
+__device__ __forceinline__ float gelu_tanh(float g) {
+  const float inner = 0.7978845608028654f * (g + 0.044715f * (g * g * g));
+  return 0.5f * g * (1.0f + tanhf(inner));
+}
+
 __device__ __forceinline__ float h2f(uint16_t h) {
   return (float)__builtin_bit_cast(_Float16, h);
 }

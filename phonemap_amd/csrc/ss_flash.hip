@@ -47,7 +47,8 @@ typedef __attribute__((address_space(1))) void* gbl_ptr_t;
 
 constexpr int kFWaves = 4;               // waves per workgroup, 16 query rows each
 constexpr int kFRows = 16 * kFWaves;     // query rows per workgroup
-constexpr int kFKeys = 64;               // keys per block
+// keys per block: 64, or 32 at head_dim 256 (the K and V^T tiles stay 64 KB)
+__host__ __device__ constexpr int flash_keys(int hd) { return hd == 256 ? 32 : 64; }
 constexpr float kPScale = 4096.0f;       // P is split as P * 2^12
 
 // K row slot swizzle: the 16 keys of one S^T operand read (8(r/4) + 4t + r%4)
@@ -84,13 +85,17 @@ __global__ void __launch_bounds__(kFWaves * 64) k_flash_rows(const AttnArgs a) {
   constexpr int NC = HD / 32;            // 32-wide slices of the head dimension
   constexpr int NDT = HD / 16;           // 16-dim tiles of O^T
   constexpr int kTQ = kFRows / G;        // tokens per workgroup
-  constexpr int kVItems = 16 * CH;       // (4-key group, chunk) staging items of V
-  static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
+  constexpr int kFKeys = flash_keys(HD);  // keys per block
+  constexpr int NS = kFKeys / 32;         // 32-key halves per block
+  constexpr int kVC = kFKeys / 8;         // 8-key chunks per V^T row
+  constexpr int kKG = kFKeys / 4;         // 4-key groups per block
+  constexpr int kVItems = kKG * CH;       // (4-key group, chunk) staging items of V
+  static_assert(HD == 64 || HD == 128 || HD == 256, "head_dim 64, 128 or 256");
   static_assert(kFKeys * CH % (kFWaves * 64) == 0, "K staging rounds");
   static_assert(kVItems <= kFWaves * 64, "V staging items");
 
   __shared__ v4u ks[2][kFKeys * CH];     // K rows, swizzled slots
-  __shared__ v4u vt[2][HD * (kFKeys / 8)];   // V^T rows of 64 keys, swizzled slots
+  __shared__ v4u vt[2][HD * kVC];        // V^T rows of the block's keys, swizzled slots
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, kq = lane >> 4;
@@ -157,7 +162,7 @@ __global__ void __launch_bounds__(kFWaves * 64) k_flash_rows(const AttnArgs a) {
     }
   };
   // V block: thread (kg, c) loads dims 8c..8c+7 of keys 4kg..4kg+3
-  const int vkg = tid % 16, vch = tid / 16;
+  const int vkg = tid % kKG, vch = tid / kKG;
   uint4 vr[4];
   auto load_v = [&](int blk) {
     if (tid < kVItems) {
@@ -178,8 +183,8 @@ __global__ void __launch_bounds__(kFWaves * 64) k_flash_rows(const AttnArgs a) {
           const uint32_t word = j < 2 ? vr[u].x : j < 4 ? vr[u].y : j < 6 ? vr[u].z : vr[u].w;
           w[u] = (j & 1) ? word >> 16 : word & 0xffffu;
         }
-        uint8_t* row = reinterpret_cast<uint8_t*>(&vt[buf][(8 * vch + j) * (kFKeys / 8)]);
-        *reinterpret_cast<uint2*>(row + 16 * ((vkg >> 1) ^ j) + 8 * (vkg & 1)) =
+        uint8_t* row = reinterpret_cast<uint8_t*>(&vt[buf][(8 * vch + j) * kVC]);
+        *reinterpret_cast<uint2*>(row + 16 * ((vkg >> 1) ^ (j & (kVC - 1))) + 8 * (vkg & 1)) =
             make_uint2(w[0] | (w[1] << 16), w[2] | (w[3] << 16));
       }
     }
@@ -206,9 +211,9 @@ __global__ void __launch_bounds__(kFWaves * 64) k_flash_rows(const AttnArgs a) {
     const int kb = blk * kFKeys;
     if (kb <= wlim) {
       // S^T tiles (s, t): keys kb + 32s + 8(n/4) + 4t + n%4 against the wave's 16 rows
-      v4f st[2][2];
+      v4f st[NS][2];
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
+      for (int s = 0; s < NS; ++s)
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
           const int key = 32 * s + 8 * (n >> 2) + 4 * t + (n & 3);
@@ -222,10 +227,10 @@ __global__ void __launch_bounds__(kFWaves * 64) k_flash_rows(const AttnArgs a) {
           st[s][t] = acc;
         }
       // lane (n, kq): element i of tile (s, t) is key kb + 32s + 8kq + 4t + i of row n
-      float sc[2][2][4];
+      float sc[NS][2][4];
       float bmax = -INFINITY;
 #pragma unroll
-      for (int s = 0; s < 2; ++s)
+      for (int s = 0; s < NS; ++s)
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
@@ -243,9 +248,9 @@ __global__ void __launch_bounds__(kFWaves * 64) k_flash_rows(const AttnArgs a) {
       l *= corr;
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) o[dt] *= corr;
-      v8h ph[2], pl[2];
+      v8h ph[NS], pl[NS];
 #pragma unroll
-      for (int s = 0; s < 2; ++s) {
+      for (int s = 0; s < NS; ++s) {
         float pv[8];
 #pragma unroll
         for (int t = 0; t < 2; ++t)
@@ -258,13 +263,13 @@ __global__ void __launch_bounds__(kFWaves * 64) k_flash_rows(const AttnArgs a) {
         split8(pv, ph[s], pl[s]);
       }
       m = mn;
-      // O^T += V^T P^T over the block's two 32-key halves
+      // O^T += V^T P^T over the block's 32-key halves
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int s = 0; s < 2; ++s) {
+        for (int s = 0; s < NS; ++s) {
           const int d = 16 * dt + n;
-          const v8h vv = __builtin_bit_cast(v8h, vt[buf][d * (kFKeys / 8) + ((4 * s + kq) ^ (d & 7))]);
+          const v8h vv = __builtin_bit_cast(v8h, vt[buf][d * kVC + ((4 * s + kq) ^ (d & (kVC - 1)))]);
           o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, ph[s], o[dt], 0, 0, 0);
           o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, pl[s], o[dt], 0, 0, 0);
         }
@@ -308,6 +313,7 @@ hipError_t launch_attention_rows(int head_dim, int group, const AttnArgs& a, hip
     return hipErrorInvalidValue;
   if (head_dim == 64) return launch_flash_hd<64>(group, a, s);
   if (head_dim == 128) return launch_flash_hd<128>(group, a, s);
+  if (head_dim == 256) return launch_flash_hd<256>(group, a, s);   // Gemma
   return hipErrorInvalidValue;
 }
 

@@ -98,7 +98,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmArgs& a, int t, int r0, 
     const float x0 = g[i] * scale;
     if constexpr (EPI == EPI_SWIGLU) {
       const float up = u[i] * scale;
-      v[i] = up * (x0 / (1.0f + expf(-x0)));   // layer_scheduler.c:540-547
+      v[i] = up * (a.act == 1 ? gelu_tanh(x0) : silu(x0));   // layer_scheduler.c:529-547
     } else {
       v[i] = x0;
     }
@@ -570,7 +570,7 @@ __global__ void __launch_bounds__(kHWaves * 64, 2) k_gemm_h(const GemmArgs a, in
         float v;
         if constexpr (EPI == EPI_SWIGLU) {
           const float up = acc[NMAT - 1][r][tt][i] * scale;
-          v = up * (x0 / (1.0f + expf(-x0)));   // layer_scheduler.c:540-547
+          v = up * (a.act == 1 ? gelu_tanh(x0) : silu(x0));   // layer_scheduler.c:529-547
         } else {
           v = x0;
         }

@@ -407,13 +407,8 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int row, bool own, c
     float out;
     if constexpr (EPI == EPI_SWIGLU) {
       const float g = v[0], u = v[NMAT - 1];
-      if (a.act == 1) {   // GeGLU (layer_scheduler.c:529-531): up * GELU(gate), tensor.c:181-190
-        const float cube = g * g * g;
-        const float inner = 0.7978845608028654f * (g + 0.044715f * cube);
-        out = u * (0.5f * g * (1.0f + tanhf(inner)));
-      } else {
-        out = u * (g / (1.0f + expf(-g)));                             // layer_scheduler.c:540-547
-      }
+      // GeGLU for Gemma (layer_scheduler.c:529-531), else SwiGLU (:540-547)
+      out = u * (a.act == 1 ? gelu_tanh(g) : silu(g));
     } else {
       out = EPI == EPI_ADD ? v[0] + pre.y : v[0];                       // layer_scheduler.c:484,566
     }

@@ -565,7 +565,7 @@ int32_t ss_hip_attention_rows(ss_hip_ctx_t* c, float* out, const float* q, const
     return fail(kErrParams, "attention_rows: bad argument (pos0 %d, %d tokens, max_seq %d)", pos0, n_tokens,
                 max_seq);
   const int group = n_heads / n_kv_heads;
-  if ((head_dim != 64 && head_dim != 128) || !ssk::attention_supported(head_dim, group))
+  if (!ssk::attention_supported(head_dim, group))
     return fail(kErrParams, "attention_rows: head_dim %d / group %d not supported", head_dim, group);
   if (set_device(c)) return kErrBackend;
   ssk::AttnArgs a;
@@ -758,8 +758,8 @@ struct ss_hip_model {
   float attn_softcap = 0.f, final_softcap = 0.f;
   bool any_post = false;     // some layer has a post norm
   float* post_y = nullptr;   // [d]: a projection's output before its post norm
-  // prompts run token by token (the prompt products have none of: F16 / F32
-  // layer matrices, the Gemma branches, post norms, softcaps, head_dim 256)
+  // prompts run token by token (the prompt products take no F16 / F32 layer
+  // matrices)
   bool token_only = false;
   float* out_norm = nullptr;
   // KV cache: [L][KVH][max_seq][hd] (+ [L][max_seq] scales for int8)
@@ -822,6 +822,7 @@ struct ss_hip_model {
   int pf_min = 0;                    // shortest prompt evaluated this way (0: the default)
   int pf_cap = 0;                    // chunk capacity (0: not set up)
   float *pf_h = nullptr, *pf_qkv = nullptr, *pf_att = nullptr, *pf_f = nullptr, *pf_ssq = nullptr;
+  float* pf_y = nullptr;   // [chunk][d]: projections before their post norm (Gemma 2)
   uint16_t* pf_xs = nullptr;         // x of a product split into fp16 parts
   float* emb = nullptr;              // [2d + 64]: pooled sum, embedding, a sum of squares
 };
@@ -1396,6 +1397,8 @@ int32_t prefill_setup(ss_hip_model* m) {
   if (int32_t rc = m_alloc(m, (void**)&m->pf_att, sizeof(float) * c * m->qdim, false)) return rc;
   if (int32_t rc = m_alloc(m, (void**)&m->pf_f, sizeof(float) * c * m->ffn, false)) return rc;
   if (int32_t rc = m_alloc(m, (void**)&m->pf_ssq, sizeof(float) * c, false)) return rc;
+  if (m->any_post)
+    if (int32_t rc = m_alloc(m, (void**)&m->pf_y, sizeof(float) * c * m->d, false)) return rc;
   const int widest = std::max(std::max(m->d, m->qdim), m->ffn);
   if (int32_t rc = m_alloc(m, (void**)&m->pf_xs, 2 * ssk::gemm_split_elems(cap, widest), false)) return rc;
   m->pf_cap = cap;
@@ -1457,22 +1460,35 @@ int32_t enqueue_layer_rows(ss_hip_model* m, int l, const DevLayer& ly, int T, in
   at.part_o = m->att_o;
   at.part_ml = m->att_ml;
   at.n_tok = T;
+  at.softcap = m->attn_softcap;   // (:446-448)
+  at.softcap_inv = m->attn_softcap > 0.f ? 1.0f / m->attn_softcap : 0.f;
   HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_attention_rows(m->hd, m->group, at, s); }));
 
-  // 3. hidden += Wo attn                                         (:470-484)
-  ssk::GemmArgs o = gemm_args(m, ly.wo, ly.t_o, m->d, m->qdim, m->pf_att, m->pf_h, T);
-  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_gemm(ssk::EPI_ADD, o, s); }));
+  // 3. hidden += Wo attn, through the post-attention norm when the layer
+  //    has one (:470-484)
+  ssk::GemmArgs o = gemm_args(m, ly.wo, ly.t_o, m->d, m->qdim, m->pf_att, ly.post_attn ? m->pf_y : m->pf_h, T);
+  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_gemm(ly.post_attn ? ssk::EPI_STORE : ssk::EPI_ADD, o, s); }));
+  if (ly.post_attn)
+    HIP_TRY(timed(m, PC_OTHER, 0, [&] {
+      return ssk::launch_post_norm_rows(m->pf_h, m->pf_y, ly.post_attn, m->d, T, m->eps, s);
+    }));
 
   // 4. rmsnorm(ffn_norm) -> gate, up -> silu(gate) * up           (:486-550)
   ssk::GemmArgs gu = gemm_args(m, ly.wg, ly.t_gu, m->ffn, m->d, m->pf_h, m->pf_f, T);
   gu.w2 = view(ly.wu, ly.t_gu, m->ffn, m->d);
   gu.nw = ly.ffn_norm;
   gu.eps = m->eps;
+  gu.act = m->gemma ? 1 : 0;   // GeGLU for Gemma (:529-531)
   HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_gemm(ssk::EPI_SWIGLU, gu, s); }));
 
-  // 5. hidden += Wdown act                                       (:552-566)
-  ssk::GemmArgs dn = gemm_args(m, ly.wd, ly.t_d, m->d, m->ffn, m->pf_f, m->pf_h, T);
-  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_gemm(ssk::EPI_ADD, dn, s); }));
+  // 5. hidden += Wdown act, through the post-FFN norm when the layer has
+  //    one (:552-566)
+  ssk::GemmArgs dn = gemm_args(m, ly.wd, ly.t_d, m->d, m->ffn, m->pf_f, ly.post_ffn ? m->pf_y : m->pf_h, T);
+  HIP_TRY(timed(m, PC_OTHER, 0, [&] { return ssk::launch_gemm(ly.post_ffn ? ssk::EPI_STORE : ssk::EPI_ADD, dn, s); }));
+  if (ly.post_ffn)
+    HIP_TRY(timed(m, PC_OTHER, 0, [&] {
+      return ssk::launch_post_norm_rows(m->pf_h, m->pf_y, ly.post_ffn, m->d, T, m->eps, s);
+    }));
   return 0;
 }
 
@@ -1704,8 +1720,7 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
     for (int i = 0; i < 2 * m->L; i++)
       if (d->post_norms[i].data) m->any_post = true;
   // (and head_dim 256: the prompt attention kernel covers 64 and 128)
-  m->token_only = m->no_products || m->gemma || m->any_post || m->attn_softcap > 0.f || m->final_softcap > 0.f ||
-                  m->hd > 128;
+  m->token_only = m->no_products;
   const float norm_add = m->gemma ? 1.f : 0.f;   // (1 + w) norms, tensor.c:133-152
   if (!d->token_embd.data || d->token_embd.cols != m->d || d->token_embd.rows < m->vocab) {
     fail(kErrParams, "model: token_embd must be [>= vocab x hidden]");

@@ -104,6 +104,7 @@ struct GemmArgs {
                              // two fp16 parts and a scale per token (fp16 products), or
                              // nullptr (fp32 products)
   int ldx, ldy, rows, cols, T, type;
+  int act;                   // EPI_SWIGLU: 0 SiLU, 1 GELU (Gemma's GeGLU)
 };
 // 16-bit words of GemmArgs::xs for T tokens of cols columns
 inline size_t gemm_split_elems(int T, int cols) {
@@ -162,7 +163,7 @@ hipError_t launch_argmax_merge(const float2* part, int n, const float* y, int* o
 hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, hipStream_t s);
 // Causal attention of a.n_tok prompt rows (token z: query a.q + z*a.tok_q,
 // positions 0..a.dpos[z] (or a.pos0 + z), output a.out + z*a.tok_o), fp16
-// cache, head_dim 64 or 128, on MFMA (ss_flash.hip).
+// cache, head_dim 64, 128 or 256, on MFMA (ss_flash.hip).
 hipError_t launch_attention_rows(int head_dim, int group, const AttnArgs& a, hipStream_t s);
 // ssq[t] = sum of x[t][c]^2 (x [T][cols])
 hipError_t launch_sumsq(const float* x, int cols, int T, float* ssq, hipStream_t s);
@@ -191,6 +192,9 @@ hipError_t launch_embed_rows(int type, PackedMat t, int cols, const int* tokens,
 // hidden * nw_out (nw_out may be nullptr). One workgroup; n a multiple of 16.
 hipError_t launch_post_norm(float* hidden, const float* y, const float* w, int n, float eps, uint32_t* xr,
                             const float* nw_out, hipStream_t s);
+// hidden[t] += rmsnorm(y[t]) * w for the T rows of a prompt (row stride n)
+hipError_t launch_post_norm_rows(float* hidden, const float* y, const float* w, int n, int T, float eps,
+                                 hipStream_t s);
 hipError_t launch_rmsnorm(float* out, const float* x, const float* w, int n, float eps,
                           hipStream_t s);
 hipError_t launch_rope(float* q, float* k, int n_heads, int n_kv_heads, int head_dim,

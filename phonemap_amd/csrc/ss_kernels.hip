@@ -696,6 +696,28 @@ __global__ void __launch_bounds__(1024) k_post_norm(float* hidden, const float* 
   }
 }
 
+// The same for the rows of a prompt: workgroup t adds the normalised row t
+// of y (n values, row stride n) to row t of hidden.
+__global__ void __launch_bounds__(1024) k_post_norm_rows(float* hidden, const float* y, const float* w, int n,
+                                                         float eps) {
+  __shared__ float red[16];
+  const int tid = threadIdx.x;
+  hidden += (size_t)blockIdx.x * n;
+  y += (size_t)blockIdx.x * n;
+  float ss = 0.f;
+  for (int i = tid; i < n; i += 1024) {
+    const float v = y[i];
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  if ((tid & 63) == 0) red[tid >> 6] = ss;
+  __syncthreads();
+  float t = 0.f;
+  for (int k = 0; k < 16; ++k) t += red[k];
+  const float sc = 1.0f / sqrtf(t / (float)n + eps);
+  for (int i = tid; i < n; i += 1024) hidden[i] = hidden[i] + y[i] * sc * w[i];
+}
+
 __global__ void k_swiglu(float* out, const float* g, const float* u, int n) {
   for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) {
     const float gv = g[i];
@@ -884,6 +906,13 @@ hipError_t launch_post_norm(float* hidden, const float* y, const float* w, int n
                             const float* nw_out, hipStream_t s) {
   if (n <= 0 || n % 16 || !hidden || !y || !w) return hipErrorInvalidValue;
   hipLaunchKernelGGL(k_post_norm, dim3(1), dim3(1024), 0, s, hidden, y, w, n, eps, xr, nw_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_post_norm_rows(float* hidden, const float* y, const float* w, int n, int T, float eps,
+                                 hipStream_t s) {
+  if (n <= 0 || T <= 0 || !hidden || !y || !w) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(k_post_norm_rows, dim3(T), dim3(1024), 0, s, hidden, y, w, n, eps);
   return hipGetLastError();
 }
 

@@ -1,7 +1,8 @@
 """Causal attention of prompt rows on MFMA (ss_hip_attention_rows) against
 the CPU oracle: token t of a chunk starting at position pos0 attends to
 positions 0..pos0+t (layer_scheduler.c:415-468 per token of
-ss_scheduler_prefill, :681-803), for every token and head.
+ss_scheduler_prefill, :681-803), for every token and head; head_dim 64, 128
+and 256 (Gemma).
 
 Bar: max |gpu - oracle| / max |oracle| <= 1e-3 over all rows (the kernel
 keeps q and P to 2^-22 through two fp16 parts each; the oracle sums in fp32
@@ -56,6 +57,8 @@ def _run(hip, H, KVH, hd, pos0, n, max_seq, seed, qscale=1.0):
     (16, 2, 64, 100, 13, 128),     # group 8
     (8, 1, 128, 0, 1, 8),          # one token
     (4, 2, 128, 200, 129, 400),    # more rows than one workgroup holds
+    (8, 4, 256, 0, 70, 128),       # head_dim 256 (Gemma): 32-key blocks
+    (8, 1, 256, 30, 33, 96),       # head_dim 256, group 8
 ])
 def test_rows_match_oracle(hip, H, KVH, hd, pos0, n, max_seq):
     print("attention rows", H, KVH, hd, pos0, n, flush=True)
@@ -90,7 +93,7 @@ def test_rows_sharp_and_small_queries(hip):
 def test_rows_reject_bad_shapes(hip):
     Q = hip.buf(4 * 4 * 64)
     KC = hip.buf(2 * 4 * 64 * 8)
-    for H, KVH, hd, max_seq, pos0, n in [(4, 4, 256, 8, 0, 1),   # head_dim 256
+    for H, KVH, hd, max_seq, pos0, n in [(4, 4, 96, 8, 0, 1),    # head_dim 96
                                           (4, 4, 64, 8, 4, 5),    # past max_seq
                                           (6, 4, 64, 8, 0, 1),    # heads not a multiple
                                           (4, 4, 64, 8, 0, 0)]:   # no tokens

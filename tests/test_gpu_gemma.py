@@ -16,9 +16,11 @@ through the public API (ss_model_load_ex on synthetic GGUFs):
 Bar: greedy tokens equal to the oracle's at every step; logits within 1e-3
 (fp16 cache) or 5e-2 (int8) of the oracle's, or, at a step where the
 oracle's own fp16 cache rounds a value across a binary16 midpoint the other
-way than fp64 does, of the fp64 model of tests/ref_model.py. Prompts run
-token by token (the prompt products do not cover these branches); the
-persistent launch falls back to graph launches.
+way than fp64 does, of the fp64 model of tests/ref_model.py. With the fp16
+cache the 9-token prompts run as MFMA products (GeGLU epilogue, post norms
+over rows, softcapped flash attention at head_dim 64 and 256); the int8
+cache runs them token by token. The persistent launch falls back to graph
+launches.
 """
 import ctypes as C
 
@@ -164,3 +166,29 @@ def test_embed_matches_oracle(tmp_path, spec):
                               got.ctypes.data_as(C.POINTER(C.c_float))) == 0, L.ss_hip_last_error()
     assert abs(np.linalg.norm(got) - 1.0) < 1e-4
     assert rel_err(got, want) <= TOL
+
+
+@pytest.mark.parametrize("spec", ["gemma2_hd256_g4", "gemma2_softcap", "gemma_hd256_g8"])
+def test_long_prompt_as_products(tmp_path, spec):
+    """A 300-token prompt through the Gemma prompt products (fp16 cache),
+    against the oracle's token-serial prefill, then decode steps."""
+    path = _file(tmp_path, spec)
+    print("gemma long prompt", spec, flush=True)
+    prompt = np.random.default_rng(12).integers(3, SPECS[spec]["vocab"], 300).tolist()
+    om = oracle.Model(path, 400, "f16")
+    rm = RefModel(path, 400, "f16")
+    with api.Model(path, max_context=400) as m:
+        lg, am = m.eval_prompt(prompt, 0)
+        olg = om.prefill(prompt, 0)
+        ok, e = _close(lg, olg, rm.prefill(prompt, 0), TOL)
+        assert ok, e
+        assert am == oracle.argmax(olg)
+        tok, pos = am, len(prompt)
+        for _ in range(6):
+            lg, am = m.eval_token(tok, pos)
+            olg = om.forward(tok, pos)
+            ok, e = _close(lg, olg, rm.forward(tok, pos), TOL)
+            assert ok, (pos, e)
+            assert am == oracle.argmax(olg), pos
+            tok, pos = am, pos + 1
+    om.close()
