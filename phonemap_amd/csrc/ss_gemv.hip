@@ -38,6 +38,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 #include <hip/hip_ext.h>
 
 #include "ss_device.h"
@@ -121,7 +123,9 @@ __device__ __forceinline__ float xput(XSlice<UT>& p, int* xw, const float* nw, i
 // over the active attention splits s of KV head kvh. A lane fetches the
 // (m, l) and 4 o values of all kMergeSplits split slots for its group of 4
 // columns (slots past the active ones reload the last active split and get
-// weight 0) before the weight loads, in one batch.
+// weight 0) before the weight loads, in one batch (loads of the active
+// slots only, each under its condition, measured 50% slower; the weight
+// loads first, 2% slower). head_dim and the group size are powers of two.
 template <int UT>
 struct MSlice {
   float2 ml[UT / 2][kMergeSplits];
@@ -130,19 +134,20 @@ struct MSlice {
 
 __device__ __forceinline__ int merge_active(const GemvArgs& a) {
   int chunk, active;
-  attn_chunks(*a.dpos + 1, a.att_ns, chunk, active);
+  attn_chunks(*a.dpos + 1, a.att_ns, a.att_split_fill, chunk, active);
   return active;
 }
 
 template <int UT>
 __device__ __forceinline__ void mfetch(MSlice<UT>& p, const GemvArgs& a, int u, int active, int lane) {
   const int hd = a.head_dim, G = a.att_group;
+  const int hs = __builtin_ctz(hd), gs = __builtin_ctz(G);
 #pragma unroll
   for (int j = 0; j < UT / 2; ++j) {
     const int gi = j * kWave + lane;
     const int col = min(u * UT * kTB * 32 + (gi >> 3) * 32 + (gi & 7) * 4, a.cols - 4);
-    const int h = col / hd, d = col % hd;
-    const int kvh = h / G, g = h % G;
+    const int h = col >> hs, d = col & (hd - 1);
+    const int kvh = h >> gs, g = h & (G - 1);
 #pragma unroll
     for (int s = 0; s < kMergeSplits; ++s) {
       const size_t i = ((size_t)kvh * a.att_ns + min(s, active - 1)) * G + g;
@@ -496,31 +501,47 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
   if (wave == 0) pre = epi_prefetch<EPI>(a, g * kRG + lane % kRG);
 
   // units go to waves round robin (one round for rows of up to S units)
+  // REC: x from the records xr. A merging kernel takes them when the
+  // attention wrote its output there itself: one active split directly,
+  // more than kMergeSplits through its last split's merge. The choice is
+  // made once, outside the loop, so each loop keeps its own load schedule.
   const int active = MERGE ? merge_active(a) : 0;
-  for (int u = wave; u < nu; u += S) {
-    if constexpr (PX) {
-      // records first: vector memory operations complete in order
-      rfetch<UT>(xw, a.xr, u, lane);
-      load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
-      vm_drain();
-      if (a.nw && lane < UT * kTB * 2) ssq += __int_as_float(xw[lane * kRW + 14]);
-    } else if constexpr (MERGE) {
-      MSlice<UT> mp;
-      mfetch<UT>(mp, a, u, active, lane);
-      load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
-      mput<UT>(mp, xw, u, nb, active, lane);
-    } else {
-      XSlice<UT> xp;
-      xfetch<UT>(xp, a.x, a.nw, u, nb, lane);
-      load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
-      ssq += xput<UT>(xp, xw, a.nw, u, nb, lane);
+  auto rounds = [&](auto rec) {
+    for (int u = wave; u < nu; u += S) {
+      if constexpr (decltype(rec)::value) {
+        // records first: vector memory operations complete in order
+        rfetch<UT>(xw, a.xr, u, lane);
+        load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
+        vm_drain();
+        if (a.nw && lane < UT * kTB * 2) ssq += __int_as_float(xw[lane * kRW + 14]);
+      } else if constexpr (MERGE) {
+        MSlice<UT> mp;
+        mfetch<UT>(mp, a, u, active, lane);
+        load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
+        mput<UT>(mp, xw, u, nb, active, lane);
+      } else {
+        XSlice<UT> xp;
+        xfetch<UT>(xp, a.x, a.nw, u, nb, lane);
+        load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
+        ssq += xput<UT>(xp, xw, a.nw, u, nb, lane);
+      }
+      if constexpr (is_float(QT)) rec_to_float<UT>(xw, lane);
+      // the slice is written and read by this wave only: LDS operations of a
+      // wave complete in order, the fence keeps the compiler from reordering
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      fma_round<QT, NMAT, UT>(acc, rd, xw, kb);
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     }
-    if constexpr (is_float(QT)) rec_to_float<UT>(xw, lane);
-    // the slice is written and read by this wave only: LDS operations of a
-    // wave complete in order, the fence keeps the compiler from reordering
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-    fma_round<QT, NMAT, UT>(acc, rd, xw, kb);
-    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  };
+  if constexpr (PX) {
+    rounds(std::true_type{});
+  } else if constexpr (MERGE) {
+    if (a.xr && (active == 1 || active > kMergeSplits))
+      rounds(std::true_type{});
+    else
+      rounds(std::false_type{});
+  } else {
+    rounds(std::false_type{});
   }
 
   // lanes r, r+16, r+32, r+48 hold row r's four block columns
@@ -987,10 +1008,13 @@ PackedMat packed_view(const void* base, int type, int64_t rows, int cols) {
 }
 
 hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t s) {
-  if (a.att_o && a.xr) return hipErrorInvalidValue;
   if (a.xr_out && epi != EPI_STORE && epi != EPI_ADD && epi != EPI_SWIGLU) return hipErrorInvalidValue;
-  if (a.att_o && ((epi != EPI_ADD && epi != EPI_STORE) || !a.att_ml || !a.dpos || a.att_ns < 1 || a.att_ns > kMergeSplits ||
-                  a.att_group < 1 || a.head_dim < 32 || a.head_dim % 32 || a.cols % a.head_dim))
+  // merge staging: more than kMergeSplits splits only with the records of
+  // the attention's own merge (xr) to fall back on; power-of-two head_dim
+  // and group
+  if (a.att_o && ((epi != EPI_ADD && epi != EPI_STORE) || !a.att_ml || !a.dpos || a.att_ns < 1 ||
+                  (a.att_ns > kMergeSplits && !a.xr) || a.att_group < 1 || (a.att_group & (a.att_group - 1)) ||
+                  a.head_dim < 32 || (a.head_dim & (a.head_dim - 1)) || a.cols % a.head_dim))
     return hipErrorInvalidValue;
   switch (dev_type(a.type)) {
     case 2: return launch_q<2>(epi, a, s);

@@ -739,6 +739,13 @@ struct ss_hip_model {
   ss_hip_ctx* ctx = nullptr;
   int L = 0, d = 0, H = 0, KVH = 0, hd = 0, rope_dim = 0, ffn = 0, vocab = 0, max_seq = 0;
   int qdim = 0, kvdim = 0, group = 0, ns = 0, embd_rows = 0;
+  // decode attention, query groups of 1 or 2: while splits of one round of
+  // loads cover the context, at most kMergeSplits are active and the Wo
+  // matvec merges them; past that, with more than kMergeSplits splits
+  // allocated, the last split of each KV head merges them (decided per
+  // token from the active count)
+  int split_fill = 0;
+  bool wo_merge_dyn = false;
   float eps = 1e-5f, theta = 10000.f;
   int kv_type = 0;
   int launch = SS_HIP_LAUNCH_SWEEP;   // mode in effect
@@ -1162,27 +1169,32 @@ int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden,
   at.out = m->attn;
   at.part_o = m->att_o;
   at.part_ml = m->att_ml;
+  at.split_fill = m->split_fill;
   // with few splits the Wo matvec merges them while staging (measured
-  // faster than the last-arriver merge for up to kMergeSplits splits)
+  // faster than the last-arriver merge for up to kMergeSplits splits); with
+  // more, the last split of each KV head merges them and writes the output
+  // as x records for Wo, or (wo_merge_dyn) only when more than kMergeSplits
+  // are active at this token's context
   const bool fused = m->ns <= ssk::kMergeSplits;
+  const bool direct = m->group <= 2;   // one active split writes Wo's records itself
   at.cnt = fused ? nullptr : m->att_cnt;
-  at.xr_out = fused ? nullptr : m->xr_att;   // otherwise the last split of each KV head merges
-                                             // and writes the output as x records for Wo
+  at.xr_out = fused && !direct ? nullptr : m->xr_att;
+  at.wo_merge = m->wo_merge_dyn;
   HIP_TRY(timed(m, PC_ATTN, 0, [&] { return ssk::launch_attention(m->hd, m->group, m->kv_type, at, s); }));
 
   // 3. hidden += Wo attn                                         (:470-484)
   // (with a post norm: y = Wo attn, then hidden += y * (1 + w) / rms(y), :474-481)
   ssk::GemvArgs o = gemv_args(ly.wo, m->attn, ly.post_attn ? m->post_y : hidden, m->d, m->qdim, ly.t_o);
-  if (fused) {
+  if (fused || m->wo_merge_dyn) {
     o.att_o = m->att_o;
     o.att_ml = m->att_ml;
     o.att_ns = m->ns;
     o.att_group = m->group;
+    o.att_split_fill = m->split_fill;
     o.head_dim = m->hd;
     o.dpos = dp;
-  } else {
-    o.xr = m->xr_att;
   }
+  if (!fused || direct) o.xr = m->xr_att;
   if (ly.post_attn) {
     HIP_TRY(timed(m, q_class(ly.t_o), matvec_bytes(ly.t_o, m->d, m->qdim, 1),
                   [&] { return ssk::launch_gemv(ssk::EPI_STORE, o, s); }));
@@ -1698,6 +1710,10 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
   m->kvdim = m->KVH * m->hd;
   m->group = group;
   m->ns = attn_splits(m->hd, m->group, m->max_seq, m->kv_type, m->KVH, c->n_cu);
+  if (m->group <= 2) {
+    m->split_fill = ssk::attn_round_positions(m->hd, m->group);
+    m->wo_merge_dyn = m->ns > ssk::kMergeSplits;
+  }
 
   auto bail = [&](void) -> ss_hip_model_t* {
     model_release(m);

@@ -78,6 +78,10 @@ struct GemvArgs {
   const float* att_o;        // [kvh][ns][G][head_dim] partial outputs, or nullptr
   const float* att_ml;       // [kvh][ns][G][2] partial (max, sum)
   int att_ns, att_group;     // splits per KV head, query heads per KV head
+  int att_split_fill;        // the attention's split_fill
+  // With att_o and xr both set, the split count decides per token: at most
+  // kMergeSplits active splits are merged while staging, more were merged
+  // by the attention's last split into the records xr.
   // x records (ss_device.h): when xr is set, x is read from these records
   // (written by the producer of x, with the RMSNorm weight nw already
   // applied and the sums of squares in word 14) instead of from x; the
@@ -128,6 +132,9 @@ struct AttnArgs {
                              // split merges into out; nullptr: the splits stay in part_o/part_ml
                              // for a merging consumer (ns <= kMergeSplits)
   uint32_t* xr_out;          // with cnt set: also the output as x records (xrec_words(n_heads * hd))
+  int split_fill;            // attn_chunks' fill (0: none)
+  int wo_merge;              // with cnt set: when at most kMergeSplits splits are active, leave
+                             // them in part_o/part_ml for the Wo matvec (which then merges them)
   int n_tok;                 // prompt rows (launch_attention_rows): token z at position dpos[z]
   int pos0;                  // (or pos0 + z when dpos is null),
   int tok_q, tok_o;          // its query at q + z*tok_q, its output at out + z*tok_o

@@ -55,7 +55,7 @@ constexpr int kSc1 = 16;
 
 __device__ __forceinline__ void attn_split(const AttnArgs& a, int& ctx, int& chunk, int& active) {
   ctx = a.dpos ? *a.dpos + 1 : a.seq_len;
-  attn_chunks(ctx, a.ns, chunk, active);
+  attn_chunks(ctx, a.ns, a.split_fill, chunk, active);
 }
 
 // Sum over aligned groups of N (4, 8 or 16) lanes, result in every lane.
@@ -84,15 +84,17 @@ __device__ __forceinline__ void attn_store4(const AttnArgs& a, int q, float4 v) 
 }
 
 // The workgroup's W waves hold per-wave (m, l, o) for the G heads in LDS:
-// combine them, then either write the output (one active split), leave the
-// split's partials for a merging consumer (a.cnt null), or write them and let
-// the last split of this KV head to finish merge all of them.
+// combine them, then either write the output (one active split, with a.cnt
+// or a.xr_out set), leave the split's partials for a merging consumer (a.cnt
+// null, or a.wo_merge with at most kMergeSplits active splits), or write
+// them and let the last split of this KV head to finish merge all of them.
 template <int HD, int G, int W>
 __device__ __forceinline__ void attn_finish(const AttnArgs& a, int kvh, int active, const float (&wm)[W][G],
                                             const float (&wl)[W][G], const float (&wo)[W][G][HD], int tid) {
   const int lane = tid & 63, wave = tid >> 6;
   constexpr int kThreads = W * 64;
-  if (a.cnt && active == 1) {
+  const bool merge_here = a.cnt && !(a.wo_merge && active <= kMergeSplits);
+  if ((a.cnt || a.xr_out) && active == 1) {
     // the only split: the output directly (the merge below with one split),
     // four consecutive outputs per thread; quads of lanes hold the 16 values
     // of one x record (G * HD / 4 is a multiple of 8)
@@ -131,7 +133,7 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, int kvh, int acti
       so = fmaf(f, wo[w][g][d], so);
       sl = fmaf(f, wl[w][g], sl);
     }
-    if (a.cnt) {   // merged below by another workgroup: coherent stores
+    if (merge_here) {   // merged below by another workgroup: coherent stores
       cstf(po + g * HD + d, so);
       if (d == 0) {
         cstf(pml + g * 2, M);
@@ -145,7 +147,7 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, int kvh, int acti
       }
     }
   }
-  if (!a.cnt) return;   // the consumer (the Wo matvec) merges the splits
+  if (!merge_here) return;   // the consumer (the Wo matvec) merges the splits
 
   // The last split of this KV head to finish merges all of them:
   // out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M).

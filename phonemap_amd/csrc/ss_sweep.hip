@@ -400,7 +400,7 @@ __device__ __forceinline__ AttnItem attn_item(const SweepArgs& a, int pos) {
   const int i = blockIdx.x;
   if (i >= a.n_kv_heads * a.ns) return it;
   int chunk, active;
-  attn_chunks(pos + 1, a.ns, chunk, active);
+  attn_chunks(pos + 1, a.ns, 0, chunk, active);
   it.kvh = i / a.ns;
   it.sp = i % a.ns;
   it.active = active;

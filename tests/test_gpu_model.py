@@ -82,8 +82,9 @@ def test_greedy_and_logits(spec, kv, launch):
 
 @pytest.mark.parametrize("kv", ["f16", "int8"])
 def test_long_context_split_merge_path(kv):
-    """A context of 1024 gives 16 attention splits per KV head: more than the
-    Wo matvec merges itself, so the separate merge kernel runs."""
+    """A context of 1024 gives 16 attention splits per KV head (query groups
+    of 8): more than the Wo matvec merges itself, so the last split of each
+    KV head merges them."""
     path = _model_file("gqa8", **GQA8)
     rng = np.random.default_rng(9)
     prompt = rng.integers(3, GQA8["vocab"], 40).tolist()
@@ -100,6 +101,42 @@ def test_long_context_split_merge_path(kv):
             assert rel_err(lg, olg) <= tol, pos
             assert am == oracle.argmax(olg)
             tok, pos = am, pos + 1
+    om.close()
+
+
+# query groups of 1 or 2 at head_dim 128: 128 positions per attention split
+WIDE = dict(n_layers=2, hidden=512, n_heads=4, n_kv_heads=2, head_dim=128, ffn=1024, vocab=1000,
+            context_length=2048, seed=5, scale_mode=1)
+
+
+@pytest.mark.parametrize("kv", ["f16", "int8"])
+def test_split_count_follows_the_context(kv):
+    """A context of 1400 allows 11 attention splits per KV head, but a split
+    covers at least 128 positions: up to position 1023 at most 8 are in use
+    and the Wo matvec merges them while staging; from 1024 on, 9 or more are,
+    and the last split of each KV head merges them. Decode at short
+    contexts, then across that boundary, against the oracle."""
+    path = _model_file("wide", **WIDE)
+    rng = np.random.default_rng(11)
+    om = oracle.Model(path, 1400, kv)
+    tol = TOL if kv == "f16" else TOL_INT8
+    with api.Model(path, max_context=1400, kv=kv) as m:
+        for n_prompt, steps in ((20, 12), (1012, 24)):
+            print("split boundary", kv, n_prompt, flush=True)
+            prompt = rng.integers(3, WIDE["vocab"], n_prompt).tolist()
+            m.reset()
+            om.reset()
+            lg, am = m.eval_prompt(prompt, 0)
+            olg = om.prefill(prompt, 0)
+            assert rel_err(lg, olg) <= tol
+            assert am == oracle.argmax(olg)
+            tok, pos = am, n_prompt
+            for _ in range(steps):
+                lg, am = m.eval_token(tok, pos)
+                olg = om.forward(tok, pos)
+                assert rel_err(lg, olg) <= tol, pos
+                assert am == oracle.argmax(olg), pos
+                tok, pos = am, pos + 1
     om.close()
 
 
