@@ -4,6 +4,14 @@ Tolerance (fp32 accumulation on both sides, different summation order):
 max |gpu - oracle| / max |oracle| <= 1e-3 for every floating-point output;
 bit-exact for integer results (argmax, int8 codes) and for pure
 dequantisation (one fp32 multiply per weight on both sides).
+
+Matvecs are also held to the elementwise form
+max_i |y_i - e_i| / max(|e_i|, 1e-6 max |e|) <= 1e-3 against the exact
+product e (fp64 over the dequantised weights). The HIP matvec meets it on
+every shape (at most 4.2e-4, on 4096 x 4096): its block dot products are
+exact integer sums, with one fp32 rounding per block. The oracle's
+sequential fp32 sum (the reference's) does not on outputs near zero:
+1.4e-3 to 2.9e-2 on the 7B shapes, printed beside the HIP figure.
 """
 import ctypes as C
 
@@ -11,7 +19,7 @@ import numpy as np
 import pytest
 
 import oracle
-from tests.util import Q4_0, Q8_0, make_blocks, rel_err
+from tests.util import Q4_0, Q8_0, dequant_np, elem_rel_err, make_blocks, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -31,7 +39,7 @@ def _matvec_case(hip, qtype, rows, cols, seed):
     got = Y.read(np.float32, rows)
     for b in (W, X, Y):
         b.free()
-    return got, want
+    return got, want, np.asarray(dequant_np(w, rows, cols, qtype), np.float64).reshape(rows, cols) @ x
 
 
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0])
@@ -39,9 +47,13 @@ def _matvec_case(hip, qtype, rows, cols, seed):
                                        (17, 14336), (9, 28672), (5, 14368)])
 def test_matvec(hip, qtype, rows, cols):
     print("matvec", qtype, rows, cols, flush=True)
-    got, want = _matvec_case(hip, qtype, rows, cols, seed=rows * 7 + cols)
+    got, want, exact = _matvec_case(hip, qtype, rows, cols, seed=rows * 7 + cols)
     assert np.all(np.isfinite(got))
     assert rel_err(got, want) <= TOL
+    e_gpu, e_orc = elem_rel_err(got, exact), elem_rel_err(want, exact)
+    print("elementwise vs exact: hip %.3g, oracle %.3g; norm-relative vs oracle %.3g" %
+          (e_gpu, e_orc, rel_err(got, want)), flush=True)
+    assert e_gpu <= TOL
 
 
 @pytest.mark.parametrize("qtype", [Q4_0, Q8_0])

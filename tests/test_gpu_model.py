@@ -80,6 +80,39 @@ def test_greedy_and_logits(spec, kv, launch):
     om.close()
 
 
+@pytest.mark.parametrize("launch", ["graph", "eager"])
+def test_int8_cache_step_at_fp32_tolerance(launch):
+    """int8 KV at the fp16 bar: the same fp16 rows written into both caches
+    through ss_kv_write become the same codes and scales (the encoding is
+    bit-exact for equal inputs), so the only rows that can differ are the
+    evaluated token's own. One step from such a cache, for several tokens at
+    the same position, must then match the oracle to 1e-3 with the same
+    argmax, and different tokens must move the logits by far more than that."""
+    spec = dict(GQA8, scale_mode=1, seed=13)
+    path = _model_file("gqa8_m1", **spec)
+    n = 200
+    kvd = spec["n_kv_heads"] * spec["head_dim"]
+    rng = np.random.default_rng(21)
+    om = oracle.Model(path, 256, "int8")
+    prev = None
+    with api.Model(path, max_context=256, kv="int8", launch=launch) as m:
+        for layer in range(spec["n_layers"]):
+            k = rng.standard_normal((n, kvd), np.float32).astype(np.float16).view(np.uint16)
+            v = rng.standard_normal((n, kvd), np.float32).astype(np.float16).view(np.uint16)
+            m.kv_write(layer, 0, k, v)
+            om.kv_write_rows(layer, 0, k, v)
+        for tok in rng.integers(3, spec["vocab"], 4).tolist():
+            print("int8 step", launch, tok, flush=True)
+            lg, am = m.eval_token(tok, n)
+            olg = om.forward(tok, n)
+            assert rel_err(lg, olg) <= TOL, tok
+            assert am == oracle.argmax(olg)
+            if prev is not None:
+                assert rel_err(olg, prev) >= 10 * TOL
+            prev = olg
+    om.close()
+
+
 @pytest.mark.parametrize("kv", ["f16", "int8"])
 def test_long_context_split_merge_path(kv):
     """A context of 1024 gives 16 attention splits per KV head (query groups

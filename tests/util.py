@@ -272,6 +272,17 @@ def rel_err(got, want):
     return float(np.max(np.abs(got - want)) / (scale if scale > 0 else 1.0))
 
 
+def elem_rel_err(got, want, floor=1e-6):
+    """max_i |got_i - want_i| / max(|want_i|, floor * max |want|): every
+    element's error relative to its own size, small elements measured
+    against floor times the largest."""
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    scale = np.max(np.abs(want))
+    den = np.maximum(np.abs(want), floor * (scale if scale > 0 else 1.0))
+    return float(np.max(np.abs(got - want) / den))
+
+
 class Buf:
     def __init__(self, dev, nbytes):
         self.dev = dev
