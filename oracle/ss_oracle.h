@@ -24,7 +24,7 @@ enum { ORC_F32 = 0, ORC_F16 = 1, ORC_Q4_0 = 2, ORC_Q4_1 = 3, ORC_Q5_0 = 6, ORC_Q
 
 /* KV cache storage modes */
 enum { ORC_KV_INT8 = 0,   /* reference: per-(layer,pos) absmax int8, layer_scheduler.c:101-125 */
-       ORC_KV_F16  = 1 }; /* north-star fp16 cache, fp32 KV structure of layer_scheduler.c.orig:289-342 */
+       ORC_KV_F16  = 1 }; /* binary16 cache (the GPU path's default), laid out as the fp32 KV of layer_scheduler.c.orig:289-342 */
 
 /* ---- element ops ---- */
 float    orc_f16_to_f32(uint16_t h);                 /* quantize.c:20-56 */
