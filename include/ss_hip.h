@@ -225,6 +225,21 @@ int32_t ss_hip_matvec_host(ss_hip_ctx_t *ctx, float *out, const void *mat, const
                            int32_t rows, int32_t cols, int32_t ggml_type);
 int32_t ss_hip_should_use_gpu(int32_t rows, int32_t cols);
 
+/* Metal's command-buffer batch (ss_metal_begin_batch / ss_metal_end_batch,
+ * metal_backend.h:59-70, metal_backend.m:307-330), which the scheduler opens
+ * around Q/K/V and around gate/up (layer_scheduler.c:353-361,509-516).
+ * Between the two calls ss_hip_matvec_host only enqueues: its true means
+ * that out will hold the product after ss_hip_end_batch, which waits for
+ * the batch once and copies every output to its host array (0, or a
+ * negative ss_error_t if a copy failed). Each call of a batch stages its
+ * own vector, so the calls may read different vectors (Metal's share one
+ * buffer). At most 16 calls of a batch are deferred, as Metal's; a further
+ * call returns false and the caller computes it on the CPU (Metal's returns
+ * true and never fills out). Beginning an open batch or ending none does
+ * nothing. */
+void ss_hip_begin_batch(ss_hip_ctx_t *ctx);
+int32_t ss_hip_end_batch(ss_hip_ctx_t *ctx);
+
 /* ---- whole-model decode ---- */
 
 typedef struct {

@@ -122,6 +122,16 @@ struct ss_hip_ctx {
   float* plug_x = nullptr;
   float* plug_y = nullptr;
   size_t plug_x_n = 0, plug_y_n = 0;
+  // an open batch (ss_hip_begin_batch): the calls' device inputs and
+  // outputs, one pair per call, and the host arrays the outputs go to
+  static constexpr int kBatchSlots = 16;   // metal_backend.m:182-185
+  bool batch = false;
+  int batch_n = 0;
+  float* batch_out[kBatchSlots] = {};
+  int32_t batch_rows[kBatchSlots] = {};
+  float* batch_x[kBatchSlots] = {};
+  float* batch_y[kBatchSlots] = {};
+  size_t batch_x_n[kBatchSlots] = {}, batch_y_n[kBatchSlots] = {};
 };
 
 // Scratch of ss_hip_attention_noalloc: the split partials (o, then (m, l))
@@ -301,6 +311,10 @@ void ss_hip_free(ss_hip_ctx_t* c) {
                   c->g_ssq, c->g_xs, c->plug_x, c->plug_y, c->smp, c->smp_io};
   for (void* b : bufs)
     if (b) hipFree(b);
+  for (int i = 0; i < ss_hip_ctx::kBatchSlots; ++i) {
+    if (c->batch_x[i]) hipFree(c->batch_x[i]);
+    if (c->batch_y[i]) hipFree(c->batch_y[i]);
+  }
   if (c->stream) hipStreamDestroy(c->stream);
   delete c;
 }
@@ -692,18 +706,48 @@ int32_t ss_hip_matvec_host(ss_hip_ctx_t* c, float* out, const void* mat, const f
     }
     c->registry[mat] = dev;
   }
-  if (ensure(c, (void**)&c->plug_x, &c->plug_x_n, sizeof(float) * cols, false) ||
-      ensure(c, (void**)&c->plug_y, &c->plug_y_n, sizeof(float) * rows, false))
+  // in a batch: this call's own input and output, the copy to out deferred
+  // to ss_hip_end_batch; a full batch leaves the call to the CPU
+  const bool batched = c->batch;
+  const int slot = c->batch_n;
+  if (batched && slot >= ss_hip_ctx::kBatchSlots) return 0;
+  float** px = batched ? &c->batch_x[slot] : &c->plug_x;
+  float** py = batched ? &c->batch_y[slot] : &c->plug_y;
+  size_t* nx = batched ? &c->batch_x_n[slot] : &c->plug_x_n;
+  size_t* ny = batched ? &c->batch_y_n[slot] : &c->plug_y_n;
+  if (ensure(c, (void**)px, nx, sizeof(float) * cols, false) || ensure(c, (void**)py, ny, sizeof(float) * rows, false))
     return 0;
-  if (hipMemcpyAsync(c->plug_x, vec, sizeof(float) * cols, hipMemcpyHostToDevice, c->stream) !=
-      hipSuccess)
-    return 0;
-  if (ss_hip_matvec(c, c->plug_y, dev, c->plug_x, rows, cols, type, nullptr)) return 0;
-  if (hipMemcpyAsync(out, c->plug_y, sizeof(float) * rows, hipMemcpyDeviceToHost, c->stream) !=
-          hipSuccess ||
+  if (hipMemcpyAsync(*px, vec, sizeof(float) * cols, hipMemcpyHostToDevice, c->stream) != hipSuccess) return 0;
+  if (ss_hip_matvec(c, *py, dev, *px, rows, cols, type, nullptr)) return 0;
+  if (batched) {
+    c->batch_out[slot] = out;
+    c->batch_rows[slot] = rows;
+    c->batch_n = slot + 1;
+    return 1;
+  }
+  if (hipMemcpyAsync(out, *py, sizeof(float) * rows, hipMemcpyDeviceToHost, c->stream) != hipSuccess ||
       hipStreamSynchronize(c->stream) != hipSuccess)
     return 0;
   return 1;
+}
+
+void ss_hip_begin_batch(ss_hip_ctx_t* c) {   // metal_backend.m:307-312
+  if (!c || c->batch) return;
+  c->batch = true;
+  c->batch_n = 0;
+}
+
+int32_t ss_hip_end_batch(ss_hip_ctx_t* c) {   // metal_backend.m:314-330
+  if (!c || !c->batch) return 0;
+  const int n = c->batch_n;
+  c->batch = false;
+  c->batch_n = 0;
+  if (set_device(c)) return kErrBackend;
+  for (int i = 0; i < n; ++i)
+    HIP_TRY(hipMemcpyAsync(c->batch_out[i], c->batch_y[i], sizeof(float) * c->batch_rows[i],
+                           hipMemcpyDeviceToHost, c->stream));
+  HIP_TRY(hipStreamSynchronize(c->stream));
+  return 0;
 }
 
 }  // extern "C"

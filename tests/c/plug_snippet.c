@@ -4,9 +4,12 @@
  * HIP branch is the INTEGRATION.md snippet, the CPU branch stands for
  * ss_dequant_matvec and only counts that it ran. Test infrastructure.
  *
- * usage: plug_snippet W.bin x.bin y.bin rows cols type
+ * usage: plug_snippet W.bin x.bin y.bin rows cols type [batch]
  * W.bin holds GGUF blocks (or F32 rows), x.bin cols fp32 values; y.bin receives rows fp32
  * values (two dispatches of the same matrix: the second reuses the upload).
+ * With "batch": 17 dispatches inside one ss_hip_begin_batch / ss_hip_end_batch,
+ * as the scheduler brackets Q/K/V (layer_scheduler.c:353-361), dispatch i
+ * reading (i + 1) x; y.bin receives the 17 outputs in order.
  * Prints "fallbacks N".
  */
 #include <stdbool.h>
@@ -56,7 +59,7 @@ static void *slurp(const char *path, size_t *n) {
 }
 
 int main(int argc, char **argv) {
-    if (argc != 7) return 2;
+    if (argc != 7 && argc != 8) return 2;
     size_t nw, nx;
     void *w = slurp(argv[1], &nw);
     float *x = (float *)slurp(argv[2], &nx);
@@ -69,6 +72,28 @@ int main(int argc, char **argv) {
         fprintf(stderr, "ss_hip_init: %s\n", ss_hip_last_error());
         return 4;
     }
+    if (argc == 8 && strcmp(argv[7], "batch") == 0) {
+        enum { N = 17 };
+        float *ys = (float *)calloc((size_t)N * rows, sizeof(float));
+        float *xs = (float *)malloc((size_t)N * cols * sizeof(float));
+        if (!ys || !xs) return 3;
+        for (int i = 0; i < N; i++)
+            for (int32_t c = 0; c < cols; c++) xs[(size_t)i * cols + c] = (float)(i + 1) * x[c];
+        ss_hip_begin_batch(sched.hip_ctx);
+        for (int i = 0; i < N; i++)
+            matmul_dispatch(&sched, ys + (size_t)i * rows, w, xs + (size_t)i * cols, rows, cols, type);
+        if (ss_hip_end_batch(sched.hip_ctx) != 0) {
+            fprintf(stderr, "ss_hip_end_batch: %s\n", ss_hip_last_error());
+            return 7;
+        }
+        FILE *f = fopen(argv[3], "wb");
+        if (!f || fwrite(ys, sizeof(float), (size_t)N * rows, f) != (size_t)N * rows) return 6;
+        fclose(f);
+        printf("fallbacks %d\n", cpu_fallbacks);
+        ss_hip_free(sched.hip_ctx);
+        return 0;
+    }
+    if (argc != 7) return 2;
     matmul_dispatch(&sched, y, w, x, rows, cols, type);
     matmul_dispatch(&sched, y2, w, x, rows, cols, type);
     if (memcmp(y, y2, (size_t)rows * sizeof(float)) != 0) return 5;
