@@ -790,6 +790,9 @@ struct ss_hip_model {
   // token from the active count)
   int split_fill = 0;
   bool wo_merge_dyn = false;
+  // query groups of 4 or 8 with more splits than Wo merges: a separate
+  // kernel merges them after the attention (ssk::launch_attention_merge)
+  bool merge_kernel = false;
   float eps = 1e-5f, theta = 10000.f;
   int kv_type = 0;
   int launch = SS_HIP_LAUNCH_SWEEP;   // mode in effect
@@ -1221,10 +1224,12 @@ int32_t enqueue_layer(ss_hip_model* m, int l, const DevLayer& ly, float* hidden,
   // are active at this token's context
   const bool fused = m->ns <= ssk::kMergeSplits;
   const bool direct = m->group <= 2;   // one active split writes Wo's records itself
-  at.cnt = fused ? nullptr : m->att_cnt;
+  at.cnt = fused || m->merge_kernel ? nullptr : m->att_cnt;
   at.xr_out = fused && !direct ? nullptr : m->xr_att;
   at.wo_merge = m->wo_merge_dyn;
   HIP_TRY(timed(m, PC_ATTN, 0, [&] { return ssk::launch_attention(m->hd, m->group, m->kv_type, at, s); }));
+  if (m->merge_kernel)
+    HIP_TRY(timed(m, PC_ATTN, 0, [&] { return ssk::launch_attention_merge(m->hd, m->group, at, s); }));
 
   // 3. hidden += Wo attn                                         (:470-484)
   // (with a post norm: y = Wo attn, then hidden += y * (1 + w) / rms(y), :474-481)
@@ -1757,6 +1762,8 @@ ss_hip_model_t* ss_hip_model_create(ss_hip_ctx_t* c, const ss_hip_model_desc_t* 
   if (m->group <= 2) {
     m->split_fill = ssk::attn_round_positions(m->hd, m->group);
     m->wo_merge_dyn = m->ns > ssk::kMergeSplits;
+  } else {
+    m->merge_kernel = m->ns > ssk::kMergeSplits;
   }
 
   auto bail = [&](void) -> ss_hip_model_t* {

@@ -168,6 +168,10 @@ hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t s);
 hipError_t launch_argmax_merge(const float2* part, int n, const float* y, int* out_idx, int* tokens,
                                int* dpos, hipStream_t s);
 hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs& a, hipStream_t s);
+// Groups of 4 or 8: merge the splits a launch_attention with a.cnt null left
+// in part_o / part_ml into out (and xr_out), after it on the same stream;
+// nothing when one split is active (the attention wrote the output).
+hipError_t launch_attention_merge(int head_dim, int group, const AttnArgs& a, hipStream_t s);
 // Causal attention of a.n_tok prompt rows (token z: query a.q + z*a.tok_q,
 // positions 0..a.dpos[z] (or a.pos0 + z), output a.out + z*a.tok_o), fp16
 // cache, head_dim 64, 128 or 256, on MFMA (ss_flash.hip).

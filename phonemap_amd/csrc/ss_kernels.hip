@@ -521,6 +521,94 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
   attn_finish<HD, G, kHgWaves>(a, kvh, active, wm, wl, wo, tid);
 }
 
+// ------------------------------------------------------------ split merge
+// The splits of a layer's attention merged after the attention kernel, for
+// groups of 4 or 8 query heads, whose splits are too many for the Wo matvec
+// to merge while staging: out = sum_s o_s e^(m_s - M) / sum_s l_s e^(m_s - M)
+// (the softmax of layer_scheduler.c:450-468 over all positions). The
+// attention leaves its partials with plain stores (a.cnt null) and, with a
+// single active split, writes the output itself, in which case this kernel
+// does nothing. Workgroup: one wave, 16 quads (64 consecutive outputs of one
+// query head) x 4 subsets of the splits; grid: n_kv_heads * G * HD / 64, so
+// the partials are read by many compute units at once rather than by one
+// workgroup per KV head.
+template <int HD, int G>
+__global__ void __launch_bounds__(kWave) k_attn_merge(const AttnArgs a) {
+  constexpr int kQuads = G * HD / 4;   // quads of one KV head's G heads
+  constexpr int kWgPerKvh = kQuads / 16;
+  constexpr int kBatch = 8;            // 16-byte loads in flight per lane
+  __shared__ float wts[kMaxSplits];
+  __shared__ float4 red[kWave];
+  const int lane = threadIdx.x;
+  const int kvh = blockIdx.x / kWgPerKvh;
+  const int q0 = (blockIdx.x % kWgPerKvh) * 16;   // first quad of the workgroup
+  const int g = q0 * 4 / HD;                      // its query head within the group
+  int ctx, chunk, active;
+  attn_split(a, ctx, chunk, active);
+  if (active <= 1) return;   // whole workgroup
+  const float* ml = a.part_ml + (size_t)kvh * a.ns * G * 2;
+  float mx = -INFINITY;
+  for (int sp = lane; sp < active; sp += kWave) mx = fmaxf(mx, ml[(sp * G + g) * 2]);
+  mx = wave_max(mx);
+  float ls = 0.f;
+  for (int sp = lane; sp < active; sp += kWave) ls += ml[(sp * G + g) * 2 + 1] * expf(ml[(sp * G + g) * 2] - mx);
+  const float inv = 1.0f / wave_sum(ls);
+  for (int sp = lane; sp < active; sp += kWave) wts[sp] = expf(ml[(sp * G + g) * 2] - mx) * inv;
+  __syncthreads();
+  const int quad = lane & 15, sub = lane >> 4;
+  const float4* po = reinterpret_cast<const float4*>(a.part_o + (size_t)kvh * a.ns * G * HD) + q0 + quad;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int sp0 = sub; sp0 < active; sp0 += 4 * kBatch) {
+    float4 v[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) v[k] = po[(size_t)min(sp0 + 4 * k, active - 1) * kQuads];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int sp = sp0 + 4 * k;
+      const float w = sp < active ? wts[sp] : 0.f;
+      acc.x = fmaf(v[k].x, w, acc.x);
+      acc.y = fmaf(v[k].y, w, acc.y);
+      acc.z = fmaf(v[k].z, w, acc.z);
+      acc.w = fmaf(v[k].w, w, acc.w);
+    }
+  }
+  red[lane] = acc;
+  __syncthreads();
+  if (sub == 0) {   // lanes 0..15: 16 aligned quads, four per x record
+#pragma unroll
+    for (int k = 1; k < 4; ++k) {
+      const float4 r = red[k * 16 + quad];
+      acc.x += r.x;
+      acc.y += r.y;
+      acc.z += r.z;
+      acc.w += r.w;
+    }
+    attn_store4(a, kvh * kQuads + q0 + quad, acc);
+  }
+}
+
+template <int HD, int G>
+hipError_t launch_merge_t(const AttnArgs& a, hipStream_t s) {
+  const dim3 grid(a.n_kv_heads * G * HD / 64);
+  KernelEvents& ev = kernel_events();
+  if (ev.start) {
+    hipExtLaunchKernelGGL((k_attn_merge<HD, G>), grid, dim3(kWave), 0, s, ev.start, ev.stop, 0, a);
+    ev.used = true;
+  } else {
+    hipLaunchKernelGGL((k_attn_merge<HD, G>), grid, dim3(kWave), 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+template <int HD>
+hipError_t launch_merge_hd(int group, const AttnArgs& a, hipStream_t s) {
+  switch (group) {
+    case 4: return launch_merge_t<HD, 4>(a, s);
+    case 8: return launch_merge_t<HD, 8>(a, s);
+    default: return hipErrorInvalidValue;
+  }
+}
+
 // ------------------------------------------------------------ embedding of a prompt
 // ss_scheduler_embed (layer_scheduler.c:864-911): every token's final hidden
 // state through the output norm (x * k_t * w, k_t = 1/sqrt(ssq_t/d + eps)),
@@ -853,6 +941,14 @@ hipError_t launch_attention(int head_dim, int group, int kv_type, const AttnArgs
   if (head_dim == 64) return launch_attn_hd<64>(group, kv_type, a, s);
   if (head_dim == 128) return launch_attn_hd<128>(group, kv_type, a, s);
   if (head_dim == 256) return launch_attn_hd<256>(group, kv_type, a, s);   // Gemma
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_attention_merge(int head_dim, int group, const AttnArgs& a, hipStream_t s) {
+  if (a.ns < 1 || a.ns > kMaxSplits || a.cnt || !a.out) return hipErrorInvalidValue;
+  if (head_dim == 64) return launch_merge_hd<64>(group, a, s);
+  if (head_dim == 128) return launch_merge_hd<128>(group, a, s);
+  if (head_dim == 256) return launch_merge_hd<256>(group, a, s);
   return hipErrorInvalidValue;
 }
 
