@@ -536,41 +536,66 @@ template <int HD, int G>
 __global__ void __launch_bounds__(kWave) k_attn_merge(const AttnArgs a) {
   constexpr int kQuads = G * HD / 4;   // quads of one KV head's G heads
   constexpr int kWgPerKvh = kQuads / 16;
-  constexpr int kBatch = 8;            // 16-byte loads in flight per lane
+  constexpr int kBatch = 8;            // 16-byte loads in flight per lane (32 splits per batch)
+  constexpr int kMlPerLane = kMaxSplits / kWave;
   __shared__ float wts[kMaxSplits];
   __shared__ float4 red[kWave];
   const int lane = threadIdx.x;
   const int kvh = blockIdx.x / kWgPerKvh;
   const int q0 = (blockIdx.x % kWgPerKvh) * 16;   // first quad of the workgroup
   const int g = q0 * 4 / HD;                      // its query head within the group
+  const int ns = a.ns;
+  const int quad = lane & 15, sub = lane >> 4;
+  const float* ml = a.part_ml + (size_t)kvh * ns * G * 2;
+  const float4* po = reinterpret_cast<const float4*>(a.part_o + (size_t)kvh * ns * G * HD) + q0 + quad;
+  // Every split's (m, l) and this lane's first batch of partial outputs are
+  // requested together with the position, before the active count is known:
+  // slots past the active splits hold values of earlier calls and are
+  // excluded by selection (never multiplied in), so no load waits for
+  // another.
+  float2 mlv[kMlPerLane];
+#pragma unroll
+  for (int k = 0; k < kMlPerLane; ++k) {
+    const int sp = lane + k * kWave;
+    mlv[k] = sp < ns ? *reinterpret_cast<const float2*>(ml + (sp * G + g) * 2) : make_float2(-INFINITY, 0.f);
+  }
+  float4 v[kBatch];
+#pragma unroll
+  for (int k = 0; k < kBatch; ++k) v[k] = po[(size_t)min(sub + 4 * k, ns - 1) * kQuads];
   int ctx, chunk, active;
   attn_split(a, ctx, chunk, active);
-  if (active <= 1) return;   // whole workgroup
-  const float* ml = a.part_ml + (size_t)kvh * a.ns * G * 2;
+  if (active <= 1) return;   // whole workgroup: the attention wrote the output
   float mx = -INFINITY;
-  for (int sp = lane; sp < active; sp += kWave) mx = fmaxf(mx, ml[(sp * G + g) * 2]);
+#pragma unroll
+  for (int k = 0; k < kMlPerLane; ++k)
+    if (lane + k * kWave < active) mx = fmaxf(mx, mlv[k].x);
   mx = wave_max(mx);
   float ls = 0.f;
-  for (int sp = lane; sp < active; sp += kWave) ls += ml[(sp * G + g) * 2 + 1] * expf(ml[(sp * G + g) * 2] - mx);
-  const float inv = 1.0f / wave_sum(ls);
-  for (int sp = lane; sp < active; sp += kWave) wts[sp] = expf(ml[(sp * G + g) * 2] - mx) * inv;
-  __syncthreads();
-  const int quad = lane & 15, sub = lane >> 4;
-  const float4* po = reinterpret_cast<const float4*>(a.part_o + (size_t)kvh * a.ns * G * HD) + q0 + quad;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int sp0 = sub; sp0 < active; sp0 += 4 * kBatch) {
-    float4 v[kBatch];
 #pragma unroll
-    for (int k = 0; k < kBatch; ++k) v[k] = po[(size_t)min(sp0 + 4 * k, active - 1) * kQuads];
+  for (int k = 0; k < kMlPerLane; ++k)
+    if (lane + k * kWave < active) ls += mlv[k].y * expf(mlv[k].x - mx);
+  const float inv = 1.0f / wave_sum(ls);
+#pragma unroll
+  for (int k = 0; k < kMlPerLane; ++k)
+    if (lane + k * kWave < active) wts[lane + k * kWave] = expf(mlv[k].x - mx) * inv;
+  __syncthreads();
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int sp0 = sub;;) {
 #pragma unroll
     for (int k = 0; k < kBatch; ++k) {
       const int sp = sp0 + 4 * k;
-      const float w = sp < active ? wts[sp] : 0.f;
-      acc.x = fmaf(v[k].x, w, acc.x);
-      acc.y = fmaf(v[k].y, w, acc.y);
-      acc.z = fmaf(v[k].z, w, acc.z);
-      acc.w = fmaf(v[k].w, w, acc.w);
+      if (sp < active) {
+        const float w = wts[sp];
+        acc.x = fmaf(v[k].x, w, acc.x);
+        acc.y = fmaf(v[k].y, w, acc.y);
+        acc.z = fmaf(v[k].z, w, acc.z);
+        acc.w = fmaf(v[k].w, w, acc.w);
+      }
     }
+    sp0 += 4 * kBatch;
+    if (sp0 >= active) break;
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) v[k] = po[(size_t)min(sp0 + 4 * k, active - 1) * kQuads];
   }
   red[lane] = acc;
   __syncthreads();
