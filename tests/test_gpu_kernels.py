@@ -244,6 +244,43 @@ def test_attention(hip, kv_type, H, KVH, hd, seq, max_seq):
     assert np.array_equal(O.read(np.float32, H * hd), got)
 
 
+@pytest.mark.parametrize("kv_type", [0, 1])
+@pytest.mark.parametrize("H,KVH,hd,seq,max_seq", [(32, 32, 128, 640, 768), (32, 4, 64, 160, 160),
+                                                   (32, 8, 128, 4224, 4352), (16, 8, 64, 65, 100),
+                                                   (64, 8, 128, 1030, 1088), (8, 4, 256, 900, 1024)])
+def test_attention_identical_keys_average_values(hip, kv_type, H, KVH, hd, seq, max_seq):
+    """Every position of a KV head holds the same key: the scores are equal
+    bit for bit (each row's dot product runs the same lanes in the same
+    order), every softmax weight is e^0 = 1, and each head's output is the
+    mean of its KV head's values over positions 0..seq-1, whichever split
+    or merge path the shape takes. A dropped or repeated position moves the
+    mean by about 1/seq of a value."""
+    print("attention identical keys", kv_type, H, KVH, hd, seq, flush=True)
+    rng = np.random.default_rng(seq + hd)
+    q = rng.standard_normal(H * hd).astype(np.float32)
+    if kv_type == 0:
+        key = rng.standard_normal((KVH, 1, hd)).astype(np.float16)
+        kc = np.ascontiguousarray(np.broadcast_to(key, (KVH, max_seq, hd)))
+        vc = rng.standard_normal((KVH, max_seq, hd)).astype(np.float16)
+        vals = vc.astype(np.float64)
+        KS = VS = None
+    else:
+        key = rng.integers(-127, 128, (KVH, 1, hd)).astype(np.int8)
+        kc = np.ascontiguousarray(np.broadcast_to(key, (KVH, max_seq, hd)))
+        vc = rng.integers(-127, 128, (KVH, max_seq, hd)).astype(np.int8)
+        vs = (rng.random(max_seq) * 0.03).astype(np.float32)
+        vals = vc.astype(np.float64) * vs.astype(np.float64)[None, :, None]
+        KS = hip.upload(np.full(max_seq, 0.02, np.float32))
+        VS = hip.upload(vs)
+    G = H // KVH
+    want = np.concatenate([vals[h // G, :seq].mean(axis=0) for h in range(H)])
+    Q, KC, VC, O = hip.upload(q), hip.upload(kc), hip.upload(vc), hip.buf(4 * H * hd)
+    rc = hip.L.ss_hip_attention(hip.ctx, O.ptr, Q.ptr, KC.ptr, VC.ptr, KS.ptr if KS else None,
+                                VS.ptr if VS else None, H, KVH, hd, max_seq, seq, kv_type, None)
+    assert rc == 0, hip.err()
+    assert rel_err(O.read(np.float32, H * hd), want) <= 1e-4
+
+
 def test_attention_single_position_is_v0(hip):
     H, KVH, hd, max_seq = 4, 4, 64, 8
     rng = np.random.default_rng(1)
