@@ -332,6 +332,10 @@ uint64_t ss_hip_model_host_bytes(const ss_hip_model_t *m);
 /* the launch mode in effect (SS_HIP_LAUNCH_*; SWEEP may have been
  * replaced by GRAPH for a shape the persistent launch does not cover) */
 int32_t ss_hip_model_launch(const ss_hip_model_t *m);
+/* Test support: launches of the fp16-MFMA prompt products since the library
+ * was loaded, per epilogue (store, add, SwiGLU) and row groups per wave (1,
+ * 2); out[2 * epilogue + rg - 1], at most n (6) entries. */
+int32_t ss_hip_gemm_launch_counts(int64_t *out, int32_t n);
 
 /* Phase timing of the persistent launch: with tracing on, every launch
  * records per workgroup its start and, for each phase p = 0 .. 5L (layer l:

@@ -32,9 +32,11 @@
  *
  * Parity unpinned: the summation order of Apple vDSP_dotpr / cblas_saxpy
  * (system frameworks, no version pin; orc_dot's order is checked against the
- * reference's own portable ss_neon_dot instead), and end-to-end logits, for
- * which the reference holds no fixture (the model functions are pinned only
- * through their pinned parts).
+ * reference's own portable ss_neon_dot instead). End-to-end logits have no
+ * reference fixture: the model functions (forward, prefill, embed) are
+ * pinned instead by an independent fp64 restatement of layer_scheduler.c
+ * (tests/ref_model.py, tests/test_cpu_model_pin.py), which three mis-wired
+ * variants of it miss by more than twenty times the bar.
  */
 #define _GNU_SOURCE
 #include "ss_oracle.h"

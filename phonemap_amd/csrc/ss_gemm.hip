@@ -24,6 +24,8 @@
 #include <hip/hip_runtime.h>
 #include <math.h>
 
+#include <atomic>
+
 #include "ss_device.h"
 #include "ss_kernels.h"
 
@@ -588,8 +590,12 @@ hipError_t launch_gemm_t(const GemmArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+std::atomic<int64_t> g_gemm_h_launches[kGemmVariants];
+
 template <int QT, int NMAT, int EPI, int RG>
 hipError_t launch_gemm_h_t(const GemmArgs& a, int ldxs, hipStream_t s) {
+  constexpr int slot = EPI == EPI_STORE ? 0 : EPI == EPI_ADD ? 1 : 2;
+  g_gemm_h_launches[2 * slot + RG - 1].fetch_add(1, std::memory_order_relaxed);
   const int ngroups = (a.rows + kRG - 1) / kRG;
   const dim3 grid((ngroups + kHWaves * RG - 1) / (kHWaves * RG), (a.T + kHTok - 1) / kHTok);
   hipLaunchKernelGGL((k_gemm_h<QT, NMAT, EPI, RG>), grid, dim3(kHWaves * 64), 0, s, a, ldxs);
@@ -636,6 +642,12 @@ int device_cus() {
 }
 
 }  // namespace
+
+const int64_t* gemm_h_launch_counts() {
+  static int64_t snap[kGemmVariants];
+  for (int i = 0; i < kGemmVariants; ++i) snap[i] = g_gemm_h_launches[i].load(std::memory_order_relaxed);
+  return snap;
+}
 
 hipError_t launch_sumsq(const float* x, int cols, int T, float* ssq, hipStream_t s) {
   if (T <= 0 || cols <= 0 || cols % 4) return hipErrorInvalidValue;

@@ -743,10 +743,19 @@ int32_t ss_hip_end_batch(ss_hip_ctx_t* c) {   // metal_backend.m:314-330
   c->batch = false;
   c->batch_n = 0;
   if (set_device(c)) return kErrBackend;
-  for (int i = 0; i < n; ++i)
-    HIP_TRY(hipMemcpyAsync(c->batch_out[i], c->batch_y[i], sizeof(float) * c->batch_rows[i],
-                           hipMemcpyDeviceToHost, c->stream));
-  HIP_TRY(hipStreamSynchronize(c->stream));
+  // every copy is attempted, so one failure does not leave the other
+  // outputs stale; the first error is reported (the caller then recomputes
+  // the whole batch on the CPU)
+  hipError_t first = hipSuccess;
+  for (int i = 0; i < n; ++i) {
+    const hipError_t e = hipMemcpyAsync(c->batch_out[i], c->batch_y[i], sizeof(float) * c->batch_rows[i],
+                                        hipMemcpyDeviceToHost, c->stream);
+    if (e != hipSuccess && first == hipSuccess) first = e;
+  }
+  const hipError_t e = hipStreamSynchronize(c->stream);
+  if (first == hipSuccess) first = e;
+  if (first != hipSuccess)
+    return fail(kErrBackend, "end_batch: %s (the batch's outputs must be recomputed)", hipGetErrorString(first));
   return 0;
 }
 
@@ -1946,6 +1955,13 @@ uint64_t ss_hip_model_bytes(const ss_hip_model_t* m) { return m ? m->bytes : 0; 
 uint64_t ss_hip_model_host_bytes(const ss_hip_model_t* m) { return m ? m->host_bytes : 0; }
 
 int32_t ss_hip_model_launch(const ss_hip_model_t* m) { return m ? m->launch : -1; }
+
+int32_t ss_hip_gemm_launch_counts(int64_t* out, int32_t n) {
+  if (!out || n < 0) return fail(kErrParams, "gemm_launch_counts: null output");
+  const int64_t* c = ssk::gemm_h_launch_counts();
+  for (int i = 0; i < n && i < ssk::kGemmVariants; ++i) out[i] = c[i];
+  return 0;
+}
 
 int32_t ss_hip_trace_enable(ss_hip_model_t* m, int32_t on) {
   if (!m) return fail(kErrParams, "null model");

@@ -183,6 +183,11 @@ hipError_t launch_sumsq(const float* x, int cols, int T, float* ssq, hipStream_t
 // parts first and the products run in fp16 (exact codes, fp32 accumulation
 // and scales); otherwise in fp32.
 hipError_t launch_gemm(int epi, const GemmArgs& a, hipStream_t s);
+// Launches of the fp16-MFMA products since the library was loaded, per
+// epilogue (EPI_STORE, EPI_ADD, EPI_SWIGLU) and row groups per wave (1, 2):
+// index 2 * epilogue_slot + RG - 1.
+constexpr int kGemmVariants = 6;
+const int64_t* gemm_h_launch_counts();
 bool attention_supported(int head_dim, int group);
 // positions one attention workgroup covers in one round of loads
 int attn_round_positions(int head_dim, int group);

@@ -116,3 +116,56 @@ def test_embed_prompt_matches_oracle(mode):
     om.close()
     assert abs(np.linalg.norm(got) - 1.0) < 1e-5
     assert rel_err(got, want) <= (TOL if kv == "f16" else 5e-2)
+
+
+# Two layers at the Llama-2-70B layer shape (d 8192, 64 query heads and 8 KV
+# heads of dim 128, FFN 28672), all Q4_0, with a small vocabulary so that the
+# oracle's prompt takes seconds.
+W70 = dict(n_layers=2, hidden=8192, n_heads=64, n_kv_heads=8, head_dim=128, ffn=28672, vocab=512,
+           context_length=1024, seed=71, scale_mode=1)
+# ss_hip_gemm_launch_counts slots: 2 * epilogue (store, add, SwiGLU) + rows per wave - 1
+ADD_RG2 = 3
+
+
+def _gemm_counts():
+    import ctypes as C
+    L = api._lib()
+    out = (C.c_int64 * 6)()
+    assert L.ss_hip_gemm_launch_counts(out, 6) == 0
+    return list(out)
+
+
+@pytest.mark.timeout(600)
+def test_prompt_at_70b_layer_width():
+    """A 600-token prompt (chunks of 512 and 88 tokens) through two layers of
+    the 70B shape, then 8 greedy steps: every logit vector within 1e-3 of the
+    oracle's prefill / forward (layer_scheduler.c:681-803, :571-679), the
+    argmax equal, and the model responding to its input (the step-to-step
+    guard of the full-shape tests). At d = 8192 and 512 tokens the Wo and
+    down products run with two row groups per wave (k_gemm_h EPI_ADD, RG 2),
+    which no smaller shape selects; the launch counters show that they ran."""
+    from tests.test_gpu_fullshape import Trace
+    path = _model_file("w70", **W70)
+    rng = np.random.default_rng(700)
+    prompt = rng.integers(3, W70["vocab"], 600).tolist()
+    ctx = len(prompt) + 9
+    print("prefill w70 600 tokens", flush=True)
+    om = oracle.Model(path, ctx, "f16")
+    tr = Trace("w70")
+    with api.Model(path, max_context=ctx) as m:
+        before = _gemm_counts()
+        lg, am = m.eval_prompt(prompt, 0)
+        after = _gemm_counts()
+        olg = om.prefill(prompt, 0)
+        tr.step(-1, lg, am, olg)
+        tok, pos = am, len(prompt)
+        for i in range(8):
+            lg, am = m.eval_token(tok, pos)
+            olg = om.forward(tok, pos)
+            tr.step(i, lg, am, olg)
+            tok, pos = am, pos + 1
+    om.close()
+    tr.done()
+    ran = after[ADD_RG2] - before[ADD_RG2]
+    print("k_gemm_h EPI_ADD RG=2 launches during the prompt:", ran, flush=True)
+    assert ran >= 2 * W70["n_layers"], (before, after)

@@ -9,9 +9,10 @@ cover a ragged token tile, one token, rows not a multiple of 16 and a
 
 Whole models (Q4_K layers with a Q6_K head as Q4_K_M files have, Q6_K,
 Q3_K, Q5_1 with Q4_1 / Q8_1 tables) evaluate a 300-token prompt as products,
-against the oracle's token-serial prefill (or, at a step where the oracle's
-fp16 cache rounds across a binary16 midpoint the other way than fp64, the
-fp64 model of tests/ref_model.py), then decode.
+against the oracle's token-serial prefill, then decode: logits within 1e-3
+(fp16 cache; 5e-2 int8) of the oracle's at every step, with the distance to
+the fp64 model of tests/ref_model.py printed beside it (OracleBar; measured
+worst against the oracle 2.4e-4).
 """
 import ctypes as C
 
@@ -21,7 +22,7 @@ import pytest
 import oracle
 from phonemap_amd import api
 from tests.ref_model import RefModel
-from tests.util import Q2_K, Q3_K, Q4_1, Q4_K, Q5_0, Q5_1, Q5_K, Q6_K, Q8_1, make_blocks, rel_err
+from tests.util import OracleBar, Q2_K, Q3_K, Q4_1, Q4_K, Q5_0, Q5_1, Q5_K, Q6_K, Q8_1, make_blocks, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -81,6 +82,11 @@ SPECS = {
     "q5_1_q4_1": dict(BASE, layer_type=Q5_1, embd_type=Q4_1, out_type=Q8_1, seed=84),
 }
 
+# Steps at which the oracle's fp16 cache rounds a K/V value across a binary16
+# midpoint the other way than exact arithmetic does ((spec, kv, step) ->
+# (oracle bar, reason)); every other step holds the oracle bar (OracleBar).
+KNOWN = {}
+
 
 @pytest.mark.parametrize("kv", ["f16", "int8"])
 @pytest.mark.parametrize("spec", sorted(SPECS))
@@ -94,18 +100,19 @@ def test_long_prompt_as_products(tmp_path, spec, kv):
     om = oracle.Model(path, 400, kv)
     rm = RefModel(path, 400, kv)
     tol = TOL if kv == "f16" else 5e-2
+    bar = OracleBar("products %s %s" % (spec, kv), tol,
+                    {k[2]: v for k, v in KNOWN.items() if k[:2] == (spec, kv)})
     with api.Model(path, max_context=400, kv=kv) as m:
         lg, am = m.eval_prompt(prompt, 0)
         olg = om.prefill(prompt, 0)
-        e = rel_err(lg, olg)
-        assert e <= tol or rel_err(lg, rm.prefill(prompt, 0)) <= tol, e
+        bar.check("prompt", lg, olg, rm.prefill(prompt, 0))
         assert am == oracle.argmax(olg)
         tok, pos = am, len(prompt)
         for _ in range(6):
             lg, am = m.eval_token(tok, pos)
             olg = om.forward(tok, pos)
-            e = rel_err(lg, olg)
-            assert e <= tol or rel_err(lg, rm.forward(tok, pos)) <= tol, (pos, e)
+            bar.check(pos, lg, olg, rm.forward(tok, pos))
             assert am == oracle.argmax(olg), pos
             tok, pos = am, pos + 1
     om.close()
+    bar.report()

@@ -17,10 +17,12 @@ CPU oracle, through the C-ABI.
   to the oracle's and logits within 1e-3 (fp16 cache; 5e-2 int8) of the
   oracle's at every step, for graph and eager launches (the persistent
   launch falls back to graph) and both cache types; prompts run token by
-  token. A step where the oracle's fp16 cache rounds a value across a
-  binary16 midpoint the other way than fp64 does moves its logits by up to
-  ~2e-3 (seed 31, position 21: oracle vs the fp64 model 1.51e-3); there the
-  bar is taken against the fp64 model of tests/ref_model.py.
+  token. The fp64 model's distance is printed beside the oracle's
+  (OracleBar). One step is listed in KNOWN: at seed 31, position 21, the
+  oracle's fp16 cache rounds a value across a binary16 midpoint the other
+  way than exact arithmetic does, and its logits leave the fp64 model's by
+  1.51e-3. The GPU is 4.7e-6 from the fp64 model there and 1.51e-3 from the
+  oracle, so that step holds the oracle at 2e-3 and the fp64 model at 1e-3.
 * Streaming mode (layers uploaded per use) gives the resident logits bit
   for bit.
 * A shape the Q4_K matvec cannot take (columns not a multiple of 256) is
@@ -34,7 +36,7 @@ import pytest
 import oracle
 from phonemap_amd import api
 from tests.ref_model import RefModel
-from tests.util import Q4_K, check_elementwise, make_q4_k, rel_err
+from tests.util import OracleBar, Q4_K, check_elementwise, make_q4_k, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
@@ -122,13 +124,14 @@ SPECS = {
 }
 
 
-def _close(lg, olg, ref, tol):
-    """Within tol of the oracle; or, at a step where the oracle's own fp16
-    cache rounded a value across a binary16 midpoint the other way (its
-    logits then leave the fp64 model's by the same amount), within tol of the
-    fp64 model."""
-    e = rel_err(lg, olg)
-    return e <= tol or rel_err(lg, ref) <= tol, e
+
+
+# Steps at which the oracle's fp16 cache rounds a K/V value across a binary16
+# midpoint the other way than exact arithmetic does ((spec, kv, step) ->
+# (oracle bar, reason)); every other step holds the oracle bar (OracleBar).
+KNOWN = {
+    ("q4k_gqa", "f16", 21): (2e-3, "the oracle's fp16 cache leaves the fp64 model by 1.51e-3 at this step"),
+}
 
 
 @pytest.mark.parametrize("kv", ["f16", "int8"])
@@ -144,27 +147,28 @@ def test_q4k_model_greedy_and_logits(tmp_path, spec, launch, kv):
     om = oracle.Model(path, 128, kv)
     rm = RefModel(path, 128, kv)
     tol = TOL if kv == "f16" else TOL_INT8
+    bar = OracleBar("q4k %s %s %s" % (spec, launch, kv), tol,
+                    {k[2]: v for k, v in KNOWN.items() if k[:2] == (spec, kv)})
     L = api._lib()
     with api.Model(path, max_context=128, kv=kv, launch=launch) as m:
         want = api.LAUNCH["graph"] if launch == "sweep" else api.LAUNCH[launch]
         assert L.ss_hip_model_launch(L.ss_model_hip(m.h)) == want
         lg, am = m.eval_prompt(prompt, 0)
         olg = om.prefill(prompt, 0)
-        ok, e = _close(lg, olg, rm.prefill(prompt, 0), tol)
-        assert ok, e
+        bar.check("prompt", lg, olg, rm.prefill(prompt, 0))
         assert am == oracle.argmax(olg)
         tok, pos, prev = am, len(prompt), olg
         changes = []
         for _ in range(16):
             lg, am = m.eval_token(tok, pos)
             olg = om.forward(tok, pos)
-            ok, e = _close(lg, olg, rm.forward(tok, pos), tol)
-            assert ok, (pos, e)
+            bar.check(pos, lg, olg, rm.forward(tok, pos))
             assert am == oracle.argmax(olg), pos
             changes.append(rel_err(olg, prev))
             tok, pos, prev = am, pos + 1, olg
         assert np.median(changes) >= 10 * TOL     # the model responds to its input
     om.close()
+    bar.report()
 
 
 def test_q4k_streaming_matches_resident(tmp_path):
