@@ -7,6 +7,8 @@
 
 #include <math.h>
 
+#include <type_traits>
+
 #include <hip/hip_ext.h>
 
 #include "ss_device.h"
@@ -399,6 +401,26 @@ struct KvRow {
       }
     }
   }
+  // the same words through a buffer view (offset in bytes; past the view's
+  // range the words read zero)
+  __device__ __forceinline__ void load(__amdgpu_buffer_rsrc_t r, int off) {
+    if constexpr (kWords == 1) {
+      w[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    } else if constexpr (kWords == 2) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+      w[0] = v[0];
+      w[1] = v[1];
+    } else {
+#pragma unroll
+      for (int i = 0; i < kWords / 4; ++i) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 0);
+        w[4 * i] = v[0];
+        w[4 * i + 1] = v[1];
+        w[4 * i + 2] = v[2];
+        w[4 * i + 3] = v[3];
+      }
+    }
+  }
   __device__ __forceinline__ float get(int i, float s) const {
     if constexpr (KVT == 0)
       return h2f((uint16_t)(w[i / 2] >> (16 * (i % 2))));
@@ -419,7 +441,10 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
   __shared__ float wm[kHgWaves][G], wl[kHgWaves][G];
   __shared__ float wo[kHgWaves][G][HD];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // the wave index as a wave-uniform (scalar) value: the per-batch buffer
+  // views derived from it stay in scalar registers
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kvh = blockIdx.y;
   int ctx, chunk, active;
   attn_split(a, ctx, chunk, active);
@@ -432,9 +457,15 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
   const int p0 = t0 + wave * per;
   const int p1 = min(t1, p0 + per);
 
-  const size_t head_base = (size_t)kvh * a.max_seq;
-  const uint8_t* kb = static_cast<const uint8_t*>(a.kc) + (head_base * HD + c * kDpl) * kEb;
-  const uint8_t* vb = static_cast<const uint8_t*>(a.vc) + (head_base * HD + c * kDpl) * kEb;
+  // K and V rows [pb, p1) of this KV head as a buffer view per batch (base
+  // and range in scalar registers): row j of the batch is one load at the
+  // constant offset j * HD * kEb past the lane's column offset, rows past p1
+  // read zero (and are masked), and no per-batch address registers are
+  // needed beside the two batches' data
+  const size_t head_base = (size_t)kvh * a.max_seq * HD * kEb;
+  const uint8_t* kbase = static_cast<const uint8_t*>(a.kc) + head_base;
+  const uint8_t* vbase = static_cast<const uint8_t*>(a.vc) + head_base;
+  const int lane_off = c * kDpl * kEb;
 
   float q[kDpl], o[kDpl];
   {
@@ -456,29 +487,45 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
     Row k[kB], v[kB];
     float ks[kB], vs[kB];
   };
-  // rows past p1 reload p1 - 1 (branch-free; masked in use)
+  // branch-free: every row of a batch is loaded (rows past p1 read zero
+  // through the view and are masked in use)
   auto load = [&](Batch& bt, int pb) {
+    const int n = max(p1 - pb, 0);
+    const __amdgpu_buffer_rsrc_t kx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(kbase + (size_t)pb * HD * kEb), (short)0, n * HD * kEb, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t vx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(vbase + (size_t)pb * HD * kEb), (short)0, n * HD * kEb, kBufferFlags);
 #pragma unroll
     for (int j = 0; j < kB; ++j) {
-      const int p = min(pb + j, p1 - 1);
-      bt.k[j].load(kb + (size_t)p * HD * kEb);
-      bt.v[j].load(vb + (size_t)p * HD * kEb);
-      if constexpr (KVT == 1) {
-        bt.ks[j] = a.ks[p];
-        bt.vs[j] = a.vs[p];
-      } else {
-        bt.ks[j] = bt.vs[j] = 1.f;
+      bt.k[j].load(kx, lane_off + j * HD * kEb);
+      bt.v[j].load(vx, lane_off + j * HD * kEb);
+    }
+    if constexpr (KVT == 1) {   // the rows' scales, one fp32 per position
+      const __amdgpu_buffer_rsrc_t ksx =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.ks + pb), (short)0, n * 4, kBufferFlags);
+      const __amdgpu_buffer_rsrc_t vsx =
+          __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.vs + pb), (short)0, n * 4, kBufferFlags);
+#pragma unroll
+      for (int j = 0; j < kB; ++j) {
+        bt.ks[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ksx, 4 * j, 0, 0));
+        bt.vs[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vsx, 4 * j, 0, 0));
       }
+    } else {
+#pragma unroll
+      for (int j = 0; j < kB; ++j) bt.ks[j] = bt.vs[j] = 1.f;
     }
   };
-  auto use = [&](const Batch& bt, int pb) {
+  // cap: the attention softcap is set (decided once, outside the loop, so the
+  // loop has no branch between a batch's loads and their use)
+  auto use = [&](const Batch& bt, int pb, auto cap) {
     float sc[kB];
 #pragma unroll
     for (int j = 0; j < kB; ++j) {
       float d = 0.f;
 #pragma unroll
       for (int i = 0; i < kDpl; ++i) d = fmaf(q[i], bt.k[j].get(i, bt.ks[j]), d);
-      d = softcap(sum_lanes<kLph>(d) * a.scale, a);   // (q . k) / sqrt(hd), layer_scheduler.c:442-448
+      d = sum_lanes<kLph>(d) * a.scale;   // (q . k) / sqrt(hd), layer_scheduler.c:442-448
+      if constexpr (decltype(cap)::value) d = softcap(d, a);
       sc[j] = pb + j < p1 ? d : -INFINITY;
     }
     float bm = sc[0];                      // live: pb < p1
@@ -498,17 +545,28 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
     }
     m = mn;
   };
-  if (p0 < p1) {
+  // the scheduling barriers keep each batch's loads ahead of the other
+  // batch's arithmetic (the scheduler would otherwise sink them to their
+  // uses, leaving one batch in flight)
+  auto batches = [&](auto cap) {
     Batch A, B;
     load(A, p0);
     for (int pb = p0;; pb += 2 * kB) {
       load(B, pb + kB);
-      use(A, pb);
+      __builtin_amdgcn_sched_barrier(0);
+      use(A, pb, cap);
       if (pb + kB >= p1) break;
       load(A, pb + 2 * kB);
-      use(B, pb + kB);
+      __builtin_amdgcn_sched_barrier(0);
+      use(B, pb + kB, cap);
       if (pb + 2 * kB >= p1) break;
     }
+  };
+  if (p0 < p1) {
+    if (a.softcap > 0.f)
+      batches(std::true_type{});
+    else
+      batches(std::false_type{});
   }
 
   if (c == 0) {
