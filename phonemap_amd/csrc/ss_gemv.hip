@@ -120,15 +120,18 @@ __device__ __forceinline__ float xput(XSlice<UT>& p, int* xw, const float* nw, i
 
 // Merge staging (the attention split merge inside the Wo matvec): x[col] for
 // col in head h = G*kvh + g is sum_s o_s * e^(m_s - M) / sum_s l_s e^(m_s - M)
-// over the active attention splits s of KV head kvh. A lane fetches the
-// (m, l) and 4 o values of all kMergeSplits split slots for its group of 4
-// columns (slots past the active ones reload the last active split and get
-// weight 0) before the weight loads, in one batch (loads of the active
-// slots only, each under its condition, measured 50% slower; the weight
-// loads first, 2% slower). head_dim and the group size are powers of two.
+// over the active attention splits s of KV head kvh. A lane fetches the 4 o
+// values of all kMergeSplits split slots for its group of 4 columns (slots
+// past the active ones reload the last active split and get weight 0), and
+// the (m, l) of one slot, lane % 8, of its head, before the weight loads, in
+// one batch. The split weights e^(m_s - M) / sum are then formed once per
+// aligned group of 8 lanes (the lanes of a group share a head: a head spans
+// head_dim / 4 >= 16 lanes) with one exponential per lane and DPP
+// reductions, and read back by every lane of the group with lane shuffles.
+// head_dim and the group size are powers of two.
 template <int UT>
 struct MSlice {
-  float2 ml[UT / 2][kMergeSplits];
+  float2 ml[UT / 2];
   float4 o[UT / 2][kMergeSplits];
 };
 
@@ -148,45 +151,49 @@ __device__ __forceinline__ void mfetch(MSlice<UT>& p, const GemvArgs& a, int u, 
     const int col = min(u * UT * kTB * 32 + (gi >> 3) * 32 + (gi & 7) * 4, a.cols - 4);
     const int h = col >> hs, d = col & (hd - 1);
     const int kvh = h >> gs, g = h & (G - 1);
+    const size_t im = ((size_t)kvh * a.att_ns + min(lane & 7, active - 1)) * G + g;
+    p.ml[j] = *reinterpret_cast<const float2*>(a.att_ml + im * 2);
 #pragma unroll
     for (int s = 0; s < kMergeSplits; ++s) {
       const size_t i = ((size_t)kvh * a.att_ns + min(s, active - 1)) * G + g;
-      p.ml[j][s] = *reinterpret_cast<const float2*>(a.att_ml + i * 2);
       p.o[j][s] = *reinterpret_cast<const float4*>(a.att_o + i * hd + d);
     }
   }
 }
 
-// Same arithmetic order as the merge in k_attn.
+// max and sum over the aligned group of 8 lanes (all 8 active), in every lane
+__device__ __forceinline__ float max8(float v) {
+  v = fmaxf(v, dpp<0xb1>(v));    // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp<0x4e>(v));    // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp<0x141>(v));   // row_half_mirror
+  return v;
+}
+
 template <int UT>
 __device__ __forceinline__ void mput(MSlice<UT>& p, int* xw, int u, int nb, int active, int lane) {
 #pragma unroll
-  for (int j = 0; j < UT / 2; ++j)
+  for (int j = 0; j < UT / 2; ++j) {
+    asm volatile("" : "+v"(p.ml[j].x), "+v"(p.ml[j].y));
 #pragma unroll
-    for (int s = 0; s < kMergeSplits; ++s) {
-      asm volatile("" : "+v"(p.ml[j][s].x), "+v"(p.ml[j][s].y));
-      pin(p.o[j][s]);
-    }
+    for (int s = 0; s < kMergeSplits; ++s) pin(p.o[j][s]);
+  }
 #pragma unroll
   for (int j = 0; j < UT / 2; ++j) {
     const int gi = j * kWave + lane;
-    float M = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < kMergeSplits; ++s)
-      if (s < active) M = fmaxf(M, p.ml[j][s].x);
-    float L = 0.f;
-#pragma unroll
-    for (int s = 0; s < kMergeSplits; ++s)
-      if (s < active) L += p.ml[j][s].y * expf(p.ml[j][s].x - M);
-    const float inv = 1.0f / L;
+    // this lane's slot: lane % 8 (slot 0 is always active, so M is finite)
+    const bool live = (lane & 7) < active;
+    const float M = max8(live ? p.ml[j].x : -INFINITY);
+    const float e = live ? expf(p.ml[j].x - M) : 0.f;
+    const float L = sum8(live ? p.ml[j].y * e : 0.f);
+    const float w = e * (1.0f / L);
     float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int s = 0; s < kMergeSplits; ++s) {
-      const float w = s < active ? expf(p.ml[j][s].x - M) * inv : 0.f;
-      t.x = fmaf(p.o[j][s].x, w, t.x);
-      t.y = fmaf(p.o[j][s].y, w, t.y);
-      t.z = fmaf(p.o[j][s].z, w, t.z);
-      t.w = fmaf(p.o[j][s].w, w, t.w);
+      const float ws = __shfl(w, (lane & ~7) | s, kWave);   // 0 past the active slots
+      t.x = fmaf(p.o[j][s].x, ws, t.x);
+      t.y = fmaf(p.o[j][s].y, ws, t.y);
+      t.z = fmaf(p.o[j][s].z, ws, t.z);
+      t.w = fmaf(p.o[j][s].w, ws, t.w);
     }
     if (u * UT * kTB + (gi >> 3) >= nb) t = make_float4(0.f, 0.f, 0.f, 0.f);
     encode4(xw + (gi >> 3) * kXW, gi & 7, t);
