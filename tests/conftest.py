@@ -12,6 +12,21 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) device")
 
 
+# The persistent one-launch-per-token sweep (SS_LAUNCH_SWEEP) measures slower
+# than graph-replayed launches at every shape (7B 515 against 734 tok/s; each
+# in-launch exchange between phases costs as much as a kernel boundary), so it
+# is kept as an opt-in launch mode: the default GPU run holds one parity case
+# per test family to the oracle, and SS_TEST_SWEEP=1 runs the whole matrix.
+SWEEP_ALL = os.environ.get("SS_TEST_SWEEP") == "1"
+
+
+def sweep_optin(representative):
+    """Skip a sweep-launch case unless it is the family's representative case
+    or SS_TEST_SWEEP=1."""
+    if not representative and not SWEEP_ALL:
+        pytest.skip("persistent sweep launch: representative cases only (SS_TEST_SWEEP=1 runs all)")
+
+
 @pytest.fixture(scope="session")
 def hip():
     """A HIP context on device 0 (GPU tests only)."""

@@ -13,6 +13,7 @@ import pytest
 
 import oracle
 from phonemap_amd import api
+from tests.conftest import sweep_optin
 from tests.util import OracleBar, rel_err
 
 pytestmark = pytest.mark.gpu
@@ -54,6 +55,8 @@ def _launch_in_effect(m):
 @pytest.mark.parametrize("spec", ["tiny", "tiny_q8", "gqa8"])
 @pytest.mark.parametrize("launch", ["sweep", "graph", "eager"])
 def test_greedy_and_logits(spec, kv, launch):
+    if launch == "sweep":
+        sweep_optin(spec == "gqa8" and kv == "f16")
     kw = {"tiny": TINY, "tiny_q8": TINY_Q8, "gqa8": GQA8}[spec]
     path = _model_file(spec, **kw)
     print("model", spec, kv, launch, flush=True)
@@ -281,6 +284,8 @@ def test_tables_with_rows_past_the_vocabulary(spec, launch):
     the vocabulary is clamped (layer_scheduler.c:186-197), the LM head reads
     the first vocab rows of the table as packed, and logits and greedy tokens
     match the oracle's."""
+    if launch == "sweep":
+        sweep_optin(spec == "padded_tied")
     kw = {"padded_tied": PADDED_TIED, "padded_out": PADDED_OUT}[spec]
     path = _model_file(spec, **kw)
     print("model", spec, launch, flush=True)

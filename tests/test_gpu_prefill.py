@@ -13,6 +13,7 @@ import pytest
 import oracle
 from phonemap_amd import api
 from tests.test_gpu_model import GQA8, TINY, TINY_Q8, TOL, _model_file
+from tests.conftest import sweep_optin
 from tests.util import rel_err
 
 pytestmark = pytest.mark.gpu
@@ -33,6 +34,8 @@ def _decode_against(m, om, tok, pos, steps):
 def test_batched_prompt_matches_oracle(spec, launch):
     """A 600-token prompt (two chunks: 512 + 88), then a 30-token prompt that
     continues it at position 600, then decode steps."""
+    if launch == "sweep":
+        sweep_optin(spec == "gqa8")
     kw = SPECS[spec]
     path = _model_file(spec, **kw)
     print("prefill", spec, launch, flush=True)
