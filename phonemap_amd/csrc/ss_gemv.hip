@@ -39,6 +39,7 @@
 #include <math.h>
 
 #include <type_traits>
+#include <utility>
 
 #include <hip/hip_ext.h>
 
@@ -483,21 +484,64 @@ __device__ __forceinline__ void epilogue(const GemvArgs& a, int row, bool own, c
 template <int QT, int NMAT>
 constexpr int gemv_max_waves() { return QT == 2 && NMAT == 1 ? 16 : 8; }
 
-template <int QT, int NMAT, int EPI, int UT, bool MERGE, bool PX>
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, unrolled at compile time
+template <class F, int... I>
+__device__ __forceinline__ void for_each_index_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void for_each_index(F&& f) {
+  for_each_index_impl(f, std::make_integer_sequence<int, N>{});
+}
+template <int I, class T>
+__device__ __forceinline__ T& pick(T& a0, T& a1, T& a2, T& a3) {
+  static_assert(I >= 0 && I < 4, "at most four rounds");
+  if constexpr (I == 0) return a0;
+  else if constexpr (I == 1) return a1;
+  else if constexpr (I == 2) return a2;
+  else return a3;
+}
+
+// A unit's x records through registers (NR > 0): lane l holds 16-byte pieces
+// l, l + 64, ... of the unit's UT*kTB*kXW words, written to the wave's LDS
+// slice just before the unit is used. Register dependencies let the compiler
+// wait for exactly the unit in use while the next one is in flight.
+template <int UT>
+struct XRec {
+  uint4 v[UT * kTB * kXW / 4 / kWave];
+};
+template <int UT>
+__device__ __forceinline__ void rload(XRec<UT>& r, const uint32_t* __restrict__ xr, int u, int lane) {
+  const uint4* src = reinterpret_cast<const uint4*>(xr + (size_t)u * UT * kTB * kXW);
+#pragma unroll
+  for (int i = 0; i < UT * kTB * kXW / 4 / kWave; ++i) r.v[i] = src[i * kWave + lane];
+}
+template <int UT>
+__device__ __forceinline__ void rput(int* xw, const XRec<UT>& r, int lane) {
+#pragma unroll
+  for (int i = 0; i < UT * kTB * kXW / 4 / kWave; ++i) reinterpret_cast<uint4*>(xw)[i * kWave + lane] = r.v[i];
+}
+
+// NR > 0 (records path, every wave with at most NR units): all of a wave's
+// units are requested at once, their records and weights in registers, and
+// used in order.
+template <int QT, int NMAT, int EPI, int UT, bool MERGE, bool PX, int NR>
 __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(const GemvArgs a) {
   extern __shared__ float4 smem4[];
   int* xs = reinterpret_cast<int*>(smem4);
+  static_assert(NR == 0 || PX, "rounds issued up front take x from the records");
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (scalar)
   const int S = blockDim.x >> 6;
   const int kb = lane / kRG;
   const int g = blockIdx.x;
   const int nb = a.cols >> 5;
   const int ntk = (nb + kTB - 1) / kTB;
   const int nu = (ntk + UT - 1) / UT;
-  int* xw = xs + wave * (UT * kTB * kXW);                          // this wave's x slice
-  float* red = reinterpret_cast<float*>(xs + S * UT * kTB * kXW);   // [NMAT][S][16], then [S]
+  constexpr int kSlice = UT * kTB * kXW;                              // words of one x slice
+  int* xw = xs + wave * kSlice;                                       // this wave's x slice
+  float* red = reinterpret_cast<float*>(xs + S * kSlice);              // [NMAT][S][16], then [S]
 
   float acc[NMAT];
 #pragma unroll
@@ -540,7 +584,38 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     }
   };
-  if constexpr (PX) {
+  // Every unit of the wave in flight at once: unit wave + i*S in round i
+  // (rounds past the row reload the last unit, branch-free, and are not
+  // used); each is used once its own loads have landed (the compiler waits
+  // for them by register while the later units' are still in flight).
+  auto rounds_all = [&]() {
+    // one named variable per round (no array the compiler could keep in
+    // scratch memory); rounds past NR are never touched
+    Round<QT, NMAT, UT> r0, r1, r2, r3;
+    XRec<UT> x0, x1, x2, x3;
+    for_each_index<NR>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      auto& r = pick<i>(r0, r1, r2, r3);
+      auto& x = pick<i>(x0, x1, x2, x3);
+      const int u = min(wave + i * S, nu - 1);
+      rload<UT>(x, a.xr, u, lane);
+      load_round<QT, NMAT, UT>(r, a, g, ntk, u, lane);
+    });
+    __builtin_amdgcn_sched_barrier(0);
+    for_each_index<NR>([&](auto ic) {
+      constexpr int i = decltype(ic)::value;
+      if (wave + i * S < nu) {   // wave-uniform
+        rput<UT>(xw, pick<i>(x0, x1, x2, x3), lane);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        if (a.nw && lane < UT * kTB * 2) ssq += __int_as_float(xw[lane * kRW + 14]);
+        fma_round<QT, NMAT, UT>(acc, pick<i>(r0, r1, r2, r3), xw, kb);
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      }
+    });
+  };
+  if constexpr (NR > 0) {
+    rounds_all();
+  } else if constexpr (PX) {
     rounds(std::true_type{});
   } else if constexpr (MERGE) {
     if (a.xr && (active == 1 || active > kMergeSplits))
@@ -908,19 +983,33 @@ __global__ void k_argmax_merge(const float2* part, int n, const float* y, int* o
   }
 }
 
-template <int QT, int NMAT, int EPI, bool MERGE = false, bool PX = false, int UT = kGemvUnit>
-hipError_t launch_t(const GemvArgs& a, hipStream_t s) {
-  GemvPlan p = gemv_plan(a.rows, a.cols, QT, NMAT, UT);
+template <int QT, int NMAT, int EPI, bool MERGE, bool PX, int UT, int NR>
+hipError_t launch_k(const GemvArgs& a, const GemvPlan& p, hipStream_t s) {
   KernelEvents& ev = kernel_events();
   if (ev.start) {
-    hipExtLaunchKernelGGL((k_gemv<QT, NMAT, EPI, UT, MERGE, PX>), dim3(p.grid), dim3(p.threads),
+    hipExtLaunchKernelGGL((k_gemv<QT, NMAT, EPI, UT, MERGE, PX, NR>), dim3(p.grid), dim3(p.threads),
                           p.lds_bytes, s, ev.start, ev.stop, 0, a);
     ev.used = true;
   } else {
-    hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, UT, MERGE, PX>), dim3(p.grid), dim3(p.threads),
+    hipLaunchKernelGGL((k_gemv<QT, NMAT, EPI, UT, MERGE, PX, NR>), dim3(p.grid), dim3(p.threads),
                        p.lds_bytes, s, a);
   }
   return hipGetLastError();
+}
+
+// Records path of Q4_0 / Q8_0 matrices whose rows take 2 to 4 units per
+// wave: every unit of a wave requested at once (NR rounds).
+template <int QT, int NMAT, int EPI, bool MERGE = false, bool PX = false, int UT = kGemvUnit>
+hipError_t launch_t(const GemvArgs& a, hipStream_t s) {
+  const GemvPlan p = gemv_plan(a.rows, a.cols, QT, NMAT, UT);
+  if constexpr (PX && !MERGE && (QT == 2 || QT == 8)) {
+    const int ntk = (a.cols / 32 + kTB - 1) / kTB;
+    const int S = p.threads / kWave, nr = ((ntk + UT - 1) / UT + S - 1) / S;
+    if (nr == 2) return launch_k<QT, NMAT, EPI, MERGE, PX, UT, 2>(a, p, s);
+    if (nr == 3) return launch_k<QT, NMAT, EPI, MERGE, PX, UT, 3>(a, p, s);
+    if (nr == 4) return launch_k<QT, NMAT, EPI, MERGE, PX, UT, 4>(a, p, s);
+  }
+  return launch_k<QT, NMAT, EPI, MERGE, PX, UT, 0>(a, p, s);
 }
 
 // x read from the producer's records (a.xr) or staged from a.x by the matvec
