@@ -605,6 +605,9 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
     for_each_index<NR>([&](auto ic) {
       constexpr int i = decltype(ic)::value;
       if (wave + i * S < nu) {   // wave-uniform
+        // a marker per round keeps the compiler from merging the rounds' uses
+        // into one block that picks its registers at run time (through memory)
+        asm volatile("; round %0" ::"n"(i));
         rput<UT>(xw, pick<i>(x0, x1, x2, x3), lane);
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         if (a.nw && lane < UT * kTB * 2) ssq += __int_as_float(xw[lane * kRW + 14]);
@@ -997,17 +1000,26 @@ hipError_t launch_k(const GemvArgs& a, const GemvPlan& p, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Records path of Q4_0 / Q8_0 matrices whose rows take 2 to 4 units per
-// wave: every unit of a wave requested at once (NR rounds).
+// Records path of Q4_0 / Q8_0 matrices with two-tile units whose rows take
+// 2 to 4 units per wave: every unit of a wave requested at once (NR rounds;
+// four-tile units would keep their records in scratch memory).
 template <int QT, int NMAT, int EPI, bool MERGE = false, bool PX = false, int UT = kGemvUnit>
 hipError_t launch_t(const GemvArgs& a, hipStream_t s) {
   const GemvPlan p = gemv_plan(a.rows, a.cols, QT, NMAT, UT);
-  if constexpr (PX && !MERGE && (QT == 2 || QT == 8)) {
+  if constexpr (PX && !MERGE && (QT == 2 || QT == 8) && UT == 2) {   // four-tile units keep their records in scratch
     const int ntk = (a.cols / 32 + kTB - 1) / kTB;
     const int S = p.threads / kWave, nr = ((ntk + UT - 1) / UT + S - 1) / S;
-    if (nr == 2) return launch_k<QT, NMAT, EPI, MERGE, PX, UT, 2>(a, p, s);
-    if (nr == 3) return launch_k<QT, NMAT, EPI, MERGE, PX, UT, 3>(a, p, s);
-    if (nr == 4) return launch_k<QT, NMAT, EPI, MERGE, PX, UT, 4>(a, p, s);
+    // more rounds per wave (up to 7 for the 8B down projection, fewer and
+    // fatter waves) measured slower than the loop over units
+    const int cap = 4;
+    if (nr <= cap) {
+      switch (nr) {
+        case 2: return launch_k<QT, NMAT, EPI, MERGE, PX, UT, 2>(a, p, s);
+        case 3: return launch_k<QT, NMAT, EPI, MERGE, PX, UT, 3>(a, p, s);
+        case 4: return launch_k<QT, NMAT, EPI, MERGE, PX, UT, 4>(a, p, s);
+        default: break;
+      }
+    }
   }
   return launch_k<QT, NMAT, EPI, MERGE, PX, UT, 0>(a, p, s);
 }
