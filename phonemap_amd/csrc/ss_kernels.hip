@@ -250,7 +250,8 @@ __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
   __shared__ float wm[kAttnWaves][G], wl[kAttnWaves][G];
   __shared__ float wo[kAttnWaves][G][HD];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
   const int kvh = blockIdx.y;
   int ctx, chunk, active;
   attn_split(a, ctx, chunk, active);
@@ -259,9 +260,13 @@ __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
   const int t1 = min(ctx, t0 + chunk);
   const int c = lane % kLpr, rsub = lane / kLpr;
 
-  const size_t head_base = (size_t)kvh * a.max_seq;
-  const uint8_t* kb = static_cast<const uint8_t*>(a.kc) + (head_base * HD + c * 8) * kEb;
-  const uint8_t* vb = static_cast<const uint8_t*>(a.vc) + (head_base * HD + c * 8) * kEb;
+  // K and V rows [r0, t1) of this KV head as a buffer view per round (base
+  // and range in scalar registers): a lane's row chunk is one load at a
+  // loop-invariant offset, rows past t1 read zero (and are masked)
+  const size_t head_base = (size_t)kvh * a.max_seq * HD * kEb;
+  const uint8_t* kbase = static_cast<const uint8_t*>(a.kc) + head_base;
+  const uint8_t* vbase = static_cast<const uint8_t*>(a.vc) + head_base;
+  auto row_in = [&](int k) { return (k * kAttnWaves + wave) * kRpi + rsub; };   // row within a round
 
   float q[G][8];
 #pragma unroll
@@ -280,33 +285,54 @@ __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
     for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
   }
 
-  for (int r0 = t0; r0 < t1; r0 += kRound) {
-    Chunk kr[kK], vr[kK];
+  // One round: kK rows of K and V per lane; two rounds in flight (the next
+  // one is requested before the current one is used).
+  struct Round {
+    Chunk k[kK], v[kK];
     float ks[kK], vs[kK];
+  };
+  auto load = [&](Round& rd, int r0) {
+    const int n = max(t1 - r0, 0);   // rows of the round inside the split
+    const __amdgpu_buffer_rsrc_t kx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(kbase + (size_t)r0 * HD * kEb), (short)0, n * HD * kEb, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t vx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(vbase + (size_t)r0 * HD * kEb), (short)0, n * HD * kEb, kBufferFlags);
 #pragma unroll
-    for (int k = 0; k < kK; ++k) {   // branch-free: positions past t1 reload t1-1 and are masked
-      const int p = min(r0 + (k * kAttnWaves + wave) * kRpi + rsub, t1 - 1);
-      kr[k] = *reinterpret_cast<const Chunk*>(kb + (size_t)p * HD * kEb);
-      vr[k] = *reinterpret_cast<const Chunk*>(vb + (size_t)p * HD * kEb);
-      if constexpr (KVT == 1) {
-        ks[k] = a.ks[p];
-        vs[k] = a.vs[p];
+    for (int k = 0; k < kK; ++k) {
+      const int off = row_in(k) * (HD * kEb) + c * 8 * kEb;
+      if constexpr (KVT == 0) {
+        rd.k[k] = __builtin_bit_cast(Chunk, __builtin_amdgcn_raw_buffer_load_b128(kx, off, 0, 0));
+        rd.v[k] = __builtin_bit_cast(Chunk, __builtin_amdgcn_raw_buffer_load_b128(vx, off, 0, 0));
+        rd.ks[k] = rd.vs[k] = 1.f;
       } else {
-        ks[k] = vs[k] = 1.f;
+        rd.k[k] = __builtin_bit_cast(Chunk, __builtin_amdgcn_raw_buffer_load_b64(kx, off, 0, 0));
+        rd.v[k] = __builtin_bit_cast(Chunk, __builtin_amdgcn_raw_buffer_load_b64(vx, off, 0, 0));
+        // the rows' scales (one fp32 per position) through views of the same rows
+        const __amdgpu_buffer_rsrc_t ksx = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(a.ks + r0), (short)0, n * 4, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t vsx = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(a.vs + r0), (short)0, n * 4, kBufferFlags);
+        rd.ks[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ksx, row_in(k) * 4, 0, 0));
+        rd.vs[k] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vsx, row_in(k) * 4, 0, 0));
       }
     }
+  };
+  // cap: the attention softcap is set (decided once, outside the loop, so the
+  // loop has no branch between a round's loads and their use)
+  auto use = [&](const Round& rd, int r0, auto cap) {
     float sc[G][kK];
 #pragma unroll
     for (int k = 0; k < kK; ++k) {
       float kv[8];
-      KE::get(kr[k], ks[k], kv);
-      const bool live = r0 + (k * kAttnWaves + wave) * kRpi + rsub < t1;
+      KE::get(rd.k[k], rd.ks[k], kv);
+      const bool live = r0 + row_in(k) < t1;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float d = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) d = fmaf(q[g][e], kv[e], d);
-        d = softcap(sum_lanes<kLpr>(d) * a.scale, a);   // (q . k) / sqrt(hd), layer_scheduler.c:442-448
+        d = sum_lanes<kLpr>(d) * a.scale;   // (q . k) / sqrt(hd), layer_scheduler.c:442-448
+        if constexpr (decltype(cap)::value) d = softcap(d, a);
         sc[g][k] = live ? d : -INFINITY;
       }
     }
@@ -327,14 +353,40 @@ __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
         const float p = expf(sc[g][k] - mref);
         ps += p;
         float vv[8];
-        KE::get(vr[k], vs[k], vv);
+        KE::get(rd.v[k], rd.vs[k], vv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[g][e] = fmaf(p, vv[e], o[g][e]);
       }
       l[g] = l[g] * corr + wave_sum(c == 0 ? ps : 0.f);
       m[g] = mn;
     }
-  }
+  };
+  // the scheduling barriers keep each round's loads ahead of the other
+  // round's arithmetic (the scheduler would otherwise sink them to their
+  // uses, leaving one round in flight)
+  // The marker starts each loop's version with a different instruction: the
+  // two would otherwise share their first round's loads, hoisted above the
+  // branch, and each copy them into its own registers, waiting for them
+  // before the second round is requested.
+  auto rounds = [&](auto cap) {
+    asm volatile("; softcap %0" ::"n"(decltype(cap)::value ? 1 : 0));
+    Round A, B;
+    load(A, t0);
+    for (int r0 = t0;; r0 += 2 * kRound) {
+      load(B, r0 + kRound);
+      __builtin_amdgcn_sched_barrier(0);
+      use(A, r0, cap);
+      if (r0 + kRound >= t1) break;
+      load(A, r0 + 2 * kRound);
+      __builtin_amdgcn_sched_barrier(0);
+      use(B, r0 + kRound, cap);
+      if (r0 + 2 * kRound >= t1) break;
+    }
+  };
+  if (a.softcap > 0.f)
+    rounds(std::true_type{});
+  else
+    rounds(std::false_type{});
 
   // rows of a wave: lanes with the same column chunk are kLpr apart
 #pragma unroll
@@ -548,7 +600,11 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
   // the scheduling barriers keep each batch's loads ahead of the other
   // batch's arithmetic (the scheduler would otherwise sink them to their
   // uses, leaving one batch in flight)
+  // The marker starts each loop's version with a different instruction (as
+  // in k_attn: shared first-batch loads would be waited for before the
+  // second batch is requested).
   auto batches = [&](auto cap) {
+    asm volatile("; softcap %0" ::"n"(decltype(cap)::value ? 1 : 0));
     Batch A, B;
     load(A, p0);
     for (int pb = p0;; pb += 2 * kB) {
