@@ -332,13 +332,80 @@ __device__ __forceinline__ void load_round(Round<QT, NMAT, UT>& f, const GemvArg
   }
 }
 
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Q4_0 and Q8_0 tiles on the matrix cores. Lane l holds block l/16 of row
+// l%16 (Q4_0: weight j in the low nibble of byte j and weight j+16 in its
+// high nibble; Q8_0: weights 0-15, then 16-31, as int8). Each 16-value half
+// of the tile is one v_mfma_i32_16x16x64_i8: lane l gives its half's 16
+// weights as column l%16 of B at k = 16(l/16) .. +15, and A is block
+// diagonal, row 4b + i holding level i of block b's x record at the same k
+// (lanes l%16 = 4(l/16) + i, i < 3; every other lane gives zeros), so
+// D[4b + i][n], register i of lane l, is the lane's own level-i sum over its
+// half: the integers the sdot4 form (q4_dot, q8_dot) adds, combined the same
+// way, so the results are bit for bit the same. zero: 16 zero bytes in LDS.
+template <int QT, int NMAT, int UT>
+__device__ __forceinline__ void mfma_round(float (&acc)[NMAT], const Round<QT, NMAT, UT>& f, const int* xs,
+                                           const int* zero, int lane) {
+  const int kb = lane >> 4;
+  const bool mine = ((lane & 15) >> 2) == kb && (lane & 3) < 3;
+  // A rows of this lane: word offsets of its level in the tile's records, or
+  // the zero record (which does not move with the tile)
+  const int* a0 = mine ? xs + kb * kXW + 4 * (lane & 3) : zero;
+  const int astep = mine ? kTB * kXW : 0;
+  const int ahalf = mine ? kRW : 0;
+  const v4i z = {0, 0, 0, 0};
+#pragma unroll
+  for (int k = 0; k < UT; ++k) {
+    const uint32_t* ra = reinterpret_cast<const uint32_t*>(xs + (k * kTB + kb) * kXW);
+    const int* pa = a0 + k * astep;
+    const v4i alo = *reinterpret_cast<const v4i*>(pa);
+    const v4i ahi = *reinterpret_cast<const v4i*>(pa + ahalf);
+    const uint2 ta = *reinterpret_cast<const uint2*>(ra + 12);         // (8 sum X, s3) of each half
+    const uint2 tb = *reinterpret_cast<const uint2*>(ra + kRW + 12);
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m) {
+      const uint32_t sw = f.sc[m][k / 2];
+      const uint32_t e = k & 1 ? sw >> 16 : sw & 0xffffu;
+      v4i blo, bhi;
+      if constexpr (QT == 2) {
+        const uint4 q = f.q[m][k][0];
+        blo = v4i{(int)(q.x & 0x0F0F0F0Fu), (int)(q.y & 0x0F0F0F0Fu), (int)(q.z & 0x0F0F0F0Fu),
+                  (int)(q.w & 0x0F0F0F0Fu)};
+        bhi = v4i{(int)((q.x >> 4) & 0x0F0F0F0Fu), (int)((q.y >> 4) & 0x0F0F0F0Fu),
+                  (int)((q.z >> 4) & 0x0F0F0F0Fu), (int)((q.w >> 4) & 0x0F0F0F0Fu)};
+      } else {
+        blo = __builtin_bit_cast(v4i, f.q[m][k][0]);
+        bhi = __builtin_bit_cast(v4i, f.q[m][k][1]);
+      }
+      const v4i dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(alo, blo, z, 0, 0, 0);
+      const v4i dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(ahi, bhi, z, 0, 0, 0);
+      float s;
+      if constexpr (QT == 2) {   // q4_dot: sum X * nibble - 8 sum X, |.| < 2^31 per half
+        const int a = (dl[0] << 14) + (dl[1] << 7) + dl[2];
+        const int b = (dh[0] << 14) + (dh[1] << 7) + dh[2];
+        s = fmaf((float)(a - (int)ta.x), __uint_as_float(ta.y), (float)(b - (int)tb.x) * __uint_as_float(tb.y));
+      } else {                   // q8_dot: levels 1-2 in one integer, level 3 added in fp32
+        const int a12 = (dl[0] << 7) + dl[1], b12 = (dh[0] << 7) + dh[1];
+        s = fmaf(fmaf((float)a12, 128.0f, (float)dl[2]), __uint_as_float(ta.y),
+                 fmaf((float)b12, 128.0f, (float)dh[2]) * __uint_as_float(tb.y));
+      }
+      acc[m] = fmaf(h2f((uint16_t)e), s, acc[m]);
+    }
+  }
+}
+
 // xs holds the unit's staged x records; kb is this lane's block within a
 // tile. Tiles past the row (last unit) meet all-zero records (s3 = 0) and
 // add exactly 0, so every tile is processed and the loads have no
 // conditional use.
 template <int QT, int NMAT, int UT>
 __device__ __forceinline__ void fma_round(float (&acc)[NMAT], const Round<QT, NMAT, UT>& f, const int* xs,
-                                          int kb) {
+                                          int kb, const int* zero, int lane) {
+  if constexpr (QT == 2 || QT == 8) {
+    mfma_round<QT, NMAT, UT>(acc, f, xs, zero, lane);
+    return;
+  }
 #pragma unroll
   for (int k = 0; k < UT; ++k) {
     const uint32_t* ra = reinterpret_cast<const uint32_t*>(xs + (k * kTB + kb) * kXW);
@@ -528,11 +595,14 @@ __device__ __forceinline__ void rput(int* xw, const XRec<UT>& r, int lane) {
 template <int QT, int NMAT, int EPI, int UT, bool MERGE, bool PX, int NR>
 __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(const GemvArgs a) {
   extern __shared__ float4 smem4[];
+  __shared__ v4i zrec[gemv_max_waves<QT, NMAT>()];   // a zero record per wave (matrix-core A rows)
   int* xs = reinterpret_cast<int*>(smem4);
   static_assert(NR == 0 || PX, "rounds issued up front take x from the records");
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (scalar)
+  // written by its own wave before any use (fences below order the accesses)
+  if ((QT == 2 || QT == 8) && lane == 0) zrec[wave] = v4i{0, 0, 0, 0};
   const int S = blockDim.x >> 6;
   const int kb = lane / kRG;
   const int g = blockIdx.x;
@@ -580,7 +650,7 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
       // the slice is written and read by this wave only: LDS operations of a
       // wave complete in order, the fence keeps the compiler from reordering
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-      fma_round<QT, NMAT, UT>(acc, rd, xw, kb);
+      fma_round<QT, NMAT, UT>(acc, rd, xw, kb, reinterpret_cast<const int*>(&zrec[wave]), lane);
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     }
   };
@@ -611,7 +681,7 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
         rput<UT>(xw, pick<i>(x0, x1, x2, x3), lane);
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         if (a.nw && lane < UT * kTB * 2) ssq += __int_as_float(xw[lane * kRW + 14]);
-        fma_round<QT, NMAT, UT>(acc, pick<i>(r0, r1, r2, r3), xw, kb);
+        fma_round<QT, NMAT, UT>(acc, pick<i>(r0, r1, r2, r3), xw, kb, reinterpret_cast<const int*>(&zrec[wave]), lane);
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
       }
     });
