@@ -343,24 +343,26 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // (lanes l%16 = 4(l/16) + i, i < 3; every other lane gives zeros), so
 // D[4b + i][n], register i of lane l, is the lane's own level-i sum over its
 // half: the integers the sdot4 form (q4_dot, q8_dot) adds, combined the same
-// way, so the results are bit for bit the same. zero: 16 zero bytes in LDS.
+// way, so the results are bit for bit the same. zero: kZeroPad<UT> zero
+// words in LDS (the A rows of the other lanes: every tile's offset from it
+// stays inside it, so the addresses differ by constants alone).
+template <int UT>
+constexpr int kZeroPad = ((UT - 1) * kTB * kXW + kRW + 4 + 3) / 4 * 4;
+
 template <int QT, int NMAT, int UT>
 __device__ __forceinline__ void mfma_round(float (&acc)[NMAT], const Round<QT, NMAT, UT>& f, const int* xs,
                                            const int* zero, int lane) {
   const int kb = lane >> 4;
   const bool mine = ((lane & 15) >> 2) == kb && (lane & 3) < 3;
-  // A rows of this lane: word offsets of its level in the tile's records, or
-  // the zero record (which does not move with the tile)
+  // A rows of this lane: its level in the tile's records, or zeros
   const int* a0 = mine ? xs + kb * kXW + 4 * (lane & 3) : zero;
-  const int astep = mine ? kTB * kXW : 0;
-  const int ahalf = mine ? kRW : 0;
   const v4i z = {0, 0, 0, 0};
 #pragma unroll
   for (int k = 0; k < UT; ++k) {
     const uint32_t* ra = reinterpret_cast<const uint32_t*>(xs + (k * kTB + kb) * kXW);
-    const int* pa = a0 + k * astep;
+    const int* pa = a0 + k * kTB * kXW;
     const v4i alo = *reinterpret_cast<const v4i*>(pa);
-    const v4i ahi = *reinterpret_cast<const v4i*>(pa + ahalf);
+    const v4i ahi = *reinterpret_cast<const v4i*>(pa + kRW);
     const uint2 ta = *reinterpret_cast<const uint2*>(ra + 12);         // (8 sum X, s3) of each half
     const uint2 tb = *reinterpret_cast<const uint2*>(ra + kRW + 12);
 #pragma unroll
@@ -595,14 +597,17 @@ __device__ __forceinline__ void rput(int* xw, const XRec<UT>& r, int lane) {
 template <int QT, int NMAT, int EPI, int UT, bool MERGE, bool PX, int NR>
 __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(const GemvArgs a) {
   extern __shared__ float4 smem4[];
-  __shared__ v4i zrec[gemv_max_waves<QT, NMAT>()];   // a zero record per wave (matrix-core A rows)
+  // zeros per wave for the matrix-core A rows (Q4_0, Q8_0)
+  __shared__ v4i zpad[gemv_max_waves<QT, NMAT>()][(QT == 2 || QT == 8) ? kZeroPad<UT> / 4 : 1];
   int* xs = reinterpret_cast<int*>(smem4);
   static_assert(NR == 0 || PX, "rounds issued up front take x from the records");
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform (scalar)
   // written by its own wave before any use (fences below order the accesses)
-  if ((QT == 2 || QT == 8) && lane == 0) zrec[wave] = v4i{0, 0, 0, 0};
+  if constexpr (QT == 2 || QT == 8) {
+    for (int i = lane; i < kZeroPad<UT> / 4; i += kWave) zpad[wave][i] = v4i{0, 0, 0, 0};
+  }
   const int S = blockDim.x >> 6;
   const int kb = lane / kRG;
   const int g = blockIdx.x;
@@ -650,7 +655,7 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
       // the slice is written and read by this wave only: LDS operations of a
       // wave complete in order, the fence keeps the compiler from reordering
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-      fma_round<QT, NMAT, UT>(acc, rd, xw, kb, reinterpret_cast<const int*>(&zrec[wave]), lane);
+      fma_round<QT, NMAT, UT>(acc, rd, xw, kb, reinterpret_cast<const int*>(zpad[wave]), lane);
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
     }
   };
@@ -681,7 +686,7 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
         rput<UT>(xw, pick<i>(x0, x1, x2, x3), lane);
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
         if (a.nw && lane < UT * kTB * 2) ssq += __int_as_float(xw[lane * kRW + 14]);
-        fma_round<QT, NMAT, UT>(acc, pick<i>(r0, r1, r2, r3), xw, kb, reinterpret_cast<const int*>(&zrec[wave]), lane);
+        fma_round<QT, NMAT, UT>(acc, pick<i>(r0, r1, r2, r3), xw, kb, reinterpret_cast<const int*>(zpad[wave]), lane);
         __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
       }
     });
