@@ -1030,24 +1030,38 @@ __global__ void __launch_bounds__(256) k_embed(PackedMat t, int cols, const int*
 
 // Picks the first maximum among per-workgroup candidates, writes it, and for
 // device-side greedy decoding appends it at tokens[pos+1] and advances pos.
-__global__ void k_argmax_merge(const float2* part, int n, const float* y, int* out_idx, int* tokens,
-                               int* dpos) {
-  __shared__ float2 wb[4];
+// One workgroup of kArgmaxThreads; each thread requests up to kArgmaxBatch
+// candidates at once (clamped addresses, the ones past n not compared) before
+// comparing any, so a 128256-row head's 8016 candidates cost one round trip
+// instead of a chain of dependent loads. `beats` is a total order on the
+// non-NaN (value, index) pairs and NaN never wins, so the result does not
+// depend on the order of the comparisons.
+constexpr int kArgmaxThreads = 1024;
+constexpr int kArgmaxBatch = 8;
+
+__global__ void __launch_bounds__(kArgmaxThreads) k_argmax_merge(const float2* part, int n, const float* y,
+                                                                 int* out_idx, int* tokens, int* dpos) {
+  __shared__ float2 wb[kArgmaxThreads / kWave];
   float bv = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = threadIdx.x; i < n; i += 256) {
-    const float2 p = part[i];
-    const int pi = __float_as_int(p.y);
-    if (beats(p.x, pi, bv, bi)) {
-      bv = p.x;
-      bi = pi;
+  for (int i0 = threadIdx.x; i0 < n; i0 += kArgmaxThreads * kArgmaxBatch) {
+    float2 p[kArgmaxBatch];
+#pragma unroll
+    for (int k = 0; k < kArgmaxBatch; ++k) p[k] = part[min(i0 + k * kArgmaxThreads, n - 1)];
+#pragma unroll
+    for (int k = 0; k < kArgmaxBatch; ++k) {
+      const int pi = __float_as_int(p[k].y);
+      if (i0 + k * kArgmaxThreads < n && beats(p[k].x, pi, bv, bi)) {
+        bv = p[k].x;
+        bi = pi;
+      }
     }
   }
   wave_best(bv, bi);
   if ((threadIdx.x & 63) == 0) wb[threadIdx.x >> 6] = make_float2(bv, __int_as_float(bi));
   __syncthreads();
   if (threadIdx.x != 0) return;
-  for (int w = 1; w < 4; ++w)
+  for (int w = 1; w < kArgmaxThreads / kWave; ++w)
     if (beats(wb[w].x, __float_as_int(wb[w].y), bv, bi)) {
       bv = wb[w].x;
       bi = __float_as_int(wb[w].y);
@@ -1218,7 +1232,7 @@ hipError_t launch_gemv(int epi, const GemvArgs& a, hipStream_t s) {
 
 hipError_t launch_argmax_merge(const float2* part, int n, const float* y, int* out_idx, int* tokens,
                                int* dpos, hipStream_t s) {
-  hipLaunchKernelGGL(k_argmax_merge, dim3(1), dim3(256), 0, s, part, n, y, out_idx, tokens, dpos);
+  hipLaunchKernelGGL(k_argmax_merge, dim3(1), dim3(kArgmaxThreads), 0, s, part, n, y, out_idx, tokens, dpos);
   return hipGetLastError();
 }
 
