@@ -94,8 +94,12 @@ __global__ void __launch_bounds__(kFWaves * 64) k_flash_rows(const AttnArgs a) {
   static_assert(kFKeys * CH % (kFWaves * 64) == 0, "K staging rounds");
   static_assert(kVItems <= kFWaves * 64, "V staging items");
 
-  __shared__ v4u ks[2][kFKeys * CH];     // K rows, swizzled slots
-  __shared__ v4u vt[2][HD * kVC];        // V^T rows of the block's keys, swizzled slots
+  // two buffers of each, as separate arrays: the loop names them at compile
+  // time, so the compiler can tell the buffer being read from the one the
+  // direct global-to-LDS loads of the next block fill, and does not wait for
+  // those loads before the current block's reads
+  __shared__ v4u ks0[kFKeys * CH], ks1[kFKeys * CH];   // K rows, swizzled slots
+  __shared__ v4u vt0[HD * kVC], vt1[HD * kVC];         // V^T rows of the block's keys, swizzled slots
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = lane & 15, kq = lane >> 4;
@@ -150,15 +154,14 @@ __global__ void __launch_bounds__(kFWaves * 64) k_flash_rows(const AttnArgs a) {
   const uint16_t* vc = static_cast<const uint16_t*>(a.vc) + head_base;
 
   // K block -> LDS (positions past ctx - 1 reload ctx - 1: finite, masked)
-  auto stage_k = [&](int blk, int buf) {
+  auto stage_k = [&](int blk, v4u* dst) {
 #pragma unroll
     for (int k = 0; k < kFKeys * CH / (kFWaves * 64); ++k) {
       const int P = k * kFWaves * 64 + wave * 64 + lane;   // LDS chunk this lane fills
       const int key = P / CH, slot = P % CH;
       const int p = min(blk * kFKeys + key, ctx - 1);
       const uint16_t* src = kc + (size_t)p * HD + 8 * (slot ^ kswz(key));
-      __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)&ks[buf][k * kFWaves * 64 + wave * 64], 16, 0,
-                                       0);
+      __builtin_amdgcn_global_load_lds((gbl_ptr_t)src, (lds_ptr_t)&dst[k * kFWaves * 64 + wave * 64], 16, 0, 0);
     }
   };
   // V block: thread (kg, c) loads dims 8c..8c+7 of keys 4kg..4kg+3
@@ -173,7 +176,7 @@ __global__ void __launch_bounds__(kFWaves * 64) k_flash_rows(const AttnArgs a) {
       }
     }
   };
-  auto store_v = [&](int buf) {   // dim 8c + j of the 4 keys -> V^T row 8c + j
+  auto store_v = [&](v4u* vdst) {   // dim 8c + j of the 4 keys -> V^T row 8c + j
     if (tid < kVItems) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -183,7 +186,7 @@ __global__ void __launch_bounds__(kFWaves * 64) k_flash_rows(const AttnArgs a) {
           const uint32_t word = j < 2 ? vr[u].x : j < 4 ? vr[u].y : j < 6 ? vr[u].z : vr[u].w;
           w[u] = (j & 1) ? word >> 16 : word & 0xffffu;
         }
-        uint8_t* row = reinterpret_cast<uint8_t*>(&vt[buf][(8 * vch + j) * kVC]);
+        uint8_t* row = reinterpret_cast<uint8_t*>(&vdst[(8 * vch + j) * kVC]);
         *reinterpret_cast<uint2*>(row + 16 * ((vkg >> 1) ^ (j & (kVC - 1))) + 8 * (vkg & 1)) =
             make_uint2(w[0] | (w[1] << 16), w[2] | (w[3] << 16));
       }
@@ -195,18 +198,18 @@ __global__ void __launch_bounds__(kFWaves * 64) k_flash_rows(const AttnArgs a) {
   for (int dt = 0; dt < NDT; ++dt) o[dt] = v4f{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, l = 0.f;   // l: this lane's share of the row's sum
 
-  stage_k(0, 0);
+  stage_k(0, ks0);
   load_v(0);
-  store_v(0);
+  store_v(vt0);
   vm_drain();
   __syncthreads();
-#pragma unroll 1
-  for (int blk = 0; blk < nblk; ++blk) {
-    const int buf = blk & 1;
+  // one block: the next block's K and V requested into the other buffers,
+  // this block's keys used from kcur / vcur
+  auto step = [&](int blk, const v4u* kcur, const v4u* vcur, v4u* knxt, v4u* vnxt) {
     const bool next = blk + 1 < nblk;
     if (next) {
-      stage_k(blk + 1, buf ^ 1);
       load_v(blk + 1);
+      stage_k(blk + 1, knxt);
     }
     const int kb = blk * kFKeys;
     if (kb <= wlim) {
@@ -220,7 +223,7 @@ __global__ void __launch_bounds__(kFWaves * 64) k_flash_rows(const AttnArgs a) {
           v4f acc = v4f{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
           for (int c = 0; c < NC; ++c) {
-            const v8h kv = __builtin_bit_cast(v8h, ks[buf][key * CH + ((4 * c + kq) ^ kswz(key))]);
+            const v8h kv = __builtin_bit_cast(v8h, kcur[key * CH + ((4 * c + kq) ^ kswz(key))]);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, qh[c], acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kv, ql[c], acc, 0, 0, 0);
           }
@@ -269,14 +272,19 @@ __global__ void __launch_bounds__(kFWaves * 64) k_flash_rows(const AttnArgs a) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
           const int d = 16 * dt + n;
-          const v8h vv = __builtin_bit_cast(v8h, vt[buf][d * kVC + ((4 * s + kq) ^ (d & (kVC - 1)))]);
+          const v8h vv = __builtin_bit_cast(v8h, vcur[d * kVC + ((4 * s + kq) ^ (d & (kVC - 1)))]);
           o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, ph[s], o[dt], 0, 0, 0);
           o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vv, pl[s], o[dt], 0, 0, 0);
         }
     }
-    if (next) store_v(buf ^ 1);
+    if (next) store_v(vnxt);
     vm_drain();   // this wave's direct LDS loads of the next block have landed
     __syncthreads();
+  };
+#pragma unroll 1
+  for (int blk = 0; blk < nblk; blk += 2) {
+    step(blk, ks0, vt0, ks1, vt1);
+    if (blk + 1 < nblk) step(blk + 1, ks1, vt1, ks0, vt0);
   }
 
   // lane (n, kq) holds dims 16dt + 4kq .. +3 of row n   (layer_scheduler.c:460-466)
