@@ -256,6 +256,10 @@ __host__ __device__ constexpr int slot_col(int s) {   // column within the block
 // Token blockIdx.x of x (times nw): the scale 1/s_t into xinv[t], then the
 // fp16 parts in slot order (ldxs: row length, a multiple of 128; columns past
 // cols are zero); with ssq set, first its sum of squares (of x alone).
+// Thread i takes the 32-column blocks i, i + 256, ...: a block is 8 float4 of
+// x (and of nw), all requested before any is used, so each pass over the row
+// is one round trip per block a thread holds; a block's four 16-byte chunks
+// of each part are then formed in registers, in slot order.
 template <int QT>
 __global__ void __launch_bounds__(256) k_split_x(const float* __restrict__ x, int ldx, const float* __restrict__ nw,
                                                  int cols, float* __restrict__ ssq, uint16_t* __restrict__ xh,
@@ -263,19 +267,46 @@ __global__ void __launch_bounds__(256) k_split_x(const float* __restrict__ x, in
   __shared__ float red[2][4];
   const int t = blockIdx.x;
   const float* xt = x + (size_t)t * ldx;
-  float ss = 0.f, mx = 0.f;
-  for (int c = threadIdx.x * 4; c < cols; c += 1024) {
-    const float4 v = *reinterpret_cast<const float4*>(xt + c);
-    ss = fmaf(v.x, v.x, ss);
-    ss = fmaf(v.y, v.y, ss);
-    ss = fmaf(v.z, v.z, ss);
-    ss = fmaf(v.w, v.w, ss);
-    float4 u = v;
+  const int nb = cols >> 5;   // cols is a multiple of 32: whole blocks
+  // block blk: v = x, u = x * nw (x when nw is null)
+  auto load_block = [&](int blk, float (&v)[32], float (&u)[32]) {
+    const float4* xp = reinterpret_cast<const float4*>(xt + 32 * blk);
+    float4 xv[8], wv[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) xv[i] = xp[i];
     if (nw) {
-      const float4 w = *reinterpret_cast<const float4*>(nw + c);
-      u = make_float4(v.x * w.x, v.y * w.y, v.z * w.z, v.w * w.w);
+      const float4* wp = reinterpret_cast<const float4*>(nw + 32 * blk);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) wv[i] = wp[i];
     }
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(u.x), fabsf(u.y)), fmaxf(fabsf(u.z), fabsf(u.w))));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      v[4 * i] = xv[i].x;
+      v[4 * i + 1] = xv[i].y;
+      v[4 * i + 2] = xv[i].z;
+      v[4 * i + 3] = xv[i].w;
+      if (nw) {
+        u[4 * i] = xv[i].x * wv[i].x;
+        u[4 * i + 1] = xv[i].y * wv[i].y;
+        u[4 * i + 2] = xv[i].z * wv[i].z;
+        u[4 * i + 3] = xv[i].w * wv[i].w;
+      } else {
+        u[4 * i] = xv[i].x;
+        u[4 * i + 1] = xv[i].y;
+        u[4 * i + 2] = xv[i].z;
+        u[4 * i + 3] = xv[i].w;
+      }
+    }
+  };
+  float ss = 0.f, mx = 0.f;
+  for (int blk = threadIdx.x; blk < nb; blk += 256) {
+    float v[32], u[32];
+    load_block(blk, v, u);
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      ss = fmaf(v[j], v[j], ss);
+      mx = fmaxf(mx, fabsf(u[j]));
+    }
   }
   ss = wave_sum(ss);
   mx = wave_max(mx);
@@ -294,27 +325,30 @@ __global__ void __launch_bounds__(256) k_split_x(const float* __restrict__ x, in
   }
   uint4* oh = reinterpret_cast<uint4*>(xh + (size_t)t * ldxs);
   uint4* ol = reinterpret_cast<uint4*>(xl + (size_t)t * ldxs);
-  for (int c = threadIdx.x; c < ldxs / 8; c += 256) {
-    const int blk = c >> 2, kq = c & 3;
-    const int base = blk * 32;
-    uint32_t h[4], l[4];
+  for (int blk = threadIdx.x; blk < ldxs / 32; blk += 256) {
+    float u[32];
+    if (blk < nb) {
+      float v[32];
+      load_block(blk, v, u);
+    } else {
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float v[2] = {0.f, 0.f};
-      if (base < cols) {   // cols is a multiple of 32: the whole block is there
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const int col = base + slot_col<QT>(8 * kq + 2 * k + q);
-          v[q] = (nw ? xt[col] * nw[col] : xt[col]) * sc;
-        }
-      }
-      const _Float16 a = (_Float16)v[0], b = (_Float16)v[1];
-      const _Float16 la = (_Float16)(v[0] - (float)a), lb = (_Float16)(v[1] - (float)b);
-      h[k] = __builtin_bit_cast(uint32_t, h2{a, b});
-      l[k] = __builtin_bit_cast(uint32_t, h2{la, lb});
+      for (int j = 0; j < 32; ++j) u[j] = 0.f;   // padding columns past cols
     }
-    oh[c] = make_uint4(h[0], h[1], h[2], h[3]);
-    ol[c] = make_uint4(l[0], l[1], l[2], l[3]);
+#pragma unroll
+    for (int kq = 0; kq < 4; ++kq) {   // chunk 4 blk + kq: slots 8 kq .. 8 kq + 7
+      uint32_t h[4], l[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float v0 = u[slot_col<QT>(8 * kq + 2 * k)] * sc;
+        const float v1 = u[slot_col<QT>(8 * kq + 2 * k + 1)] * sc;
+        const _Float16 a = (_Float16)v0, b = (_Float16)v1;
+        const _Float16 la = (_Float16)(v0 - (float)a), lb = (_Float16)(v1 - (float)b);
+        h[k] = __builtin_bit_cast(uint32_t, h2{a, b});
+        l[k] = __builtin_bit_cast(uint32_t, h2{la, lb});
+      }
+      oh[4 * blk + kq] = make_uint4(h[0], h[1], h[2], h[3]);
+      ol[4 * blk + kq] = make_uint4(l[0], l[1], l[2], l[3]);
+    }
   }
 }
 
