@@ -237,6 +237,10 @@ struct QTraits<14> {           // Q6_K: 6-bit codes - 32 as int8
 // 16-value half) and one fp32 rounding per half.
 constexpr int kRW = 16;    // words per x record
 
+// Raw buffer view flags (dword 3 of the descriptor). Loads past the view's
+// range return zero.
+constexpr int kBufferFlags = 0x00020000;
+
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 typedef __attribute__((address_space(1))) void* gbl_ptr_t;
 template <int CTRL>

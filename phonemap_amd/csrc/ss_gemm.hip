@@ -591,14 +591,37 @@ __global__ void __launch_bounds__(kHWaves * 64, 2) k_gemm_h(const GemmArgs a, in
   }
 
   // epilogue: lane holds row g*16 + n of tokens t0 + 16tt + 4kq + i
-  float tsc[kHTiles][4];   // per token: 1/s_t, times the RMSNorm scale
+  // per token: 1/s_t, times the RMSNorm scale. The sums of squares come
+  // through a buffer view (empty without a norm weight: reads return 0 and
+  // the scale is 1), so no branch separates the loads and all are in flight
+  // together.
+  const __amdgpu_buffer_rsrc_t sr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(a.ssq), (short)0, a.nw ? a.T * 4 : 0, kBufferFlags);
+  float tsc[kHTiles][4];
 #pragma unroll
   for (int tt = 0; tt < kHTiles; ++tt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int t = min(t0 + tt * 16 + 4 * kq + i, a.T - 1);
-      tsc[tt][i] = xinv[t] * (a.nw ? 1.0f / sqrtf(a.ssq[t] / (float)a.cols + a.eps) : 1.0f);
+      const float ss = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(sr, t * 4, 0, 0));
+      const float rn = 1.0f / sqrtf(ss / (float)a.cols + a.eps);
+      tsc[tt][i] = xinv[t] * (a.nw ? rn : 1.0f);
     }
+  // the accumulating form reads every old value before it writes any (a
+  // load after a store to y would wait for it: the compiler cannot tell the
+  // addresses apart); clamped addresses, used only where the output exists
+  float yo[kHRG][kHTiles][4];
+  if constexpr (EPI == EPI_ADD) {
+#pragma unroll
+    for (int r = 0; r < kHRG; ++r) {
+      const int row = min((g0 + r) * kRG + n, a.rows - 1);
+#pragma unroll
+      for (int tt = 0; tt < kHTiles; ++tt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          yo[r][tt][i] = a.y[(size_t)min(t0 + tt * 16 + 4 * kq + i, a.T - 1) * a.ldy + row];
+    }
+  }
 #pragma unroll
   for (int r = 0; r < kHRG; ++r) {
     const int g = g0 + r;
@@ -620,7 +643,10 @@ __global__ void __launch_bounds__(kHWaves * 64, 2) k_gemm_h(const GemmArgs a, in
           v = x0;
         }
         float* yp = a.y + (size_t)t * a.ldy + row;
-        *yp = EPI == EPI_ADD ? *yp + v : v;
+        if constexpr (EPI == EPI_ADD)
+          *yp = yo[r][tt][i] + v;
+        else
+          *yp = v;
       }
   }
 }

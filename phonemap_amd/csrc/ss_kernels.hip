@@ -50,9 +50,8 @@ struct KvElem<1> {   // int8 codes times the position's scale (layer_scheduler.c
   }
 };
 
-// Raw buffer view flags (dword 3 of the descriptor) and the sc1 cache
-// policy bit: loads through such a view read the device-coherent level.
-constexpr int kBufferFlags = 0x00020000;
+// The sc1 cache policy bit: loads through a raw buffer view with it read
+// the device-coherent level.
 constexpr int kSc1 = 16;
 
 __device__ __forceinline__ void attn_split(const AttnArgs& a, int& ctx, int& chunk, int& active) {
