@@ -444,19 +444,18 @@ __device__ __forceinline__ void fma_round(float (&acc)[NMAT], const Round<QT, NM
 }
 
 // Pre-encoded x: the unit's records (UT tiles x 4 blocks x 2 records of
-// 64 B, written by the producer of x) copied straight into this wave's LDS
-// region, 16 bytes per lane per instruction. The record buffer is padded
-// with zero records to a multiple of 8 tiles, so the last unit of a row
-// reads zeros past the vector.
+// 64 B, written by the producer of x), 16 bytes per lane per piece, loaded
+// into registers before the unit's weights and written to this wave's LDS
+// slice once they land. The record buffer is padded with zero records to a
+// multiple of 8 tiles, so the last unit of a row reads zeros past the
+// vector. The pieces are separate named registers (an array or a struct
+// here is kept in scratch memory), and going through registers lets the
+// compiler wait for each tile's loads alone: a direct global-to-LDS copy of
+// the records makes it wait for every load of the unit before the first LDS
+// read.
 template <int UT>
-__device__ __forceinline__ void rfetch(int* xw, const uint32_t* __restrict__ xr, int u, int lane) {
-  constexpr int kPieces = UT * kTB * kXW / 4;   // 16-byte pieces of the unit
-  const uint32_t* src = xr + (size_t)u * UT * kTB * kXW;
-#pragma unroll
-  for (int i = 0; i < kPieces; i += kWave)
-    __builtin_amdgcn_global_load_lds((gbl_ptr_t)(src + (size_t)(i + lane) * 4), (lds_ptr_t)(xw + i * 4), 16, 0,
-                                     0);
-}
+constexpr int kRecPieces = UT * kTB * kXW / 4 / kWave;   // 16-byte record pieces per lane
+static_assert(kRecPieces<2> >= 1 && kRecPieces<8> <= 4, "one to four record pieces per lane");
 
 // Epilogue in wave 0: every lane holds row `row`'s final value(s) v[]; lanes
 // with `own` set (one per row) write.
@@ -636,9 +635,19 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
     for (int u = wave; u < nu; u += S) {
       if constexpr (decltype(rec)::value) {
         // records first: vector memory operations complete in order
-        rfetch<UT>(xw, a.xr, u, lane);
+        constexpr int kXP = kRecPieces<UT>;
+        const uint4* xsrc = reinterpret_cast<const uint4*>(a.xr + (size_t)u * UT * kTB * kXW) + lane;
+        const uint4 x0 = xsrc[0];
+        const uint4 x1 = kXP > 1 ? xsrc[kWave] : x0;
+        const uint4 x2 = kXP > 2 ? xsrc[2 * kWave] : x0;
+        const uint4 x3 = kXP > 3 ? xsrc[3 * kWave] : x0;
         load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
-        vm_drain();
+        uint4* xd = reinterpret_cast<uint4*>(xw) + lane;
+        xd[0] = x0;
+        if constexpr (kXP > 1) xd[kWave] = x1;
+        if constexpr (kXP > 2) xd[2 * kWave] = x2;
+        if constexpr (kXP > 3) xd[3 * kWave] = x3;
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");   // other lanes' pieces are written
         if (a.nw && lane < UT * kTB * 2) ssq += __int_as_float(xw[lane * kRW + 14]);
       } else if constexpr (MERGE) {
         MSlice<UT> mp;
