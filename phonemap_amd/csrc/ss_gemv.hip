@@ -615,7 +615,10 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
   const int nu = (ntk + UT - 1) / UT;
   constexpr int kSlice = UT * kTB * kXW;                              // words of one x slice
   int* xw = xs + wave * kSlice;                                       // this wave's x slice
-  float* red = reinterpret_cast<float*>(xs + S * kSlice);              // [NMAT][S][16], then [S]
+  // [NMAT][16 rows][kMaxS waves], then [kMaxS]: a row's wave partials are
+  // contiguous (16-byte aligned: kSlice is a multiple of 4 words)
+  constexpr int kMaxS = gemv_max_waves<QT, NMAT>();
+  float* red = reinterpret_cast<float*>(xs + S * kSlice);
 
   float acc[NMAT];
 #pragma unroll
@@ -718,29 +721,44 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
   for (int m = 0; m < NMAT; ++m) {
     acc[m] += __shfl_xor(acc[m], 16, kWave);
     acc[m] += __shfl_xor(acc[m], 32, kWave);
-    if (lane < kRG) red[(m * S + wave) * kRG + lane] = acc[m];
+    if (lane < kRG) red[(m * kRG + lane) * kMaxS + wave] = acc[m];
   }
   if (a.nw) {
     const float w = wave_sum(ssq);
-    if (lane == 0) red[NMAT * S * kRG + wave] = w;
+    if (lane == 0) red[NMAT * kRG * kMaxS + wave] = w;
   }
   __syncthreads();
   if (wave != 0) return;
   const int r = lane % kRG;
+  // every wave's partials requested at once, 16 bytes per read (slots past
+  // S hold no partial and are not added), then added in wave order
   float v[NMAT];
+  float4 pw[NMAT][kMaxS / 4], pn[kMaxS / 4];
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+    for (int i = 0; i < kMaxS / 4; ++i) pw[m][i] = reinterpret_cast<const float4*>(red + (m * kRG + r) * kMaxS)[i];
+#pragma unroll
+  for (int i = 0; i < kMaxS / 4; ++i) pn[i] = reinterpret_cast<const float4*>(red + NMAT * kRG * kMaxS)[i];
+  auto part = [](const float4& q, int k) { return k == 0 ? q.x : k == 1 ? q.y : k == 2 ? q.z : q.w; };
 #pragma unroll
   for (int m = 0; m < NMAT; ++m) {
     float s = 0.f;
-    for (int w = 0; w < S; ++w) s += red[(m * S + w) * kRG + r];
+#pragma unroll
+    for (int w = 0; w < kMaxS; ++w)
+      if (w < S) s += part(pw[m][w / 4], w % 4);
     v[m] = s;
   }
-  if (a.nw) {   // RMSNorm scale of tensor.c:114-131: 1 / sqrt(mean(x^2) + eps)
-    float t = 0.f;
-    for (int w = 0; w < S; ++w) t += red[NMAT * S * kRG + w];
-    const float scale = 1.0f / sqrtf(t / (float)a.cols + a.eps);
+  // RMSNorm scale of tensor.c:114-131: 1 / sqrt(mean(x^2) + eps), or exactly
+  // 1 without a norm weight (its slots then hold no sums); branch-free, so
+  // the norm partials are requested with the row partials
+  float t = 0.f;
 #pragma unroll
-    for (int m = 0; m < NMAT; ++m) v[m] *= scale;
-  }
+  for (int w = 0; w < kMaxS; ++w)
+    if (w < S) t += part(pn[w / 4], w % 4);
+  const float scale = a.nw ? 1.0f / sqrtf(t / (float)a.cols + a.eps) : 1.0f;
+#pragma unroll
+  for (int m = 0; m < NMAT; ++m) v[m] *= scale;
   epilogue<EPI, NMAT>(a, g * kRG + r, lane < kRG, v, pre);
 }
 
@@ -1173,7 +1191,8 @@ GemvPlan gemv_plan(int rows, int cols, int type, int nmat, int unit) {
   p.unit = ut;
   p.grid = groups;
   p.threads = S * kWave;
-  p.lds_bytes = (size_t)S * ut * kTB * kXW * sizeof(int) + (size_t)(nmat * S * kRG + S) * sizeof(float);
+  // the x slices, then the wave partials padded to smax waves per row
+  p.lds_bytes = (size_t)S * ut * kTB * kXW * sizeof(int) + (size_t)(nmat * kRG * smax + smax) * sizeof(float);
   return p;
 }
 
