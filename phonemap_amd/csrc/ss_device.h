@@ -78,14 +78,16 @@ __device__ __forceinline__ void wave_best(float& bv, int& bi) {
 
 // Attention split of positions 0..ctx-1 over ns workgroups per KV head:
 // chunk positions each, `active` of them non-empty. chunk is ctx / ns
-// rounded up, at least 32, and with fill > 0 at least the smaller of fill
-// and ctx / kMergeSplits rounded up: while splits of at most `fill`
-// positions cover the context, at most kMergeSplits of them are active (a
-// consumer merges that many while staging). Shared by the attention kernel
-// and the consumers that merge its splits, which must pass the same fill.
+// rounded up, at least 32, and with fill > 0 at least fill (one round of
+// attention loads). So while ns * fill covers the context every split is
+// one round starting at split * fill, which the attention can compute
+// before it reads the position, and while kMergeSplits * fill covers it at
+// most kMergeSplits splits are active (a consumer merges that many while
+// staging). Shared by the attention kernel and the consumers that merge
+// its splits, which must pass the same fill.
 __device__ __forceinline__ void attn_chunks(int ctx, int ns, int fill, int& chunk, int& active) {
   chunk = (ctx + ns - 1) / ns;
-  if (fill > 0) chunk = max(chunk, min(fill, (ctx + kMergeSplits - 1) / kMergeSplits));
+  if (fill > 0) chunk = max(chunk, fill);
   if (chunk < 32) chunk = 32;
   active = (ctx + chunk - 1) / chunk;
 }

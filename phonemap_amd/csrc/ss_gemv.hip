@@ -142,8 +142,11 @@ __device__ __forceinline__ int merge_active(const GemvArgs& a) {
   return active;
 }
 
+// lim: slots at or past lim reload slot lim - 1 (the active count, or, before
+// the position is read, the launch's split count: mput then excludes the
+// slots past the active ones by selection)
 template <int UT>
-__device__ __forceinline__ void mfetch(MSlice<UT>& p, const GemvArgs& a, int u, int active, int lane) {
+__device__ __forceinline__ void mfetch(MSlice<UT>& p, const GemvArgs& a, int u, int lim, int lane) {
   const int hd = a.head_dim, G = a.att_group;
   const int hs = __builtin_ctz(hd), gs = __builtin_ctz(G);
 #pragma unroll
@@ -152,11 +155,11 @@ __device__ __forceinline__ void mfetch(MSlice<UT>& p, const GemvArgs& a, int u, 
     const int col = min(u * UT * kTB * 32 + (gi >> 3) * 32 + (gi & 7) * 4, a.cols - 4);
     const int h = col >> hs, d = col & (hd - 1);
     const int kvh = h >> gs, g = h & (G - 1);
-    const size_t im = ((size_t)kvh * a.att_ns + min(lane & 7, active - 1)) * G + g;
+    const size_t im = ((size_t)kvh * a.att_ns + min(lane & 7, lim - 1)) * G + g;
     p.ml[j] = *reinterpret_cast<const float2*>(a.att_ml + im * 2);
 #pragma unroll
     for (int s = 0; s < kMergeSplits; ++s) {
-      const size_t i = ((size_t)kvh * a.att_ns + min(s, active - 1)) * G + g;
+      const size_t i = ((size_t)kvh * a.att_ns + min(s, lim - 1)) * G + g;
       p.o[j][s] = *reinterpret_cast<const float4*>(a.att_o + i * hd + d);
     }
   }
@@ -191,10 +194,13 @@ __device__ __forceinline__ void mput(MSlice<UT>& p, int* xw, int u, int nb, int 
 #pragma unroll
     for (int s = 0; s < kMergeSplits; ++s) {
       const float ws = __shfl(w, (lane & ~7) | s, kWave);   // 0 past the active slots
-      t.x = fmaf(p.o[j][s].x, ws, t.x);
-      t.y = fmaf(p.o[j][s].y, ws, t.y);
-      t.z = fmaf(p.o[j][s].z, ws, t.z);
-      t.w = fmaf(p.o[j][s].w, ws, t.w);
+      // a slot past the active ones may hold an earlier token's partials:
+      // selected out, never multiplied in
+      const float4 o = s < active ? p.o[j][s] : make_float4(0.f, 0.f, 0.f, 0.f);
+      t.x = fmaf(o.x, ws, t.x);
+      t.y = fmaf(o.y, ws, t.y);
+      t.z = fmaf(o.z, ws, t.z);
+      t.w = fmaf(o.w, ws, t.w);
     }
     if (u * UT * kTB + (gi >> 3) >= nb) t = make_float4(0.f, 0.f, 0.f, 0.f);
     encode4(xw + (gi >> 3) * kXW, gi & 7, t);
@@ -633,43 +639,51 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
   // attention wrote its output there itself: one active split directly,
   // more than kMergeSplits through its last split's merge. The choice is
   // made once, outside the loop, so each loop keeps its own load schedule.
-  const int active = MERGE ? merge_active(a) : 0;
-  auto rounds = [&](auto rec) {
-    for (int u = wave; u < nu; u += S) {
-      if constexpr (decltype(rec)::value) {
-        // records first: vector memory operations complete in order
-        constexpr int kXP = kRecPieces<UT>;
-        const uint4* xsrc = reinterpret_cast<const uint4*>(a.xr + (size_t)u * UT * kTB * kXW) + lane;
-        const uint4 x0 = xsrc[0];
-        const uint4 x1 = kXP > 1 ? xsrc[kWave] : x0;
-        const uint4 x2 = kXP > 2 ? xsrc[2 * kWave] : x0;
-        const uint4 x3 = kXP > 3 ? xsrc[3 * kWave] : x0;
-        load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
-        uint4* xd = reinterpret_cast<uint4*>(xw) + lane;
-        xd[0] = x0;
-        if constexpr (kXP > 1) xd[kWave] = x1;
-        if constexpr (kXP > 2) xd[2 * kWave] = x2;
-        if constexpr (kXP > 3) xd[3 * kWave] = x3;
-        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");   // other lanes' pieces are written
-        if (a.nw && lane < UT * kTB * 2) ssq += __int_as_float(xw[lane * kRW + 14]);
-      } else if constexpr (MERGE) {
-        MSlice<UT> mp;
-        mfetch<UT>(mp, a, u, active, lane);
-        load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
-        mput<UT>(mp, xw, u, nb, active, lane);
-      } else {
-        XSlice<UT> xp;
-        xfetch<UT>(xp, a.x, a.nw, u, nb, lane);
-        load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
-        ssq += xput<UT>(xp, xw, a.nw, u, nb, lane);
-      }
-      if constexpr (is_float(QT)) rec_to_float<UT>(xw, lane);
-      // the slice is written and read by this wave only: LDS operations of a
-      // wave complete in order, the fence keeps the compiler from reordering
-      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-      fma_round<QT, NMAT, UT>(acc, rd, xw, kb, reinterpret_cast<const int*>(zpad[wave]), lane);
-      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  // LOAD: the unit's weights are requested here (otherwise before the loop).
+  auto unit = [&](int u, auto rec, auto load, int active) {
+    if constexpr (decltype(rec)::value) {
+      // records first: vector memory operations complete in order
+      constexpr int kXP = kRecPieces<UT>;
+      const uint4* xsrc = reinterpret_cast<const uint4*>(a.xr + (size_t)u * UT * kTB * kXW) + lane;
+      const uint4 x0 = xsrc[0];
+      const uint4 x1 = kXP > 1 ? xsrc[kWave] : x0;
+      const uint4 x2 = kXP > 2 ? xsrc[2 * kWave] : x0;
+      const uint4 x3 = kXP > 3 ? xsrc[3 * kWave] : x0;
+      if constexpr (decltype(load)::value) load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
+      uint4* xd = reinterpret_cast<uint4*>(xw) + lane;
+      xd[0] = x0;
+      if constexpr (kXP > 1) xd[kWave] = x1;
+      if constexpr (kXP > 2) xd[2 * kWave] = x2;
+      if constexpr (kXP > 3) xd[3 * kWave] = x3;
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");   // other lanes' pieces are written
+      if (a.nw && lane < UT * kTB * 2) ssq += __int_as_float(xw[lane * kRW + 14]);
+    } else if constexpr (MERGE) {
+      MSlice<UT> mp;
+      mfetch<UT>(mp, a, u, active, lane);
+      if constexpr (decltype(load)::value) load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
+      mput<UT>(mp, xw, u, nb, active, lane);
+    } else {
+      XSlice<UT> xp;
+      xfetch<UT>(xp, a.x, a.nw, u, nb, lane);
+      if constexpr (decltype(load)::value) load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
+      ssq += xput<UT>(xp, xw, a.nw, u, nb, lane);
     }
+    if constexpr (is_float(QT)) rec_to_float<UT>(xw, lane);
+    // the slice is written and read by this wave only: LDS operations of a
+    // wave complete in order, the fence keeps the compiler from reordering
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    fma_round<QT, NMAT, UT>(acc, rd, xw, kb, reinterpret_cast<const int*>(zpad[wave]), lane);
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  };
+  // PRE: the first unit's weights were requested before the loop (the first
+  // unit is peeled, so no branch sits around a load)
+  auto rounds = [&](auto rec, auto pre, int active) {
+    int u0 = wave;
+    if constexpr (decltype(pre)::value) {
+      unit(wave, rec, std::false_type{}, active);
+      u0 += S;
+    }
+    for (int u = u0; u < nu; u += S) unit(u, rec, std::true_type{}, active);
   };
   // Every unit of the wave in flight at once: unit wave + i*S in round i
   // (rounds past the row reload the last unit, branch-free, and are not
@@ -706,14 +720,29 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
   if constexpr (NR > 0) {
     rounds_all();
   } else if constexpr (PX) {
-    rounds(std::true_type{});
+    rounds(std::true_type{}, std::false_type{}, 0);
   } else if constexpr (MERGE) {
-    if (a.xr && (active == 1 || active > kMergeSplits))
-      rounds(std::true_type{});
-    else
-      rounds(std::false_type{});
+    // The first unit's split partials (every launched split: the position
+    // is not read yet) and weights are requested before the position, which
+    // picks the x path and the active splits; the partials come first, so
+    // the merge does not wait for the weights. wave < S <= nu: every wave
+    // has a first unit.
+    MSlice<UT> mp0;
+    mfetch<UT>(mp0, a, wave, min(a.att_ns, kMergeSplits), lane);
+    load_round<QT, NMAT, UT>(rd, a, g, ntk, wave, lane);
+    const int active = merge_active(a);
+    if (a.xr && (active == 1 || active > kMergeSplits)) {
+      rounds(std::true_type{}, std::true_type{}, active);
+    } else {
+      mput<UT>(mp0, xw, wave, nb, active, lane);
+      if constexpr (is_float(QT)) rec_to_float<UT>(xw, lane);
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      fma_round<QT, NMAT, UT>(acc, rd, xw, kb, reinterpret_cast<const int*>(zpad[wave]), lane);
+      __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+      for (int u = wave + S; u < nu; u += S) unit(u, std::false_type{}, std::true_type{}, active);
+    }
   } else {
-    rounds(std::false_type{});
+    rounds(std::false_type{}, std::false_type{}, 0);
   }
 
   // lanes r, r+16, r+32, r+48 hold row r's four block columns

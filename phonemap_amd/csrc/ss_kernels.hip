@@ -236,7 +236,11 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, int kvh, int acti
   if (tid == 0) cst(a.cnt + kvh, 0u);   // every split of this launch has arrived: ready for the next
 }
 
-template <int HD, int G, int KVT>
+// FIX: every split is one round of kRound positions starting at split *
+// kRound (fill = kRound and ns * kRound covers the cache): the query and the
+// round are requested before the position is read, rows past the context
+// are masked in use, and a split past the active ones leaves after its loads.
+template <int HD, int G, int KVT, bool FIX>
 __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
   using KE = KvElem<KVT>;
   using Chunk = typename KE::Chunk;
@@ -252,11 +256,15 @@ __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform (scalar)
   const int kvh = blockIdx.y;
-  int ctx, chunk, active;
-  attn_split(a, ctx, chunk, active);
-  if ((int)blockIdx.x >= active) return;   // whole workgroup
+  int ctx = 0, chunk = kRound, active = 0;
+  if constexpr (!FIX) {
+    attn_split(a, ctx, chunk, active);
+    if ((int)blockIdx.x >= active) return;   // whole workgroup
+  }
   const int t0 = blockIdx.x * chunk;
-  const int t1 = min(ctx, t0 + chunk);
+  // the end of the split's rows: with FIX, until the position is read, the
+  // end of its round inside the cache (the loads' range)
+  int t1 = FIX ? min(t0 + kRound, a.max_seq) : min(ctx, t0 + chunk);
   const int c = lane % kLpr, rsub = lane / kLpr;
 
   // K and V rows [r0, t1) of this KV head as a buffer view per round (base
@@ -382,10 +390,21 @@ __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
       if (r0 + 2 * kRound >= t1) break;
     }
   };
-  if (a.softcap > 0.f)
+  if constexpr (FIX) {
+    Round A;
+    load(A, t0);
+    attn_split(a, ctx, chunk, active);       // chunk == kRound
+    if ((int)blockIdx.x >= active) return;   // whole workgroup
+    t1 = min(ctx, t0 + kRound);
+    if (a.softcap > 0.f)
+      use(A, t0, std::true_type{});
+    else
+      use(A, t0, std::false_type{});
+  } else if (a.softcap > 0.f) {
     rounds(std::true_type{});
-  else
+  } else {
     rounds(std::false_type{});
+  }
 
   // rows of a wave: lanes with the same column chunk are kLpr apart
 #pragma unroll
@@ -1002,17 +1021,23 @@ hipError_t launch_attn_t(int kv_type, const AttnArgs& a, hipStream_t s) {
     }
     return hipGetLastError();
   } else {
-    if (ev.start) {
-      if (kv_type == 0)
-        hipExtLaunchKernelGGL((k_attn<HD, G, 0>), grid, dim3(kAttnWaves * 64), 0, s, ev.start, ev.stop, 0, a);
-      else
-        hipExtLaunchKernelGGL((k_attn<HD, G, 1>), grid, dim3(kAttnWaves * 64), 0, s, ev.start, ev.stop, 0, a);
-      ev.used = true;
-    } else if (kv_type == 0) {
-      hipLaunchKernelGGL((k_attn<HD, G, 0>), grid, dim3(kAttnWaves * 64), 0, s, a);
-    } else {
-      hipLaunchKernelGGL((k_attn<HD, G, 1>), grid, dim3(kAttnWaves * 64), 0, s, a);
-    }
+    // one-round splits whose starts do not depend on the context (the split
+    // rule of attn_chunks with fill = one round and ns rounds covering the
+    // cache)
+    const int round = attn_round_positions(HD, G);
+    const bool fix = a.split_fill == round && (long)a.ns * round >= a.max_seq;
+    auto go = [&](auto kernel) {
+      if (ev.start) {
+        hipExtLaunchKernelGGL(kernel, grid, dim3(kAttnWaves * 64), 0, s, ev.start, ev.stop, 0, a);
+        ev.used = true;
+      } else {
+        hipLaunchKernelGGL(kernel, grid, dim3(kAttnWaves * 64), 0, s, a);
+      }
+    };
+    if (kv_type == 0)
+      fix ? go(k_attn<HD, G, 0, true>) : go(k_attn<HD, G, 0, false>);
+    else
+      fix ? go(k_attn<HD, G, 1, true>) : go(k_attn<HD, G, 1, false>);
     return hipGetLastError();
   }
 }
@@ -1037,8 +1062,8 @@ const void* attn_kernel_t(int kv_type) {
     return kv_type == 0 ? reinterpret_cast<const void*>(&k_attn_hg<HD, G, 0>)
                         : reinterpret_cast<const void*>(&k_attn_hg<HD, G, 1>);
   else
-    return kv_type == 0 ? reinterpret_cast<const void*>(&k_attn<HD, G, 0>)
-                        : reinterpret_cast<const void*>(&k_attn<HD, G, 1>);
+    return kv_type == 0 ? reinterpret_cast<const void*>(&k_attn<HD, G, 0, false>)
+                        : reinterpret_cast<const void*>(&k_attn<HD, G, 1, false>);
 }
 template <int HD>
 const void* attn_kernel_hd(int group, int kv_type) {
