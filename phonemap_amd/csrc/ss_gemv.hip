@@ -596,10 +596,17 @@ __device__ __forceinline__ void rput(int* xw, const XRec<UT>& r, int lane) {
   for (int i = 0; i < UT * kTB * kXW / 4 / kWave; ++i) reinterpret_cast<uint4*>(xw)[i * kWave + lane] = r.v[i];
 }
 
+// MERGE: how the matvec stages x. kMergeNone: from x or its records.
+// Otherwise it merges the attention's split partials while staging (or, as
+// the attention left them, takes its records): kMergeEarly with at most
+// kMergeSplits splits launched requests the first unit's partials and
+// weights before it reads the position; kMergeLate reads the position first.
+constexpr int kMergeNone = 0, kMergeEarly = 1, kMergeLate = 2;
+
 // NR > 0 (records path, every wave with at most NR units): all of a wave's
 // units are requested at once, their records and weights in registers, and
 // used in order.
-template <int QT, int NMAT, int EPI, int UT, bool MERGE, bool PX, int NR>
+template <int QT, int NMAT, int EPI, int UT, int MERGE, bool PX, int NR>
 __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(const GemvArgs a) {
   extern __shared__ float4 smem4[];
   // zeros per wave for the matrix-core A rows (Q4_0, Q8_0)
@@ -657,7 +664,7 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
       if constexpr (kXP > 3) xd[3 * kWave] = x3;
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");   // other lanes' pieces are written
       if (a.nw && lane < UT * kTB * 2) ssq += __int_as_float(xw[lane * kRW + 14]);
-    } else if constexpr (MERGE) {
+    } else if constexpr (MERGE != kMergeNone) {
       MSlice<UT> mp;
       mfetch<UT>(mp, a, u, active, lane);
       if constexpr (decltype(load)::value) load_round<QT, NMAT, UT>(rd, a, g, ntk, u, lane);
@@ -721,17 +728,29 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
     rounds_all();
   } else if constexpr (PX) {
     rounds(std::true_type{}, std::false_type{}, 0);
-  } else if constexpr (MERGE) {
-    // The first unit's split partials (every launched split: the position
-    // is not read yet) and weights are requested before the position, which
-    // picks the x path and the active splits; the partials come first, so
-    // the merge does not wait for the weights. wave < S <= nu: every wave
-    // has a first unit.
+  } else if constexpr (MERGE == kMergeEarly) {
+    // At most kMergeSplits splits launched: past one active split, Wo
+    // merges them. The first unit's split partials (every launched split:
+    // the position is not read yet) and weights are requested before the
+    // position, which picks the x path and the active splits; the partials
+    // come first, so the merge does not wait for the weights. wave < S <= nu:
+    // every wave has a first unit.
     MSlice<UT> mp0;
     mfetch<UT>(mp0, a, wave, min(a.att_ns, kMergeSplits), lane);
     load_round<QT, NMAT, UT>(rd, a, g, ntk, wave, lane);
     const int active = merge_active(a);
     if (a.xr && (active == 1 || active > kMergeSplits)) {
+      // the partials are not needed here; this use keeps the compiler from
+      // moving their loads into the other branch, behind the position
+#pragma unroll
+      for (int j = 0; j < UT / 2; ++j) {
+        asm volatile("" ::"v"(mp0.ml[j].x), "v"(mp0.ml[j].y));
+#pragma unroll
+        for (int s = 0; s < kMergeSplits; ++s) {
+          const float4 o = mp0.o[j][s];
+          asm volatile("" ::"v"(o.x), "v"(o.y), "v"(o.z), "v"(o.w));
+        }
+      }
       rounds(std::true_type{}, std::true_type{}, active);
     } else {
       mput<UT>(mp0, xw, wave, nb, active, lane);
@@ -741,6 +760,16 @@ __global__ void __launch_bounds__((gemv_max_waves<QT, NMAT>() * 64)) k_gemv(cons
       __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
       for (int u = wave + S; u < nu; u += S) unit(u, std::false_type{}, std::true_type{}, active);
     }
+  } else if constexpr (MERGE == kMergeLate) {
+    // More splits launched (long contexts): past kMergeSplits active ones
+    // the attention's last split merges them into records, so the position
+    // is read first (requesting the partials before it would read them for
+    // nothing there).
+    const int active = merge_active(a);
+    if (a.xr && (active == 1 || active > kMergeSplits))
+      rounds(std::true_type{}, std::false_type{}, active);
+    else
+      rounds(std::false_type{}, std::false_type{}, active);
   } else {
     rounds(std::false_type{}, std::false_type{}, 0);
   }
@@ -1131,7 +1160,7 @@ __global__ void __launch_bounds__(kArgmaxThreads) k_argmax_merge(const float2* p
   }
 }
 
-template <int QT, int NMAT, int EPI, bool MERGE, bool PX, int UT, int NR>
+template <int QT, int NMAT, int EPI, int MERGE, bool PX, int UT, int NR>
 hipError_t launch_k(const GemvArgs& a, const GemvPlan& p, hipStream_t s) {
   KernelEvents& ev = kernel_events();
   if (ev.start) {
@@ -1148,10 +1177,10 @@ hipError_t launch_k(const GemvArgs& a, const GemvPlan& p, hipStream_t s) {
 // Records path of Q4_0 / Q8_0 matrices with two-tile units whose rows take
 // 2 to 4 units per wave: every unit of a wave requested at once (NR rounds;
 // four-tile units would keep their records in scratch memory).
-template <int QT, int NMAT, int EPI, bool MERGE = false, bool PX = false, int UT = kGemvUnit>
+template <int QT, int NMAT, int EPI, int MERGE = kMergeNone, bool PX = false, int UT = kGemvUnit>
 hipError_t launch_t(const GemvArgs& a, hipStream_t s) {
   const GemvPlan p = gemv_plan(a.rows, a.cols, QT, NMAT, UT);
-  if constexpr (PX && !MERGE && (QT == 2 || QT == 8) && UT == 2) {   // four-tile units keep their records in scratch
+  if constexpr (PX && MERGE == kMergeNone && (QT == 2 || QT == 8) && UT == 2) {   // four-tile units keep their records in scratch
     const int ntk = (a.cols / 32 + kTB - 1) / kTB;
     const int S = p.threads / kWave, nr = ((ntk + UT - 1) / UT + S - 1) / S;
     // more rounds per wave (up to 7 for the 8B down projection, fewer and
@@ -1189,8 +1218,14 @@ hipError_t launch_qkv(const GemvArgs& a, hipStream_t s) {
 template <int QT>
 hipError_t launch_q(int epi, const GemvArgs& a, hipStream_t s) {
   switch (epi) {
-    case EPI_STORE: return a.att_o ? launch_t<QT, 1, EPI_STORE, true>(a, s) : launch_x<QT, 1, EPI_STORE>(a, s);
-    case EPI_ADD: return a.att_o ? launch_t<QT, 1, EPI_ADD, true>(a, s) : launch_x<QT, 1, EPI_ADD>(a, s);
+    case EPI_STORE:
+      if (!a.att_o) return launch_x<QT, 1, EPI_STORE>(a, s);
+      return a.att_ns <= kMergeSplits ? launch_t<QT, 1, EPI_STORE, kMergeEarly>(a, s)
+                                      : launch_t<QT, 1, EPI_STORE, kMergeLate>(a, s);
+    case EPI_ADD:
+      if (!a.att_o) return launch_x<QT, 1, EPI_ADD>(a, s);
+      return a.att_ns <= kMergeSplits ? launch_t<QT, 1, EPI_ADD, kMergeEarly>(a, s)
+                                      : launch_t<QT, 1, EPI_ADD, kMergeLate>(a, s);
     case EPI_SWIGLU: return launch_x<QT, 2, EPI_SWIGLU>(a, s);
     case EPI_QKV: return launch_qkv<QT>(a, s);
     case EPI_LOGITS: return launch_x<QT, 1, EPI_LOGITS>(a, s);
