@@ -92,6 +92,12 @@ __device__ __forceinline__ void attn_chunks(int ctx, int ns, int fill, int& chun
   active = (ctx + chunk - 1) / chunk;
 }
 
+// The strided split of the grouped-head attention (groups of 4 or 8 query
+// heads): split s holds positions s, s + ns, s + 2 ns, ..., so the first
+// min(ctx, ns) splits are non-empty. Shared by that attention and the
+// consumers that merge its splits.
+__device__ __forceinline__ int attn_strided_active(int ctx, int ns) { return min(ctx, ns); }
+
 // Packed weight tiles: 16 rows x 4 blocks of 32 columns, one block chunk per
 // lane (layout documented in ss_gemv.hip).
 constexpr int kRowsPerTile = 16;

@@ -136,7 +136,10 @@ struct MSlice {
   float4 o[UT / 2][kMergeSplits];
 };
 
+// the attention's active splits: the strided rule for groups of 4 or 8
+// query heads, the range rule of attn_chunks for 1 or 2
 __device__ __forceinline__ int merge_active(const GemvArgs& a) {
+  if (a.att_group >= 4) return attn_strided_active(*a.dpos + 1, a.att_ns);
   int chunk, active;
   attn_chunks(*a.dpos + 1, a.att_ns, a.att_split_fill, chunk, active);
   return active;

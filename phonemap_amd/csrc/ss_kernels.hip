@@ -54,8 +54,11 @@ struct KvElem<1> {   // int8 codes times the position's scale (layer_scheduler.c
 // the device-coherent level.
 constexpr int kSc1 = 16;
 
+// positions of the context: the device position + 1, or the launch's
+__device__ __forceinline__ int attn_ctx(const AttnArgs& a) { return a.dpos ? *a.dpos + 1 : a.seq_len; }
+
 __device__ __forceinline__ void attn_split(const AttnArgs& a, int& ctx, int& chunk, int& active) {
-  ctx = a.dpos ? *a.dpos + 1 : a.seq_len;
+  ctx = attn_ctx(a);
   attn_chunks(ctx, a.ns, a.split_fill, chunk, active);
 }
 
@@ -126,7 +129,7 @@ __device__ __forceinline__ void attn_finish(const AttnArgs& a, int kvh, int acti
     const int g = i / HD, d = i % HD;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < W; ++w) M = fmaxf(M, wm[w][g]);   // finite: wave 0 has position t0
+    for (int w = 0; w < W; ++w) M = fmaxf(M, wm[w][g]);   // finite: wave 0 holds the split's first position
     float so = 0.f, sl = 0.f;
 #pragma unroll
     for (int w = 0; w < W; ++w) {
@@ -434,12 +437,19 @@ __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
 // head l / (64/G) of the group and dims [c*DPL, c*DPL + DPL), c = l % (64/G),
 // DPL = HD*G/64, so a wave covers all G heads of one K/V row at once (64
 // lanes x DPL = G x HD multiply-adds per position). Scores are summed over
-// the 64/G lanes of a head with DPP. Each wave takes a contiguous share of the
-// workgroup's positions in batches of B rows (all of a batch's K and V
-// loaded before any is used, the next batch's loads issued before the
-// current one is used), keeps an online softmax per head (every lane of a
-// head holds the same m, l), and the waves are combined at the end by
-// attn_finish. Per lane: DPL query values, DPL outputs and two batches.
+// the 64/G lanes of a head with DPP. The positions are split by stride,
+// not by range: workgroup s of a KV head holds positions s, s + ns,
+// s + 2 ns, ..., and wave w of it the positions s + ns (w + 8 r), r = 0, 1,
+// ..., so the rows of every batch are known at launch and the first two
+// batches are requested together with the query, before the position is
+// read (a range split needs the context to place its rows). The first
+// min(ctx, ns) workgroups are active (attn_strided_active, which the
+// consumers merging the splits use too). Each wave takes its rows in
+// batches of B (all of a batch's K and V loaded before any is used, the
+// next batch's loads issued before the current one is used), keeps an
+// online softmax per head (every lane of a head holds the same m, l), and
+// the waves are combined at the end by attn_finish. Per lane: DPL query
+// values, DPL outputs and two batches.
 constexpr int kHgWaves = 8;
 
 // B: rows of K and V per lane per batch; two batches (the one in use and
@@ -505,6 +515,7 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
   constexpr int kDpl = HD / kLph;          // dims per lane
   constexpr int kB = hg_batch(HD, G);
   constexpr int kEb = KVT == 0 ? 2 : 1;
+  constexpr int kRowB = HD * kEb;          // bytes of a K or V row
   using Row = KvRow<KVT, kDpl>;
   static_assert(kLph == 8 || kLph == 16, "heads of 8 or 16 lanes");
 
@@ -516,23 +527,19 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
   // views derived from it stay in scalar registers
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kvh = blockIdx.y;
-  int ctx, chunk, active;
-  attn_split(a, ctx, chunk, active);
-  if ((int)blockIdx.x >= active) return;   // whole workgroup
-  const int t0 = blockIdx.x * chunk;
-  const int t1 = min(ctx, t0 + chunk);
   const int h = lane / kLph, c = lane % kLph;
-  // this wave's positions: a contiguous share of [t0, t1) (wave 0's holds t0)
-  const int per = (t1 - t0 + kHgWaves - 1) / kHgWaves;
-  const int p0 = t0 + wave * per;
-  const int p1 = min(t1, p0 + per);
+  // this wave's rows: positions pw + rstride * r, r = 0, 1, ...; batch b
+  // holds rows b * kB .. b * kB + kB - 1
+  const int ns = a.ns;
+  const int pw = (int)blockIdx.x + ns * wave;
+  const int rstride = ns * kHgWaves;
+  const int rstep = rstride * kRowB;       // bytes between the wave's rows
 
-  // K and V rows [pb, p1) of this KV head as a buffer view per batch (base
-  // and range in scalar registers): row j of the batch is one load at the
-  // constant offset j * HD * kEb past the lane's column offset, rows past p1
-  // read zero (and are masked), and no per-batch address registers are
-  // needed beside the two batches' data
-  const size_t head_base = (size_t)kvh * a.max_seq * HD * kEb;
+  // K and V rows of one batch of this KV head as a buffer view per batch
+  // (base and range in scalar registers): row j of the batch is one load at
+  // j * rstep past the lane's column offset, and rows at or past the view's
+  // limit read zero
+  const size_t head_base = (size_t)kvh * a.max_seq * kRowB;
   const uint8_t* kbase = static_cast<const uint8_t*>(a.kc) + head_base;
   const uint8_t* vbase = static_cast<const uint8_t*>(a.vc) + head_base;
   const int lane_off = c * kDpl * kEb;
@@ -552,23 +559,26 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < kDpl; ++i) o[i] = 0.f;
   float m = -INFINITY, l = 0.f;
+  int ctx = 0;
 
   struct Batch {
     Row k[kB], v[kB];
     float ks[kB], vs[kB];
   };
-  // branch-free: every row of a batch is loaded (rows past p1 read zero
-  // through the view and are masked in use)
-  auto load = [&](Batch& bt, int pb) {
-    const int n = max(p1 - pb, 0);
+  // batch b's rows below lim (the cache's end before the position is read,
+  // the context after); branch-free: every row is loaded and rows past lim
+  // read zero
+  auto load = [&](Batch& bt, int b, int lim) {
+    const int pb = pw + rstride * kB * b;
+    const int n = max(lim - pb, 0);
     const __amdgpu_buffer_rsrc_t kx = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(kbase + (size_t)pb * HD * kEb), (short)0, n * HD * kEb, kBufferFlags);
+        const_cast<uint8_t*>(kbase + (size_t)pb * kRowB), (short)0, n * kRowB, kBufferFlags);
     const __amdgpu_buffer_rsrc_t vx = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(vbase + (size_t)pb * HD * kEb), (short)0, n * HD * kEb, kBufferFlags);
+        const_cast<uint8_t*>(vbase + (size_t)pb * kRowB), (short)0, n * kRowB, kBufferFlags);
 #pragma unroll
     for (int j = 0; j < kB; ++j) {
-      bt.k[j].load(kx, lane_off + j * HD * kEb);
-      bt.v[j].load(vx, lane_off + j * HD * kEb);
+      bt.k[j].load(kx, lane_off + j * rstep);
+      bt.v[j].load(vx, lane_off + j * rstep);
     }
     if constexpr (KVT == 1) {   // the rows' scales, one fp32 per position
       const __amdgpu_buffer_rsrc_t ksx =
@@ -577,71 +587,119 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
           __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.vs + pb), (short)0, n * 4, kBufferFlags);
 #pragma unroll
       for (int j = 0; j < kB; ++j) {
-        bt.ks[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ksx, 4 * j, 0, 0));
-        bt.vs[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vsx, 4 * j, 0, 0));
+        bt.ks[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(ksx, 4 * j * rstride, 0, 0));
+        bt.vs[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vsx, 4 * j * rstride, 0, 0));
       }
     } else {
 #pragma unroll
       for (int j = 0; j < kB; ++j) bt.ks[j] = bt.vs[j] = 1.f;
     }
   };
+  // Rows at or past the context are masked: score -inf, and a V row of
+  // zeros (the first two batches are read up to the cache's end, and a row
+  // there holds whatever an earlier sequence left, so its weight 0 must not
+  // meet a non-finite value). A wave with no row below the context (its
+  // first batch all masked) keeps m = -inf, l = 0, o = 0.
   // cap: the attention softcap is set (decided once, outside the loop, so the
   // loop has no branch between a batch's loads and their use)
-  auto use = [&](const Batch& bt, int pb, auto cap) {
+  auto use = [&](const Batch& bt, int b, auto cap) {
+    const int pb = pw + rstride * kB * b;
     float sc[kB];
+    bool live[kB];
 #pragma unroll
     for (int j = 0; j < kB; ++j) {
+      live[j] = pb + j * rstride < ctx;
       float d = 0.f;
 #pragma unroll
       for (int i = 0; i < kDpl; ++i) d = fmaf(q[i], bt.k[j].get(i, bt.ks[j]), d);
       d = sum_lanes<kLph>(d) * a.scale;   // (q . k) / sqrt(hd), layer_scheduler.c:442-448
       if constexpr (decltype(cap)::value) d = softcap(d, a);
-      sc[j] = pb + j < p1 ? d : -INFINITY;
+      sc[j] = live[j] ? d : -INFINITY;
     }
-    float bm = sc[0];                      // live: pb < p1
+    float bm = sc[0];
 #pragma unroll
     for (int j = 1; j < kB; ++j) bm = fmaxf(bm, sc[j]);
     const float mn = fmaxf(m, bm);
-    const float corr = expf(m - mn);      // 0 on the first batch (m = -inf)
+    const float mref = mn == -INFINITY ? 0.f : mn;   // nothing live yet: every weight 0
+    const float corr = expf(m - mref);               // 0 while m = -inf
     l *= corr;
 #pragma unroll
     for (int i = 0; i < kDpl; ++i) o[i] *= corr;
 #pragma unroll
     for (int j = 0; j < kB; ++j) {
-      const float pj = expf(sc[j] - mn);
+      const float pj = expf(sc[j] - mref);
       l += pj;
+      Row v = bt.v[j];
+      float vs = bt.vs[j];
+      if constexpr (KVT == 0) {
 #pragma unroll
-      for (int i = 0; i < kDpl; ++i) o[i] = fmaf(pj, bt.v[j].get(i, bt.vs[j]), o[i]);
+        for (int w = 0; w < Row::kWords; ++w) v.w[w] = live[j] ? v.w[w] : 0u;
+      } else {
+        vs = live[j] ? vs : 0.f;   // int8 codes are finite: a zero scale zeroes the row
+      }
+#pragma unroll
+      for (int i = 0; i < kDpl; ++i) o[i] = fmaf(pj, v.get(i, vs), o[i]);
     }
     m = mn;
   };
-  // the scheduling barriers keep each batch's loads ahead of the other
-  // batch's arithmetic (the scheduler would otherwise sink them to their
-  // uses, leaving one batch in flight)
-  // The marker starts each loop's version with a different instruction (as
-  // in k_attn: shared first-batch loads would be waited for before the
-  // second batch is requested).
-  auto batches = [&](auto cap) {
-    asm volatile("; softcap %0" ::"n"(decltype(cap)::value ? 1 : 0));
-    Batch A, B;
-    load(A, p0);
-    for (int pb = p0;; pb += 2 * kB) {
-      load(B, pb + kB);
-      __builtin_amdgcn_sched_barrier(0);
-      use(A, pb, cap);
-      if (pb + kB >= p1) break;
-      load(A, pb + 2 * kB);
-      __builtin_amdgcn_sched_barrier(0);
-      use(B, pb + kB, cap);
-      if (pb + 2 * kB >= p1) break;
+  // a use of a batch's registers, on a path that does not read them: keeps
+  // their loads where they are written (ahead of the position's read) rather
+  // than sunk to the path that does
+  auto pin = [&](const Batch& bt) {
+#pragma unroll
+    for (int j = 0; j < kB; ++j) {
+#pragma unroll
+      for (int w = 0; w < Row::kWords; ++w) asm volatile("" ::"v"(bt.k[j].w[w]), "v"(bt.v[j].w[w]));
+      if constexpr (KVT == 1) asm volatile("" ::"v"(bt.ks[j]), "v"(bt.vs[j]));
     }
   };
-  if (p0 < p1) {
-    if (a.softcap > 0.f)
-      batches(std::true_type{});
-    else
-      batches(std::false_type{});
-  }
+  // The query, the position and batches 0 and 1 are requested together (the
+  // position first: loads complete in order, so the wait for it does not
+  // include the batches). The scheduling barriers keep each batch's loads
+  // ahead of the other batch's arithmetic (the scheduler would otherwise
+  // sink them to their uses, leaving one batch in flight). The marker
+  // starts each version with a different instruction (shared first loads
+  // would be hoisted above the branch and copied into each version's
+  // registers, a wait for them before the second batch is requested).
+  // Returns the active split count.
+  auto run = [&](auto cap) -> int {
+    asm volatile("; softcap %0" ::"n"(decltype(cap)::value ? 1 : 0));
+    // the device position through a view (of range 0, reading zero, when
+    // the launch gives the context): no branch, so nothing waits for it
+    // before the batches are requested
+    const __amdgpu_buffer_rsrc_t px = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<int*>(a.dpos), (short)0, a.dpos ? 4 : 0, kBufferFlags);
+    const int dp = __builtin_amdgcn_raw_buffer_load_b32(px, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    Batch A, B;
+    load(A, 0, a.max_seq);
+    load(B, 1, a.max_seq);
+    __builtin_amdgcn_sched_barrier(0);
+    ctx = a.dpos ? dp + 1 : a.seq_len;
+    const int active = attn_strided_active(ctx, ns);
+    if ((int)blockIdx.x >= active) {   // whole workgroup
+      pin(A);
+      pin(B);
+#pragma unroll
+      for (int i = 0; i < kDpl; ++i) asm volatile("" ::"v"(q[i]));
+      return active;
+    }
+    const int nr = pw < ctx ? (ctx - 1 - pw) / rstride + 1 : 0;   // the wave's rows below ctx
+    const int nb = (nr + kB - 1) / kB;
+    for (int b = 0;; b += 2) {
+      use(A, b, cap);
+      if (b + 1 >= nb) break;
+      load(A, b + 2, ctx);
+      __builtin_amdgcn_sched_barrier(0);
+      use(B, b + 1, cap);
+      if (b + 2 >= nb) break;
+      load(B, b + 3, ctx);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    return active;
+  };
+  const int active = a.softcap > 0.f ? run(std::true_type{}) : run(std::false_type{});
+  if ((int)blockIdx.x >= active) return;
 
   if (c == 0) {
     wm[wave][h] = m;   // a wave without positions: -inf and 0, weight 0 below
@@ -694,8 +752,7 @@ __global__ void __launch_bounds__(kWave) k_attn_merge(const AttnArgs a) {
   float4 v[kBatch];
 #pragma unroll
   for (int k = 0; k < kBatch; ++k) v[k] = po[(size_t)min(sub + 4 * k, ns - 1) * kQuads];
-  int ctx, chunk, active;
-  attn_split(a, ctx, chunk, active);
+  const int active = attn_strided_active(attn_ctx(a), ns);
   if (active <= 1) return;   // whole workgroup: the attention wrote the output
   float mx = -INFINITY;
 #pragma unroll
