@@ -655,7 +655,8 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
   };
   // The query, the position and batches 0 and 1 are requested together (the
   // position first: loads complete in order, so the wait for it does not
-  // include the batches). The scheduling barriers keep each batch's loads
+  // include the batches); then each use is followed by the request of the
+  // batch two further on. The scheduling barriers keep each batch's loads
   // ahead of the other batch's arithmetic (the scheduler would otherwise
   // sink them to their uses, leaving one batch in flight). The marker
   // starts each version with a different instruction (shared first loads
@@ -686,15 +687,34 @@ __global__ void __launch_bounds__(kHgWaves * 64) k_attn_hg(const AttnArgs a) {
     }
     const int nr = pw < ctx ? (ctx - 1 - pw) / rstride + 1 : 0;   // the wave's rows below ctx
     const int nb = (nr + kB - 1) / kB;
-    for (int b = 0;; b += 2) {
+    // No batch past the wave's last is requested: a load returns in order
+    // behind the others, out of range or not, and the barrier before the
+    // waves combine waits for it, a whole round trip at the tail. So pairs
+    // of batches run while both reloads are needed, and the last one to
+    // three batches are taken apart. The barriers before the reloads keep
+    // each use ahead of its batch's reload (a reload overlapping the use
+    // would take fresh registers, copied back at the loop's end, which
+    // waits for every load).
+    int b = 0;
+    for (; b + 3 < nb; b += 2) {
       use(A, b, cap);
-      if (b + 1 >= nb) break;
+      __builtin_amdgcn_sched_barrier(0);
       load(A, b + 2, ctx);
       __builtin_amdgcn_sched_barrier(0);
       use(B, b + 1, cap);
-      if (b + 2 >= nb) break;
+      __builtin_amdgcn_sched_barrier(0);
       load(B, b + 3, ctx);
       __builtin_amdgcn_sched_barrier(0);
+    }
+    use(A, b, cap);   // a wave without rows: all masked
+    if (b + 2 < nb) {
+      __builtin_amdgcn_sched_barrier(0);
+      load(A, b + 2, ctx);
+      __builtin_amdgcn_sched_barrier(0);
+      use(B, b + 1, cap);
+      use(A, b + 2, cap);
+    } else if (b + 1 < nb) {
+      use(B, b + 1, cap);
     }
     return active;
   };
