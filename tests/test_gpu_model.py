@@ -83,6 +83,28 @@ def test_greedy_and_logits(spec, kv, launch):
     om.close()
 
 
+@pytest.mark.parametrize("kv", ["f16", "int8"])
+def test_decode_from_position_zero(kv):
+    """Query groups of 8 with 4 attention splits per KV head (split s holds
+    positions s, s + 4, ...), decoding from position 0: at position 0 one
+    split is active and the attention writes Wo's x records itself; at
+    positions 1-3, two to four splits are active and Wo merges them while
+    staging, the inactive ones selected out. Logits within the bar of the
+    oracle's at every step, identical argmax."""
+    path = _model_file("gqa8", **GQA8)
+    om = oracle.Model(path, 128, kv)
+    tol = TOL if kv == "f16" else TOL_INT8
+    with api.Model(path, max_context=128, kv=kv) as m:
+        tok = 17
+        for pos in range(8):
+            lg, am = m.eval_token(tok, pos)
+            olg = om.forward(tok, pos)
+            assert rel_err(lg, olg) <= tol, pos
+            assert am == oracle.argmax(olg) == int(np.argmax(lg)), pos
+            tok = am
+    om.close()
+
+
 @pytest.mark.parametrize("launch", ["graph", "eager"])
 def test_int8_cache_step_at_fp32_tolerance(launch):
     """int8 KV at the fp16 bar: the same fp16 rows written into both caches
@@ -128,8 +150,9 @@ def test_long_context_split_merge_path(kv):
     attention splits per KV head (one workgroup per compute unit), merged by
     k_attn_merge into Wo's x records. K/V injected at positions 0..1099 (the
     same fp16 rows into the oracle's cache), then decode from position 1100:
-    splits of 32 positions, so 35 are active. That takes the merge kernel
-    past its first batch of 32 splits, with (m, l) slots up to 127. Logits
+    split s takes positions s, s + 128, ..., so all 128 are active. That
+    takes the merge kernel through four batches of 32 splits, with (m, l)
+    slots up to 127. Logits
     within the bar of the oracle's at every step (the fp64 model's distance
     printed beside it), identical argmax, and the model responding to its
     input."""
