@@ -39,6 +39,11 @@ struct KvElem<0> {   // binary16, 8 elements = 16 bytes
     }
     (void)s;
   }
+  // the chunk, or zeros for a row that is not live
+  static __device__ __forceinline__ Chunk live_or_zero(const Chunk& c, float& s, bool live) {
+    (void)s;
+    return make_uint4(live ? c.x : 0u, live ? c.y : 0u, live ? c.z : 0u, live ? c.w : 0u);
+  }
 };
 template <>
 struct KvElem<1> {   // int8 codes times the position's scale (layer_scheduler.c:120-125)
@@ -47,6 +52,11 @@ struct KvElem<1> {   // int8 codes times the position's scale (layer_scheduler.c
     const uint32_t w[2] = {c.x, c.y};
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[i] = (float)(int8_t)((w[i / 4] >> (8 * (i % 4))) & 0xffu) * s;
+  }
+  // a row that is not live: scale 0 (the codes are finite)
+  static __device__ __forceinline__ Chunk live_or_zero(const Chunk& c, float& s, bool live) {
+    s = live ? s : 0.f;
+    return c;
   }
 };
 
@@ -346,6 +356,16 @@ __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
         sc[g][k] = live ? d : -INFINITY;
       }
     }
+    // V rows, zeroed where not live: a row past the end reads zero, or, in a
+    // round requested before the position was read, whatever an earlier
+    // sequence left there, and its weight 0 must not meet a non-finite value
+    typename KE::Chunk vm[kK];
+    float vsm[kK];
+#pragma unroll
+    for (int k = 0; k < kK; ++k) {
+      vsm[k] = rd.vs[k];
+      vm[k] = KE::live_or_zero(rd.v[k], vsm[k], r0 + row_in(k) < t1);
+    }
 #pragma unroll
     for (int g = 0; g < G; ++g) {
       float mt = sc[g][0];
@@ -363,7 +383,7 @@ __global__ void __launch_bounds__(kAttnWaves * 64) k_attn(const AttnArgs a) {
         const float p = expf(sc[g][k] - mref);
         ps += p;
         float vv[8];
-        KE::get(rd.v[k], rd.vs[k], vv);
+        KE::get(vm[k], vsm[k], vv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[g][e] = fmaf(p, vv[e], o[g][e]);
       }

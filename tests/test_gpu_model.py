@@ -105,6 +105,35 @@ def test_decode_from_position_zero(kv):
     om.close()
 
 
+@pytest.mark.parametrize("spec", ["tiny", "gqa8"])
+def test_stale_rows_past_the_context(spec):
+    """The attention requests its first rows before it reads the device
+    position: the whole first round (groups of 2) or batches up to the
+    cache's end (groups of 8), rows past the context included, masked once
+    the context is known. Rows 8..127 of every layer's cache hold fp16 NaN
+    and Inf (as a cache may after an earlier sequence): decoding positions
+    0..7 must match the oracle, whose cache holds only the live rows."""
+    kw = {"tiny": TINY, "gqa8": GQA8}[spec]
+    path = _model_file(spec, **kw)
+    kvd = kw["n_kv_heads"] * kw["head_dim"]
+    bad = np.full((120, kvd), 0x7E00, np.uint16)   # quiet NaN
+    bad[::2] = 0x7C00                              # +Inf
+    om = oracle.Model(path, 128, "f16")
+    with api.Model(path, max_context=128, kv="f16") as m:
+        m.reset()
+        for layer in range(kw["n_layers"]):
+            m.kv_write(layer, 8, bad, bad)
+        tok = 23
+        for pos in range(8):
+            lg, am = m.eval_token(tok, pos)
+            olg = om.forward(tok, pos)
+            assert np.all(np.isfinite(lg)), pos
+            assert rel_err(lg, olg) <= TOL, pos
+            assert am == oracle.argmax(olg), pos
+            tok = am
+    om.close()
+
+
 @pytest.mark.parametrize("launch", ["graph", "eager"])
 def test_int8_cache_step_at_fp32_tolerance(launch):
     """int8 KV at the fp16 bar: the same fp16 rows written into both caches
